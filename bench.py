@@ -1,0 +1,217 @@
+#!/usr/bin/env python
+"""Benchmark of the MI355X q2fp8 pruned decode.
+
+Workload: one decode-attention step ("layer-step") of batch 1 over a 32K
+context, 32 query / 8 KV heads, head dim 128.  K is 2-bit (groups of 32 along
+D, fp16 scale/zero per token) plus an fp8 e4m3 residual, V is bf16, paged in
+64-token pages through a seeded random page table; 16 heavy tokens per query
+head are planted (cosine 0.8 with q).  Inputs are synthetic (seeded), already
+resident in HBM when timing starts.
+
+To keep the 256 MB Infinity Cache from serving repeated steps, R (default 24)
+copies of the cache live in distinct pages and consecutive steps rotate over
+them; the R steps are captured in one HIP graph that is replayed.
+
+Prints one JSON line: value = microseconds per layer-step (lower is better),
+with the achieved HBM bandwidth on the algorithmic bytes, the roofline object
+of the decode and the CPU oracle timed on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "ffa-speedtest_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E peak (AMD spec)
+PAGE = 64
+
+
+def algorithmic_bytes(T_list, HKV, HQ, kept_tokens_heads, D=128):
+    """Bytes one layer-step must touch: every token's codes + g32 scale/zero, the fp8 residual and bf16 V of
+    kept tokens, q, o and the page table."""
+    every = sum(T_list) * HKV * (D // 4 + (D // 32) * 4)
+    kept = kept_tokens_heads * (D + 2 * D)
+    consts = len(T_list) * HQ * D * 2 * 2 + sum(-(-t // PAGE) for t in T_list) * 4
+    return every + kept + consts
+
+
+def kept_token_heads(mask, T, SBS):
+    """Tokens (x KV heads) inside kept blocks, counting only tokens < T."""
+    import torch
+
+    nb = mask.shape[-1]
+    valid = torch.clamp(T - torch.arange(nb, device=mask.device) * SBS, min=0, max=SBS)
+    return int((mask.to(torch.int64) * valid).sum().item())
+
+
+def cpu_baseline(q, k, v, BS, SBS, delta, seconds):
+    """The numpy oracle on this host (1 thread) on the same workload: microseconds per layer-step."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import q2fp8 as O
+
+    kf = k.float().numpy()
+    pk, s, z, r = O.quantize_g32(kf, "e4m3fn")  # cache building, not timed
+    qf, vf = q.float().numpy(), v.float().numpy()
+    times = []
+    with threadpool_limits(1):
+        t_end = time.perf_counter() + seconds
+        while True:
+            t0 = time.perf_counter()
+            O.decode(qf, pk, s, z, vf, r, res_fmt="e4m3fn", BS=BS, SBS=SBS, delta=delta, scale_mode="g32",
+                     out_dtype="bf16")
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() > t_end and len(times) >= 3:
+                break
+    del np
+    return statistics.median(times) * 1e6, len(times)
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=480, help="timed layer-steps")
+    ap.add_argument("--warmup", type=int, default=96, help="untimed layer-steps")
+    ap.add_argument("--rotations", type=int, default=24, help="distinct cache copies (defeats the 256 MB MALL)")
+    ap.add_argument("--T", type=int, default=32768)
+    ap.add_argument("--BS", type=int, default=64)
+    ap.add_argument("--SBS", type=int, default=64)
+    ap.add_argument("--delta", type=float, default=5.0)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build runs on one GPU: the decode shards by KV head / sequence without "
+                                   "changing the per-GPU kernel (see DESIGN.md); --gpus must be 1"}))
+        sys.exit(2)
+
+    import torch
+
+    from ffa_mi355x import synth
+    from ffa_mi355x.decode import DecodeWorkspace
+    from ffa_mi355x.paged import PagedQ2Cache
+
+    dev = torch.device("cuda:0")
+    B, HQ, HKV, D, T, R = 1, 32, 8, 128, args.T, args.rotations
+    t_setup = time.perf_counter()
+    q, k, v = synth.attention_inputs(B=B, T=T, HQ=HQ, HKV=HKV, D=D, seed=0, n_heavy=16, cos=0.8)
+    npg = -(-T // PAGE)
+    bt0, _ = synth.page_tables([T], seed=0)
+    cache = PagedQ2Cache(npg * R, HKV, dev)
+    kd, vd = k.to(dev), v.to(dev)
+    pos = torch.zeros(B, dtype=torch.int32, device=dev)
+    bts = []
+    for r in range(R):
+        bt = (bt0 + r * npg).to(dev)
+        cache.append(kd, vd, pos, bt)
+        bts.append(bt)
+    qd = q.to(dev)
+    del kd, vd
+    ws = DecodeWorkspace(B, HQ, HKV, T, args.BS, args.SBS, dev, torch.bfloat16)
+    seq_lens = torch.full((B,), T, dtype=torch.int32, device=dev)
+
+    def step(r):
+        cache.decode(qd, bts[r], seq_lens, T=T, BS=args.BS, SBS=args.SBS, delta=args.delta, workspace=ws)
+
+    for r in range(R):  # eager warmup of every rotation
+        step(r)
+    step(0)
+    torch.cuda.synchronize()
+    outs = [ws.o.clone()]
+    mask = ws.mask_buf.clone()
+    step(R - 1)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], ws.o), "rotations must give identical outputs"
+
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        step(0)  # prime on the capture stream
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph, stream=stream):
+        for r in range(R):
+            step(r)
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t_setup
+
+    n_warm = max(1, math.ceil(args.warmup / R))
+    n_rep = max(1, math.ceil(args.steps / R))
+    for _ in range(n_warm):
+        graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], ws.o), "graph replay must match eager"
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    cur = torch.cuda.current_stream()
+    start.record(cur)
+    for _ in range(n_rep):
+        graph.replay()
+    end.record(cur)
+    torch.cuda.synchronize()
+    steps = n_rep * R
+    ms_total = start.elapsed_time(end)
+    us_per_step = ms_total * 1e3 / steps
+
+    kept_th = kept_token_heads(mask, T, args.SBS)
+    keep_frac = float(mask.float().mean().item())
+    nbytes = algorithmic_bytes([T] * B, HKV, HQ, kept_th, D)
+    achieved_gbs = nbytes / (us_per_step * 1e-6) / 1e9
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu_us, n = cpu_baseline(q, k, v, args.BS, args.SBS, args.delta, args.cpu_seconds)
+        cpu = {"value": round(cpu_us, 1), "unit": "us/layer", "cores": 1, "kind": "port",
+               "sample": f"full workload (B=1, T={T}, 32/8/128, g32 q2 + e4m3 residual), numpy oracle, "
+                         f"1 thread, median of {n} runs; cache quantization not timed"}
+
+    line = {
+        "metric": "q2fp8 decode-attn us/layer + HBM TB/s (% of peak) at 32K ctx, bs=1",
+        "value": round(us_per_step, 3),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": n_warm * R,
+        "ms_per_step": round(us_per_step / 1e3, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q2+fp8(e4m3) K, bf16 V; f16/bf16 MFMA, f32 accumulate",
+        "data": "synthetic (seeded N(0,1) bf16 with planted heavy tokens)",
+        "hbm_tbps": round(achieved_gbs / 1e3, 4),
+        "hbm_pct_peak": round(100.0 * achieved_gbs / HBM_PEAK_GBS, 2),
+        "config": {
+            "workload": "BASELINE config 2: q2fp8 pruned decode, bs=1, 32K ctx, 32/8/128, 64-token pages",
+            "B": B, "T": T, "HQ": HQ, "HKV": HKV, "D": D, "BS": args.BS, "SBS": args.SBS, "delta": args.delta,
+            "keep_fraction": round(keep_frac, 4), "algorithmic_bytes": nbytes, "rotations": R,
+            "timing": "HIP graph of R rotated steps, hipEvent over the replays",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "decode step (score/prune/exact kernel + merge kernel), per launch",
+        },
+        "cpu_baseline": cpu,
+        "setup_s": round(setup_s, 1),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

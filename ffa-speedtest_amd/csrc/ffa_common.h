@@ -1,0 +1,124 @@
+// Shared device helpers for the gfx950 kernels of this library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ffa {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ---------------------------------------------------------------------------
+// scalar conversions
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  // round-to-nearest-even, NaN kept quiet (same rule as torch's bf16 cast)
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t b) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)b);
+}
+
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// load element i of a float tensor of runtime dtype (0=f16, 1=bf16, 2=f32)
+__device__ __forceinline__ float load_any(const void *p, size_t i, int dt) {
+  if (dt == 2) return ((const float *)p)[i];
+  uint32_t b = ((const uint16_t *)p)[i];
+  return dt == 1 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+}
+
+__device__ __forceinline__ void store_any(void *p, size_t i, int dt, float v) {
+  if (dt == 2) {
+    ((float *)p)[i] = v;
+  } else if (dt == 1) {
+    ((uint16_t *)p)[i] = (uint16_t)f32_to_bf16_bits(v);
+  } else {
+    ((uint16_t *)p)[i] = (uint16_t)f32_to_f16_bits(v);
+  }
+}
+
+// round a float to the given float dtype and back (0=f16, 1=bf16, 2=f32)
+__device__ __forceinline__ float round_to(float v, int dt) {
+  if (dt == 2) return v;
+  if (dt == 1) return bf16_bits_to_f32(f32_to_bf16_bits(v));
+  return (float)(_Float16)v;
+}
+
+// ---------------------------------------------------------------------------
+// fp8 (OCP e4m3fn / e5m2) encode with torch's rules: RNE, e4m3fn overflow -> NaN,
+// e5m2 overflow -> inf.  Written from the format definitions.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t f32_to_fp8(float x, int e4m3) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7fffffffu;
+  const int mbits = e4m3 ? 3 : 2;
+  const int bias = e4m3 ? 7 : 15;
+  const int emin = 1 - bias;  // smallest normal exponent
+  if (a > 0x7f800000u) return sign | 0x7fu;  // NaN
+  if (a == 0x7f800000u) return e4m3 ? (sign | 0x7fu) : (sign | 0x7cu);
+  const int e = (int)(a >> 23) - 127;  // unbiased exponent of the input (normal inputs)
+  uint32_t bits;
+  if (a < 0x00800000u || e < emin) {
+    // result is subnormal (or zero) in fp8: quantum 2^(emin - mbits); RNE via float add
+    // (|x| < 2^emin, so x + 2^(emin) * 2^? ... use explicit integer rounding)
+    const float q = __uint_as_float((uint32_t)(127 + emin - mbits) << 23);  // 2^(emin-mbits)
+    const float r = __uint_as_float(a) / q;                                 // exact (power of 2)
+    const float ri = __builtin_rintf(r);                                    // RNE
+    bits = (uint32_t)ri;  // may equal 1 << mbits => smallest normal, encodes correctly
+  } else {
+    // normal: keep mbits of mantissa with RNE
+    const uint32_t shift = 23 - mbits;
+    uint32_t mant = a & 0x7fffffu;
+    uint32_t keep = mant >> shift;
+    const uint32_t rem = mant & ((1u << shift) - 1u);
+    const uint32_t half = 1u << (shift - 1);
+    uint32_t exp8 = (uint32_t)(e + bias);
+    if (rem > half || (rem == half && (keep & 1u))) {
+      keep += 1;
+      if (keep == (1u << mbits)) {
+        keep = 0;
+        exp8 += 1;
+      }
+    }
+    bits = (exp8 << mbits) | keep;
+  }
+  if (e4m3) {
+    if (bits > 0x7eu) return sign | 0x7fu;  // beyond 448 -> NaN
+  } else {
+    if (bits > 0x7bu) return sign | 0x7cu;  // beyond 57344 -> inf
+  }
+  return sign | bits;
+}
+
+// ---------------------------------------------------------------------------
+// lane exchange
+// ---------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+constexpr int kRowRor4 = 0x124;
+constexpr int kRowRor8 = 0x128;
+
+__device__ __forceinline__ float xor_max(float x, int m) { return fmaxf(x, __shfl_xor(x, m)); }
+__device__ __forceinline__ float xor_sum(float x, int m) { return x + __shfl_xor(x, m); }
+
+}  // namespace ffa

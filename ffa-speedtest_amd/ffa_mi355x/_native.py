@@ -1,0 +1,143 @@
+"""ctypes binding of libffa_mi355x.so (the C ABI declared in include/ffa_mi355x.h).
+
+The library is the only compute path: if it is missing or does not load,
+every entry point raises; there is no CPU or PyTorch fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libffa_mi355x.so"
+
+# element type codes (ffa_mi355x.h)
+DT_F16, DT_BF16, DT_F32, DT_FP8_E4M3, DT_FP8_E5M2, DT_NONE = range(6)
+LAYOUT_CONTIG, LAYOUT_PAGED = 0, 1
+SCALE_CHANNEL, SCALE_G32 = 0, 1
+
+EXPORTS = (
+    "ffa_q2fp8_decode_nchunks",
+    "ffa_q2fp8_decode",
+    "ffa_q2_quantize_nsplit",
+    "ffa_q2_quantize_channel",
+    "ffa_kproj_rope_q2_channel",
+    "ffa_kproj_rope_q2_append",
+    "ffa_q2_quantize_g32_append",
+    "ffa_last_error",
+    "ffa_version",
+)
+
+_TORCH_DT = {
+    torch.float16: DT_F16,
+    torch.bfloat16: DT_BF16,
+    torch.float32: DT_F32,
+    torch.float8_e4m3fn: DT_FP8_E4M3,
+    torch.float8_e5m2: DT_FP8_E5M2,
+}
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _TORCH_DT[dt]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {dt}") from None
+
+
+class DecodeArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("q_dtype", ctypes.c_int),
+        ("k_q", ctypes.c_void_p),
+        ("k_scale", ctypes.c_void_p),
+        ("k_zero", ctypes.c_void_p),
+        ("scale_dtype", ctypes.c_int),
+        ("scale_mode", ctypes.c_int),
+        ("k_residual", ctypes.c_void_p),
+        ("res_dtype", ctypes.c_int),
+        ("v", ctypes.c_void_p),
+        ("v_dtype", ctypes.c_int),
+        ("layout", ctypes.c_int),
+        ("block_table", ctypes.c_void_p),
+        ("bt_stride", ctypes.c_int),
+        ("seq_lens", ctypes.c_void_p),
+        ("B", ctypes.c_int),
+        ("T", ctypes.c_int),
+        ("HQ", ctypes.c_int),
+        ("HKV", ctypes.c_int),
+        ("scale", ctypes.c_float),
+        ("BS", ctypes.c_int),
+        ("SBS", ctypes.c_int),
+        ("delta", ctypes.c_float),
+        ("threshold_in", ctypes.c_void_p),
+        ("threshold_out", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("out_dtype", ctypes.c_int),
+        ("m_buf", ctypes.c_void_p),
+        ("l_buf", ctypes.c_void_p),
+        ("o_buf", ctypes.c_void_p),
+        ("nchunks", ctypes.c_int),
+        ("mask", ctypes.c_void_p),
+        ("ntbs", ctypes.c_int),
+    ]
+
+
+_lib = None
+_lock = threading.Lock()
+
+
+def lib() -> ctypes.CDLL:
+    """Load the native library once; raise if it is absent (no fallback)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
+                "(hipcc --offload-arch=gfx950).  There is no CPU fallback."
+            )
+        L = ctypes.CDLL(str(LIB_PATH))
+        vp, ci, cf = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+        L.ffa_last_error.restype = ctypes.c_char_p
+        L.ffa_version.restype = ctypes.c_char_p
+        L.ffa_q2fp8_decode_nchunks.argtypes = [ci, ci, ci]
+        L.ffa_q2fp8_decode_nchunks.restype = ci
+        L.ffa_q2fp8_decode.argtypes = [ctypes.POINTER(DecodeArgs), vp]
+        L.ffa_q2fp8_decode.restype = ci
+        L.ffa_q2_quantize_nsplit.argtypes = [ci]
+        L.ffa_q2_quantize_nsplit.restype = ci
+        L.ffa_q2_quantize_channel.argtypes = [vp, ci, ci, ci, ci, ci, vp, vp, vp, vp, ci, vp, vp]
+        L.ffa_q2_quantize_channel.restype = ci
+        L.ffa_kproj_rope_q2_channel.argtypes = [vp, vp, vp, ci, vp, vp, ci, ci, ci, ci, ci, ci, vp, vp, vp, vp, vp,
+                                                ci, vp, vp]
+        L.ffa_kproj_rope_q2_channel.restype = ci
+        L.ffa_kproj_rope_q2_append.argtypes = [vp, vp, vp, ci, vp, vp, ci, ci, ci, ci, vp, vp, ci, vp, vp, vp, vp,
+                                               ci, vp, vp, ci, vp]
+        L.ffa_kproj_rope_q2_append.restype = ci
+        L.ffa_q2_quantize_g32_append.argtypes = [vp, ci, ci, ci, ci, vp, vp, ci, vp, vp, vp, vp, ci, vp, vp, vp]
+        L.ffa_q2_quantize_g32_append.restype = ci
+        _lib = L
+        return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = lib().ffa_last_error().decode(errors="replace")
+        if rc == -2:
+            raise NotImplementedError(f"{what}: {msg}")
+        if rc == -1:
+            raise ValueError(f"{what}: {msg}")
+        raise RuntimeError(f"{what}: {msg} (rc={rc})")
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream

@@ -1,0 +1,158 @@
+"""Host side of the q2fp8 pruned decode: validation, scratch, one C-ABI call.
+
+The launch sequence replaces stage1 + stage2 of
+ffa-q2fp8/attn_kernel/attn_kernel_v1210_fused_bsz_q2fp8.py:283-304; the
+argument checks mirror :211-281 (same exception types).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _native as N
+
+HEAD_DIM = 128
+
+
+def _cdiv(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+def decode_nchunks(T: int, BS: int, SBS: int) -> int:
+    return int(N.lib().ffa_q2fp8_decode_nchunks(int(T), int(BS), int(SBS)))
+
+
+def decode_ntbs(T: int, BS: int, SBS: int) -> int:
+    return _cdiv(T, BS) * _cdiv(BS, SBS)
+
+
+class DecodeWorkspace:
+    """Caller-owned scratch of one decode shape (graph-capture friendly).
+
+    Mirrors Q2FP8DecodeWorkspace (ffa-q2fp8-h100/attn_kernel/attn_kernel_v1210_fused_bsz_q2fp8.py:232-257):
+    o, m_buf, l_buf, o_buf, mask_buf, threshold_buf.  Partials are kept per
+    64-token chunk (m_buf/l_buf [B, HQ, nchunks], o_buf [B, HQ, nchunks, 128]),
+    mask_buf holds one byte per prune block [B, HKV, NTBS].
+    """
+
+    def __init__(self, B, HQ, HKV, T, BS, SBS, device, dtype):
+        self.B, self.HQ, self.HKV, self.T = int(B), int(HQ), int(HKV), int(T)
+        self.BS, self.SBS = int(BS), int(SBS)
+        self.V = HEAD_DIM
+        self.device = torch.device(device)
+        self.dtype = dtype
+        self.nchunks = decode_nchunks(T, BS, SBS)
+        self.NTBS = decode_ntbs(T, BS, SBS)
+        self.o = torch.empty((B, HQ, HEAD_DIM), device=device, dtype=dtype)
+        self.m_buf = torch.empty((B, HQ, self.nchunks), device=device, dtype=torch.float32)
+        self.l_buf = torch.empty((B, HQ, self.nchunks), device=device, dtype=torch.float32)
+        self.o_buf = torch.empty((B, HQ, self.nchunks, HEAD_DIM), device=device, dtype=torch.float32)
+        self.mask_buf = torch.empty((B, HKV, self.NTBS), device=device, dtype=torch.int8)
+        self.threshold_buf = torch.empty((B, HQ), device=device, dtype=torch.float32)
+
+    def matches(self, B, HQ, HKV, T, BS, SBS, device, dtype) -> bool:
+        return (
+            self.B == int(B)
+            and self.HQ == int(HQ)
+            and self.HKV == int(HKV)
+            and self.nchunks >= decode_nchunks(T, BS, SBS)
+            and self.NTBS == decode_ntbs(T, BS, SBS)
+            and self.device == torch.device(device)
+            and self.dtype == dtype
+        )
+
+
+def _res_code(k_residual, use_res: bool) -> int:
+    if not use_res:
+        return N.DT_NONE
+    if k_residual.dtype in (torch.float8_e4m3fn, torch.float8_e5m2):
+        return N.dtype_code(k_residual.dtype)
+    raise ValueError(f"k_residual must be float8_e4m3fn or float8_e5m2, got {k_residual.dtype}")
+
+
+def run_decode(
+    *,
+    q: torch.Tensor,  # [B, HQ, 128]
+    k_q: torch.Tensor,
+    k_scale: torch.Tensor,
+    k_zero: torch.Tensor,
+    v: torch.Tensor,
+    k_residual,
+    layout: int,
+    scale_mode: int,
+    T: int,
+    HKV: int,
+    scale: float,
+    BS: int,
+    SBS: int,
+    delta: float,
+    use_res: bool,
+    precomputed_threshold=None,
+    block_table=None,
+    seq_lens=None,
+    workspace: DecodeWorkspace | None = None,
+) -> DecodeWorkspace:
+    """Launch one decode step; returns the workspace holding o / mask / thresholds."""
+    B, HQ, D = q.shape
+    if D != HEAD_DIM:
+        raise NotImplementedError(f"head_dim {D} is not supported (this build implements {HEAD_DIM})")
+    if v.shape[-1 if layout == N.LAYOUT_CONTIG else -2] != HEAD_DIM:
+        raise NotImplementedError("value head dim must be 128")
+    if workspace is None:
+        workspace = DecodeWorkspace(B, HQ, HKV, T, BS, SBS, q.device, q.dtype)
+    elif not workspace.matches(B, HQ, HKV, T, BS, SBS, q.device, q.dtype):
+        raise ValueError("workspace shape/device/dtype mismatch")
+    th_in = None
+    if precomputed_threshold is not None:
+        th_in = precomputed_threshold.to(torch.float32).contiguous()
+    a = N.DecodeArgs()
+    a.q = q.data_ptr()
+    a.q_dtype = N.dtype_code(q.dtype)
+    a.k_q = k_q.data_ptr()
+    a.k_scale = k_scale.data_ptr()
+    a.k_zero = k_zero.data_ptr()
+    a.scale_dtype = N.dtype_code(k_scale.dtype)
+    a.scale_mode = scale_mode
+    a.k_residual = k_residual.data_ptr() if use_res else None
+    a.res_dtype = _res_code(k_residual, use_res)
+    a.v = v.data_ptr()
+    a.v_dtype = N.dtype_code(v.dtype)
+    a.layout = layout
+    a.block_table = block_table.data_ptr() if block_table is not None else None
+    a.bt_stride = block_table.shape[1] if block_table is not None else 0
+    a.seq_lens = seq_lens.data_ptr() if seq_lens is not None else None
+    a.B, a.T, a.HQ, a.HKV = B, int(T), HQ, int(HKV)
+    a.scale = float(scale)
+    a.BS, a.SBS = int(BS), int(SBS)
+    a.delta = float(delta)
+    a.threshold_in = th_in.data_ptr() if th_in is not None else None
+    a.threshold_out = workspace.threshold_buf.data_ptr()
+    a.out = workspace.o.data_ptr()
+    a.out_dtype = N.dtype_code(workspace.o.dtype)
+    a.m_buf = workspace.m_buf.data_ptr()
+    a.l_buf = workspace.l_buf.data_ptr()
+    a.o_buf = workspace.o_buf.data_ptr()
+    a.nchunks = workspace.nchunks
+    a.mask = workspace.mask_buf.data_ptr()
+    a.ntbs = workspace.NTBS
+    rc = N.lib().ffa_q2fp8_decode(ctypes.byref(a), ctypes.c_void_p(N.stream_of(q.device)))
+    N.check(rc, "ffa_q2fp8_decode")
+    return workspace
+
+
+def skip_ratio_of(mask: torch.Tensor, seq_lens=None, BS=None, SBS=None) -> float:
+    """1 - kept/total blocks (attn_kernel...q2fp8.py:293-297); ragged lengths count their own blocks."""
+    kept = mask.to(torch.int32).sum()
+    if seq_lens is None:
+        total = mask.numel()
+    else:
+        HKV = mask.shape[1]
+        total = sum(decode_ntbs(int(t), BS, SBS) for t in seq_lens.tolist()) * HKV
+    return float((1.0 - kept.float() / float(total)).item())
+
+
+def default_scale(D: int) -> float:
+    return 1.0 / math.sqrt(D)

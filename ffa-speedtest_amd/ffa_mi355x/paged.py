@@ -1,0 +1,89 @@
+"""Paged q2fp8 KV cache (64-token pages) and its decode / append entry points.
+
+The reference keeps one contiguous [B, T, HKV, D] cache per batch
+(ffa-q2fp8/attn_kernel/attn_kernel_v1210_fused_bsz_q2fp8.py:192-197).  This
+build adds a page pool shared by all sequences, laid out for the gfx950
+kernels (all per (page, KV head) blocks contiguous):
+
+    k_q      [P, HKV, 4, 64, 8]  u8    2-bit codes, group-major (32 codes/8 bytes per token and group)
+    k_scale  [P, HKV, 4, 64]     f16   g32 scale per token and group
+    k_zero   [P, HKV, 4, 64]     f16   g32 zero point
+    k_res    [P, HKV, 64, 128]   fp8   residual (e4m3fn by default)
+    v        [P, HKV, 128, 64]   bf16  V^T pages (token-minor)
+
+block_table[b, i] is the pool page of tokens [64 i, 64 i + 64) of sequence b;
+seq_lens[b] is its length.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _native as N
+from .decode import HEAD_DIM, DecodeWorkspace, run_decode
+
+PAGE = 64
+
+
+class PagedQ2Cache:
+    def __init__(self, num_pages, HKV, device, res_dtype=torch.float8_e4m3fn, v_dtype=torch.bfloat16):
+        self.P, self.HKV = int(num_pages), int(HKV)
+        self.device = torch.device(device)
+        self.res_dtype, self.v_dtype = res_dtype, v_dtype
+        P, H = self.P, self.HKV
+        self.k_q = torch.zeros((P, H, 4, PAGE, 8), dtype=torch.uint8, device=device)
+        self.k_scale = torch.zeros((P, H, 4, PAGE), dtype=torch.float16, device=device)
+        self.k_zero = torch.zeros((P, H, 4, PAGE), dtype=torch.float16, device=device)
+        self.k_res = torch.zeros((P, H, PAGE, HEAD_DIM), dtype=res_dtype, device=device)
+        self.v = torch.zeros((P, H, HEAD_DIM, PAGE), dtype=v_dtype, device=device)
+
+    def nbytes_per_page(self) -> int:
+        return sum(t[0].numel() * t.element_size() for t in (self.k_q, self.k_scale, self.k_zero, self.k_res, self.v))
+
+    # ------------------------------------------------------------------ writes
+    def append(self, k: torch.Tensor, v: torch.Tensor | None, pos: torch.Tensor, block_table: torch.Tensor):
+        """g32-quantize k [B, Tn, HKV, 128] and write it (and v) at positions pos[b] + n."""
+        B, Tn, HKV, D = k.shape
+        if HKV != self.HKV or D != HEAD_DIM:
+            raise ValueError("k shape does not match the cache")
+        k = k.contiguous()
+        if v is not None:
+            if v.shape != k.shape:
+                raise ValueError("v must have the shape of k")
+            v = v.to(self.v_dtype).contiguous()
+        pos = pos.to(torch.int32).contiguous()
+        block_table = block_table.to(torch.int32).contiguous()
+        rc = N.lib().ffa_q2_quantize_g32_append(
+            k.data_ptr(), N.dtype_code(k.dtype), B, Tn, HKV, pos.data_ptr(), block_table.data_ptr(),
+            block_table.shape[1], self.k_q.data_ptr(), self.k_scale.data_ptr(), self.k_zero.data_ptr(),
+            self.k_res.data_ptr(), N.dtype_code(self.res_dtype), N.ptr(v), self.v.data_ptr(),
+            N.stream_of(k.device))
+        N.check(rc, "ffa_q2_quantize_g32_append")
+
+    # ------------------------------------------------------------------ decode
+    def decode(self, q, block_table, seq_lens=None, *, T=None, scale=None, BS=64, SBS=None, delta=5.0,
+               precomputed_threshold=None, use_fp8_residual=True, workspace: DecodeWorkspace | None = None):
+        """Pruned decode of q [B, HQ, 128] (or [B, 1, HQ, 128]) over the paged cache."""
+        if q.ndim == 4:
+            if q.shape[1] != 1:
+                raise AssertionError("decode takes one query token per sequence")
+            q = q[:, 0]
+        q = q.contiguous()
+        B, HQ, D = q.shape
+        SBS = BS if SBS is None else SBS
+        block_table = block_table.to(torch.int32).contiguous()
+        if seq_lens is not None:
+            seq_lens = seq_lens.to(torch.int32).contiguous()
+        if T is None:
+            if seq_lens is None:
+                raise ValueError("give T or seq_lens")
+            T = int(seq_lens.max().item())
+        if block_table.shape[0] != B or block_table.shape[1] * PAGE < T:
+            raise ValueError("block_table must be [B, >= ceil(T/64)]")
+        scale = 1.0 / math.sqrt(D) if scale is None else scale
+        return run_decode(
+            q=q, k_q=self.k_q, k_scale=self.k_scale, k_zero=self.k_zero, v=self.v, k_residual=self.k_res,
+            layout=N.LAYOUT_PAGED, scale_mode=N.SCALE_G32, T=T, HKV=self.HKV, scale=scale, BS=BS, SBS=SBS,
+            delta=delta, use_res=use_fp8_residual, precomputed_threshold=precomputed_threshold,
+            block_table=block_table, seq_lens=seq_lens, workspace=workspace)

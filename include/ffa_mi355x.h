@@ -1,0 +1,172 @@
+/*
+ * ffa_mi355x.h -- C ABI of the MI355X (gfx950) quantized-K pruned decode path.
+ *
+ * Plain pointers and sizes only.  Every pointer is a device pointer owned by
+ * the caller; the library never allocates or frees device memory and never
+ * synchronises the stream.  All calls are asynchronous on `stream`
+ * (a hipStream_t passed as void*).  Return value: 0 on success, otherwise a
+ * negative FFA_E_* code; ffa_last_error() then returns a message
+ * (thread-local, valid until the next call on the same thread).
+ *
+ * Reference interfaces replaced (paths relative to the reference checkout):
+ *   ffa_q2fp8_decode          ffa-q2fp8/attn_kernel/attn_kernel_v1210_fused_bsz_q2fp8.py:283-304
+ *                             (stage-1 launch :283-291 + stage-2 launch :299-304 of
+ *                              attn_forward_decode_quantized :191-309)
+ *   ffa_q2_quantize_channel   ffa-q2fp8/run_attn_bench_q2.py:78-105
+ *                             (quantize_k_2bit_fp8_residual; same as
+ *                              ffa-q2fp8/fused_kproj_rope_q2fp8.py:40-68)
+ *   ffa_kproj_rope_q2_channel ffa-q2fp8/fused_kproj_rope_q2fp8.py:492-542
+ *                             (the two Triton launches of kproj_rope_quantize_triton)
+ *   ffa_q2_quantize_g32_append no reference counterpart: g32 quantize + paged append of
+ *                             given K rows (BASELINE configs 2 and 5 cache layout)
+ *   ffa_kproj_rope_q2_append  no reference counterpart: BASELINE config 5 append of
+ *                             K-proj + RoPE + g32 quantize into the paged cache
+ *                             (incremental quantisation is a TODO in the reference,
+ *                              ffa-q2fp8/OPTIMIZATION_NOTES.md:23-26)
+ */
+#ifndef FFA_MI355X_H
+#define FFA_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element type codes */
+enum {
+  FFA_DT_F16 = 0,
+  FFA_DT_BF16 = 1,
+  FFA_DT_F32 = 2,
+  FFA_DT_FP8_E4M3 = 3, /* OCP float8_e4m3fn */
+  FFA_DT_FP8_E5M2 = 4, /* OCP float8_e5m2 */
+  FFA_DT_NONE = 5      /* no residual */
+};
+
+/* KV-cache layouts */
+enum {
+  /* reference layout (attn_kernel_v1210_fused_bsz_q2fp8.py:192-197):
+     k_q [B,T,HKV,32] u8, k_residual [B,T,HKV,128], v [B,T,HKV,128],
+     per-channel k_scale/k_zero [B,HKV,128] */
+  FFA_LAYOUT_CONTIG = 0,
+  /* paged layout, 64-token pages from a pool of P pages:
+     k_q        [P, HKV, 4 groups, 64 tokens, 8 bytes]   (group-major codes)
+     k_scale    [P, HKV, 4 groups, 64 tokens] fp16       (g32 mode)
+     k_zero     [P, HKV, 4 groups, 64 tokens] fp16       (g32 mode)
+     k_residual [P, HKV, 64 tokens, 128] fp8
+     v          [P, HKV, 128, 64 tokens]                 (V^T pages)
+     block_table[b, i] = pool page holding tokens [64i, 64i+64) of sequence b */
+  FFA_LAYOUT_PAGED = 1
+};
+
+/* scale/zero modes */
+enum {
+  FFA_SCALE_CHANNEL = 0, /* one scale/zero per (b, hkv, d) over all tokens (reference) */
+  FFA_SCALE_G32 = 1      /* one fp16 scale/zero per token per 32-wide group along d */
+};
+
+enum {
+  FFA_OK = 0,
+  FFA_E_INVALID = -1,     /* argument/shape error */
+  FFA_E_UNSUPPORTED = -2, /* valid request this build does not implement */
+  FFA_E_LAUNCH = -3       /* HIP launch error */
+};
+
+/*
+ * Arguments of one pruned decode step.  Shapes use B sequences, HQ query
+ * heads, HKV KV heads (G = HQ/HKV <= 4), head dim D = DV = 128.
+ *
+ * Scratch (caller-owned, see ffa_q2fp8_decode_nchunks):
+ *   m_buf, l_buf [B, HQ, nchunks] f32; o_buf [B, HQ, nchunks, 128] f32;
+ *   mask [B, HKV, ntbs] i8 (1 = block kept, written for every block).
+ */
+typedef struct ffa_q2fp8_decode_args {
+  const void *q; /* [B, HQ, 128], dtype q_dtype */
+  int q_dtype;
+  const uint8_t *k_q;
+  const void *k_scale;
+  const void *k_zero;
+  int scale_dtype; /* F16/BF16/F32 for CHANNEL mode, F16 for G32 */
+  int scale_mode;
+  const uint8_t *k_residual; /* may be NULL when res_dtype == FFA_DT_NONE */
+  int res_dtype;             /* FP8_E4M3, FP8_E5M2 or NONE */
+  const void *v;
+  int v_dtype; /* F16 or BF16 */
+  int layout;
+  const int32_t *block_table; /* [B, bt_stride] (paged only) */
+  int bt_stride;
+  const int32_t *seq_lens; /* [B] or NULL (all sequences have length T) */
+  int B, T, HQ, HKV;
+  float scale;                /* softmax scale (1/sqrt(D) by default) */
+  int BS, SBS;                /* threshold block size / prune block size */
+  float delta;                /* threshold margin in log2-scaled units */
+  const float *threshold_in;  /* [B, HQ] or NULL (probe windows are used) */
+  float *threshold_out;       /* [B, HQ] or NULL */
+  void *out;                  /* [B, HQ, 128], dtype out_dtype */
+  int out_dtype;
+  float *m_buf, *l_buf, *o_buf;
+  int nchunks;
+  int8_t *mask;
+  int ntbs;
+} ffa_q2fp8_decode_args;
+
+/* Number of 64-token chunks the scratch buffers must hold for max length T. */
+int ffa_q2fp8_decode_nchunks(int T, int BS, int SBS);
+
+int ffa_q2fp8_decode(const ffa_q2fp8_decode_args *args, void *stream);
+
+/*
+ * Reference quantizer (per-channel scale/zero over T, tau = k_dtype):
+ *   k [B,T,HKV,D] -> k_q [B,T,HKV,ceil(D/4)] u8, scale/zero [B,HKV,D] (k_dtype),
+ *   residual [B,T,HKV,D] fp8 (res_dtype).  Needs scratch f32 minmax
+ *   [2, B, nsplit, HKV*D] with nsplit = ffa_q2_quantize_nsplit(T).
+ */
+int ffa_q2_quantize_nsplit(int T);
+int ffa_q2_quantize_channel(const void *k, int k_dtype, int B, int T, int HKV, int D, uint8_t *k_q,
+                            void *scale, void *zero, uint8_t *residual, int res_dtype, float *minmax,
+                            void *stream);
+
+/*
+ * Fused K projection + RoPE + per-channel q2 quantize (reference producer).
+ *   h [B,T,H] (bf16/fp16), w_k [HKV*D, H] (same dtype), bias [HKV*D] or NULL,
+ *   cos/sin [T, D] (cs_dtype = F32 or the h dtype).  The RoPE output dtype is
+ *   the promotion of h and cos dtypes (reference type promotion).
+ *   Outputs as ffa_q2_quantize_channel; k_scratch [B,T,HKV,D] of the
+ *   promoted dtype receives the rotated K.
+ */
+int ffa_kproj_rope_q2_channel(const void *h, const void *w_k, const void *bias, int h_dtype, const void *cos,
+                              const void *sin, int cs_dtype, int B, int T, int H, int HKV, int D,
+                              void *k_scratch, uint8_t *k_q, void *scale, void *zero, uint8_t *residual,
+                              int res_dtype, float *minmax, void *stream);
+
+/*
+ * Fused K projection + RoPE + g32 quantize + append into the paged cache.
+ *   h [B, Tn, H]; token n of sequence b goes to position pos[b] + n.
+ *   cos/sin [B, Tn, D] f32 (per-token rows).  v_new [B, Tn, HKV, 128] (v_dtype)
+ *   or NULL.  Writes codes/scale/zero/residual/V^T into the paged pools.
+ */
+int ffa_kproj_rope_q2_append(const void *h, const void *w_k, const void *bias, int h_dtype, const float *cos,
+                             const float *sin, int B, int Tn, int H, int HKV, const int32_t *pos,
+                             const int32_t *block_table, int bt_stride, uint8_t *k_q_pages, void *scale_pages,
+                             void *zero_pages, uint8_t *res_pages, int res_dtype, const void *v_new,
+                             void *v_pages, int v_dtype, void *stream);
+
+/*
+ * g32 quantize + append of given K rows into the paged cache (no projection):
+ *   k [B, Tn, HKV, 128] (F16/BF16/F32); token n of sequence b goes to
+ *   position pos[b] + n.  Same quantization rules as ffa_kproj_rope_q2_append.
+ *   v_new [B, Tn, HKV, 128] (2-byte dtype of the V pool) or NULL.
+ */
+int ffa_q2_quantize_g32_append(const void *k, int k_dtype, int B, int Tn, int HKV, const int32_t *pos,
+                               const int32_t *block_table, int bt_stride, uint8_t *k_q_pages, void *scale_pages,
+                               void *zero_pages, uint8_t *res_pages, int res_dtype, const void *v_new, void *v_pages,
+                               void *stream);
+
+const char *ffa_last_error(void);
+const char *ffa_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FFA_MI355X_H */

@@ -1,0 +1,132 @@
+"""GPU parity of the q2fp8 pruned decode (HIP kernels through the C ABI) against the CPU oracle.
+
+Bar: survivor mask identical except blocks whose
+margin max_g(block_max - th) is within 1e-3 (their count is printed);
+attention output within max-abs 2e-2 and mean-abs 2e-3 in bf16.  The output
+is compared with the oracle evaluated under the GPU's own mask, so that a
+near-threshold flip is not mistaken for an arithmetic error.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import (assert_out_close, compare_masks, contig_case, f32, oracle_paged, paged_case, to_gpu_contig,
+                     to_gpu_paged)
+from oracle import q2fp8 as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize(
+    "tau,res,T,BS,SBS,delta,heavy",
+    [
+        ("fp16", "e5m2", 1000, 128, None, 5.0, 0),   # reference defaults (BS=128, SBS=BS, e5m2)
+        ("bf16", "e5m2", 4096, 64, 64, 5.0, 16),
+        ("bf16", "e4m3fn", 4096, 64, 32, 3.0, 16),
+        ("fp16", "e5m2", 777, 64, 16, 2.0, 4),
+        ("bf16", "e5m2", 2048, 256, 128, 4.0, 8),
+        ("bf16", "e5m2", 1300, 256, 256, 4.0, 8),
+    ],
+)
+def test_contig_reference_layout(gpu, tau, res, T, BS, SBS, delta, heavy):
+    import attn_kernel.attn_kernel_v1210_fused_bsz_q2fp8 as K
+
+    case = contig_case(B=2, T=T, HQ=32, HKV=8, tau=tau, res=res, seed=T, n_heavy=heavy)
+    g = to_gpu_contig(case, gpu)
+    SBSv = BS if SBS is None else SBS
+    ws = K.allocate_q2fp8_decode_workspace(g["q"], g["k_q"], g["v"], BS=BS, SBS=SBS)
+    o, sr = K.attn_forward_decode_quantized(g["q"], g["k_q"], g["k_scale"], g["k_zero"], g["v"],
+                                            k_residual=g["k_residual"], BS=BS, SBS=SBS, delta=delta,
+                                            return_skip_ratio=True, workspace=ws)
+    torch.cuda.synchronize()
+    q, v = f32(case["q"]), f32(case["v"])
+    o_ref, diag = O.decode(q, case["k_q"], case["k_scale"], case["k_zero"], v, case["k_res"], res_fmt=res, BS=BS,
+                           SBS=SBSv, delta=delta, out_dtype=tau)
+    mask = ws.mask_buf.cpu().numpy()
+    far, near, near_total = compare_masks(mask, diag)
+    print(f"[mask] T={T} BS={BS} SBS={SBSv} skip={sr:.3f} oracle_skip={diag['skip_ratio']:.3f} "
+          f"mismatch_far={far} mismatch_near={near} near_blocks={near_total}")
+    assert far == 0
+    assert abs(sr - (1 - mask[..., : diag['mask'].shape[-1]].sum() / diag['mask'].size)) < 1e-9
+    th_gpu = ws.threshold_buf.cpu().numpy()
+    assert np.abs(th_gpu - diag["threshold"]).max() < 2e-3
+    o_forced, _ = O.decode(q, case["k_q"], case["k_scale"], case["k_zero"], v, case["k_res"], res_fmt=res, BS=BS,
+                           SBS=SBSv, delta=delta, out_dtype=tau, force_mask=mask)
+    mx, mean = assert_out_close(f32(o), o_forced, "contig")
+    print(f"[out] max_abs={mx:.3e} mean_abs={mean:.3e}")
+
+
+@pytest.mark.parametrize(
+    "B,T,seq_lens,BS,SBS,delta,interleave",
+    [
+        (1, 4096, None, 64, 64, 5.0, True),
+        (2, 3000, [3000, 1111], 64, 64, 5.0, True),
+        (3, 2500, [2500, 640, 65], 128, 32, 4.0, True),
+        (1, 1024, None, 64, 16, 5.0, False),
+    ],
+)
+def test_paged_g32(gpu, B, T, seq_lens, BS, SBS, delta, interleave):
+    case = paged_case(B=B, T=T, HQ=32, HKV=8, seed=B * 7 + T, n_heavy=16, seq_lens=seq_lens, interleave=interleave)
+    cache = to_gpu_paged(case, gpu)
+    q = case["q"].to(gpu)
+    bt = case["block_table"].to(gpu)
+    sl = torch.tensor(case["lens"], dtype=torch.int32, device=gpu)
+    ws = cache.decode(q, bt, sl, T=T, BS=BS, SBS=SBS, delta=delta)
+    torch.cuda.synchronize()
+    o_ref, diag = oracle_paged(case, BS=BS, SBS=SBS, delta=delta)
+    mask = ws.mask_buf.cpu().numpy()
+    far, near, near_total = compare_masks(mask, diag)
+    kept = mask.sum() / sum(-(-t // SBS) for t in case["lens"]) / 8
+    print(f"[mask] B={B} T={T} keep={kept:.3f} oracle_skip={diag['skip_ratio']:.3f} mismatch_far={far} "
+          f"mismatch_near={near} near_blocks={near_total}")
+    assert far == 0
+    o_forced, _ = oracle_paged(case, BS=BS, SBS=SBS, delta=delta, force_mask=mask)
+    mx, mean = assert_out_close(f32(ws.o), o_forced, "paged")
+    print(f"[out] max_abs={mx:.3e} mean_abs={mean:.3e}")
+
+
+def test_paged_page_permutation_invariance(gpu):
+    """Identity and permuted page tables over the same logical cache give bit-identical outputs."""
+    c1 = paged_case(B=1, T=2048, HQ=32, HKV=8, seed=5, n_heavy=16, interleave=False)
+    c2 = paged_case(B=1, T=2048, HQ=32, HKV=8, seed=5, n_heavy=16, interleave=True)
+    assert not np.array_equal(c1["block_table"].numpy(), c2["block_table"].numpy())
+    outs = []
+    for c in (c1, c2):
+        cache = to_gpu_paged(c, gpu)
+        ws = cache.decode(c["q"].to(gpu), c["block_table"].to(gpu), T=2048, BS=64, delta=5.0)
+        torch.cuda.synchronize()
+        outs.append((ws.o.clone(), ws.mask_buf.clone()))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+
+
+def test_precomputed_threshold_and_no_residual(gpu):
+    case = paged_case(B=1, T=2048, HQ=32, HKV=8, seed=13, n_heavy=16)
+    cache = to_gpu_paged(case, gpu)
+    q, bt = case["q"].to(gpu), case["block_table"].to(gpu)
+    ws = cache.decode(q, bt, T=2048, BS=64, delta=5.0)
+    th = ws.threshold_buf.clone()
+    o1, m1 = ws.o.clone(), ws.mask_buf.clone()
+    ws2 = cache.decode(q, bt, T=2048, BS=64, delta=99.0, precomputed_threshold=th)
+    torch.cuda.synchronize()
+    assert torch.equal(m1, ws2.mask_buf) and torch.equal(o1, ws2.o)
+    ws3 = cache.decode(q, bt, T=2048, BS=64, delta=5.0, use_fp8_residual=False)
+    torch.cuda.synchronize()
+    o_ref, diag = oracle_paged(case, BS=64, delta=5.0, use_fp8_residual=False,
+                               force_mask=ws3.mask_buf.cpu().numpy())
+    assert_out_close(f32(ws3.o), o_ref, "no-residual")
+
+
+def test_extreme_deltas(gpu):
+    case = paged_case(B=1, T=1500, HQ=32, HKV=8, seed=21, n_heavy=4)
+    cache = to_gpu_paged(case, gpu)
+    q, bt = case["q"].to(gpu), case["block_table"].to(gpu)
+    ws = cache.decode(q, bt, T=1500, BS=64, delta=-math.inf)
+    torch.cuda.synchronize()
+    assert ws.mask_buf.sum().item() == 0 and (ws.o == 0).all()
+    ws = cache.decode(q, bt, T=1500, BS=64, delta=math.inf)
+    torch.cuda.synchronize()
+    assert ws.mask_buf.sum().item() == ws.mask_buf.numel()
+    o_ref, _ = oracle_paged(case, BS=64, delta=math.inf)
+    assert_out_close(f32(ws.o), o_ref, "delta=inf")

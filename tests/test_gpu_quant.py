@@ -1,0 +1,151 @@
+"""GPU quantizers and K producers vs the CPU oracle.
+
+Quantized bytes (codes, scale, zero, residual) must be bit-exact given the
+same K; the K-projection GEMM accumulates in fp32 in its own order, so the
+rotated K is compared with a tolerance and the bytes are compared against the
+oracle quantizer applied to the GPU's own K.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import FP8_DT, TORCH_DT, f32
+from oracle import producer as OP
+from oracle import q2fp8 as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("tau", ["bf16", "fp16", "fp32"])
+@pytest.mark.parametrize("fmt", ["e5m2", "e4m3fn"])
+def test_quantize_per_channel_bit_exact(gpu, tau, fmt):
+    from ffa_mi355x import quant
+
+    g = torch.Generator().manual_seed(1)
+    k = (torch.randn(2, 1500, 8, 128, generator=g) * 2).to(TORCH_DT[tau])
+    k[:, :, 3, 5] = 0.25  # constant channel
+    kq, s, z, r = quant.quantize_per_channel(k.to(gpu), FP8_DT[fmt])
+    torch.cuda.synchronize()
+    pk, so, zo, ro = O.quantize_per_channel(f32(k), tau, fmt)
+    assert np.array_equal(kq.cpu().numpy(), pk)
+    assert np.array_equal(f32(s), so) and np.array_equal(f32(z), zo)
+    assert np.array_equal(r.view(torch.uint8).cpu().numpy(), ro)
+
+
+def test_quantize_per_channel_odd_head_dim(gpu):
+    from ffa_mi355x import quant
+
+    g = torch.Generator().manual_seed(2)
+    k = torch.randn(1, 77, 2, 6, generator=g).half()
+    kq, s, z, r = quant.quantize_per_channel(k.to(gpu), torch.float8_e5m2)
+    pk, so, zo, ro = O.quantize_per_channel(f32(k), "fp16", "e5m2")
+    assert np.array_equal(kq.cpu().numpy(), pk) and np.array_equal(r.view(torch.uint8).cpu().numpy(), ro)
+
+
+def test_g32_append_bit_exact(gpu):
+    from ffa_mi355x import synth
+    from ffa_mi355x.paged import PagedQ2Cache
+
+    B, T, HKV = 3, 300, 8
+    g = torch.Generator().manual_seed(3)
+    k = (torch.randn(B, T, HKV, 128, generator=g) * 3).bfloat16()
+    v = torch.randn(B, T, HKV, 128, generator=g).bfloat16()
+    bt, P = synth.page_tables([T] * B, seed=3)
+    cache = PagedQ2Cache(P, HKV, gpu)
+    # two appends: a prefix of 200 tokens, then the remaining 100 at position 200
+    pos0 = torch.zeros(B, dtype=torch.int32)
+    cache.append(k[:, :200].to(gpu), v[:, :200].to(gpu), pos0.to(gpu), bt.to(gpu))
+    cache.append(k[:, 200:].to(gpu), v[:, 200:].to(gpu), (pos0 + 200).to(gpu), bt.to(gpu))
+    torch.cuda.synchronize()
+    pk, s, z, r = O.quantize_g32(f32(k), "e4m3fn")
+    kq_pool = cache.k_q.cpu().numpy()
+    s_pool = cache.k_scale.float().cpu().numpy()
+    z_pool = cache.k_zero.float().cpu().numpy()
+    r_pool = cache.k_res.view(torch.uint8).cpu().numpy()
+    v_pool = cache.v.view(torch.int16).cpu().numpy()
+    vb = v.view(torch.int16).numpy()
+    for b in range(B):
+        for t in range(0, T, 64):
+            page, n = int(bt[b, t // 64]), min(64, T - t)
+            assert np.array_equal(kq_pool[page, :, :, :n].transpose(2, 0, 1, 3).reshape(n, HKV, 32), pk[b, t:t + n])
+            assert np.array_equal(s_pool[page, :, :, :n].transpose(2, 0, 1), s[b, t:t + n])
+            assert np.array_equal(z_pool[page, :, :, :n].transpose(2, 0, 1), z[b, t:t + n])
+            assert np.array_equal(r_pool[page, :, :n].transpose(1, 0, 2), r[b, t:t + n])
+            assert np.array_equal(v_pool[page, :, :, :n].transpose(2, 0, 1), vb[b, t:t + n])
+
+
+@pytest.mark.parametrize("h_dtype,cs_dtype", [("bf16", "fp32"), ("fp16", "fp16"), ("bf16", "bf16")])
+def test_kproj_rope_channel(gpu, h_dtype, cs_dtype):
+    from ffa_mi355x import quant
+
+    B, T, H, HKV, D = 2, 40, 512, 4, 64
+    g = torch.Generator().manual_seed(4)
+    h = torch.randn(B, T, H, generator=g).to(TORCH_DT[h_dtype])
+    w = (torch.randn(HKV * D, H, generator=g) * 0.05).to(TORCH_DT[h_dtype])
+    inv = 1.0 / (10000.0 ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
+    ang = torch.outer(torch.arange(T, dtype=torch.float32), inv)
+    emb = torch.cat([ang, ang], -1)
+    cos, sin = emb.cos().to(TORCH_DT[cs_dtype]), emb.sin().to(TORCH_DT[cs_dtype])
+    (kq, s, z, r), k_gpu = quant.kproj_rope_q2_channel(h.to(gpu), w.to(gpu), cos.to(gpu), sin.to(gpu), HKV, D,
+                                                       fp8_dtype=torch.float8_e5m2, return_k=True)
+    torch.cuda.synchronize()
+    k_ref, odt = OP.kproj_rope(f32(h), f32(w), f32(cos), f32(sin), HKV, D, h_dtype=h_dtype, cs_dtype=cs_dtype)
+    kg = f32(k_gpu)
+    # GEMM accumulation order differs: allow one ulp of the h dtype (relative) after RoPE
+    tol = {"bf16": 2 ** -7, "fp16": 2 ** -10, "fp32": 2 ** -7}[h_dtype] * 2
+    assert np.abs(kg - k_ref).max() <= tol * (np.abs(k_ref).max() + 1e-3)
+    assert (kg != k_ref).mean() < 0.05
+    # quantization of the GPU's own K is bit-exact
+    pk, so, zo, ro = O.quantize_per_channel(kg, odt, "e5m2")
+    assert np.array_equal(kq.cpu().numpy(), pk)
+    assert np.array_equal(f32(s), so) and np.array_equal(f32(z), zo)
+    assert np.array_equal(r.view(torch.uint8).cpu().numpy(), ro)
+
+
+def test_reference_smoke_test(gpu):
+    """The reference's own smoke check (fused_kproj_rope_q2fp8.py:569-625) passes for the drop-in."""
+    import fused_kproj_rope_q2fp8 as FK
+
+    FK.run_smoke_test(gpu, torch.float16, torch.float8_e5m2, B=2, T=32, H=256, HKV=4, K=64)
+
+
+def test_kproj_append_config5_small(gpu):
+    """K-proj (theta 5e5, positions 65536+) + g32 quantize + paged append, then decode over the cache."""
+    from ffa_mi355x import quant, synth
+    from ffa_mi355x.paged import PagedQ2Cache
+
+    B, H, HKV, T0 = 4, 512, 8, 700
+    g = torch.Generator().manual_seed(5)
+    h = torch.randn(B, 1, H, generator=g).bfloat16()
+    w = (torch.randn(H, HKV * 128, generator=g) * 0.02).bfloat16()  # [in, out] orientation
+    pos = torch.full((B,), T0, dtype=torch.int32) + torch.arange(B, dtype=torch.int32)
+    inv = 1.0 / (500000.0 ** (torch.arange(0, 128, 2, dtype=torch.float32) / 128))
+    ang = pos.float()[:, None] * inv[None, :]
+    emb = torch.cat([ang, ang], -1)[:, None, :]  # [B, 1, 128]
+    cos, sin = emb.cos(), emb.sin()
+    lens = [int(p) + 1 for p in pos]
+    bt, P = synth.page_tables(lens, seed=5)
+    cache = PagedQ2Cache(P, HKV, gpu)
+    v_new = torch.randn(B, 1, HKV, 128, generator=g).bfloat16()
+    quant.kproj_rope_q2_append(cache, h.to(gpu), w.to(gpu), cos.to(gpu), sin.to(gpu), pos.to(gpu), bt.to(gpu),
+                               v_new=v_new.to(gpu))
+    torch.cuda.synchronize()
+    k_ref = OP.kproj_rope_rows(f32(h), f32(w).T, f32(cos), f32(sin), HKV)
+    pk, s, z, r = O.quantize_g32(k_ref, "e4m3fn")
+    kq_pool = cache.k_q.cpu().numpy()
+    s_pool = cache.k_scale.float().cpu().numpy()
+    r_pool = cache.k_res.view(torch.uint8).cpu().numpy()
+    mism = 0
+    for b in range(B):
+        page, slot = int(bt[b, int(pos[b]) // 64]), int(pos[b]) % 64
+        codes_gpu = O.unpack_2bit(kq_pool[page, :, :, slot].reshape(HKV, 32), 128)
+        codes_ref = O.unpack_2bit(pk[b, 0], 128)
+        mism += int((codes_gpu != codes_ref).sum())
+        assert np.allclose(s_pool[page, :, :, slot], s[b, 0], rtol=2e-2, atol=1e-4)
+        res_gpu = O.fp8_decode(r_pool[page, :, slot], "e4m3fn") if hasattr(O, "fp8_decode") else None
+        assert res_gpu is not None
+        deq_gpu = codes_gpu.astype(np.float32) * np.repeat(s_pool[page, :, :, slot], 32, -1)
+        assert np.isfinite(deq_gpu).all()
+        vg = cache.v[page, :, :, slot].cpu()
+        assert torch.equal(vg, v_new[b, 0])
+    assert mism <= 0.01 * B * HKV * 128

@@ -1,0 +1,80 @@
+"""The C-ABI library loads and exports what include/*.h declares (no GPU calls)."""
+import ctypes
+import inspect
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared_functions():
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        for m in re.finditer(r"^\s*(?:const\s+)?\w+\s*\*?\s*(ffa_\w+)\s*\(", text, flags=re.M):
+            names.add(m.group(1))
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    from ffa_mi355x import _native as N
+
+    L = N.lib()
+    declared = _declared_functions()
+    assert declared, "no declarations found"
+    missing = [n for n in declared if not hasattr(L, n)]
+    assert not missing, f"missing exports: {missing}"
+    assert set(N.EXPORTS) == declared
+
+
+def test_host_only_helpers():
+    from ffa_mi355x import _native as N
+
+    L = N.lib()
+    assert L.ffa_version().startswith(b"ffa_mi355x")
+    # 32K tokens, 64-token chunks, 4 chunks per workgroup
+    assert L.ffa_q2fp8_decode_nchunks(32768, 64, 64) == 512
+    assert L.ffa_q2fp8_decode_nchunks(100, 128, 128) == 4
+    assert L.ffa_q2_quantize_nsplit(32768) == 64
+
+
+def test_invalid_arguments_are_rejected_without_launch():
+    from ffa_mi355x import _native as N
+
+    L = N.lib()
+    a = N.DecodeArgs()
+    a.B, a.T, a.HQ, a.HKV = 1, 128, 40, 8  # G = 5 -> unsupported
+    a.BS, a.SBS = 64, 64
+    rc = L.ffa_q2fp8_decode(ctypes.byref(a), None)
+    assert rc == -2 and b"group" in L.ffa_last_error()
+    a.HQ = 32
+    a.SBS = 48
+    assert L.ffa_q2fp8_decode(ctypes.byref(a), None) == -2
+    a.SBS = 64
+    a.q_dtype, a.out_dtype, a.v_dtype, a.res_dtype = 0, 0, 9, 3
+    assert L.ffa_q2fp8_decode(ctypes.byref(a), None) == -1
+
+
+def test_drop_in_signatures_match_reference():
+    import attn_kernel.attn_kernel_v1210_fused_bsz_q2fp8 as K
+
+    params = list(inspect.signature(K.attn_forward_decode_quantized).parameters)
+    ref = ["q", "k_q", "k_scale", "k_zero", "v", "k_residual", "k_bits", "scale", "BS", "SBS", "delta",
+           "return_skip_ratio", "precomputed_threshold", "use_fp8_residual"]
+    assert params[: len(ref)] == ref
+    sig = inspect.signature(K.attn_forward_decode_quantized)
+    assert sig.parameters["BS"].default == 128 and sig.parameters["delta"].default == 5.0
+    assert sig.parameters["use_fp8_residual"].default is True
+
+
+def test_drop_in_rejects_cpu_tensors():
+    import torch
+
+    import attn_kernel.attn_kernel_v1210_fused_bsz_q2fp8 as K
+
+    q = torch.zeros(1, 1, 4, 128)
+    with pytest.raises(AssertionError):
+        K.attn_forward_decode_quantized(q, torch.zeros(1, 8, 1, 32, dtype=torch.uint8), torch.zeros(1, 1, 128),
+                                        torch.zeros(1, 1, 128), torch.zeros(1, 8, 1, 128))
