@@ -123,11 +123,71 @@ struct VTraits<kVF16> {
   }
 };
 
+// 32 consecutive elements of a float tensor (dtype 0=f16, 1=bf16, 2=f32): raw 16-byte loads
+// first (all issued back to back), conversion afterwards.
+struct Raw32 {
+  uint4 v[8];
+};
+__device__ __forceinline__ void raw32_load(Raw32 &r, const void *ptr, size_t off, int dt) {
+  if (dt == 2) {
+    const uint4 *q = (const uint4 *)((const float *)ptr + off);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r.v[i] = q[i];
+  } else {
+    const uint4 *q = (const uint4 *)((const uint16_t *)ptr + off);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.v[i] = q[i];
+  }
+}
+__device__ __forceinline__ void raw32_to_f32(const Raw32 &r, int dt, float *out) {
+  if (dt == 2) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      out[4 * i + 0] = __uint_as_float(r.v[i].x);
+      out[4 * i + 1] = __uint_as_float(r.v[i].y);
+      out[4 * i + 2] = __uint_as_float(r.v[i].z);
+      out[4 * i + 3] = __uint_as_float(r.v[i].w);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t w[4] = {r.v[i].x, r.v[i].y, r.v[i].z, r.v[i].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t lo = w[k] & 0xffffu, hi = w[k] >> 16;
+        out[8 * i + 2 * k] = dt == 1 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
+        out[8 * i + 2 * k + 1] = dt == 1 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ uint32_t f16x2_bits(f16x2 v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ f16x2 bits_f16x2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
+
+// Reference-layout dequantization of 8 channels: k_hat = fp16(c * s + z) with one rounding
+// (c*s is exact in fp32, so this equals the reference's fp16(fp32(fp32(c*s) + z))).
+// h holds 8 codes (code e at bits 2e); sp/zp hold the (s, z) fp16 pairs of channels (2q, 2q+1).
+__device__ __forceinline__ f16x8 dequant8_channel(uint32_t h, const uint32_t *sp, const uint32_t *zp) {
+  const uint32_t y = h | (h << 14);  // code 2q at bits 4q, code 2q+1 at bits 16+4q
+  const f16x2 m1024 = {(_Float16)-1024.f, (_Float16)-1024.f};
+  u32x4 r;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t pat = ((y >> (4 * q)) & 0x00030003u) | 0x64006400u;  // fp16 1024 + c
+    const f16x2 c = bits_f16x2(pat) + m1024;                          // exact codes
+    r[q] = f16x2_bits(__builtin_elementwise_fma(c, bits_f16x2(sp[q]), bits_f16x2(zp[q])));
+  }
+  return __builtin_bit_cast(f16x8, r);
+}
+
+__device__ __forceinline__ f16x8 add_f16x8(f16x8 a, f16x8 b) { return a + b; }
+
 template <int LAYOUT, int SMODE, int RES, int VT>
 __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p) {
   typedef VTraits<VT> VTr;
   const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int bh = blockIdx.y;
   const int b = bh / p.HKV;
   const int hkv = bh - b * p.HKV;
@@ -137,214 +197,225 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
   const int Tb = p.seq_lens ? p.seq_lens[b] : p.T;
   const int NTB = (Tb + p.BS - 1) / p.BS;
   const int NTBS_b = NTB * (p.BS / p.SBS);
+  const int SBS = p.SBS;
 
-  const int mrow = lane & 15;  // MFMA row / column index inside a 16-lane group
-  const int kc = lane >> 4;    // k-chunk of the MFMA operands == channel group
+  const int mrow = lane & 15;  // MFMA row (A) / column (B) index
+  const int kc = lane >> 4;    // k-chunk of the operands == channel group of the A lane
   const int n = mrow;          // output column = (j, i)
-  const int jg = n >> 2;       // channel group of the output column
-  const int ir = n & 3;        // query row of the output column
+  const int jg = n >> 2;
+  const int ir = n & 3;
   const bool row_ok = ir < G;
+  const bool active = t0 < Tb;
+  const bool do_probe = (p.th_in == nullptr) && wv < 2;
+  const int pa = wv == 0 ? 0 : (NTB - 1) * 16;  // probe window (attn_kernel...q2fp8.py:58-73)
 
   __shared__ float s_probe[2][4];
   __shared__ float s_pmax[kWaves][4];
   __shared__ uint8_t s_vstage[LAYOUT == kContig ? kWaves * kPage * kVRow : 4];
 
-  // ---------------------------------------------------------------- q setup
-  // Lane (kc, n=(j,i)) holds q_i on channels 32*kc .. 32*kc+31.
-  const int hq = hkv * G + ir;
-  float qv[32];
-  float sc[32];  // per-channel scale (channel mode) for the folded operand
-  float zsum = 0.f;
-  {
-    const size_t qbase = ((size_t)b * p.HQ + (row_ok ? hq : hkv * G)) * kD + 32 * kc;
-#pragma unroll
-    for (int e = 0; e < 32; ++e) {
-      float x = load_any(p.q, qbase + e, p.q_dtype);
-      qv[e] = row_ok ? (float)(_Float16)x : 0.f;  // q16 (attn_kernel...q2fp8.py:47)
-    }
-    if constexpr (SMODE == kChannel) {
-      const size_t sbase = ((size_t)b * p.HKV + hkv) * kD + 32 * kc;
-#pragma unroll
-      for (int e = 0; e < 32; ++e) {
-        sc[e] = load_any(p.ks, sbase + e, p.s_dtype);
-        zsum += qv[e] * load_any(p.kz, sbase + e, p.s_dtype);
-      }
+  // ------------------------------------------------ phase 0: page ids (scalar)
+  int pg = 0, ppg = 0;
+  if constexpr (LAYOUT == kPaged) {
+    const int32_t *btr = p.bt + (size_t)b * p.bt_stride;
+    if (active) pg = btr[chunk];
+    if (do_probe) ppg = btr[pa >> 6];
+  }
+
+  // ------------------------------------------------ phase 1: score-phase loads
+  const int hq = hkv * G + (row_ok ? ir : 0);
+  Raw32 qraw, sraw, zraw;
+  raw32_load(qraw, p.q, ((size_t)b * p.HQ + hq) * kD + 32 * kc, p.q_dtype);
+  if constexpr (SMODE == kChannel) {
+    raw32_load(sraw, p.ks, ((size_t)b * p.HKV + hkv) * kD + 32 * kc, p.s_dtype);
+    raw32_load(zraw, p.kz, ((size_t)b * p.HKV + hkv) * kD + 32 * kc, p.s_dtype);
+  }
+  // own chunk: token of MFMA row m in tile tau is 4m + tau
+  uint64_t x[4] = {0, 0, 0, 0};
+  uint4 gs[2], gz[2];  // g32 scale/zero of tokens 16kc..16kc+15, group jg
+  if (active) {
+    if constexpr (LAYOUT == kPaged) {
+      const uint4 *cp = (const uint4 *)(p.kq + ((((size_t)pg * p.HKV + hkv) * 4 + kc) * kPage + 4 * mrow) * 8);
+      const uint4 c0 = cp[0], c1 = cp[1];
+      x[0] = ((uint64_t)c0.y << 32) | c0.x;
+      x[1] = ((uint64_t)c0.w << 32) | c0.z;
+      x[2] = ((uint64_t)c1.y << 32) | c1.x;
+      x[3] = ((uint64_t)c1.w << 32) | c1.z;
     } else {
 #pragma unroll
-      for (int e = 0; e < 32; ++e) {
-        sc[e] = 1.f;
-        zsum += qv[e];
+      for (int tau = 0; tau < 4; ++tau) {
+        const int t = min(t0 + 4 * mrow + tau, Tb - 1);
+        x[tau] = *(const uint64_t *)(p.kq + (((size_t)b * p.T + t) * p.HKV + hkv) * 32 + 8 * kc);
       }
     }
+    if constexpr (SMODE == kG32) {
+      const size_t so = (((size_t)pg * p.HKV + hkv) * 4 + jg) * kPage + 16 * kc;
+      gs[0] = ((const uint4 *)((const uint16_t *)p.ks + so))[0];
+      gs[1] = ((const uint4 *)((const uint16_t *)p.ks + so))[1];
+      gz[0] = ((const uint4 *)((const uint16_t *)p.kz + so))[0];
+      gz[1] = ((const uint4 *)((const uint16_t *)p.kz + so))[1];
+    }
   }
-  // Coarse operand for MFMA m' = 2h + s: element 2q+half <-> channel 32kc + 16h + 4s + q + 8half,
-  // divided by 4^q; nonzero only when kc == j (the column's group).
+  uint64_t px = 0;
+  uint2 pgs = make_uint2(0, 0), pgz = make_uint2(0, 0);
+  if (do_probe) {
+    const int tok = pa + mrow;
+    if constexpr (LAYOUT == kPaged) {
+      px = *(const uint64_t *)(p.kq + ((((size_t)ppg * p.HKV + hkv) * 4 + kc) * kPage + (tok & (kPage - 1))) * 8);
+      if constexpr (SMODE == kG32) {
+        const size_t so = (((size_t)ppg * p.HKV + hkv) * 4 + jg) * kPage + ((pa & (kPage - 1)) + 4 * kc);
+        pgs = *(const uint2 *)((const uint16_t *)p.ks + so);
+        pgz = *(const uint2 *)((const uint16_t *)p.kz + so);
+      }
+    } else {
+      const int t = min(tok, Tb - 1);
+      px = *(const uint64_t *)(p.kq + (((size_t)b * p.T + t) * p.HKV + hkv) * 32 + 8 * kc);
+    }
+  }
+
+  // ------------------------------------------------ phase 2: operands and scores
+  float qv[32];
+  raw32_to_f32(qraw, p.q_dtype, qv);
+#pragma unroll
+  for (int e = 0; e < 32; ++e) qv[e] = row_ok ? (float)(_Float16)qv[e] : 0.f;  // q16 (attn_kernel...q2fp8.py:47)
+
+  // B operands.  g32 (folded scales): MFMA m' = 2h + s, element 2q+half <-> channel
+  // 32kc + 16h + 4s + q + 8half, divided by 4^q.  channel (explicit dequant): element e of
+  // MFMA m' <-> channel 32kc + 8m' + e.  Both only on the column's own group (kc == j).
   f16x8 qa[4];
+  float zq = 0.f;
+  uint32_t spair[16], zpair[16];
+  if constexpr (SMODE == kG32) {
 #pragma unroll
-  for (int mp = 0; mp < 4; ++mp) {
-    const int h = mp >> 1, s = mp & 1;
+    for (int mp = 0; mp < 4; ++mp) {
+      const int h = mp >> 1, s = mp & 1;
 #pragma unroll
-    for (int qq = 0; qq < 4; ++qq) {
+      for (int qq = 0; qq < 4; ++qq) {
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const int ch = 16 * h + 4 * s + qq + 8 * half;
-        const float inv = qq == 0 ? 1.f : (qq == 1 ? 0.25f : (qq == 2 ? 0.0625f : 0.015625f));
-        float val = (kc == jg) ? (qv[ch] * sc[ch]) * inv : 0.f;
-        qa[mp][2 * qq + half] = (_Float16)val;
+        for (int half = 0; half < 2; ++half) {
+          const int ch = 16 * h + 4 * s + qq + 8 * half;
+          const float inv = qq == 0 ? 1.f : (qq == 1 ? 0.25f : (qq == 2 ? 0.0625f : 0.015625f));
+          qa[mp][2 * qq + half] = (_Float16)((kc == jg) ? qv[ch] * inv : 0.f);
+        }
       }
     }
+    float qs = 0.f;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) qs += qv[e];
+    zq = __shfl(qs, (jg << 4) | n) * (1.0f / 16777216.f);  // sum_{d in group j} q16, in 2^-24 units
+  } else {
+#pragma unroll
+    for (int mp = 0; mp < 4; ++mp)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qa[mp][e] = (_Float16)((kc == jg) ? qv[8 * mp + e] : 0.f);
+    float sv[32], zv[32];
+    raw32_to_f32(sraw, p.s_dtype, sv);
+    raw32_to_f32(zraw, p.s_dtype, zv);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      spair[i] = f32_to_f16_bits(sv[2 * i]) | (f32_to_f16_bits(sv[2 * i + 1]) << 16);
+      zpair[i] = f32_to_f16_bits(zv[2 * i]) | (f32_to_f16_bits(zv[2 * i + 1]) << 16);
+    }
   }
-  // Refine operand for MFMA m': element e <-> channel 32kc + 8m' + e (all groups).
+  // residual operand (g32): element e of MFMA m' <-> channel 32kc + 8m' + e, every column.
   f16x8 qr[4];
+  if constexpr (SMODE == kG32 && RES != kResNone) {
 #pragma unroll
-  for (int mp = 0; mp < 4; ++mp)
+    for (int mp = 0; mp < 4; ++mp)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) qr[mp][e] = (_Float16)qv[8 * mp + e];
-  // Per-(j,i) constant of the epilogue: sum_{d in group j} q16 (g32) or
-  // sum_{d in chunk j} q16 * z (channel); computed by the lanes with kc == j.
-  const float zq = __shfl(zsum, (jg << 4) | n);
+      for (int e = 0; e < 8; ++e) qr[mp][e] = (_Float16)qv[8 * mp + e];
+  }
 
-  const float qk_scale = p.scale;
-
-  // ------------------------------------------------------- coarse score tile
-  // Computes raw scores (before *scale*log2e) of 16 tokens for the lane's column.
-  //   tok_row(mrow) : token handled by MFMA row `mrow`
-  //   outputs racc[u] for rows 4*kc + u
-  auto score_tile = [&](const uint64_t x, const float *s4, const float *z4, float *racc) {
+  // raw scores of one 16-token tile for the lane's column, summed over groups:
+  //   g32: R' = sum_j s_j * D_j + z_j * zq_j   (units of 2^-24 of the dot product)
+  //   channel: R = sum_j D_j                    (dot product)
+  auto score_tile = [&](uint64_t xx, const uint32_t *s4, const uint32_t *z4, float *out) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    const uint32_t wlo = (uint32_t)x, whi = (uint32_t)(x >> 32);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes_to_f16x8(wlo, 0), qa[0], acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes_to_f16x8(wlo, 1), qa[1], acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes_to_f16x8(whi, 0), qa[2], acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes_to_f16x8(whi, 1), qa[3], acc, 0, 0, 0);
+    const uint32_t wlo = (uint32_t)xx, whi = (uint32_t)(xx >> 32);
+    if constexpr (SMODE == kG32) {
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes_to_f16x8(wlo, 0), qa[0], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes_to_f16x8(wlo, 1), qa[1], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes_to_f16x8(whi, 0), qa[2], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes_to_f16x8(whi, 1), qa[3], acc, 0, 0, 0);
+    } else {
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant8_channel(wlo & 0xffffu, spair + 0, zpair + 0), qa[0], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant8_channel(wlo >> 16, spair + 4, zpair + 4), qa[1], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant8_channel(whi & 0xffffu, spair + 8, zpair + 8), qa[2], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant8_channel(whi >> 16, spair + 12, zpair + 12), qa[3], acc, 0, 0, 0);
+    }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       float r;
       if constexpr (SMODE == kG32) {
-        r = (s4[u] * 16777216.f) * acc[u] + z4[u] * zq;
+        const float su = f16_bits_to_f32((s4[u >> 1] >> (16 * (u & 1))) & 0xffffu);
+        const float zu = f16_bits_to_f32((z4[u >> 1] >> (16 * (u & 1))) & 0xffffu);
+        r = __builtin_fmaf(su, acc[u], zu * zq);
       } else {
-        r = 16777216.f * acc[u] + zq;
+        r = acc[u];
       }
       r += dpp<kRowRor4>(r);
       r += dpp<kRowRor8>(r);
-      racc[u] = r;
+      out[u] = r;
     }
   };
+  const float cs1 = SMODE == kG32 ? p.scale * 16777216.f : p.scale;  // (R * cs1) * log2e = log2-scaled score
 
-  auto token_codes = [&](int tok, int pg) -> uint64_t {
-    // 32 codes of channel group kc for token `tok` (sequence position)
-    if constexpr (LAYOUT == kPaged) {
-      const size_t off = (((size_t)pg * p.HKV + hkv) * 4 + kc) * (kPage * 8) + (size_t)(tok & (kPage - 1)) * 8;
-      return *(const uint64_t *)(p.kq + off);
-    } else {
-      const int t = min(tok, Tb - 1);
-      const size_t off = (((size_t)b * p.T + t) * p.HKV + hkv) * 32 + 8 * kc;
-      return *(const uint64_t *)(p.kq + off);
-    }
-  };
-
-  // ------------------------------------------------------------ probe windows
-  if (p.th_in == nullptr && wv < 2) {
-    const int a = wv == 0 ? 0 : (NTB - 1) * 16;  // attn_kernel...q2fp8.py:58-73
-    const int pg = (LAYOUT == kPaged) ? p.bt[(size_t)b * p.bt_stride + (a >> 6)] : 0;
-    const uint64_t x = token_codes(a + mrow, pg);
-    float s4[4] = {1.f, 1.f, 1.f, 1.f}, z4[4] = {0.f, 0.f, 0.f, 0.f};
-    if constexpr (SMODE == kG32) {
-      const size_t sb = (((size_t)pg * p.HKV + hkv) * 4 + jg) * kPage + ((a & (kPage - 1)) + 4 * kc);
-      const uint2 sv = *(const uint2 *)((const uint16_t *)p.ks + sb);
-      const uint2 zv = *(const uint2 *)((const uint16_t *)p.kz + sb);
-      s4[0] = f16_bits_to_f32(sv.x & 0xffff);
-      s4[1] = f16_bits_to_f32(sv.x >> 16);
-      s4[2] = f16_bits_to_f32(sv.y & 0xffff);
-      s4[3] = f16_bits_to_f32(sv.y >> 16);
-      z4[0] = f16_bits_to_f32(zv.x & 0xffff);
-      z4[1] = f16_bits_to_f32(zv.x >> 16);
-      z4[2] = f16_bits_to_f32(zv.y & 0xffff);
-      z4[3] = f16_bits_to_f32(zv.y >> 16);
-    }
-    float r[4];
-    score_tile(x, s4, z4, r);
+  // probe windows
+  if (do_probe) {
+    const uint32_t s4[2] = {pgs.x, pgs.y}, z4[2] = {pgz.x, pgz.y};
+    float r4[4];
+    score_tile(px, s4, z4, r4);
     float mx = -INFINITY;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int t = a + 4 * kc + u;
-      const float sv = (r[u] * qk_scale) * kLog2e;
-      mx = fmaxf(mx, t < Tb ? sv : -INFINITY);
+      const int t = pa + 4 * kc + u;
+      mx = fmaxf(mx, t < Tb ? (r4[u] * cs1) * kLog2e : -INFINITY);
     }
     mx = xor_max(mx, 16);
     mx = xor_max(mx, 32);
-    if (lane < 4) s_probe[wv][lane] = mx;  // lane == ir here (kc == 0, jg == 0)
+    if (lane < 4) s_probe[wv][lane] = mx;  // lane == ir here
   }
 
-  // ---------------------------------------------------------- chunk scores
-  const bool active = t0 < Tb;
-  float R[16];  // raw coarse scores of tokens t0 + 16*kc + k, column (j,i) (identical across j)
-  int pg = 0;
+  // own chunk: R[k] = raw score of token t0 + 16kc + k (k = 4u + tau)
+  float R[16];
   if (active) {
-    if constexpr (LAYOUT == kPaged) pg = p.bt[(size_t)b * p.bt_stride + chunk];
-    // token of MFMA row m in tile tau is 4m + tau (within the chunk)
-    uint64_t x[4];
-    if constexpr (LAYOUT == kPaged) {
-      const size_t off = (((size_t)pg * p.HKV + hkv) * 4 + kc) * (kPage * 8) + (size_t)(4 * mrow) * 8;
-      const uint4 v0 = *(const uint4 *)(p.kq + off);
-      const uint4 v1 = *(const uint4 *)(p.kq + off + 16);
-      x[0] = ((uint64_t)v0.y << 32) | v0.x;
-      x[1] = ((uint64_t)v0.w << 32) | v0.z;
-      x[2] = ((uint64_t)v1.y << 32) | v1.x;
-      x[3] = ((uint64_t)v1.w << 32) | v1.z;
-    } else {
-#pragma unroll
-      for (int tau = 0; tau < 4; ++tau) x[tau] = token_codes(t0 + 4 * mrow + tau, 0);
-    }
-    float s16[16], z16[16];
-    if constexpr (SMODE == kG32) {
-      const size_t sb = (((size_t)pg * p.HKV + hkv) * 4 + jg) * kPage + 16 * kc;
-      const uint4 *sp = (const uint4 *)((const uint16_t *)p.ks + sb);
-      const uint4 *zp = (const uint4 *)((const uint16_t *)p.kz + sb);
-      uint32_t sw[8], zw[8];
-      const uint4 s0 = sp[0], s1 = sp[1], z0 = zp[0], z1 = zp[1];
-      sw[0] = s0.x; sw[1] = s0.y; sw[2] = s0.z; sw[3] = s0.w;
-      sw[4] = s1.x; sw[5] = s1.y; sw[6] = s1.z; sw[7] = s1.w;
-      zw[0] = z0.x; zw[1] = z0.y; zw[2] = z0.z; zw[3] = z0.w;
-      zw[4] = z1.x; zw[5] = z1.y; zw[6] = z1.z; zw[7] = z1.w;
-#pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        s16[k] = f16_bits_to_f32((sw[k >> 1] >> (16 * (k & 1))) & 0xffff);
-        z16[k] = f16_bits_to_f32((zw[k >> 1] >> (16 * (k & 1))) & 0xffff);
-      }
-    } else {
-#pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        s16[k] = 1.f;
-        z16[k] = 0.f;
-      }
-    }
+    const uint32_t sw[8] = {gs[0].x, gs[0].y, gs[0].z, gs[0].w, gs[1].x, gs[1].y, gs[1].z, gs[1].w};
+    const uint32_t zw[8] = {gz[0].x, gz[0].y, gz[0].z, gz[0].w, gz[1].x, gz[1].y, gz[1].z, gz[1].w};
 #pragma unroll
     for (int tau = 0; tau < 4; ++tau) {
-      float s4[4], z4[4], r[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        s4[u] = s16[4 * u + tau];
-        z4[u] = z16[4 * u + tau];
+      // scale/zero of tokens 4u + tau (u = 0..3) as fp16 pairs (u=0,1), (u=2,3)
+      uint32_t s4[2], z4[2];
+      if constexpr (SMODE == kG32) {
+        const int sh = 16 * (tau & 1);
+        const int wi = tau >> 1;
+        // token 4u+tau sits in word (4u+tau)/2 = 2u + wi, half tau&1
+        s4[0] = ((sw[0 + wi] >> sh) & 0xffffu) | (((sw[2 + wi] >> sh) & 0xffffu) << 16);
+        s4[1] = ((sw[4 + wi] >> sh) & 0xffffu) | (((sw[6 + wi] >> sh) & 0xffffu) << 16);
+        z4[0] = ((zw[0 + wi] >> sh) & 0xffffu) | (((zw[2 + wi] >> sh) & 0xffffu) << 16);
+        z4[1] = ((zw[4 + wi] >> sh) & 0xffffu) | (((zw[6 + wi] >> sh) & 0xffffu) << 16);
       }
-      score_tile(x[tau], s4, z4, r);
+      float r4[4];
+      score_tile(x[tau], s4, z4, r4);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) R[4 * u + tau] = r[u];
+      for (int u = 0; u < 4; ++u) R[4 * u + tau] = r4[u];
+    }
+    if (t0 + kPage > Tb) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k)
+        if (t0 + 16 * kc + k >= Tb) R[k] = -INFINITY;
     }
   } else {
 #pragma unroll
-    for (int k = 0; k < 16; ++k) R[k] = 0.f;
+    for (int k = 0; k < 16; ++k) R[k] = -INFINITY;
   }
 
-  // coarse log2-scaled scores, masked
-  float S[16];
+  // ------------------------------------------------ prune
+  float mx = R[0];
 #pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const int t = t0 + 16 * kc + k;
-    const float sv = (R[k] * qk_scale) * kLog2e;
-    S[k] = (active && t < Tb && row_ok) ? sv : -INFINITY;
-  }
-
+  for (int k = 1; k < 16; ++k) mx = fmaxf(mx, R[k]);
+  mx = (mx * cs1) * kLog2e;
+  if (SBS >= 32) mx = xor_max(mx, 16);
+  if (SBS >= 64) mx = xor_max(mx, 32);
+  if (SBS > kPage && lane < 4) s_pmax[wv][lane] = mx;
   __syncthreads();
   float th;
   if (p.th_in != nullptr) {
@@ -352,52 +423,29 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
   } else {
     th = row_ok ? fmaxf(s_probe[0][ir], s_probe[1][ir]) - p.delta : INFINITY;
   }
-  if (p.th_out != nullptr && blockIdx.x == 0 && threadIdx.x < G) {
-    p.th_out[(size_t)b * p.HQ + hkv * G + threadIdx.x] = th;  // lane == ir for threadIdx < 4
-  }
-
-  // ------------------------------------------------------------------ prune
-  // block max over the lane's 16 tokens, then over lane groups per SBS
-  float mx = S[0];
-#pragma unroll
-  for (int k = 1; k < 16; ++k) mx = fmaxf(mx, S[k]);
-  const int SBS = p.SBS;
-  if (SBS >= 32) mx = xor_max(mx, 16);
-  if (SBS >= 64) mx = xor_max(mx, 32);
+  if (p.th_out != nullptr && blockIdx.x == 0 && threadIdx.x < G) p.th_out[(size_t)b * p.HQ + hkv * G + threadIdx.x] = th;
   if (SBS > kPage) {
-    if (lane < 4) s_pmax[wv][lane] = mx;
-  }
-  __syncthreads();
-  if (SBS > kPage) {
-    const int wpb = SBS / kPage;  // waves per block
+    const int wpb = SBS / kPage;
     const int w0 = (wv / wpb) * wpb;
     float m2 = -INFINITY;
     for (int w = w0; w < w0 + wpb; ++w) m2 = fmaxf(m2, s_pmax[w][ir]);
     mx = m2;
   }
-  // "prune iff all rows below" (strict <), rows >= G do not vote
-  const bool notbelow = row_ok && !(mx < th);
-  const uint64_t bal = __ballot(notbelow);
-  // keep flag of the sub-block holding the lane's tokens
-  uint32_t keep16;
-  if (SBS == 16) {
-    keep16 = ((bal >> (16 * kc)) & 0xffffull) != 0;
-  } else if (SBS == 32) {
-    keep16 = ((bal >> (32 * (kc >> 1))) & 0xffffffffull) != 0;
-  } else {
-    keep16 = bal != 0;
-  }
-  // mask entries of the sub-blocks starting in this chunk
+  // prune iff every row of the group is below its threshold (strict <); rows >= G do not vote
+  const uint64_t bal = __ballot(row_ok && !(mx < th));
+  bool keep16;
+  if (SBS == 16) keep16 = ((bal >> (16 * kc)) & 0xffffull) != 0;
+  else if (SBS == 32) keep16 = ((bal >> (32 * (kc >> 1))) & 0xffffffffull) != 0;
+  else keep16 = bal != 0;
   {
     int8_t *mrow_ptr = p.mask + ((size_t)b * p.HKV + hkv) * p.ntbs;
     if (SBS <= kPage) {
       const int per = kPage / SBS;
       const int jb = t0 / SBS;
       if (lane < per && jb + lane < p.ntbs) {
-        const int sub = lane;  // sub-block index inside the chunk
-        const int kcs = sub * (SBS / 16);
-        const bool kk = SBS == 16   ? ((bal >> (16 * kcs)) & 0xffffull) != 0
-                        : SBS == 32 ? ((bal >> (16 * kcs)) & 0xffffffffull) != 0
+        const int sh = lane * SBS;  // first lane bit of the sub-block (16 lanes per 16 tokens)
+        const bool kk = SBS == 16   ? ((bal >> sh) & 0xffffull) != 0
+                        : SBS == 32 ? ((bal >> sh) & 0xffffffffull) != 0
                                     : bal != 0;
         mrow_ptr[jb + lane] = (jb + lane < NTBS_b && kk) ? 1 : 0;
       }
@@ -406,24 +454,23 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
       if (jb < p.ntbs) mrow_ptr[jb] = (jb < NTBS_b && bal != 0) ? 1 : 0;
     }
   }
-  const bool any_keep = __ballot(keep16 != 0) != 0;
-
-  const size_t row_base = (size_t)b * p.HQ + hkv * G;  // first query row of the group
+  const bool any_keep = bal != 0;
+  const size_t row_base = (size_t)b * p.HQ + hkv * G;
   if (!any_keep || !active) {
-    if (kc == 0 && jg == 0 && row_ok && chunk < p.nch) {
+    if (kc == 0 && jg == 0 && row_ok) {
       p.m_buf[(row_base + ir) * p.nch + chunk] = -INFINITY;
       p.l_buf[(row_base + ir) * p.nch + chunk] = 0.f;
     }
     return;
   }
 
-  // ------------------------------------------------------------- exact pass
-  // refined raw score = coarse raw + q . r   (r = fp8 residual, exact in fp16)
+  // ------------------------------------------------ phase 3: exact pass of a kept chunk
+  // issue the residual and V loads together
+  uint4 rr[4][2];
   if constexpr (RES != kResNone) {
-    uint4 rr[4][2];
 #pragma unroll
     for (int tau = 0; tau < 4; ++tau) {
-      const int tk = 4 * mrow + tau;  // token inside the chunk
+      const int tk = 4 * mrow + tau;
       size_t off;
       if constexpr (LAYOUT == kPaged) {
         off = (((size_t)pg * p.HKV + hkv) * kPage + tk) * kD + 32 * kc;
@@ -434,26 +481,65 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
       rr[tau][0] = *(const uint4 *)(p.kr + off);
       rr[tau][1] = *(const uint4 *)(p.kr + off + 16);
     }
+  }
+  uint4 vv[8][2];
+  uint8_t *st = s_vstage + (LAYOUT == kContig ? wv * kPage * kVRow : 0);
+  if constexpr (LAYOUT == kPaged) {
+    const uint16_t *vp = (const uint16_t *)p.v + (((size_t)pg * p.HKV + hkv) * 128) * kPage;
 #pragma unroll
-    for (int tau = 0; tau < 4; ++tau) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16x8<RES>(rr[tau][0].x, rr[tau][0].y), qr[0], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16x8<RES>(rr[tau][0].z, rr[tau][0].w), qr[1], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16x8<RES>(rr[tau][1].x, rr[tau][1].y), qr[2], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16x8<RES>(rr[tau][1].z, rr[tau][1].w), qr[3], acc, 0, 0, 0);
+    for (int nu = 0; nu < 8; ++nu)
 #pragma unroll
-      for (int u = 0; u < 4; ++u) R[4 * u + tau] += acc[u];
+      for (int kap = 0; kap < 2; ++kap) vv[nu][kap] = *(const uint4 *)(vp + (size_t)(16 * nu + n) * kPage + 16 * kc + 8 * kap);
+  } else {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int idx = r * 64 + lane;
+      const int tk = idx >> 4, vc = idx & 15;
+      const int t = min(t0 + tk, Tb - 1);
+      vv[r >> 1][r & 1] = *(const uint4 *)((const uint16_t *)p.v + (((size_t)b * p.T + t) * p.HKV + hkv) * 128 + 8 * vc);
     }
   }
-  // active tokens: valid and inside a kept sub-block
+
+  if constexpr (RES != kResNone) {
+#pragma unroll
+    for (int tau = 0; tau < 4; ++tau) {
+      if constexpr (SMODE == kG32) {
+        // refined = coarse + q . r   (exact fp16 residual, every column carries q_i)
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16x8<RES>(rr[tau][0].x, rr[tau][0].y), qr[0], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16x8<RES>(rr[tau][0].z, rr[tau][0].w), qr[1], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16x8<RES>(rr[tau][1].x, rr[tau][1].y), qr[2], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16x8<RES>(rr[tau][1].z, rr[tau][1].w), qr[3], acc, 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) R[4 * u + tau] = __builtin_fmaf(acc[u], 1.0f / 16777216.f, R[4 * u + tau]);
+      } else {
+        // reference: k_tilde = fp16(k_hat + fp16(res)) (attn_kernel...q2fp8.py:109-115), full re-score
+        const uint64_t xx = x[tau];
+        const uint32_t wlo = (uint32_t)xx, whi = (uint32_t)(xx >> 32);
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(add_f16x8(dequant8_channel(wlo & 0xffffu, spair + 0, zpair + 0), fp8x8_to_f16x8<RES>(rr[tau][0].x, rr[tau][0].y)), qa[0], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(add_f16x8(dequant8_channel(wlo >> 16, spair + 4, zpair + 4), fp8x8_to_f16x8<RES>(rr[tau][0].z, rr[tau][0].w)), qa[1], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(add_f16x8(dequant8_channel(whi & 0xffffu, spair + 8, zpair + 8), fp8x8_to_f16x8<RES>(rr[tau][1].x, rr[tau][1].y)), qa[2], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(add_f16x8(dequant8_channel(whi >> 16, spair + 12, zpair + 12), fp8x8_to_f16x8<RES>(rr[tau][1].z, rr[tau][1].w)), qa[3], acc, 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          float r = acc[u];
+          r += dpp<kRowRor4>(r);
+          r += dpp<kRowRor8>(r);
+          R[4 * u + tau] = r;
+        }
+      }
+    }
+  }
+
+  // softmax partial over the active tokens (valid and in a kept sub-block)
   float P[16];
   float mrow_max = -INFINITY;
 #pragma unroll
   for (int k = 0; k < 16; ++k) {
     const int t = t0 + 16 * kc + k;
-    const float sv = (R[k] * qk_scale) * kLog2e;
     const bool act = row_ok && t < Tb && keep16;
-    P[k] = act ? sv : -INFINITY;
+    P[k] = act ? (R[k] * cs1) * kLog2e : -INFINITY;
     mrow_max = fmaxf(mrow_max, P[k]);
   }
   mrow_max = xor_max(mrow_max, 16);
@@ -468,63 +554,59 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
   lsum = xor_sum(lsum, 16);
   lsum = xor_sum(lsum, 32);
 
-  // P operand (A) of the P.V MFMA for K-chunk kap: element e <-> token 16*kc + 8*kap + e
-  typename VTr::vec pa[2];
+  // P operand (A) of P.V for K-chunk kap: element e <-> token 16*kc + 8*kap + e
+  typename VTr::vec pa2[2];
 #pragma unroll
   for (int kap = 0; kap < 2; ++kap) {
     u32x4 w;
 #pragma unroll
     for (int e = 0; e < 4; ++e) w[e] = VTr::pack2(P[8 * kap + 2 * e], P[8 * kap + 2 * e + 1]);
-    pa[kap] = __builtin_bit_cast(typename VTr::vec, w);
+    pa2[kap] = __builtin_bit_cast(typename VTr::vec, w);
   }
 
   const bool partial = (t0 + kPage) > Tb;
   f32x4 oacc[8];
 #pragma unroll
   for (int nu = 0; nu < 8; ++nu) oacc[nu] = f32x4{0.f, 0.f, 0.f, 0.f};
-
   if constexpr (LAYOUT == kPaged) {
-    const uint16_t *vp = (const uint16_t *)p.v + (((size_t)pg * p.HKV + hkv) * 128) * kPage;
 #pragma unroll
     for (int nu = 0; nu < 8; ++nu) {
 #pragma unroll
       for (int kap = 0; kap < 2; ++kap) {
-        const int vcol = 16 * nu + n;
-        const int tk = 16 * kc + 8 * kap;
-        uint4 vv = *(const uint4 *)(vp + (size_t)vcol * kPage + tk);
+        uint4 v4 = vv[nu][kap];
         if (partial) {
-          // zero V of tokens past the sequence end (their page slots are not data)
-          uint32_t w4[4] = {vv.x, vv.y, vv.z, vv.w};
+          // V of page slots past the sequence end is not data: zero it
+          const int tk = 16 * kc + 8 * kap;
+          uint32_t w4[4] = {v4.x, v4.y, v4.z, v4.w};
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int ta = t0 + tk + 2 * e;
             if (ta >= Tb) w4[e] &= 0xffff0000u;
             if (ta + 1 >= Tb) w4[e] &= 0x0000ffffu;
           }
-          vv = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+          v4 = make_uint4(w4[0], w4[1], w4[2], w4[3]);
         }
-        u32x4 w = {vv.x, vv.y, vv.z, vv.w};
-        oacc[nu] = VTr::mfma(pa[kap], __builtin_bit_cast(typename VTr::vec, w), oacc[nu]);
+        const u32x4 w = {v4.x, v4.y, v4.z, v4.w};
+        oacc[nu] = VTr::mfma(pa2[kap], __builtin_bit_cast(typename VTr::vec, w), oacc[nu]);
       }
     }
   } else {
-    // stage the chunk's V tile [64 tokens][128] into LDS (row pitch kVRow), then read columns
-    uint8_t *st = s_vstage + wv * kPage * kVRow;
+    // contiguous layout: stage the V tile [64 tokens][128] through LDS, then read columns
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int idx = r * 64 + lane;
       const int tk = idx >> 4, vc = idx & 15;
-      const int t = min(t0 + tk, Tb - 1);
-      const uint4 vv = *(const uint4 *)((const uint16_t *)p.v + (((size_t)b * p.T + t) * p.HKV + hkv) * 128 + 8 * vc);
+      const uint4 v4 = vv[r >> 1][r & 1];
       uint32_t *d = (uint32_t *)(st + tk * kVRow + 16 * vc);
       const bool ok = (t0 + tk) < Tb;
-      d[0] = ok ? vv.x : 0u;
-      d[1] = ok ? vv.y : 0u;
-      d[2] = ok ? vv.z : 0u;
-      d[3] = ok ? vv.w : 0u;
+      d[0] = ok ? v4.x : 0u;
+      d[1] = ok ? v4.y : 0u;
+      d[2] = ok ? v4.z : 0u;
+      d[3] = ok ? v4.w : 0u;
     }
-    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
     for (int nu = 0; nu < 8; ++nu) {
 #pragma unroll
@@ -538,38 +620,38 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
           const uint32_t hi = *(const uint16_t *)(st + (tk + 2 * e + 1) * kVRow + 2 * vcol);
           w[e] = lo | (hi << 16);
         }
-        oacc[nu] = VTr::mfma(pa[kap], __builtin_bit_cast(typename VTr::vec, w), oacc[nu]);
+        oacc[nu] = VTr::mfma(pa2[kap], __builtin_bit_cast(typename VTr::vec, w), oacc[nu]);
       }
     }
   }
 
-  // write the chunk partial: lanes 0..15 hold rows 0..3 of columns 16*nu + n
-  if (chunk < p.nch) {
-    if (lane < 16) {
+  // chunk partial: lanes 0..15 hold rows 0..3 of columns 16*nu + n
+  if (lane < 16) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        if (u < G) {
-          float *op = p.o_buf + ((row_base + u) * p.nch + chunk) * 128 + n;
+    for (int u = 0; u < 4; ++u) {
+      if (u < G) {
+        float *op = p.o_buf + ((row_base + u) * p.nch + chunk) * 128 + n;
 #pragma unroll
-          for (int nu = 0; nu < 8; ++nu) op[16 * nu] = oacc[nu][u];
-        }
+        for (int nu = 0; nu < 8; ++nu) op[16 * nu] = oacc[nu][u];
       }
     }
-    if (kc == 0 && jg == 0 && row_ok) {
-      p.m_buf[(row_base + ir) * p.nch + chunk] = mrow_max;
-      p.l_buf[(row_base + ir) * p.nch + chunk] = lsum;
-    }
+  }
+  if (kc == 0 && jg == 0 && row_ok) {
+    p.m_buf[(row_base + ir) * p.nch + chunk] = mrow_max;
+    p.l_buf[(row_base + ir) * p.nch + chunk] = lsum;
   }
 }
 
 // --------------------------------------------------------------------------
 // Log-sum-exp merge of the chunk partials (attn_kernel...q2fp8.py:142-171).
-// One workgroup (128 threads = 2 waves) per (sequence, query head).  Kept
-// chunks (l > 0) are compacted with a wave ballot into LDS, in chunk order.
+// One workgroup (256 threads) per (sequence, query head).  Kept chunks (l > 0)
+// are compacted with a wave ballot into LDS in chunk order; then 4 slices of
+// 64 threads each accumulate a quarter of them (2 columns per thread, 8
+// independent loads in flight) and the slices are combined through LDS.
 // --------------------------------------------------------------------------
-constexpr int kMergeSeg = 1024;
+constexpr int kMergeSeg = 2048;
 
-__global__ __launch_bounds__(128) void q2fp8_merge_kernel(const DecodeParams p) {
+__global__ __launch_bounds__(256) void q2fp8_merge_kernel(const DecodeParams p) {
   const int row = blockIdx.x;  // b * HQ + hq
   const int b = row / p.HQ;
   const int tid = threadIdx.x;
@@ -582,65 +664,99 @@ __global__ __launch_bounds__(128) void q2fp8_merge_kernel(const DecodeParams p) 
 
   __shared__ int s_list[kMergeSeg];
   __shared__ float s_w[kMergeSeg];
-  __shared__ float s_red[2];
-  __shared__ int s_cnt[2];
+  __shared__ float s_red[4];
+  __shared__ int s_cnt[4];
+  __shared__ float2 s_part[4][64];
 
-  float Mrun = -INFINITY, Arun = 0.f, Orun = 0.f;
+  float Mrun = -INFINITY, Arun = 0.f;
+  float2 Orun = make_float2(0.f, 0.f);
   for (int seg = 0; seg < nchb; seg += kMergeSeg) {
     const int segn = min(kMergeSeg, nchb - seg);
-    // pass 1: segment max over kept chunks
+    // segment max over kept chunks
     float mloc = -INFINITY;
-    for (int c = tid; c < segn; c += 128) {
-      const float l = lrow[seg + c];
-      if (l > 0.f) mloc = fmaxf(mloc, mrow[seg + c]);
-    }
+    for (int c = tid; c < segn; c += 256)
+      if (lrow[seg + c] > 0.f) mloc = fmaxf(mloc, mrow[seg + c]);
     for (int o = 32; o >= 1; o >>= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, o));
     if (lane == 0) s_red[wv] = mloc;
     __syncthreads();
-    const float Mseg = fmaxf(s_red[0], s_red[1]);
-    // pass 2: compact kept chunks, in order, with their weights 2^(m - Mseg)
+    const float Mseg = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    // ordered compaction of kept chunks with their weights 2^(m - Mseg)
     int base = 0;
-    for (int c0 = 0; c0 < segn; c0 += 128) {
+    float aloc = 0.f;
+    for (int c0 = 0; c0 < segn; c0 += 256) {
       const int c = c0 + tid;
       bool keep = false;
       float wgt = 0.f;
       if (c < segn) {
         const float l = lrow[seg + c];
         keep = l > 0.f;
-        if (keep) wgt = exp2f(mrow[seg + c] - Mseg);
+        if (keep) {
+          wgt = exp2f(mrow[seg + c] - Mseg);
+          aloc += l * wgt;
+        }
       }
       const uint64_t bal = __ballot(keep);
       const int before = __popcll(bal & ((1ull << lane) - 1ull));
+      __syncthreads();
       if (lane == 0) s_cnt[wv] = __popcll(bal);
       __syncthreads();
-      const int off = base + (wv ? s_cnt[0] : 0) + before;
+      int off = base + before;
+      for (int w = 0; w < wv; ++w) off += s_cnt[w];
       if (keep) {
         s_list[off] = seg + c;
         s_w[off] = wgt;
       }
-      base += s_cnt[0] + s_cnt[1];
-      __syncthreads();
+      base += s_cnt[0] + s_cnt[1] + s_cnt[2] + s_cnt[3];
     }
-    // pass 3: accumulate (every thread owns one output column)
-    float A = 0.f, O = 0.f;
-    for (int k = 0; k < base; ++k) {
-      const int c = s_list[k];
-      const float wgt = s_w[k];
-      A += lrow[c] * wgt;
-      O += orow[(size_t)c * 128 + tid] * wgt;
+    for (int o = 32; o >= 1; o >>= 1) aloc += __shfl_xor(aloc, o);
+    __syncthreads();
+    if (lane == 0) s_red[wv] = aloc;
+    __syncthreads();
+    const float Aseg = s_red[0] + s_red[1] + s_red[2] + s_red[3];
+    // accumulate: slice wv takes kept entries k = wv, wv+4, ...; thread owns columns 2*lane, 2*lane+1
+    float2 o2 = make_float2(0.f, 0.f);
+    int k = wv;
+    for (; k + 12 < base; k += 16) {
+      float2 v[4];
+      float w[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        v[u] = *(const float2 *)(orow + (size_t)s_list[k + 4 * u] * 128 + 2 * lane);
+        w[u] = s_w[k + 4 * u];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        o2.x = __builtin_fmaf(v[u].x, w[u], o2.x);
+        o2.y = __builtin_fmaf(v[u].y, w[u], o2.y);
+      }
     }
+    for (; k < base; k += 4) {
+      const float2 v = *(const float2 *)(orow + (size_t)s_list[k] * 128 + 2 * lane);
+      o2.x = __builtin_fmaf(v.x, s_w[k], o2.x);
+      o2.y = __builtin_fmaf(v.y, s_w[k], o2.y);
+    }
+    s_part[wv][lane] = o2;
+    __syncthreads();
     if (base > 0) {
+      const float2 a0 = s_part[0][lane], a1 = s_part[1][lane], a2 = s_part[2][lane], a3 = s_part[3][lane];
+      const float ox = (a0.x + a1.x) + (a2.x + a3.x);
+      const float oy = (a0.y + a1.y) + (a2.y + a3.y);
       const float Mn = fmaxf(Mrun, Mseg);
-      const float a = (Mrun == -INFINITY) ? 0.f : exp2f(Mrun - Mn);
-      const float bb = exp2f(Mseg - Mn);
-      Arun = Arun * a + A * bb;
-      Orun = Orun * a + O * bb;
+      const float ar = (Mrun == -INFINITY) ? 0.f : exp2f(Mrun - Mn);
+      const float br = exp2f(Mseg - Mn);
+      Arun = Arun * ar + Aseg * br;
+      Orun.x = Orun.x * ar + ox * br;
+      Orun.y = Orun.y * ar + oy * br;
       Mrun = Mn;
     }
     __syncthreads();
   }
-  const float res = (Arun == 0.f) ? 0.f : Orun / Arun;
-  store_any(p.out, (size_t)row * 128 + tid, p.out_dtype, res);
+  if (wv == 0) {
+    const float rx = (Arun == 0.f) ? 0.f : Orun.x / Arun;
+    const float ry = (Arun == 0.f) ? 0.f : Orun.y / Arun;
+    store_any(p.out, (size_t)row * 128 + 2 * lane, p.out_dtype, rx);
+    store_any(p.out, (size_t)row * 128 + 2 * lane + 1, p.out_dtype, ry);
+  }
 }
 
 }  // namespace ffa
@@ -760,7 +876,7 @@ extern "C" int ffa_q2fp8_decode(const ffa_q2fp8_decode_args *a, void *stream) {
     e = dispatch_rv<ffa::kContig, ffa::kChannel>(p, a->res_dtype, a->v_dtype, grid, st);
   }
   if (e != hipSuccess) return set_err(FFA_E_LAUNCH, hipGetErrorString(e));
-  hipLaunchKernelGGL(ffa::q2fp8_merge_kernel, dim3(a->B * a->HQ), dim3(128), 0, st, p);
+  hipLaunchKernelGGL(ffa::q2fp8_merge_kernel, dim3(a->B * a->HQ), dim3(256), 0, st, p);
   e = hipGetLastError();
   if (e != hipSuccess) return set_err(FFA_E_LAUNCH, hipGetErrorString(e));
   return FFA_OK;

@@ -26,6 +26,18 @@ from .decode import HEAD_DIM, DecodeWorkspace, run_decode
 PAGE = 64
 
 
+def check_append_fits(pos: torch.Tensor, Tn: int, block_table: torch.Tensor, num_pages: int) -> None:
+    """Host-side bounds check of an append (positions and page ids must stay inside the table / pool)."""
+    if block_table.shape[0] != pos.shape[0]:
+        raise ValueError("block_table must have one row per sequence")
+    last = int(pos.max().item()) + Tn - 1
+    if int(pos.min().item()) < 0 or last >= block_table.shape[1] * PAGE:
+        raise ValueError("append positions exceed the block table")
+    used = block_table[:, : last // PAGE + 1]
+    if int(used.min().item()) < 0 or int(used.max().item()) >= num_pages:
+        raise ValueError("block table references pages outside the pool")
+
+
 class PagedQ2Cache:
     def __init__(self, num_pages, HKV, device, res_dtype=torch.float8_e4m3fn, v_dtype=torch.bfloat16):
         self.P, self.HKV = int(num_pages), int(HKV)
@@ -54,6 +66,7 @@ class PagedQ2Cache:
             v = v.to(self.v_dtype).contiguous()
         pos = pos.to(torch.int32).contiguous()
         block_table = block_table.to(torch.int32).contiguous()
+        check_append_fits(pos, Tn, block_table, self.P)
         rc = N.lib().ffa_q2_quantize_g32_append(
             k.data_ptr(), N.dtype_code(k.dtype), B, Tn, HKV, pos.data_ptr(), block_table.data_ptr(),
             block_table.shape[1], self.k_q.data_ptr(), self.k_scale.data_ptr(), self.k_zero.data_ptr(),

@@ -4,7 +4,7 @@ from __future__ import annotations
 import torch
 
 from . import _native as N
-from .paged import PagedQ2Cache
+from .paged import PagedQ2Cache, check_append_fits
 
 
 def _normalize_k_weight(w_k: torch.Tensor, in_dim: int) -> torch.Tensor:
@@ -102,6 +102,7 @@ def kproj_rope_q2_append(cache: PagedQ2Cache, h, w_k, cos_rows, sin_rows, pos, b
     sin_rows = sin_rows.float().reshape(B, Tn, 128).contiguous()
     pos = pos.to(device=h.device, dtype=torch.int32).contiguous()
     block_table = block_table.to(device=h.device, dtype=torch.int32).contiguous()
+    check_append_fits(pos, Tn, block_table, cache.P)
     if v_new is not None:
         v_new = v_new.to(cache.v_dtype).contiguous()
     bias = bias.to(h.dtype).contiguous() if bias is not None else None

@@ -13,7 +13,10 @@ checkout):
                          scale/zero per token).  The reference has no such
                          quantizer; the rules mirror the per-channel one.
 * decode                 ffa-q2fp8/attn_kernel/attn_kernel_v1210_fused_bsz_q2fp8.py
-                         stage1 :10-139, stage2 :142-171, wrapper :191-309
+                         stage1 :10-139, stage2 :142-171, wrapper :191-309.
+                         per_channel mode rounds dequantized and refined K to fp16
+                         as the reference's tl.dot inputs do (:93, :109-115); g32 mode
+                         (no reference counterpart) keeps them exact.
 * threshold_external     ffa-fp8/attn_kernel/attn_kernel_v1208_fused_bsz_fp8.py:174-234
 * decode_bruteforce      same semantics as `decode`, written as scalar loops
                          for tiny shapes (an independent second statement).
@@ -116,22 +119,24 @@ def quantize_g32(k: np.ndarray, fp8: str = "e4m3fn", group: int = 32):
 
 
 def dequant(codes_packed, scale, zero, D: int, mode: str):
-    """k_hat = fp16(fp32(fp32(c) * fp32(s)) + fp32(z)) (attn_kernel...q2fp8.py:93).
+    """Dequantized 2-bit K.
 
-    per_channel: scale/zero [B, HKV, D] broadcast over T.
-    g32:         scale/zero [B, T, HKV, D/32] (one per token per group).
+    per_channel (reference, attn_kernel...q2fp8.py:93): k_hat = fp16(fp32(fp32(c) * s) + z),
+        scale/zero [B, HKV, D] broadcast over T.
+    g32 (this build's paged format): k_hat = c * s + z evaluated exactly (float64), no
+        fp16 rounding; scale/zero [B, T, HKV, D/32] fp16 values, one per token and group.
     """
     c = unpack_2bit(codes_packed, D).astype(F32)
     if mode == "per_channel":
         s = np.asarray(scale, F32)[:, None]
         z = np.asarray(zero, F32)[:, None]
-    elif mode == "g32":
+        return round_f16((c * s).astype(F32) + z)
+    if mode == "g32":
         g = D // np.asarray(scale).shape[-1]
-        s = np.repeat(np.asarray(scale, F32), g, axis=-1)
-        z = np.repeat(np.asarray(zero, F32), g, axis=-1)
-    else:
-        raise ValueError(mode)
-    return round_f16((c * s).astype(F32) + z)
+        s = np.repeat(np.asarray(scale, np.float64), g, axis=-1)
+        z = np.repeat(np.asarray(zero, np.float64), g, axis=-1)
+        return c.astype(np.float64) * s + z
+    raise ValueError(mode)
 
 
 # ----------------------------------------------------------------------------
@@ -280,7 +285,10 @@ def decode(
                 continue
             if use_res:
                 r16 = fp8_decode(k_residual[b, :Tb, h], res_fmt)  # exact in fp16
-                ktil = round_f16(khat + r16)  # (:109-115)
+                if scale_mode == "per_channel":
+                    ktil = round_f16(khat + r16)  # (:109-115)
+                else:
+                    ktil = khat + r16.astype(np.float64)  # g32: exact
                 S = _score(q16, ktil, scale)
             else:
                 S = Sq
@@ -372,16 +380,17 @@ def decode_bruteforce(q, k_q, k_scale, k_zero, v, k_residual=None, *, res_fmt="e
         c = (byte >> (2 * (d % 4))) & 3
         if scale_mode == "per_channel":
             s, z = k_scale[b, h, d], k_zero[b, h, d]
-        else:
-            s, z = k_scale[b, t, h, d // 32], k_zero[b, t, h, d // 32]
-        return f16(np.float32(np.float32(np.float32(c) * np.float32(s)) + np.float32(z)))
+            return f16(np.float32(np.float32(np.float32(c) * np.float32(s)) + np.float32(z)))
+        s, z = k_scale[b, t, h, d // 32], k_zero[b, t, h, d // 32]
+        return float(c) * float(s) + float(z)
 
     def score(b, h, g, t, refined):
         acc = 0.0
         for d in range(D):
             kv = khat(b, t, h, d)
             if refined:
-                kv = f16(np.float32(kv) + fp8_decode(k_residual[b, t, h, d], res_fmt))
+                r = float(fp8_decode(k_residual[b, t, h, d], res_fmt))
+                kv = f16(np.float32(kv) + r) if scale_mode == "per_channel" else kv + r
             acc += f16(q[b, h * G + g, d]) * kv
         return float(np.float32(np.float32(np.float32(acc) * sc) * L2E))
 

@@ -49,9 +49,10 @@ def test_contig_reference_layout(gpu, tau, res, T, BS, SBS, delta, heavy):
     print(f"[mask] T={T} BS={BS} SBS={SBSv} skip={sr:.3f} oracle_skip={diag['skip_ratio']:.3f} "
           f"mismatch_far={far} mismatch_near={near} near_blocks={near_total}")
     assert far == 0
-    assert abs(sr - (1 - mask[..., : diag['mask'].shape[-1]].sum() / diag['mask'].size)) < 1e-9
+    assert abs(sr - (1 - mask[..., : diag['mask'].shape[-1]].sum() / diag['mask'].size)) < 1e-6
+    # the GPU dequantizes K to fp16 exactly as the reference does: thresholds agree to fp32 rounding
     th_gpu = ws.threshold_buf.cpu().numpy()
-    assert np.abs(th_gpu - diag["threshold"]).max() < 2e-3
+    assert np.abs(th_gpu - diag["threshold"]).max() < 1e-4
     o_forced, _ = O.decode(q, case["k_q"], case["k_scale"], case["k_zero"], v, case["k_res"], res_fmt=res, BS=BS,
                            SBS=SBSv, delta=delta, out_dtype=tau, force_mask=mask)
     mx, mean = assert_out_close(f32(o), o_forced, "contig")
@@ -76,6 +77,7 @@ def test_paged_g32(gpu, B, T, seq_lens, BS, SBS, delta, interleave):
     ws = cache.decode(q, bt, sl, T=T, BS=BS, SBS=SBS, delta=delta)
     torch.cuda.synchronize()
     o_ref, diag = oracle_paged(case, BS=BS, SBS=SBS, delta=delta)
+    assert np.abs(ws.threshold_buf.cpu().numpy() - diag["threshold"]).max() < 1e-4
     mask = ws.mask_buf.cpu().numpy()
     far, near, near_total = compare_masks(mask, diag)
     kept = mask.sum() / sum(-(-t // SBS) for t in case["lens"]) / 8
