@@ -22,8 +22,13 @@
 //     r the fp8 residual (another f16 MFMA), exp2 softmax, P.V with a bf16/f16
 //     MFMA reading V^T pages (16-byte loads) or V staged through LDS for the
 //     contiguous reference layout.
-//   * partials (m, l, o) per 64-token chunk, merged by a second kernel that
-//     compacts the kept chunks with a wave ballot.
+//   * partials (m, l, o) per 64-token chunk; the last workgroup of each
+//     (sequence, KV head) -- found with an atomic completion counter -- merges
+//     them (kept chunks compacted in order with a wave ballot), so one launch
+//     does the whole step.
+//   * each wave owns two consecutive chunks; the grid is 1-D with the
+//     (sequence, KV head) unit fastest, so with B*HKV a multiple of 8 a unit's
+//     workgroups share one XCD and its L2.
 #include "ffa_common.h"
 #include "ffa_mi355x.h"
 
@@ -34,6 +39,9 @@ namespace ffa {
 constexpr int kD = 128;
 constexpr int kPage = 64;
 constexpr int kWaves = 4;
+constexpr int kPPW = 2;                      // 64-token chunks (pages) per wave
+constexpr int kChunksPerWG = kWaves * kPPW;  // 512 tokens per workgroup
+constexpr int kMergeSeg = 512;               // kept-chunk list segment of the merge
 constexpr int kVRow = 260;  // LDS row pitch (bytes) of the staged V tile: 256 + 4 keeps banks apart
 
 struct DecodeParams {
@@ -50,6 +58,7 @@ struct DecodeParams {
   void *out;
   float *m_buf, *l_buf, *o_buf;
   int8_t *mask;
+  int *counters;
   int q_dtype, s_dtype, out_dtype;
   int bt_stride;
   int B, T, HQ, HKV, G;
@@ -188,12 +197,17 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
   typedef VTraits<VT> VTr;
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int bh = blockIdx.y;
-  const int b = bh / p.HKV;
-  const int hkv = bh - b * p.HKV;
+  // 1-D grid: unit u = (b, hkv) is the fastest index, so with B*HKV a multiple of 8 every
+  // workgroup of one unit lands on the same XCD (dispatch is round-robin over the 8 XCDs)
+  // and the unit's partials stay in that XCD's L2 for the merge.
+  const int U = p.B * p.HKV;
+  const int u = blockIdx.x % U;
+  const int cg = blockIdx.x / U;
+  const int ngroups = gridDim.x / U;
+  const int b = u / p.HKV;
+  const int hkv = u - b * p.HKV;
   const int G = p.G;
-  const int chunk = blockIdx.x * kWaves + wv;
-  const int t0 = chunk * kPage;
+  const int c0 = cg * kChunksPerWG + wv * kPPW;  // first chunk of this wave
   const int Tb = p.seq_lens ? p.seq_lens[b] : p.T;
   const int NTB = (Tb + p.BS - 1) / p.BS;
   const int NTBS_b = NTB * (p.BS / p.SBS);
@@ -205,19 +219,24 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
   const int jg = n >> 2;
   const int ir = n & 3;
   const bool row_ok = ir < G;
-  const bool active = t0 < Tb;
   const bool do_probe = (p.th_in == nullptr) && wv < 2;
   const int pa = wv == 0 ? 0 : (NTB - 1) * 16;  // probe window (attn_kernel...q2fp8.py:58-73)
 
   __shared__ float s_probe[2][4];
-  __shared__ float s_pmax[kWaves][4];
+  __shared__ float s_wmax[kWaves][4];
+  __shared__ int s_last;
+  __shared__ int s_list[4][kMergeSeg];
+  __shared__ float s_w[4][kMergeSeg];
   __shared__ uint8_t s_vstage[LAYOUT == kContig ? kWaves * kPage * kVRow : 4];
 
-  // ------------------------------------------------ phase 0: page ids (scalar)
-  int pg = 0, ppg = 0;
+  // ------------------------------------------------ phase 0: page ids (scalar loads)
+  int pg[kPPW] = {0, 0};
+  int ppg = 0;
   if constexpr (LAYOUT == kPaged) {
     const int32_t *btr = p.bt + (size_t)b * p.bt_stride;
-    if (active) pg = btr[chunk];
+#pragma unroll
+    for (int j = 0; j < kPPW; ++j)
+      if ((c0 + j) * kPage < Tb) pg[j] = btr[c0 + j];
     if (do_probe) ppg = btr[pa >> 6];
   }
 
@@ -229,30 +248,36 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
     raw32_load(sraw, p.ks, ((size_t)b * p.HKV + hkv) * kD + 32 * kc, p.s_dtype);
     raw32_load(zraw, p.kz, ((size_t)b * p.HKV + hkv) * kD + 32 * kc, p.s_dtype);
   }
-  // own chunk: token of MFMA row m in tile tau is 4m + tau
-  uint64_t x[4] = {0, 0, 0, 0};
-  uint4 gs[2], gz[2];  // g32 scale/zero of tokens 16kc..16kc+15, group jg
-  if (active) {
-    if constexpr (LAYOUT == kPaged) {
-      const uint4 *cp = (const uint4 *)(p.kq + ((((size_t)pg * p.HKV + hkv) * 4 + kc) * kPage + 4 * mrow) * 8);
-      const uint4 c0 = cp[0], c1 = cp[1];
-      x[0] = ((uint64_t)c0.y << 32) | c0.x;
-      x[1] = ((uint64_t)c0.w << 32) | c0.z;
-      x[2] = ((uint64_t)c1.y << 32) | c1.x;
-      x[3] = ((uint64_t)c1.w << 32) | c1.z;
-    } else {
+  // token of MFMA row m in tile tau is 4m + tau (within a chunk)
+  uint64_t x[kPPW][4];
+  uint4 gs[kPPW][2], gz[kPPW][2];  // g32 scale/zero of tokens 16kc..16kc+15, group jg
 #pragma unroll
-      for (int tau = 0; tau < 4; ++tau) {
-        const int t = min(t0 + 4 * mrow + tau, Tb - 1);
-        x[tau] = *(const uint64_t *)(p.kq + (((size_t)b * p.T + t) * p.HKV + hkv) * 32 + 8 * kc);
+  for (int j = 0; j < kPPW; ++j) {
+    const int t0 = (c0 + j) * kPage;
+#pragma unroll
+    for (int tau = 0; tau < 4; ++tau) x[j][tau] = 0;
+    if (t0 < Tb) {
+      if constexpr (LAYOUT == kPaged) {
+        const uint4 *cp = (const uint4 *)(p.kq + ((((size_t)pg[j] * p.HKV + hkv) * 4 + kc) * kPage + 4 * mrow) * 8);
+        const uint4 q0 = cp[0], q1 = cp[1];
+        x[j][0] = ((uint64_t)q0.y << 32) | q0.x;
+        x[j][1] = ((uint64_t)q0.w << 32) | q0.z;
+        x[j][2] = ((uint64_t)q1.y << 32) | q1.x;
+        x[j][3] = ((uint64_t)q1.w << 32) | q1.z;
+        if constexpr (SMODE == kG32) {
+          const size_t so = (((size_t)pg[j] * p.HKV + hkv) * 4 + jg) * kPage + 16 * kc;
+          gs[j][0] = ((const uint4 *)((const uint16_t *)p.ks + so))[0];
+          gs[j][1] = ((const uint4 *)((const uint16_t *)p.ks + so))[1];
+          gz[j][0] = ((const uint4 *)((const uint16_t *)p.kz + so))[0];
+          gz[j][1] = ((const uint4 *)((const uint16_t *)p.kz + so))[1];
+        }
+      } else {
+#pragma unroll
+        for (int tau = 0; tau < 4; ++tau) {
+          const int t = min(t0 + 4 * mrow + tau, Tb - 1);
+          x[j][tau] = *(const uint64_t *)(p.kq + (((size_t)b * p.T + t) * p.HKV + hkv) * 32 + 8 * kc);
+        }
       }
-    }
-    if constexpr (SMODE == kG32) {
-      const size_t so = (((size_t)pg * p.HKV + hkv) * 4 + jg) * kPage + 16 * kc;
-      gs[0] = ((const uint4 *)((const uint16_t *)p.ks + so))[0];
-      gs[1] = ((const uint4 *)((const uint16_t *)p.ks + so))[1];
-      gz[0] = ((const uint4 *)((const uint16_t *)p.kz + so))[0];
-      gz[1] = ((const uint4 *)((const uint16_t *)p.kz + so))[1];
     }
   }
   uint64_t px = 0;
@@ -343,79 +368,95 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant8_channel(whi >> 16, spair + 12, zpair + 12), qa[3], acc, 0, 0, 0);
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int uu = 0; uu < 4; ++uu) {
       float r;
       if constexpr (SMODE == kG32) {
-        const float su = f16_bits_to_f32((s4[u >> 1] >> (16 * (u & 1))) & 0xffffu);
-        const float zu = f16_bits_to_f32((z4[u >> 1] >> (16 * (u & 1))) & 0xffffu);
-        r = __builtin_fmaf(su, acc[u], zu * zq);
+        const float su = f16_bits_to_f32((s4[uu >> 1] >> (16 * (uu & 1))) & 0xffffu);
+        const float zu = f16_bits_to_f32((z4[uu >> 1] >> (16 * (uu & 1))) & 0xffffu);
+        r = __builtin_fmaf(su, acc[uu], zu * zq);
       } else {
-        r = acc[u];
+        r = acc[uu];
       }
       r += dpp<kRowRor4>(r);
       r += dpp<kRowRor8>(r);
-      out[u] = r;
+      out[uu] = r;
     }
   };
   const float cs1 = SMODE == kG32 ? p.scale * 16777216.f : p.scale;  // (R * cs1) * log2e = log2-scaled score
 
-  // probe windows
+  // probe windows (waves 0 and 1)
   if (do_probe) {
     const uint32_t s4[2] = {pgs.x, pgs.y}, z4[2] = {pgz.x, pgz.y};
     float r4[4];
     score_tile(px, s4, z4, r4);
     float mx = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int t = pa + 4 * kc + u;
-      mx = fmaxf(mx, t < Tb ? (r4[u] * cs1) * kLog2e : -INFINITY);
+    for (int uu = 0; uu < 4; ++uu) {
+      const int t = pa + 4 * kc + uu;
+      mx = fmaxf(mx, t < Tb ? (r4[uu] * cs1) * kLog2e : -INFINITY);
     }
     mx = xor_max(mx, 16);
     mx = xor_max(mx, 32);
     if (lane < 4) s_probe[wv][lane] = mx;  // lane == ir here
   }
 
-  // own chunk: R[k] = raw score of token t0 + 16kc + k (k = 4u + tau)
-  float R[16];
-  if (active) {
-    const uint32_t sw[8] = {gs[0].x, gs[0].y, gs[0].z, gs[0].w, gs[1].x, gs[1].y, gs[1].z, gs[1].w};
-    const uint32_t zw[8] = {gz[0].x, gz[0].y, gz[0].z, gz[0].w, gz[1].x, gz[1].y, gz[1].z, gz[1].w};
+  // own chunks: R[j][k] = raw score of token (c0+j)*64 + 16kc + k (k = 4u + tau)
+  float R[kPPW][16];
 #pragma unroll
-    for (int tau = 0; tau < 4; ++tau) {
-      // scale/zero of tokens 4u + tau (u = 0..3) as fp16 pairs (u=0,1), (u=2,3)
-      uint32_t s4[2], z4[2];
-      if constexpr (SMODE == kG32) {
-        const int sh = 16 * (tau & 1);
-        const int wi = tau >> 1;
-        // token 4u+tau sits in word (4u+tau)/2 = 2u + wi, half tau&1
-        s4[0] = ((sw[0 + wi] >> sh) & 0xffffu) | (((sw[2 + wi] >> sh) & 0xffffu) << 16);
-        s4[1] = ((sw[4 + wi] >> sh) & 0xffffu) | (((sw[6 + wi] >> sh) & 0xffffu) << 16);
-        z4[0] = ((zw[0 + wi] >> sh) & 0xffffu) | (((zw[2 + wi] >> sh) & 0xffffu) << 16);
-        z4[1] = ((zw[4 + wi] >> sh) & 0xffffu) | (((zw[6 + wi] >> sh) & 0xffffu) << 16);
+  for (int j = 0; j < kPPW; ++j) {
+    const int t0 = (c0 + j) * kPage;
+    if (t0 < Tb) {
+      const uint32_t sw[8] = {gs[j][0].x, gs[j][0].y, gs[j][0].z, gs[j][0].w,
+                              gs[j][1].x, gs[j][1].y, gs[j][1].z, gs[j][1].w};
+      const uint32_t zw[8] = {gz[j][0].x, gz[j][0].y, gz[j][0].z, gz[j][0].w,
+                              gz[j][1].x, gz[j][1].y, gz[j][1].z, gz[j][1].w};
+#pragma unroll
+      for (int tau = 0; tau < 4; ++tau) {
+        // scale/zero of tokens 4u + tau (u = 0..3) as fp16 pairs (u=0,1), (u=2,3)
+        uint32_t s4[2] = {0u, 0u}, z4[2] = {0u, 0u};
+        if constexpr (SMODE == kG32) {
+          const int sh = 16 * (tau & 1);
+          const int wi = tau >> 1;  // token 4u+tau sits in word 2u + wi, half tau&1
+          s4[0] = ((sw[0 + wi] >> sh) & 0xffffu) | (((sw[2 + wi] >> sh) & 0xffffu) << 16);
+          s4[1] = ((sw[4 + wi] >> sh) & 0xffffu) | (((sw[6 + wi] >> sh) & 0xffffu) << 16);
+          z4[0] = ((zw[0 + wi] >> sh) & 0xffffu) | (((zw[2 + wi] >> sh) & 0xffffu) << 16);
+          z4[1] = ((zw[4 + wi] >> sh) & 0xffffu) | (((zw[6 + wi] >> sh) & 0xffffu) << 16);
+        }
+        float r4[4];
+        score_tile(x[j][tau], s4, z4, r4);
+#pragma unroll
+        for (int uu = 0; uu < 4; ++uu) R[j][4 * uu + tau] = r4[uu];
       }
-      float r4[4];
-      score_tile(x[tau], s4, z4, r4);
+      if (t0 + kPage > Tb) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) R[4 * u + tau] = r4[u];
+        for (int k = 0; k < 16; ++k)
+          if (t0 + 16 * kc + k >= Tb) R[j][k] = -INFINITY;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) R[j][k] = -INFINITY;
     }
-    if (t0 + kPage > Tb) {
-#pragma unroll
-      for (int k = 0; k < 16; ++k)
-        if (t0 + 16 * kc + k >= Tb) R[k] = -INFINITY;
-    }
-  } else {
-#pragma unroll
-    for (int k = 0; k < 16; ++k) R[k] = -INFINITY;
   }
 
   // ------------------------------------------------ prune
-  float mx = R[0];
+  // block maxima in log2-scaled units: per 16 tokens (lane), then per SBS
+  float mxp[kPPW];
 #pragma unroll
-  for (int k = 1; k < 16; ++k) mx = fmaxf(mx, R[k]);
-  mx = (mx * cs1) * kLog2e;
-  if (SBS >= 32) mx = xor_max(mx, 16);
-  if (SBS >= 64) mx = xor_max(mx, 32);
-  if (SBS > kPage && lane < 4) s_pmax[wv][lane] = mx;
+  for (int j = 0; j < kPPW; ++j) {
+    float m = R[j][0];
+#pragma unroll
+    for (int k = 1; k < 16; ++k) m = fmaxf(m, R[j][k]);
+    m = (m * cs1) * kLog2e;
+    if (SBS >= 32) m = xor_max(m, 16);
+    if (SBS >= 64) m = xor_max(m, 32);
+    mxp[j] = m;
+  }
+  if (SBS >= 128) {
+    const float m = fmaxf(mxp[0], mxp[1]);
+    mxp[0] = m;
+    mxp[1] = m;
+  }
+  if (SBS > 128 && lane < 4) s_wmax[wv][lane] = mxp[0];
   __syncthreads();
   float th;
   if (p.th_in != nullptr) {
@@ -423,340 +464,317 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
   } else {
     th = row_ok ? fmaxf(s_probe[0][ir], s_probe[1][ir]) - p.delta : INFINITY;
   }
-  if (p.th_out != nullptr && blockIdx.x == 0 && threadIdx.x < G) p.th_out[(size_t)b * p.HQ + hkv * G + threadIdx.x] = th;
-  if (SBS > kPage) {
-    const int wpb = SBS / kPage;
+  if (p.th_out != nullptr && cg == 0 && threadIdx.x < G) p.th_out[(size_t)b * p.HQ + hkv * G + threadIdx.x] = th;
+  if (SBS > 128) {
+    const int wpb = SBS / (kPage * kPPW);
     const int w0 = (wv / wpb) * wpb;
     float m2 = -INFINITY;
-    for (int w = w0; w < w0 + wpb; ++w) m2 = fmaxf(m2, s_pmax[w][ir]);
-    mx = m2;
+    for (int w = w0; w < w0 + wpb; ++w) m2 = fmaxf(m2, s_wmax[w][ir]);
+    mxp[0] = m2;
+    mxp[1] = m2;
   }
   // prune iff every row of the group is below its threshold (strict <); rows >= G do not vote
-  const uint64_t bal = __ballot(row_ok && !(mx < th));
-  bool keep16;
-  if (SBS == 16) keep16 = ((bal >> (16 * kc)) & 0xffffull) != 0;
-  else if (SBS == 32) keep16 = ((bal >> (32 * (kc >> 1))) & 0xffffffffull) != 0;
-  else keep16 = bal != 0;
-  {
+  uint64_t bal[kPPW];
+  bool keep16[kPPW];
+#pragma unroll
+  for (int j = 0; j < kPPW; ++j) {
+    bal[j] = __ballot(row_ok && !(mxp[j] < th));
+    if (SBS == 16) keep16[j] = ((bal[j] >> (16 * kc)) & 0xffffull) != 0;
+    else if (SBS == 32) keep16[j] = ((bal[j] >> (32 * (kc >> 1))) & 0xffffffffull) != 0;
+    else keep16[j] = bal[j] != 0;
+    // mask entries of the prune blocks starting in this chunk
+    const int t0 = (c0 + j) * kPage;
     int8_t *mrow_ptr = p.mask + ((size_t)b * p.HKV + hkv) * p.ntbs;
     if (SBS <= kPage) {
       const int per = kPage / SBS;
       const int jb = t0 / SBS;
       if (lane < per && jb + lane < p.ntbs) {
-        const int sh = lane * SBS;  // first lane bit of the sub-block (16 lanes per 16 tokens)
-        const bool kk = SBS == 16   ? ((bal >> sh) & 0xffffull) != 0
-                        : SBS == 32 ? ((bal >> sh) & 0xffffffffull) != 0
-                                    : bal != 0;
+        const int sh = lane * SBS;
+        const bool kk = SBS == 16   ? ((bal[j] >> sh) & 0xffffull) != 0
+                        : SBS == 32 ? ((bal[j] >> sh) & 0xffffffffull) != 0
+                                    : bal[j] != 0;
         mrow_ptr[jb + lane] = (jb + lane < NTBS_b && kk) ? 1 : 0;
       }
     } else if ((t0 % SBS) == 0 && lane == 0) {
       const int jb = t0 / SBS;
-      if (jb < p.ntbs) mrow_ptr[jb] = (jb < NTBS_b && bal != 0) ? 1 : 0;
+      if (jb < p.ntbs) mrow_ptr[jb] = (jb < NTBS_b && bal[j] != 0) ? 1 : 0;
     }
   }
-  const bool any_keep = bal != 0;
+
+  // ------------------------------------------------ phase 3: exact pass of kept chunks
   const size_t row_base = (size_t)b * p.HQ + hkv * G;
-  if (!any_keep || !active) {
-    if (kc == 0 && jg == 0 && row_ok) {
-      p.m_buf[(row_base + ir) * p.nch + chunk] = -INFINITY;
-      p.l_buf[(row_base + ir) * p.nch + chunk] = 0.f;
-    }
-    return;
-  }
-
-  // ------------------------------------------------ phase 3: exact pass of a kept chunk
-  // issue the residual and V loads together
-  uint4 rr[4][2];
-  if constexpr (RES != kResNone) {
 #pragma unroll
-    for (int tau = 0; tau < 4; ++tau) {
-      const int tk = 4 * mrow + tau;
-      size_t off;
-      if constexpr (LAYOUT == kPaged) {
-        off = (((size_t)pg * p.HKV + hkv) * kPage + tk) * kD + 32 * kc;
-      } else {
-        const int t = min(t0 + tk, Tb - 1);
-        off = (((size_t)b * p.T + t) * p.HKV + hkv) * kD + 32 * kc;
+  for (int j = 0; j < kPPW; ++j) {
+    const int chunk = c0 + j;
+    const int t0 = chunk * kPage;
+    if (t0 >= Tb) continue;
+    if (bal[j] == 0) {
+      if (kc == 0 && jg == 0 && row_ok) {
+        p.m_buf[(row_base + ir) * p.nch + chunk] = -INFINITY;
+        p.l_buf[(row_base + ir) * p.nch + chunk] = 0.f;
       }
-      rr[tau][0] = *(const uint4 *)(p.kr + off);
-      rr[tau][1] = *(const uint4 *)(p.kr + off + 16);
+      continue;
     }
-  }
-  uint4 vv[8][2];
-  uint8_t *st = s_vstage + (LAYOUT == kContig ? wv * kPage * kVRow : 0);
-  if constexpr (LAYOUT == kPaged) {
-    const uint16_t *vp = (const uint16_t *)p.v + (((size_t)pg * p.HKV + hkv) * 128) * kPage;
+    float Rj[16];
 #pragma unroll
-    for (int nu = 0; nu < 8; ++nu)
+    for (int k = 0; k < 16; ++k) Rj[k] = R[j][k];
+    // issue the residual and V loads together
+    uint4 rr[4][2];
+    if constexpr (RES != kResNone) {
 #pragma unroll
-      for (int kap = 0; kap < 2; ++kap) vv[nu][kap] = *(const uint4 *)(vp + (size_t)(16 * nu + n) * kPage + 16 * kc + 8 * kap);
-  } else {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int idx = r * 64 + lane;
-      const int tk = idx >> 4, vc = idx & 15;
-      const int t = min(t0 + tk, Tb - 1);
-      vv[r >> 1][r & 1] = *(const uint4 *)((const uint16_t *)p.v + (((size_t)b * p.T + t) * p.HKV + hkv) * 128 + 8 * vc);
+      for (int tau = 0; tau < 4; ++tau) {
+        const int tk = 4 * mrow + tau;
+        size_t off;
+        if constexpr (LAYOUT == kPaged) {
+          off = (((size_t)pg[j] * p.HKV + hkv) * kPage + tk) * kD + 32 * kc;
+        } else {
+          const int t = min(t0 + tk, Tb - 1);
+          off = (((size_t)b * p.T + t) * p.HKV + hkv) * kD + 32 * kc;
+        }
+        rr[tau][0] = *(const uint4 *)(p.kr + off);
+        rr[tau][1] = *(const uint4 *)(p.kr + off + 16);
+      }
     }
-  }
+    uint4 vv[8][2];
+    uint8_t *st = s_vstage + (LAYOUT == kContig ? wv * kPage * kVRow : 0);
+    if constexpr (LAYOUT == kPaged) {
+      const uint16_t *vp = (const uint16_t *)p.v + (((size_t)pg[j] * p.HKV + hkv) * 128) * kPage;
+#pragma unroll
+      for (int nu = 0; nu < 8; ++nu)
+#pragma unroll
+        for (int kap = 0; kap < 2; ++kap)
+          vv[nu][kap] = *(const uint4 *)(vp + (size_t)(16 * nu + n) * kPage + 16 * kc + 8 * kap);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int idx = r * 64 + lane;
+        const int tk = idx >> 4, vc = idx & 15;
+        const int t = min(t0 + tk, Tb - 1);
+        vv[r >> 1][r & 1] = *(const uint4 *)((const uint16_t *)p.v + (((size_t)b * p.T + t) * p.HKV + hkv) * 128 + 8 * vc);
+      }
+    }
 
-  if constexpr (RES != kResNone) {
+    if constexpr (RES != kResNone) {
 #pragma unroll
-    for (int tau = 0; tau < 4; ++tau) {
-      if constexpr (SMODE == kG32) {
-        // refined = coarse + q . r   (exact fp16 residual, every column carries q_i)
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16x8<RES>(rr[tau][0].x, rr[tau][0].y), qr[0], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16x8<RES>(rr[tau][0].z, rr[tau][0].w), qr[1], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16x8<RES>(rr[tau][1].x, rr[tau][1].y), qr[2], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16x8<RES>(rr[tau][1].z, rr[tau][1].w), qr[3], acc, 0, 0, 0);
+      for (int tau = 0; tau < 4; ++tau) {
+        if constexpr (SMODE == kG32) {
+          // refined = coarse + q . r   (exact fp16 residual, every column carries q_i)
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16x8<RES>(rr[tau][0].x, rr[tau][0].y), qr[0], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16x8<RES>(rr[tau][0].z, rr[tau][0].w), qr[1], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16x8<RES>(rr[tau][1].x, rr[tau][1].y), qr[2], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16x8<RES>(rr[tau][1].z, rr[tau][1].w), qr[3], acc, 0, 0, 0);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) R[4 * u + tau] = __builtin_fmaf(acc[u], 1.0f / 16777216.f, R[4 * u + tau]);
-      } else {
-        // reference: k_tilde = fp16(k_hat + fp16(res)) (attn_kernel...q2fp8.py:109-115), full re-score
-        const uint64_t xx = x[tau];
-        const uint32_t wlo = (uint32_t)xx, whi = (uint32_t)(xx >> 32);
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(add_f16x8(dequant8_channel(wlo & 0xffffu, spair + 0, zpair + 0), fp8x8_to_f16x8<RES>(rr[tau][0].x, rr[tau][0].y)), qa[0], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(add_f16x8(dequant8_channel(wlo >> 16, spair + 4, zpair + 4), fp8x8_to_f16x8<RES>(rr[tau][0].z, rr[tau][0].w)), qa[1], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(add_f16x8(dequant8_channel(whi & 0xffffu, spair + 8, zpair + 8), fp8x8_to_f16x8<RES>(rr[tau][1].x, rr[tau][1].y)), qa[2], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(add_f16x8(dequant8_channel(whi >> 16, spair + 12, zpair + 12), fp8x8_to_f16x8<RES>(rr[tau][1].z, rr[tau][1].w)), qa[3], acc, 0, 0, 0);
+          for (int uu = 0; uu < 4; ++uu) Rj[4 * uu + tau] = __builtin_fmaf(acc[uu], 1.0f / 16777216.f, Rj[4 * uu + tau]);
+        } else {
+          // reference: k_tilde = fp16(k_hat + fp16(res)) (attn_kernel...q2fp8.py:109-115), full re-score
+          const uint64_t xx = x[j][tau];
+          const uint32_t wlo = (uint32_t)xx, whi = (uint32_t)(xx >> 32);
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(add_f16x8(dequant8_channel(wlo & 0xffffu, spair + 0, zpair + 0), fp8x8_to_f16x8<RES>(rr[tau][0].x, rr[tau][0].y)), qa[0], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(add_f16x8(dequant8_channel(wlo >> 16, spair + 4, zpair + 4), fp8x8_to_f16x8<RES>(rr[tau][0].z, rr[tau][0].w)), qa[1], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(add_f16x8(dequant8_channel(whi & 0xffffu, spair + 8, zpair + 8), fp8x8_to_f16x8<RES>(rr[tau][1].x, rr[tau][1].y)), qa[2], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(add_f16x8(dequant8_channel(whi >> 16, spair + 12, zpair + 12), fp8x8_to_f16x8<RES>(rr[tau][1].z, rr[tau][1].w)), qa[3], acc, 0, 0, 0);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          float r = acc[u];
-          r += dpp<kRowRor4>(r);
-          r += dpp<kRowRor8>(r);
-          R[4 * u + tau] = r;
+          for (int uu = 0; uu < 4; ++uu) {
+            float r = acc[uu];
+            r += dpp<kRowRor4>(r);
+            r += dpp<kRowRor8>(r);
+            Rj[4 * uu + tau] = r;
+          }
         }
       }
     }
-  }
 
-  // softmax partial over the active tokens (valid and in a kept sub-block)
-  float P[16];
-  float mrow_max = -INFINITY;
+    // softmax partial over the active tokens (valid and in a kept sub-block)
+    float P[16];
+    float mrow_max = -INFINITY;
 #pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const int t = t0 + 16 * kc + k;
-    const bool act = row_ok && t < Tb && keep16;
-    P[k] = act ? (R[k] * cs1) * kLog2e : -INFINITY;
-    mrow_max = fmaxf(mrow_max, P[k]);
-  }
-  mrow_max = xor_max(mrow_max, 16);
-  mrow_max = xor_max(mrow_max, 32);
-  float lsum = 0.f;
+    for (int k = 0; k < 16; ++k) {
+      const int t = t0 + 16 * kc + k;
+      const bool act = row_ok && t < Tb && keep16[j];
+      P[k] = act ? (Rj[k] * cs1) * kLog2e : -INFINITY;
+      mrow_max = fmaxf(mrow_max, P[k]);
+    }
+    mrow_max = xor_max(mrow_max, 16);
+    mrow_max = xor_max(mrow_max, 32);
+    float lsum = 0.f;
 #pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const float e = (P[k] == -INFINITY) ? 0.f : exp2f(P[k] - mrow_max);
-    P[k] = e;
-    lsum += e;
-  }
-  lsum = xor_sum(lsum, 16);
-  lsum = xor_sum(lsum, 32);
+    for (int k = 0; k < 16; ++k) {
+      const float e = (P[k] == -INFINITY) ? 0.f : exp2f(P[k] - mrow_max);
+      P[k] = e;
+      lsum += e;
+    }
+    lsum = xor_sum(lsum, 16);
+    lsum = xor_sum(lsum, 32);
 
-  // P operand (A) of P.V for K-chunk kap: element e <-> token 16*kc + 8*kap + e
-  typename VTr::vec pa2[2];
+    // P operand (A) of P.V for K-chunk kap: element e <-> token 16*kc + 8*kap + e
+    typename VTr::vec pa2[2];
 #pragma unroll
-  for (int kap = 0; kap < 2; ++kap) {
-    u32x4 w;
+    for (int kap = 0; kap < 2; ++kap) {
+      u32x4 w;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) w[e] = VTr::pack2(P[8 * kap + 2 * e], P[8 * kap + 2 * e + 1]);
-    pa2[kap] = __builtin_bit_cast(typename VTr::vec, w);
-  }
+      for (int e = 0; e < 4; ++e) w[e] = VTr::pack2(P[8 * kap + 2 * e], P[8 * kap + 2 * e + 1]);
+      pa2[kap] = __builtin_bit_cast(typename VTr::vec, w);
+    }
 
-  const bool partial = (t0 + kPage) > Tb;
-  f32x4 oacc[8];
+    const bool partial = (t0 + kPage) > Tb;
+    f32x4 oacc[8];
 #pragma unroll
-  for (int nu = 0; nu < 8; ++nu) oacc[nu] = f32x4{0.f, 0.f, 0.f, 0.f};
-  if constexpr (LAYOUT == kPaged) {
+    for (int nu = 0; nu < 8; ++nu) oacc[nu] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (LAYOUT == kPaged) {
 #pragma unroll
-    for (int nu = 0; nu < 8; ++nu) {
+      for (int nu = 0; nu < 8; ++nu) {
 #pragma unroll
-      for (int kap = 0; kap < 2; ++kap) {
-        uint4 v4 = vv[nu][kap];
-        if (partial) {
-          // V of page slots past the sequence end is not data: zero it
+        for (int kap = 0; kap < 2; ++kap) {
+          uint4 v4 = vv[nu][kap];
+          if (partial) {
+            // V of page slots past the sequence end is not data: zero it
+            const int tk = 16 * kc + 8 * kap;
+            uint32_t w4[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int ta = t0 + tk + 2 * e;
+              if (ta >= Tb) w4[e] &= 0xffff0000u;
+              if (ta + 1 >= Tb) w4[e] &= 0x0000ffffu;
+            }
+            v4 = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+          }
+          const u32x4 w = {v4.x, v4.y, v4.z, v4.w};
+          oacc[nu] = VTr::mfma(pa2[kap], __builtin_bit_cast(typename VTr::vec, w), oacc[nu]);
+        }
+      }
+    } else {
+      // contiguous layout: stage the V tile [64 tokens][128] through LDS, then read columns
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int idx = r * 64 + lane;
+        const int tk = idx >> 4, vc = idx & 15;
+        const uint4 v4 = vv[r >> 1][r & 1];
+        uint32_t *d = (uint32_t *)(st + tk * kVRow + 16 * vc);
+        const bool ok = (t0 + tk) < Tb;
+        d[0] = ok ? v4.x : 0u;
+        d[1] = ok ? v4.y : 0u;
+        d[2] = ok ? v4.z : 0u;
+        d[3] = ok ? v4.w : 0u;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int nu = 0; nu < 8; ++nu) {
+#pragma unroll
+        for (int kap = 0; kap < 2; ++kap) {
+          const int vcol = 16 * nu + n;
           const int tk = 16 * kc + 8 * kap;
-          uint32_t w4[4] = {v4.x, v4.y, v4.z, v4.w};
+          u32x4 w;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const int ta = t0 + tk + 2 * e;
-            if (ta >= Tb) w4[e] &= 0xffff0000u;
-            if (ta + 1 >= Tb) w4[e] &= 0x0000ffffu;
+            const uint32_t lo = *(const uint16_t *)(st + (tk + 2 * e) * kVRow + 2 * vcol);
+            const uint32_t hi = *(const uint16_t *)(st + (tk + 2 * e + 1) * kVRow + 2 * vcol);
+            w[e] = lo | (hi << 16);
           }
-          v4 = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+          oacc[nu] = VTr::mfma(pa2[kap], __builtin_bit_cast(typename VTr::vec, w), oacc[nu]);
         }
-        const u32x4 w = {v4.x, v4.y, v4.z, v4.w};
-        oacc[nu] = VTr::mfma(pa2[kap], __builtin_bit_cast(typename VTr::vec, w), oacc[nu]);
+      }
+      // the tile of the next kept chunk reuses the staging buffer
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+
+    // chunk partial: lanes 0..15 hold rows 0..3 of columns 16*nu + n
+    if (lane < 16) {
+#pragma unroll
+      for (int uu = 0; uu < 4; ++uu) {
+        if (uu < G) {
+          float *op = p.o_buf + ((row_base + uu) * p.nch + chunk) * 128 + n;
+#pragma unroll
+          for (int nu = 0; nu < 8; ++nu) op[16 * nu] = oacc[nu][uu];
+        }
       }
     }
-  } else {
-    // contiguous layout: stage the V tile [64 tokens][128] through LDS, then read columns
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int idx = r * 64 + lane;
-      const int tk = idx >> 4, vc = idx & 15;
-      const uint4 v4 = vv[r >> 1][r & 1];
-      uint32_t *d = (uint32_t *)(st + tk * kVRow + 16 * vc);
-      const bool ok = (t0 + tk) < Tb;
-      d[0] = ok ? v4.x : 0u;
-      d[1] = ok ? v4.y : 0u;
-      d[2] = ok ? v4.z : 0u;
-      d[3] = ok ? v4.w : 0u;
+    if (kc == 0 && jg == 0 && row_ok) {
+      p.m_buf[(row_base + ir) * p.nch + chunk] = mrow_max;
+      p.l_buf[(row_base + ir) * p.nch + chunk] = lsum;
+    }
+  }
+
+  // ------------------------------------------------ phase 4: the last workgroup of the unit merges
+  __threadfence();  // publish this wave's partials device-wide
+  __syncthreads();
+  if (threadIdx.x == 0) s_last = atomicAdd(p.counters + u, 1) == ngroups - 1;
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();  // acquire the other workgroups' partials
+  if (threadIdx.x == 0) p.counters[u] = 0;  // ready for the next call
+  if (wv >= G) return;
+  // wave wv merges query row i = wv of the group (attn_kernel...q2fp8.py:142-171)
+  const size_t row = row_base + wv;
+  const int nchb = min((Tb + kPage - 1) / kPage, p.nch);
+  const float *mr = p.m_buf + row * p.nch;
+  const float *lr = p.l_buf + row * p.nch;
+  const float *orow = p.o_buf + row * p.nch * 128;
+  float M = -INFINITY;
+  for (int c = lane; c < nchb; c += 64)
+    if (lr[c] > 0.f) M = fmaxf(M, mr[c]);
+  for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+  float A = 0.f;
+  float2 O = make_float2(0.f, 0.f);
+  for (int seg = 0; seg < nchb; seg += kMergeSeg) {
+    const int segn = min(kMergeSeg, nchb - seg);
+    // ordered compaction of kept chunks (wave ballot) with their weights 2^(m - M)
+    int cnt = 0;
+    for (int cb = 0; cb < segn; cb += 64) {
+      const int c = seg + cb + lane;
+      bool keep = false;
+      float wgt = 0.f;
+      if (cb + lane < segn) {
+        const float l = lr[c];
+        keep = l > 0.f;
+        if (keep) {
+          wgt = exp2f(mr[c] - M);
+          A += l * wgt;
+        }
+      }
+      const uint64_t bl = __ballot(keep);
+      const int pos = cnt + __popcll(bl & ((1ull << lane) - 1ull));
+      if (keep) {
+        s_list[wv][pos] = c;
+        s_w[wv][pos] = wgt;
+      }
+      cnt += __popcll(bl);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // every lane owns columns 2*lane, 2*lane+1; 8 independent loads in flight
+    int k = 0;
+    for (; k + 8 <= cnt; k += 8) {
+      float2 v[8];
 #pragma unroll
-    for (int nu = 0; nu < 8; ++nu) {
+      for (int e = 0; e < 8; ++e) v[e] = *(const float2 *)(orow + (size_t)s_list[wv][k + e] * 128 + 2 * lane);
 #pragma unroll
-      for (int kap = 0; kap < 2; ++kap) {
-        const int vcol = 16 * nu + n;
-        const int tk = 16 * kc + 8 * kap;
-        u32x4 w;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t lo = *(const uint16_t *)(st + (tk + 2 * e) * kVRow + 2 * vcol);
-          const uint32_t hi = *(const uint16_t *)(st + (tk + 2 * e + 1) * kVRow + 2 * vcol);
-          w[e] = lo | (hi << 16);
-        }
-        oacc[nu] = VTr::mfma(pa2[kap], __builtin_bit_cast(typename VTr::vec, w), oacc[nu]);
+      for (int e = 0; e < 8; ++e) {
+        const float wgt = s_w[wv][k + e];
+        O.x = __builtin_fmaf(v[e].x, wgt, O.x);
+        O.y = __builtin_fmaf(v[e].y, wgt, O.y);
       }
     }
+    for (; k < cnt; ++k) {
+      const float2 v = *(const float2 *)(orow + (size_t)s_list[wv][k] * 128 + 2 * lane);
+      O.x = __builtin_fmaf(v.x, s_w[wv][k], O.x);
+      O.y = __builtin_fmaf(v.y, s_w[wv][k], O.y);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
-
-  // chunk partial: lanes 0..15 hold rows 0..3 of columns 16*nu + n
-  if (lane < 16) {
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      if (u < G) {
-        float *op = p.o_buf + ((row_base + u) * p.nch + chunk) * 128 + n;
-#pragma unroll
-        for (int nu = 0; nu < 8; ++nu) op[16 * nu] = oacc[nu][u];
-      }
-    }
-  }
-  if (kc == 0 && jg == 0 && row_ok) {
-    p.m_buf[(row_base + ir) * p.nch + chunk] = mrow_max;
-    p.l_buf[(row_base + ir) * p.nch + chunk] = lsum;
-  }
-}
-
-// --------------------------------------------------------------------------
-// Log-sum-exp merge of the chunk partials (attn_kernel...q2fp8.py:142-171).
-// One workgroup (256 threads) per (sequence, query head).  Kept chunks (l > 0)
-// are compacted with a wave ballot into LDS in chunk order; then 4 slices of
-// 64 threads each accumulate a quarter of them (2 columns per thread, 8
-// independent loads in flight) and the slices are combined through LDS.
-// --------------------------------------------------------------------------
-constexpr int kMergeSeg = 2048;
-
-__global__ __launch_bounds__(256) void q2fp8_merge_kernel(const DecodeParams p) {
-  const int row = blockIdx.x;  // b * HQ + hq
-  const int b = row / p.HQ;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wv = tid >> 6;
-  const int Tb = p.seq_lens ? p.seq_lens[b] : p.T;
-  const int nchb = min((Tb + kPage - 1) / kPage, p.nch);
-  const float *mrow = p.m_buf + (size_t)row * p.nch;
-  const float *lrow = p.l_buf + (size_t)row * p.nch;
-  const float *orow = p.o_buf + (size_t)row * p.nch * 128;
-
-  __shared__ int s_list[kMergeSeg];
-  __shared__ float s_w[kMergeSeg];
-  __shared__ float s_red[4];
-  __shared__ int s_cnt[4];
-  __shared__ float2 s_part[4][64];
-
-  float Mrun = -INFINITY, Arun = 0.f;
-  float2 Orun = make_float2(0.f, 0.f);
-  for (int seg = 0; seg < nchb; seg += kMergeSeg) {
-    const int segn = min(kMergeSeg, nchb - seg);
-    // segment max over kept chunks
-    float mloc = -INFINITY;
-    for (int c = tid; c < segn; c += 256)
-      if (lrow[seg + c] > 0.f) mloc = fmaxf(mloc, mrow[seg + c]);
-    for (int o = 32; o >= 1; o >>= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, o));
-    if (lane == 0) s_red[wv] = mloc;
-    __syncthreads();
-    const float Mseg = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-    // ordered compaction of kept chunks with their weights 2^(m - Mseg)
-    int base = 0;
-    float aloc = 0.f;
-    for (int c0 = 0; c0 < segn; c0 += 256) {
-      const int c = c0 + tid;
-      bool keep = false;
-      float wgt = 0.f;
-      if (c < segn) {
-        const float l = lrow[seg + c];
-        keep = l > 0.f;
-        if (keep) {
-          wgt = exp2f(mrow[seg + c] - Mseg);
-          aloc += l * wgt;
-        }
-      }
-      const uint64_t bal = __ballot(keep);
-      const int before = __popcll(bal & ((1ull << lane) - 1ull));
-      __syncthreads();
-      if (lane == 0) s_cnt[wv] = __popcll(bal);
-      __syncthreads();
-      int off = base + before;
-      for (int w = 0; w < wv; ++w) off += s_cnt[w];
-      if (keep) {
-        s_list[off] = seg + c;
-        s_w[off] = wgt;
-      }
-      base += s_cnt[0] + s_cnt[1] + s_cnt[2] + s_cnt[3];
-    }
-    for (int o = 32; o >= 1; o >>= 1) aloc += __shfl_xor(aloc, o);
-    __syncthreads();
-    if (lane == 0) s_red[wv] = aloc;
-    __syncthreads();
-    const float Aseg = s_red[0] + s_red[1] + s_red[2] + s_red[3];
-    // accumulate: slice wv takes kept entries k = wv, wv+4, ...; thread owns columns 2*lane, 2*lane+1
-    float2 o2 = make_float2(0.f, 0.f);
-    int k = wv;
-    for (; k + 12 < base; k += 16) {
-      float2 v[4];
-      float w[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        v[u] = *(const float2 *)(orow + (size_t)s_list[k + 4 * u] * 128 + 2 * lane);
-        w[u] = s_w[k + 4 * u];
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        o2.x = __builtin_fmaf(v[u].x, w[u], o2.x);
-        o2.y = __builtin_fmaf(v[u].y, w[u], o2.y);
-      }
-    }
-    for (; k < base; k += 4) {
-      const float2 v = *(const float2 *)(orow + (size_t)s_list[k] * 128 + 2 * lane);
-      o2.x = __builtin_fmaf(v.x, s_w[k], o2.x);
-      o2.y = __builtin_fmaf(v.y, s_w[k], o2.y);
-    }
-    s_part[wv][lane] = o2;
-    __syncthreads();
-    if (base > 0) {
-      const float2 a0 = s_part[0][lane], a1 = s_part[1][lane], a2 = s_part[2][lane], a3 = s_part[3][lane];
-      const float ox = (a0.x + a1.x) + (a2.x + a3.x);
-      const float oy = (a0.y + a1.y) + (a2.y + a3.y);
-      const float Mn = fmaxf(Mrun, Mseg);
-      const float ar = (Mrun == -INFINITY) ? 0.f : exp2f(Mrun - Mn);
-      const float br = exp2f(Mseg - Mn);
-      Arun = Arun * ar + Aseg * br;
-      Orun.x = Orun.x * ar + ox * br;
-      Orun.y = Orun.y * ar + oy * br;
-      Mrun = Mn;
-    }
-    __syncthreads();
-  }
-  if (wv == 0) {
-    const float rx = (Arun == 0.f) ? 0.f : Orun.x / Arun;
-    const float ry = (Arun == 0.f) ? 0.f : Orun.y / Arun;
-    store_any(p.out, (size_t)row * 128 + 2 * lane, p.out_dtype, rx);
-    store_any(p.out, (size_t)row * 128 + 2 * lane + 1, p.out_dtype, ry);
-  }
+  for (int o = 32; o >= 1; o >>= 1) A += __shfl_xor(A, o);
+  const float rx = (A == 0.f) ? 0.f : O.x / A;
+  const float ry = (A == 0.f) ? 0.f : O.y / A;
+  store_any(p.out, row * 128 + 2 * lane, p.out_dtype, rx);
+  store_any(p.out, row * 128 + 2 * lane + 1, p.out_dtype, ry);
 }
 
 }  // namespace ffa
@@ -781,8 +799,8 @@ extern "C" int ffa_q2fp8_decode_nchunks(int T, int BS, int SBS) {
   if (T <= 0 || BS <= 0 || SBS <= 0) return 0;
   const long ntb = (T + BS - 1) / BS;
   const long tokens = ntb * BS;  // the sub-blocks cover ceil(T/BS)*BS tokens
-  const long wgs = (tokens + ffa::kWaves * ffa::kPage - 1) / (ffa::kWaves * ffa::kPage);
-  return (int)(wgs * ffa::kWaves);
+  const long wgs = (tokens + ffa::kChunksPerWG * ffa::kPage - 1) / (ffa::kChunksPerWG * ffa::kPage);
+  return (int)(wgs * ffa::kChunksPerWG);
 }
 
 template <int L, int S, int R, int V>
@@ -848,6 +866,7 @@ extern "C" int ffa_q2fp8_decode(const ffa_q2fp8_decode_args *a, void *stream) {
   p.l_buf = a->l_buf;
   p.o_buf = a->o_buf;
   p.mask = a->mask;
+  p.counters = a->counters;
   p.q_dtype = a->q_dtype;
   p.s_dtype = a->scale_dtype;
   p.out_dtype = a->out_dtype;
@@ -865,7 +884,8 @@ extern "C" int ffa_q2fp8_decode(const ffa_q2fp8_decode_args *a, void *stream) {
   p.ntbs = a->ntbs;
 
   hipStream_t st = (hipStream_t)stream;
-  dim3 grid(need / ffa::kWaves, a->B * a->HKV);
+  if (!a->counters) return set_err(FFA_E_INVALID, "counters buffer is null");
+  dim3 grid((need / ffa::kChunksPerWG) * a->B * a->HKV);
   hipError_t e;
   if (a->layout == FFA_LAYOUT_PAGED) {
     if (a->scale_mode == FFA_SCALE_G32)
@@ -875,9 +895,6 @@ extern "C" int ffa_q2fp8_decode(const ffa_q2fp8_decode_args *a, void *stream) {
   } else {
     e = dispatch_rv<ffa::kContig, ffa::kChannel>(p, a->res_dtype, a->v_dtype, grid, st);
   }
-  if (e != hipSuccess) return set_err(FFA_E_LAUNCH, hipGetErrorString(e));
-  hipLaunchKernelGGL(ffa::q2fp8_merge_kernel, dim3(a->B * a->HQ), dim3(256), 0, st, p);
-  e = hipGetLastError();
   if (e != hipSuccess) return set_err(FFA_E_LAUNCH, hipGetErrorString(e));
   return FFA_OK;
 }
