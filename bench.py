@@ -204,7 +204,7 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "q2fp8_decode_kernel (score, prune, exact pass and merge in one launch)",
+            "kernel": "decode step = q2fp8_decode_kernel + q2fp8_merge_kernel (back to back in the graph)",
         },
         "cpu_baseline": cpu,
         "setup_s": round(setup_s, 1),

@@ -22,10 +22,10 @@
 //     r the fp8 residual (another f16 MFMA), exp2 softmax, P.V with a bf16/f16
 //     MFMA reading V^T pages (16-byte loads) or V staged through LDS for the
 //     contiguous reference layout.
-//   * partials (m, l, o) per 64-token chunk; the last workgroup of each
-//     (sequence, KV head) -- found with an atomic completion counter -- merges
-//     them (kept chunks compacted in order with a wave ballot), so one launch
-//     does the whole step.
+//   * partials (m, l, o) per 64-token chunk, merged by a second kernel that
+//     compacts the kept chunks in order with a wave ballot (back to back in a
+//     HIP graph; a device-wide flag in the first kernel would need an L2
+//     write-back per wave, which costs more than the second launch).
 //   * each wave owns two consecutive chunks; the grid is 1-D with the
 //     (sequence, KV head) unit fastest, so with B*HKV a multiple of 8 a unit's
 //     workgroups share one XCD and its L2.
@@ -58,7 +58,6 @@ struct DecodeParams {
   void *out;
   float *m_buf, *l_buf, *o_buf;
   int8_t *mask;
-  int *counters;
   int q_dtype, s_dtype, out_dtype;
   int bt_stride;
   int B, T, HQ, HKV, G;
@@ -203,7 +202,6 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
   const int U = p.B * p.HKV;
   const int u = blockIdx.x % U;
   const int cg = blockIdx.x / U;
-  const int ngroups = gridDim.x / U;
   const int b = u / p.HKV;
   const int hkv = u - b * p.HKV;
   const int G = p.G;
@@ -224,9 +222,6 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
 
   __shared__ float s_probe[2][4];
   __shared__ float s_wmax[kWaves][4];
-  __shared__ int s_last;
-  __shared__ int s_list[4][kMergeSeg];
-  __shared__ float s_w[4][kMergeSeg];
   __shared__ uint8_t s_vstage[LAYOUT == kContig ? kWaves * kPage * kVRow : 4];
 
   // ------------------------------------------------ phase 0: page ids (scalar loads)
@@ -700,81 +695,118 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
     }
   }
 
-  // ------------------------------------------------ phase 4: the last workgroup of the unit merges
-  __threadfence();  // publish this wave's partials device-wide
-  __syncthreads();
-  if (threadIdx.x == 0) s_last = atomicAdd(p.counters + u, 1) == ngroups - 1;
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();  // acquire the other workgroups' partials
-  if (threadIdx.x == 0) p.counters[u] = 0;  // ready for the next call
-  if (wv >= G) return;
-  // wave wv merges query row i = wv of the group (attn_kernel...q2fp8.py:142-171)
-  const size_t row = row_base + wv;
+}
+
+
+// --------------------------------------------------------------------------
+// Log-sum-exp merge of the chunk partials (attn_kernel...q2fp8.py:142-171).
+// One workgroup (4 waves) per (sequence, query head).  Wave 0 loads m, l of a
+// segment of chunks in one batch, takes the max over kept chunks (l > 0) and
+// compacts them in chunk order with a ballot; the 4 waves then each
+// accumulate every 4th kept chunk (2 columns per lane, all loads of a wave in
+// flight together) and the slices are summed in a fixed order.
+// --------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void q2fp8_merge_kernel(const DecodeParams p) {
+  const int row = blockIdx.x;  // b * HQ + hq
+  const int b = row / p.HQ;
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int Tb = p.seq_lens ? p.seq_lens[b] : p.T;
   const int nchb = min((Tb + kPage - 1) / kPage, p.nch);
-  const float *mr = p.m_buf + row * p.nch;
-  const float *lr = p.l_buf + row * p.nch;
-  const float *orow = p.o_buf + row * p.nch * 128;
-  float M = -INFINITY;
-  for (int c = lane; c < nchb; c += 64)
-    if (lr[c] > 0.f) M = fmaxf(M, mr[c]);
-  for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+  const float *mr = p.m_buf + (size_t)row * p.nch;
+  const float *lr = p.l_buf + (size_t)row * p.nch;
+  const float *orow = p.o_buf + (size_t)row * p.nch * 128;
+
+  __shared__ int s_list[kMergeSeg];
+  __shared__ float s_w[kMergeSeg];
+  __shared__ int s_cnt;
+  __shared__ float s_m, s_a;
+  __shared__ float2 s_part[4][64];
+
+  // global max over kept chunks (wave 0), all m/l loads of a segment in flight together
+  if (wv == 0) {
+    float M = -INFINITY;
+    for (int seg = 0; seg < nchb; seg += kMergeSeg) {
+      float mv[kMergeSeg / 64], lv[kMergeSeg / 64];
+#pragma unroll
+      for (int k = 0; k < kMergeSeg / 64; ++k) {
+        const int c = seg + 64 * k + lane;
+        mv[k] = c < nchb ? mr[c] : -INFINITY;
+        lv[k] = c < nchb ? lr[c] : 0.f;
+      }
+#pragma unroll
+      for (int k = 0; k < kMergeSeg / 64; ++k)
+        if (lv[k] > 0.f) M = fmaxf(M, mv[k]);
+    }
+    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+    if (lane == 0) s_m = M;
+  }
+  __syncthreads();
+  const float M = s_m;
   float A = 0.f;
   float2 O = make_float2(0.f, 0.f);
   for (int seg = 0; seg < nchb; seg += kMergeSeg) {
-    const int segn = min(kMergeSeg, nchb - seg);
-    // ordered compaction of kept chunks (wave ballot) with their weights 2^(m - M)
-    int cnt = 0;
-    for (int cb = 0; cb < segn; cb += 64) {
-      const int c = seg + cb + lane;
-      bool keep = false;
-      float wgt = 0.f;
-      if (cb + lane < segn) {
-        const float l = lr[c];
-        keep = l > 0.f;
+    if (wv == 0) {
+      float mv[kMergeSeg / 64], lv[kMergeSeg / 64];
+#pragma unroll
+      for (int k = 0; k < kMergeSeg / 64; ++k) {
+        const int c = seg + 64 * k + lane;
+        mv[k] = c < nchb ? mr[c] : -INFINITY;
+        lv[k] = c < nchb ? lr[c] : 0.f;
+      }
+      int cnt = 0;
+      float a = 0.f;
+#pragma unroll
+      for (int k = 0; k < kMergeSeg / 64; ++k) {
+        const bool keep = lv[k] > 0.f;
+        const float wgt = keep ? exp2f(mv[k] - M) : 0.f;
+        a += lv[k] * wgt;
+        const uint64_t bl = __ballot(keep);
+        const int pos = cnt + __popcll(bl & ((1ull << lane) - 1ull));
         if (keep) {
-          wgt = exp2f(mr[c] - M);
-          A += l * wgt;
+          s_list[pos] = seg + 64 * k + lane;
+          s_w[pos] = wgt;
         }
+        cnt += __popcll(bl);
       }
-      const uint64_t bl = __ballot(keep);
-      const int pos = cnt + __popcll(bl & ((1ull << lane) - 1ull));
-      if (keep) {
-        s_list[wv][pos] = c;
-        s_w[wv][pos] = wgt;
+      for (int o = 32; o >= 1; o >>= 1) a += __shfl_xor(a, o);
+      if (lane == 0) {
+        s_cnt = cnt;
+        s_a = a;
       }
-      cnt += __popcll(bl);
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // every lane owns columns 2*lane, 2*lane+1; 8 independent loads in flight
-    int k = 0;
-    for (; k + 8 <= cnt; k += 8) {
-      float2 v[8];
+    __syncthreads();
+    const int cnt = s_cnt;
+    A += s_a;
+    // slice wv: kept entries wv, wv+4, ...; 16 loads in flight per batch
+    for (int k0 = wv; k0 < cnt; k0 += 64) {
+      float2 v[16];
+      float w[16];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = *(const float2 *)(orow + (size_t)s_list[wv][k + e] * 128 + 2 * lane);
+      for (int e = 0; e < 16; ++e) {
+        const int k = k0 + 4 * e;
+        w[e] = k < cnt ? s_w[k] : 0.f;
+        v[e] = k < cnt ? *(const float2 *)(orow + (size_t)s_list[k] * 128 + 2 * lane) : make_float2(0.f, 0.f);
+      }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float wgt = s_w[wv][k + e];
-        O.x = __builtin_fmaf(v[e].x, wgt, O.x);
-        O.y = __builtin_fmaf(v[e].y, wgt, O.y);
+      for (int e = 0; e < 16; ++e) {
+        O.x = __builtin_fmaf(v[e].x, w[e], O.x);
+        O.y = __builtin_fmaf(v[e].y, w[e], O.y);
       }
     }
-    for (; k < cnt; ++k) {
-      const float2 v = *(const float2 *)(orow + (size_t)s_list[wv][k] * 128 + 2 * lane);
-      O.x = __builtin_fmaf(v.x, s_w[wv][k], O.x);
-      O.y = __builtin_fmaf(v.y, s_w[wv][k], O.y);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    __syncthreads();
   }
-  for (int o = 32; o >= 1; o >>= 1) A += __shfl_xor(A, o);
-  const float rx = (A == 0.f) ? 0.f : O.x / A;
-  const float ry = (A == 0.f) ? 0.f : O.y / A;
-  store_any(p.out, row * 128 + 2 * lane, p.out_dtype, rx);
-  store_any(p.out, row * 128 + 2 * lane + 1, p.out_dtype, ry);
+  s_part[wv][lane] = O;
+  __syncthreads();
+  if (wv == 0) {
+    const float2 a0 = s_part[0][lane], a1 = s_part[1][lane], a2 = s_part[2][lane], a3 = s_part[3][lane];
+    const float ox = (a0.x + a1.x) + (a2.x + a3.x);
+    const float oy = (a0.y + a1.y) + (a2.y + a3.y);
+    const float rx = (A == 0.f) ? 0.f : ox / A;
+    const float ry = (A == 0.f) ? 0.f : oy / A;
+    store_any(p.out, (size_t)row * 128 + 2 * lane, p.out_dtype, rx);
+    store_any(p.out, (size_t)row * 128 + 2 * lane + 1, p.out_dtype, ry);
+  }
 }
 
 }  // namespace ffa
@@ -866,7 +898,6 @@ extern "C" int ffa_q2fp8_decode(const ffa_q2fp8_decode_args *a, void *stream) {
   p.l_buf = a->l_buf;
   p.o_buf = a->o_buf;
   p.mask = a->mask;
-  p.counters = a->counters;
   p.q_dtype = a->q_dtype;
   p.s_dtype = a->scale_dtype;
   p.out_dtype = a->out_dtype;
@@ -884,7 +915,6 @@ extern "C" int ffa_q2fp8_decode(const ffa_q2fp8_decode_args *a, void *stream) {
   p.ntbs = a->ntbs;
 
   hipStream_t st = (hipStream_t)stream;
-  if (!a->counters) return set_err(FFA_E_INVALID, "counters buffer is null");
   dim3 grid((need / ffa::kChunksPerWG) * a->B * a->HKV);
   hipError_t e;
   if (a->layout == FFA_LAYOUT_PAGED) {
@@ -895,6 +925,9 @@ extern "C" int ffa_q2fp8_decode(const ffa_q2fp8_decode_args *a, void *stream) {
   } else {
     e = dispatch_rv<ffa::kContig, ffa::kChannel>(p, a->res_dtype, a->v_dtype, grid, st);
   }
+  if (e != hipSuccess) return set_err(FFA_E_LAUNCH, hipGetErrorString(e));
+  hipLaunchKernelGGL(ffa::q2fp8_merge_kernel, dim3(a->B * a->HQ), dim3(256), 0, st, p);
+  e = hipGetLastError();
   if (e != hipSuccess) return set_err(FFA_E_LAUNCH, hipGetErrorString(e));
   return FFA_OK;
 }

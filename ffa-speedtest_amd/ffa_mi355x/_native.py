@@ -81,7 +81,6 @@ class DecodeArgs(ctypes.Structure):
         ("nchunks", ctypes.c_int),
         ("mask", ctypes.c_void_p),
         ("ntbs", ctypes.c_int),
-        ("counters", ctypes.c_void_p),
     ]
 
 

@@ -35,8 +35,7 @@ class DecodeWorkspace:
     Mirrors Q2FP8DecodeWorkspace (ffa-q2fp8-h100/attn_kernel/attn_kernel_v1210_fused_bsz_q2fp8.py:232-257):
     o, m_buf, l_buf, o_buf, mask_buf, threshold_buf.  Partials are kept per
     64-token chunk (m_buf/l_buf [B, HQ, nchunks], o_buf [B, HQ, nchunks, 128]),
-    mask_buf holds one byte per prune block [B, HKV, NTBS]; counters [B*HKV]
-    serve the in-kernel merge (zeroed once here, left zero by each call).
+    mask_buf holds one byte per prune block [B, HKV, NTBS].
     """
 
     def __init__(self, B, HQ, HKV, T, BS, SBS, device, dtype):
@@ -53,8 +52,6 @@ class DecodeWorkspace:
         self.o_buf = torch.empty((B, HQ, self.nchunks, HEAD_DIM), device=device, dtype=torch.float32)
         self.mask_buf = torch.empty((B, HKV, self.NTBS), device=device, dtype=torch.int8)
         self.threshold_buf = torch.empty((B, HQ), device=device, dtype=torch.float32)
-        # completion counters of the fused merge: zero here, left zero by every call
-        self.counters = torch.zeros((B * HKV,), device=device, dtype=torch.int32)
 
     def matches(self, B, HQ, HKV, T, BS, SBS, device, dtype) -> bool:
         return (
@@ -141,7 +138,6 @@ def run_decode(
     a.nchunks = workspace.nchunks
     a.mask = workspace.mask_buf.data_ptr()
     a.ntbs = workspace.NTBS
-    a.counters = workspace.counters.data_ptr()
     rc = N.lib().ffa_q2fp8_decode(ctypes.byref(a), ctypes.c_void_p(N.stream_of(q.device)))
     N.check(rc, "ffa_q2fp8_decode")
     return workspace

@@ -78,12 +78,9 @@ enum {
  *
  * Scratch (caller-owned, see ffa_q2fp8_decode_nchunks):
  *   m_buf, l_buf [B, HQ, nchunks] f32; o_buf [B, HQ, nchunks, 128] f32;
- *   mask [B, HKV, ntbs] i8 (1 = block kept, written for every block);
- *   counters [B * HKV] i32, zero before the first call (the kernel leaves them
- *   zero again, so the same buffer serves every later call and graph replay).
- * One launch: score, prune, exact pass and the log-sum-exp merge (done by the
- * last workgroup of each (sequence, KV head)).  Calls that share scratch must
- * be ordered on one stream.
+ *   mask [B, HKV, ntbs] i8 (1 = block kept, written for every block).
+ * Two launches on `stream`: score + prune + exact pass, then the log-sum-exp
+ * merge.  Calls that share scratch must be ordered on one stream.
  */
 typedef struct ffa_q2fp8_decode_args {
   const void *q; /* [B, HQ, 128], dtype q_dtype */
@@ -113,7 +110,6 @@ typedef struct ffa_q2fp8_decode_args {
   int nchunks;
   int8_t *mask;
   int ntbs;
-  int32_t *counters;
 } ffa_q2fp8_decode_args;
 
 /* Number of 64-token chunks the scratch buffers must hold for max length T. */
