@@ -117,7 +117,8 @@ __device__ __forceinline__ void g32_quantize_store(const float *kv, int page, in
   uint32_t *cp = (uint32_t *)(kq_pages + ((((size_t)page * HKV + hkv) * 4 + g) * 64 + slot) * 8);
   cp[0] = words[0];
   cp[1] = words[1];
-  const size_t so = (((size_t)page * HKV + hkv) * 4 + g) * 64 + slot;
+  const int ss = 16 * (slot >> 4) + 4 * (slot & 3) + ((slot >> 2) & 3);  // tile-major scale slot
+  const size_t so = (((size_t)page * HKV + hkv) * 4 + g) * 64 + ss;
   s_pages[so] = (uint16_t)f32_to_f16_bits(sc);
   z_pages[so] = (uint16_t)f32_to_f16_bits(zr);
 }

@@ -22,10 +22,12 @@
 //     r the fp8 residual (another f16 MFMA), exp2 softmax, P.V with a bf16/f16
 //     MFMA reading V^T pages (16-byte loads) or V staged through LDS for the
 //     contiguous reference layout.
-//   * partials (m, l, o) per 64-token chunk, merged by a second kernel that
-//     compacts the kept chunks in order with a wave ballot (back to back in a
-//     HIP graph; a device-wide flag in the first kernel would need an L2
-//     write-back per wave, which costs more than the second launch).
+//   * the 8 chunk partials (m, l, o) of a workgroup are merged in LDS into one
+//     partial per 512 tokens; a second kernel merges those with one batch of
+//     loads (back to back in a HIP graph; a device-wide completion flag in the
+//     first kernel would need an L2 write-back per wave, which costs more).
+//   * the q operands of the MFMAs are built once per workgroup (one per wave)
+//     and shared through LDS.
 //   * each wave owns two consecutive chunks; the grid is 1-D with the
 //     (sequence, KV head) unit fastest, so with B*HKV a multiple of 8 a unit's
 //     workgroups share one XCD and its L2.
@@ -41,7 +43,6 @@ constexpr int kPage = 64;
 constexpr int kWaves = 4;
 constexpr int kPPW = 2;                      // 64-token chunks (pages) per wave
 constexpr int kChunksPerWG = kWaves * kPPW;  // 512 tokens per workgroup
-constexpr int kMergeSeg = 512;               // kept-chunk list segment of the merge
 constexpr int kVRow = 260;  // LDS row pitch (bytes) of the staged V tile: 256 + 4 keeps banks apart
 
 struct DecodeParams {
@@ -64,7 +65,7 @@ struct DecodeParams {
   float scale;
   int BS, SBS;
   float delta;
-  int nch, ntbs;
+  int nparts, ntbs;
 };
 
 enum { kContig = 0, kPaged = 1 };
@@ -191,24 +192,25 @@ __device__ __forceinline__ f16x8 dequant8_channel(uint32_t h, const uint32_t *sp
 
 __device__ __forceinline__ f16x8 add_f16x8(f16x8 a, f16x8 b) { return a + b; }
 
+// Position of token t (0..63) inside a page row of g32 scales / zeros.  Tile-major:
+// the scores of MFMA tile tau hold tokens 16k + 4u + tau (u = 0..3), whose scales
+// then sit at 16k + 4tau + u, one 8-byte load per lane and tile.
+__host__ __device__ constexpr int scale_pos(int t) { return 16 * (t >> 4) + 4 * (t & 3) + ((t >> 2) & 3); }
+
 template <int LAYOUT, int SMODE, int RES, int VT>
 __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p) {
   typedef VTraits<VT> VTr;
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // 1-D grid: unit u = (b, hkv) is the fastest index, so with B*HKV a multiple of 8 every
-  // workgroup of one unit lands on the same XCD (dispatch is round-robin over the 8 XCDs)
-  // and the unit's partials stay in that XCD's L2 for the merge.
+  // 1-D grid, unit u = (b, hkv) fastest: with B*HKV a multiple of 8 the workgroups of a
+  // unit land on one XCD (dispatch is round-robin over the 8 XCDs) and share its L2.
   const int U = p.B * p.HKV;
   const int u = blockIdx.x % U;
-  const int cg = blockIdx.x / U;
+  const int cg = blockIdx.x / U;  // workgroup index along the sequence = partial slot
   const int b = u / p.HKV;
   const int hkv = u - b * p.HKV;
   const int G = p.G;
   const int c0 = cg * kChunksPerWG + wv * kPPW;  // first chunk of this wave
-  const int Tb = p.seq_lens ? p.seq_lens[b] : p.T;
-  const int NTB = (Tb + p.BS - 1) / p.BS;
-  const int NTBS_b = NTB * (p.BS / p.SBS);
   const int SBS = p.SBS;
 
   const int mrow = lane & 15;  // MFMA row (A) / column (B) index
@@ -217,14 +219,33 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
   const int jg = n >> 2;
   const int ir = n & 3;
   const bool row_ok = ir < G;
+  const int hq = hkv * G + (row_ok ? ir : 0);
+
+  __shared__ uint4 s_qa[4][64];  // B operands of the 4 score MFMAs, per lane
+  __shared__ uint4 s_qr[4][64];  // B operands of the 4 residual MFMAs (g32)
+  __shared__ uint4 s_sp[4][64];  // channel mode: fp16 (scale, scale) pairs of 8 channels
+  __shared__ uint4 s_zp2[4][64]; // channel mode: fp16 (zero, zero) pairs
+  __shared__ float s_zs[4][64];  // g32: partial sums of q16 over 8 channels
+  __shared__ float s_probe[2][4];
+  __shared__ float s_wmax[kWaves][4];
+  __shared__ float s_pm[kChunksPerWG][4], s_pl[kChunksPerWG][4];
+  __shared__ float s_po[kChunksPerWG][4][128];
+  __shared__ uint8_t s_vstage[LAYOUT == kContig ? kWaves * kPage * kVRow : 4];
+
+  // ------------------------------------------------ phase 1: loads
+  // q of this lane's (row, group): every wave builds one of the four MFMA operands
+  Raw32 qraw, sraw, zraw;
+  raw32_load(qraw, p.q, ((size_t)b * p.HQ + hq) * kD + 32 * kc, p.q_dtype);
+  if constexpr (SMODE == kChannel) {
+    raw32_load(sraw, p.ks, ((size_t)b * p.HKV + hkv) * kD + 32 * kc, p.s_dtype);
+    raw32_load(zraw, p.kz, ((size_t)b * p.HKV + hkv) * kD + 32 * kc, p.s_dtype);
+  }
+  const int Tb = p.seq_lens ? p.seq_lens[b] : p.T;
+  const int NTB = (Tb + p.BS - 1) / p.BS;
+  const int NTBS_b = NTB * (p.BS / p.SBS);
   const bool do_probe = (p.th_in == nullptr) && wv < 2;
   const int pa = wv == 0 ? 0 : (NTB - 1) * 16;  // probe window (attn_kernel...q2fp8.py:58-73)
 
-  __shared__ float s_probe[2][4];
-  __shared__ float s_wmax[kWaves][4];
-  __shared__ uint8_t s_vstage[LAYOUT == kContig ? kWaves * kPage * kVRow : 4];
-
-  // ------------------------------------------------ phase 0: page ids (scalar loads)
   int pg[kPPW] = {0, 0};
   int ppg = 0;
   if constexpr (LAYOUT == kPaged) {
@@ -234,18 +255,9 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
       if ((c0 + j) * kPage < Tb) pg[j] = btr[c0 + j];
     if (do_probe) ppg = btr[pa >> 6];
   }
-
-  // ------------------------------------------------ phase 1: score-phase loads
-  const int hq = hkv * G + (row_ok ? ir : 0);
-  Raw32 qraw, sraw, zraw;
-  raw32_load(qraw, p.q, ((size_t)b * p.HQ + hq) * kD + 32 * kc, p.q_dtype);
-  if constexpr (SMODE == kChannel) {
-    raw32_load(sraw, p.ks, ((size_t)b * p.HKV + hkv) * kD + 32 * kc, p.s_dtype);
-    raw32_load(zraw, p.kz, ((size_t)b * p.HKV + hkv) * kD + 32 * kc, p.s_dtype);
-  }
-  // token of MFMA row m in tile tau is 4m + tau (within a chunk)
+  // own chunks: the token of MFMA row m in tile tau is 4m + tau
   uint64_t x[kPPW][4];
-  uint4 gs[kPPW][2], gz[kPPW][2];  // g32 scale/zero of tokens 16kc..16kc+15, group jg
+  uint4 gs[kPPW][2], gz[kPPW][2];  // g32 scale/zero of group jg, tokens 16kc + 4u + tau at [tau/2].(2 words)
 #pragma unroll
   for (int j = 0; j < kPPW; ++j) {
     const int t0 = (c0 + j) * kPage;
@@ -275,10 +287,12 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
       }
     }
   }
+  // probe tile: MFMA row m <-> token pa + 4(m & 3) + (m >> 2), so that the output rows
+  // 4kc + u hold tokens pa + 4u + kc, whose g32 scales are contiguous (scale_pos)
   uint64_t px = 0;
   uint2 pgs = make_uint2(0, 0), pgz = make_uint2(0, 0);
   if (do_probe) {
-    const int tok = pa + mrow;
+    const int tok = pa + 4 * (mrow & 3) + (mrow >> 2);
     if constexpr (LAYOUT == kPaged) {
       px = *(const uint64_t *)(p.kq + ((((size_t)ppg * p.HKV + hkv) * 4 + kc) * kPage + (tok & (kPage - 1))) * 8);
       if constexpr (SMODE == kG32) {
@@ -292,63 +306,93 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
     }
   }
 
-  // ------------------------------------------------ phase 2: operands and scores
-  float qv[32];
-  raw32_to_f32(qraw, p.q_dtype, qv);
-#pragma unroll
-  for (int e = 0; e < 32; ++e) qv[e] = row_ok ? (float)(_Float16)qv[e] : 0.f;  // q16 (attn_kernel...q2fp8.py:47)
-
-  // B operands.  g32 (folded scales): MFMA m' = 2h + s, element 2q+half <-> channel
-  // 32kc + 16h + 4s + q + 8half, divided by 4^q.  channel (explicit dequant): element e of
-  // MFMA m' <-> channel 32kc + 8m' + e.  Both only on the column's own group (kc == j).
-  f16x8 qa[4];
-  float zq = 0.f;
-  uint32_t spair[16], zpair[16];
-  if constexpr (SMODE == kG32) {
-#pragma unroll
-    for (int mp = 0; mp < 4; ++mp) {
-      const int h = mp >> 1, s = mp & 1;
+  // ------------------------------------------------ phase 2a: B operands, built once per workgroup
+  // wave w builds, for every lane, the operand of MFMA m' = w:
+  //   g32 score:    element 2q+half <-> channel 32kc + 16h + 4s + q + 8half (m' = 2h+s), times 4^-q
+  //   channel score: element e <-> channel 32kc + 8m' + e
+  //   residual:     element e <-> channel 32kc + 8m' + e (every column)
+  // Score operands are nonzero only on the column's own group (kc == j).
+  {
+    float qv[32];
+    raw32_to_f32(qraw, p.q_dtype, qv);
+    const int w = wv;
+    u32x4 a4, r4;
+    if constexpr (SMODE == kG32) {
+      const int h = w >> 1, s = w & 1;
 #pragma unroll
       for (int qq = 0; qq < 4; ++qq) {
+        const float inv = qq == 0 ? 1.f : (qq == 1 ? 0.25f : (qq == 2 ? 0.0625f : 0.015625f));
+        float e2[2];
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
-          const int ch = 16 * h + 4 * s + qq + 8 * half;
-          const float inv = qq == 0 ? 1.f : (qq == 1 ? 0.25f : (qq == 2 ? 0.0625f : 0.015625f));
-          qa[mp][2 * qq + half] = (_Float16)((kc == jg) ? qv[ch] * inv : 0.f);
+          const float q16 = (float)(_Float16)qv[16 * h + 4 * s + qq + 8 * half];
+          e2[half] = (row_ok && kc == jg) ? q16 * inv : 0.f;
         }
+        a4[qq] = f32_to_f16_bits(e2[0]) | (f32_to_f16_bits(e2[1]) << 16);
       }
+      float zs = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) zs += (float)(_Float16)qv[8 * w + e];
+      s_zs[w][lane] = row_ok ? zs : 0.f;
+    } else {
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const float e0 = (row_ok && kc == jg) ? (float)(_Float16)qv[8 * w + 2 * qq] : 0.f;
+        const float e1 = (row_ok && kc == jg) ? (float)(_Float16)qv[8 * w + 2 * qq + 1] : 0.f;
+        a4[qq] = f32_to_f16_bits(e0) | (f32_to_f16_bits(e1) << 16);
+      }
+      float sv[32], zv[32];
+      raw32_to_f32(sraw, p.s_dtype, sv);
+      raw32_to_f32(zraw, p.s_dtype, zv);
+      uint4 sp, zp;
+      sp.x = f32_to_f16_bits(sv[8 * w + 0]) | (f32_to_f16_bits(sv[8 * w + 1]) << 16);
+      sp.y = f32_to_f16_bits(sv[8 * w + 2]) | (f32_to_f16_bits(sv[8 * w + 3]) << 16);
+      sp.z = f32_to_f16_bits(sv[8 * w + 4]) | (f32_to_f16_bits(sv[8 * w + 5]) << 16);
+      sp.w = f32_to_f16_bits(sv[8 * w + 6]) | (f32_to_f16_bits(sv[8 * w + 7]) << 16);
+      zp.x = f32_to_f16_bits(zv[8 * w + 0]) | (f32_to_f16_bits(zv[8 * w + 1]) << 16);
+      zp.y = f32_to_f16_bits(zv[8 * w + 2]) | (f32_to_f16_bits(zv[8 * w + 3]) << 16);
+      zp.z = f32_to_f16_bits(zv[8 * w + 4]) | (f32_to_f16_bits(zv[8 * w + 5]) << 16);
+      zp.w = f32_to_f16_bits(zv[8 * w + 6]) | (f32_to_f16_bits(zv[8 * w + 7]) << 16);
+      s_sp[w][lane] = sp;
+      s_zp2[w][lane] = zp;
     }
-    float qs = 0.f;
 #pragma unroll
-    for (int e = 0; e < 32; ++e) qs += qv[e];
-    zq = __shfl(qs, (jg << 4) | n) * (1.0f / 16777216.f);  // sum_{d in group j} q16, in 2^-24 units
-  } else {
+    for (int qq = 0; qq < 4; ++qq) {
+      const float e0 = row_ok ? (float)(_Float16)qv[8 * w + 2 * qq] : 0.f;
+      const float e1 = row_ok ? (float)(_Float16)qv[8 * w + 2 * qq + 1] : 0.f;
+      r4[qq] = f32_to_f16_bits(e0) | (f32_to_f16_bits(e1) << 16);
+    }
+    s_qa[w][lane] = make_uint4(a4[0], a4[1], a4[2], a4[3]);
+    s_qr[w][lane] = make_uint4(r4[0], r4[1], r4[2], r4[3]);
+  }
+  __syncthreads();
+  f16x8 qa[4], qr[4];
+  uint32_t spair[16], zpair[16];
+  float zq = 0.f;
 #pragma unroll
-    for (int mp = 0; mp < 4; ++mp)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qa[mp][e] = (_Float16)((kc == jg) ? qv[8 * mp + e] : 0.f);
-    float sv[32], zv[32];
-    raw32_to_f32(sraw, p.s_dtype, sv);
-    raw32_to_f32(zraw, p.s_dtype, zv);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      spair[i] = f32_to_f16_bits(sv[2 * i]) | (f32_to_f16_bits(sv[2 * i + 1]) << 16);
-      zpair[i] = f32_to_f16_bits(zv[2 * i]) | (f32_to_f16_bits(zv[2 * i + 1]) << 16);
+  for (int mp = 0; mp < 4; ++mp) {
+    const uint4 a = s_qa[mp][lane];
+    qa[mp] = __builtin_bit_cast(f16x8, u32x4{a.x, a.y, a.z, a.w});
+    if constexpr (SMODE == kG32 && RES != kResNone) {
+      const uint4 r = s_qr[mp][lane];
+      qr[mp] = __builtin_bit_cast(f16x8, u32x4{r.x, r.y, r.z, r.w});
+    }
+    if constexpr (SMODE == kChannel) {
+      const uint4 sp = s_sp[mp][lane], zp = s_zp2[mp][lane];
+      spair[4 * mp + 0] = sp.x; spair[4 * mp + 1] = sp.y; spair[4 * mp + 2] = sp.z; spair[4 * mp + 3] = sp.w;
+      zpair[4 * mp + 0] = zp.x; zpair[4 * mp + 1] = zp.y; zpair[4 * mp + 2] = zp.z; zpair[4 * mp + 3] = zp.w;
     }
   }
-  // residual operand (g32): element e of MFMA m' <-> channel 32kc + 8m' + e, every column.
-  f16x8 qr[4];
-  if constexpr (SMODE == kG32 && RES != kResNone) {
-#pragma unroll
-    for (int mp = 0; mp < 4; ++mp)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qr[mp][e] = (_Float16)qv[8 * mp + e];
+  if constexpr (SMODE == kG32) {
+    const int src = (jg << 4) | n;  // lane of the column's own group, same query row
+    zq = ((s_zs[0][src] + s_zs[1][src]) + (s_zs[2][src] + s_zs[3][src])) * (1.0f / 16777216.f);
   }
 
   // raw scores of one 16-token tile for the lane's column, summed over groups:
   //   g32: R' = sum_j s_j * D_j + z_j * zq_j   (units of 2^-24 of the dot product)
   //   channel: R = sum_j D_j                    (dot product)
-  auto score_tile = [&](uint64_t xx, const uint32_t *s4, const uint32_t *z4, float *out) {
+  // s2/z2: fp16 (s, z) of the 4 output rows u, packed (u=0,1), (u=2,3)
+  auto score_tile = [&](uint64_t xx, uint32_t s2lo, uint32_t s2hi, uint32_t z2lo, uint32_t z2hi, float *out) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     const uint32_t wlo = (uint32_t)xx, whi = (uint32_t)(xx >> 32);
     if constexpr (SMODE == kG32) {
@@ -366,8 +410,9 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
     for (int uu = 0; uu < 4; ++uu) {
       float r;
       if constexpr (SMODE == kG32) {
-        const float su = f16_bits_to_f32((s4[uu >> 1] >> (16 * (uu & 1))) & 0xffffu);
-        const float zu = f16_bits_to_f32((z4[uu >> 1] >> (16 * (uu & 1))) & 0xffffu);
+        const uint32_t sw = uu < 2 ? s2lo : s2hi, zw = uu < 2 ? z2lo : z2hi;
+        const float su = f16_bits_to_f32((sw >> (16 * (uu & 1))) & 0xffffu);
+        const float zu = f16_bits_to_f32((zw >> (16 * (uu & 1))) & 0xffffu);
         r = __builtin_fmaf(su, acc[uu], zu * zq);
       } else {
         r = acc[uu];
@@ -379,23 +424,21 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
   };
   const float cs1 = SMODE == kG32 ? p.scale * 16777216.f : p.scale;  // (R * cs1) * log2e = log2-scaled score
 
-  // probe windows (waves 0 and 1)
+  // ------------------------------------------------ phase 2b: scores
   if (do_probe) {
-    const uint32_t s4[2] = {pgs.x, pgs.y}, z4[2] = {pgz.x, pgz.y};
     float r4[4];
-    score_tile(px, s4, z4, r4);
+    score_tile(px, pgs.x, pgs.y, pgz.x, pgz.y, r4);
     float mx = -INFINITY;
 #pragma unroll
     for (int uu = 0; uu < 4; ++uu) {
-      const int t = pa + 4 * kc + uu;
+      const int t = pa + 4 * uu + kc;
       mx = fmaxf(mx, t < Tb ? (r4[uu] * cs1) * kLog2e : -INFINITY);
     }
     mx = xor_max(mx, 16);
     mx = xor_max(mx, 32);
     if (lane < 4) s_probe[wv][lane] = mx;  // lane == ir here
   }
-
-  // own chunks: R[j][k] = raw score of token (c0+j)*64 + 16kc + k (k = 4u + tau)
+  // R[j][k] = raw score of token (c0+j)*64 + 16kc + k (k = 4u + tau)
   float R[kPPW][16];
 #pragma unroll
   for (int j = 0; j < kPPW; ++j) {
@@ -407,18 +450,8 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
                               gz[j][1].x, gz[j][1].y, gz[j][1].z, gz[j][1].w};
 #pragma unroll
       for (int tau = 0; tau < 4; ++tau) {
-        // scale/zero of tokens 4u + tau (u = 0..3) as fp16 pairs (u=0,1), (u=2,3)
-        uint32_t s4[2] = {0u, 0u}, z4[2] = {0u, 0u};
-        if constexpr (SMODE == kG32) {
-          const int sh = 16 * (tau & 1);
-          const int wi = tau >> 1;  // token 4u+tau sits in word 2u + wi, half tau&1
-          s4[0] = ((sw[0 + wi] >> sh) & 0xffffu) | (((sw[2 + wi] >> sh) & 0xffffu) << 16);
-          s4[1] = ((sw[4 + wi] >> sh) & 0xffffu) | (((sw[6 + wi] >> sh) & 0xffffu) << 16);
-          z4[0] = ((zw[0 + wi] >> sh) & 0xffffu) | (((zw[2 + wi] >> sh) & 0xffffu) << 16);
-          z4[1] = ((zw[4 + wi] >> sh) & 0xffffu) | (((zw[6 + wi] >> sh) & 0xffffu) << 16);
-        }
         float r4[4];
-        score_tile(x[j][tau], s4, z4, r4);
+        score_tile(x[j][tau], sw[2 * tau], sw[2 * tau + 1], zw[2 * tau], zw[2 * tau + 1], r4);
 #pragma unroll
         for (int uu = 0; uu < 4; ++uu) R[j][4 * uu + tau] = r4[uu];
       }
@@ -434,7 +467,6 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
   }
 
   // ------------------------------------------------ prune
-  // block maxima in log2-scaled units: per 16 tokens (lane), then per SBS
   float mxp[kPPW];
 #pragma unroll
   for (int j = 0; j < kPPW; ++j) {
@@ -477,7 +509,6 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
     if (SBS == 16) keep16[j] = ((bal[j] >> (16 * kc)) & 0xffffull) != 0;
     else if (SBS == 32) keep16[j] = ((bal[j] >> (32 * (kc >> 1))) & 0xffffffffull) != 0;
     else keep16[j] = bal[j] != 0;
-    // mask entries of the prune blocks starting in this chunk
     const int t0 = (c0 + j) * kPage;
     int8_t *mrow_ptr = p.mask + ((size_t)b * p.HKV + hkv) * p.ntbs;
     if (SBS <= kPage) {
@@ -496,24 +527,22 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
     }
   }
 
-  // ------------------------------------------------ phase 3: exact pass of kept chunks
-  const size_t row_base = (size_t)b * p.HQ + hkv * G;
+  // ------------------------------------------------ phase 3: exact pass of kept chunks -> LDS partials
 #pragma unroll
   for (int j = 0; j < kPPW; ++j) {
-    const int chunk = c0 + j;
-    const int t0 = chunk * kPage;
-    if (t0 >= Tb) continue;
-    if (bal[j] == 0) {
-      if (kc == 0 && jg == 0 && row_ok) {
-        p.m_buf[(row_base + ir) * p.nch + chunk] = -INFINITY;
-        p.l_buf[(row_base + ir) * p.nch + chunk] = 0.f;
+    const int pslot = wv * kPPW + j;
+    const int t0 = (c0 + j) * kPage;
+    if (t0 >= Tb || bal[j] == 0) {
+      if (lane < 4) {
+        s_pm[pslot][lane] = -INFINITY;
+        s_pl[pslot][lane] = 0.f;
       }
       continue;
     }
     float Rj[16];
 #pragma unroll
     for (int k = 0; k < 16; ++k) Rj[k] = R[j][k];
-    // issue the residual and V loads together
+    // residual and V loads issued together
     uint4 rr[4][2];
     if constexpr (RES != kResNone) {
 #pragma unroll
@@ -678,134 +707,139 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 
-    // chunk partial: lanes 0..15 hold rows 0..3 of columns 16*nu + n
+    // chunk partial into LDS: lanes 0..15 hold rows 0..3 of columns 16*nu + n
     if (lane < 16) {
 #pragma unroll
-      for (int uu = 0; uu < 4; ++uu) {
-        if (uu < G) {
-          float *op = p.o_buf + ((row_base + uu) * p.nch + chunk) * 128 + n;
+      for (int uu = 0; uu < 4; ++uu)
 #pragma unroll
-          for (int nu = 0; nu < 8; ++nu) op[16 * nu] = oacc[nu][uu];
-        }
-      }
+        for (int nu = 0; nu < 8; ++nu) s_po[pslot][uu][16 * nu + n] = oacc[nu][uu];
     }
-    if (kc == 0 && jg == 0 && row_ok) {
-      p.m_buf[(row_base + ir) * p.nch + chunk] = mrow_max;
-      p.l_buf[(row_base + ir) * p.nch + chunk] = lsum;
+    if (lane < 4) {  // lane == ir, kc == 0, jg == 0
+      s_pm[pslot][lane] = row_ok ? mrow_max : -INFINITY;
+      s_pl[pslot][lane] = row_ok ? lsum : 0.f;
     }
   }
 
+  // ------------------------------------------------ phase 4: workgroup partial (8 chunks) -> global
+  __syncthreads();
+  {
+    const int i = wv;         // query row handled by this wave
+    const int c2 = 2 * lane;  // columns c2, c2 + 1
+    if (i < G) {
+      float M = -INFINITY;
+#pragma unroll
+      for (int ps = 0; ps < kChunksPerWG; ++ps)
+        if (s_pl[ps][i] > 0.f) M = fmaxf(M, s_pm[ps][i]);
+      float A = 0.f, ox = 0.f, oy = 0.f;
+#pragma unroll
+      for (int ps = 0; ps < kChunksPerWG; ++ps) {
+        const float l = s_pl[ps][i];
+        if (l > 0.f) {
+          const float wgt = exp2f(s_pm[ps][i] - M);
+          A = __builtin_fmaf(l, wgt, A);
+          ox = __builtin_fmaf(s_po[ps][i][c2], wgt, ox);
+          oy = __builtin_fmaf(s_po[ps][i][c2 + 1], wgt, oy);
+        }
+      }
+      const size_t row = (size_t)b * p.HQ + hkv * G + i;
+      if (lane == 0) {
+        p.m_buf[row * p.nparts + cg] = A > 0.f ? M : -INFINITY;
+        p.l_buf[row * p.nparts + cg] = A;
+      }
+      if (A > 0.f) *(float2 *)(p.o_buf + (row * p.nparts + cg) * 128 + c2) = make_float2(ox, oy);
+    }
+  }
 }
 
-
 // --------------------------------------------------------------------------
-// Log-sum-exp merge of the chunk partials (attn_kernel...q2fp8.py:142-171).
-// One workgroup (4 waves) per (sequence, query head).  Wave 0 loads m, l of a
-// segment of chunks in one batch, takes the max over kept chunks (l > 0) and
-// compacts them in chunk order with a ballot; the 4 waves then each
-// accumulate every 4th kept chunk (2 columns per lane, all loads of a wave in
-// flight together) and the slices are summed in a fixed order.
+// Log-sum-exp merge of the workgroup partials (attn_kernel...q2fp8.py:142-171).
+// One workgroup per (sequence, query head); thread t handles partial t/4
+// (+64 r) and a 32-column quarter.  m, l and the first 64 partials' o are
+// loaded in one batch; the weighted sums are reduced in a fixed order in LDS.
 // --------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void q2fp8_merge_kernel(const DecodeParams p) {
   const int row = blockIdx.x;  // b * HQ + hq
   const int b = row / p.HQ;
-  const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wv = tid >> 6;
+  const int k0 = tid >> 2, q4 = tid & 3;
   const int Tb = p.seq_lens ? p.seq_lens[b] : p.T;
-  const int nchb = min((Tb + kPage - 1) / kPage, p.nch);
-  const float *mr = p.m_buf + (size_t)row * p.nch;
-  const float *lr = p.l_buf + (size_t)row * p.nch;
-  const float *orow = p.o_buf + (size_t)row * p.nch * 128;
+  const int nparts = min((Tb + kChunksPerWG * kPage - 1) / (kChunksPerWG * kPage), p.nparts);
+  const float *mr = p.m_buf + (size_t)row * p.nparts;
+  const float *lr = p.l_buf + (size_t)row * p.nparts;
+  const float *orow = p.o_buf + (size_t)row * p.nparts * 128;
+  __shared__ float s_red[4];
+  __shared__ float s_o[64][129];
+  __shared__ float s_half[2][128];
 
-  __shared__ int s_list[kMergeSeg];
-  __shared__ float s_w[kMergeSeg];
-  __shared__ int s_cnt;
-  __shared__ float s_m, s_a;
-  __shared__ float2 s_part[4][64];
-
-  // global max over kept chunks (wave 0), all m/l loads of a segment in flight together
-  if (wv == 0) {
-    float M = -INFINITY;
-    for (int seg = 0; seg < nchb; seg += kMergeSeg) {
-      float mv[kMergeSeg / 64], lv[kMergeSeg / 64];
+  // batch 0: m, l and o of partial k0 (o selected by l > 0, so stale slots are never used)
+  float m0 = -INFINITY, l0 = 0.f;
+  float4 o0[8];
+  if (k0 < nparts) {
+    m0 = mr[k0];
+    l0 = lr[k0];
+    const float4 *op = (const float4 *)(orow + (size_t)k0 * 128 + 32 * q4);
 #pragma unroll
-      for (int k = 0; k < kMergeSeg / 64; ++k) {
-        const int c = seg + 64 * k + lane;
-        mv[k] = c < nchb ? mr[c] : -INFINITY;
-        lv[k] = c < nchb ? lr[c] : 0.f;
-      }
-#pragma unroll
-      for (int k = 0; k < kMergeSeg / 64; ++k)
-        if (lv[k] > 0.f) M = fmaxf(M, mv[k]);
-    }
-    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
-    if (lane == 0) s_m = M;
+    for (int e = 0; e < 8; ++e) o0[e] = op[e];
   }
+  float M = l0 > 0.f ? m0 : -INFINITY;
+  for (int k = k0 + 64; k < nparts; k += 64)
+    if (lr[k] > 0.f) M = fmaxf(M, mr[k]);
+  for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+  if (lane == 0) s_red[wv] = M;
   __syncthreads();
-  const float M = s_m;
+  M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+  __syncthreads();
+
   float A = 0.f;
-  float2 O = make_float2(0.f, 0.f);
-  for (int seg = 0; seg < nchb; seg += kMergeSeg) {
-    if (wv == 0) {
-      float mv[kMergeSeg / 64], lv[kMergeSeg / 64];
+  float acc[32];
+  {
+    const bool keep = l0 > 0.f;
+    const float wgt = keep ? exp2f(m0 - M) : 0.f;
+    A = keep ? l0 * wgt : 0.f;
 #pragma unroll
-      for (int k = 0; k < kMergeSeg / 64; ++k) {
-        const int c = seg + 64 * k + lane;
-        mv[k] = c < nchb ? mr[c] : -INFINITY;
-        lv[k] = c < nchb ? lr[c] : 0.f;
-      }
-      int cnt = 0;
-      float a = 0.f;
-#pragma unroll
-      for (int k = 0; k < kMergeSeg / 64; ++k) {
-        const bool keep = lv[k] > 0.f;
-        const float wgt = keep ? exp2f(mv[k] - M) : 0.f;
-        a += lv[k] * wgt;
-        const uint64_t bl = __ballot(keep);
-        const int pos = cnt + __popcll(bl & ((1ull << lane) - 1ull));
-        if (keep) {
-          s_list[pos] = seg + 64 * k + lane;
-          s_w[pos] = wgt;
-        }
-        cnt += __popcll(bl);
-      }
-      for (int o = 32; o >= 1; o >>= 1) a += __shfl_xor(a, o);
-      if (lane == 0) {
-        s_cnt = cnt;
-        s_a = a;
-      }
+    for (int e = 0; e < 8; ++e) {
+      acc[4 * e + 0] = keep ? o0[e].x * wgt : 0.f;
+      acc[4 * e + 1] = keep ? o0[e].y * wgt : 0.f;
+      acc[4 * e + 2] = keep ? o0[e].z * wgt : 0.f;
+      acc[4 * e + 3] = keep ? o0[e].w * wgt : 0.f;
     }
-    __syncthreads();
-    const int cnt = s_cnt;
-    A += s_a;
-    // slice wv: kept entries wv, wv+4, ...; 16 loads in flight per batch
-    for (int k0 = wv; k0 < cnt; k0 += 64) {
-      float2 v[16];
-      float w[16];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int k = k0 + 4 * e;
-        w[e] = k < cnt ? s_w[k] : 0.f;
-        v[e] = k < cnt ? *(const float2 *)(orow + (size_t)s_list[k] * 128 + 2 * lane) : make_float2(0.f, 0.f);
-      }
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        O.x = __builtin_fmaf(v[e].x, w[e], O.x);
-        O.y = __builtin_fmaf(v[e].y, w[e], O.y);
-      }
-    }
-    __syncthreads();
   }
-  s_part[wv][lane] = O;
+  for (int k = k0 + 64; k < nparts; k += 64) {
+    const float l = lr[k];
+    if (l > 0.f) {
+      const float wgt = exp2f(mr[k] - M);
+      A = __builtin_fmaf(l, wgt, A);
+      const float4 *op = (const float4 *)(orow + (size_t)k * 128 + 32 * q4);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float4 v = op[e];
+        acc[4 * e + 0] = __builtin_fmaf(v.x, wgt, acc[4 * e + 0]);
+        acc[4 * e + 1] = __builtin_fmaf(v.y, wgt, acc[4 * e + 1]);
+        acc[4 * e + 2] = __builtin_fmaf(v.z, wgt, acc[4 * e + 2]);
+        acc[4 * e + 3] = __builtin_fmaf(v.w, wgt, acc[4 * e + 3]);
+      }
+    }
+  }
+  // A: one count per partial (quarter 0 threads)
+  float a = q4 == 0 ? A : 0.f;
+  for (int o = 32; o >= 1; o >>= 1) a += __shfl_xor(a, o);
+  if (lane == 0) s_red[wv] = a;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) s_o[k0][32 * q4 + e] = acc[e];
   __syncthreads();
-  if (wv == 0) {
-    const float2 a0 = s_part[0][lane], a1 = s_part[1][lane], a2 = s_part[2][lane], a3 = s_part[3][lane];
-    const float ox = (a0.x + a1.x) + (a2.x + a3.x);
-    const float oy = (a0.y + a1.y) + (a2.y + a3.y);
-    const float rx = (A == 0.f) ? 0.f : ox / A;
-    const float ry = (A == 0.f) ? 0.f : oy / A;
-    store_any(p.out, (size_t)row * 128 + 2 * lane, p.out_dtype, rx);
-    store_any(p.out, (size_t)row * 128 + 2 * lane + 1, p.out_dtype, ry);
+  const float Atot = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+  {
+    const int c = tid & 127, h = tid >> 7;
+    float s = 0.f;
+#pragma unroll 8
+    for (int k = 32 * h; k < 32 * h + 32; ++k) s += s_o[k][c];
+    s_half[h][c] = s;
+  }
+  __syncthreads();
+  if (tid < 128) {
+    const float o = s_half[0][tid] + s_half[1][tid];
+    store_any(p.out, (size_t)row * 128 + tid, p.out_dtype, Atot == 0.f ? 0.f : o / Atot);
   }
 }
 
@@ -827,12 +861,11 @@ extern "C" __attribute__((visibility("hidden"))) int ffa_set_error_internal(int 
 }
 extern "C" const char *ffa_version(void) { return "ffa_mi355x 0.1 (gfx950)"; }
 
-extern "C" int ffa_q2fp8_decode_nchunks(int T, int BS, int SBS) {
+extern "C" int ffa_q2fp8_decode_nparts(int T, int BS, int SBS) {
   if (T <= 0 || BS <= 0 || SBS <= 0) return 0;
   const long ntb = (T + BS - 1) / BS;
   const long tokens = ntb * BS;  // the sub-blocks cover ceil(T/BS)*BS tokens
-  const long wgs = (tokens + ffa::kChunksPerWG * ffa::kPage - 1) / (ffa::kChunksPerWG * ffa::kPage);
-  return (int)(wgs * ffa::kChunksPerWG);
+  return (int)((tokens + ffa::kChunksPerWG * ffa::kPage - 1) / (ffa::kChunksPerWG * ffa::kPage));
 }
 
 template <int L, int S, int R, int V>
@@ -877,8 +910,8 @@ extern "C" int ffa_q2fp8_decode(const ffa_q2fp8_decode_args *a, void *stream) {
     return set_err(FFA_E_UNSUPPORTED, "contiguous layout supports per-channel scales only");
   if (a->scale_mode == FFA_SCALE_G32 && a->scale_dtype != FFA_DT_F16)
     return set_err(FFA_E_INVALID, "g32 scales must be fp16");
-  const int need = ffa_q2fp8_decode_nchunks(a->T, a->BS, a->SBS);
-  if (a->nchunks < need) return set_err(FFA_E_INVALID, "scratch holds too few chunks");
+  const int need = ffa_q2fp8_decode_nparts(a->T, a->BS, a->SBS);
+  if (a->nparts < need) return set_err(FFA_E_INVALID, "scratch holds too few partial slots");
   const int ntbs = ((a->T + a->BS - 1) / a->BS) * (a->BS / a->SBS);
   if (a->ntbs < ntbs) return set_err(FFA_E_INVALID, "mask holds too few blocks");
 
@@ -911,11 +944,11 @@ extern "C" int ffa_q2fp8_decode(const ffa_q2fp8_decode_args *a, void *stream) {
   p.BS = a->BS;
   p.SBS = a->SBS;
   p.delta = a->delta;
-  p.nch = a->nchunks;
+  p.nparts = a->nparts;
   p.ntbs = a->ntbs;
 
   hipStream_t st = (hipStream_t)stream;
-  dim3 grid((need / ffa::kChunksPerWG) * a->B * a->HKV);
+  dim3 grid(need * a->B * a->HKV);
   hipError_t e;
   if (a->layout == FFA_LAYOUT_PAGED) {
     if (a->scale_mode == FFA_SCALE_G32)

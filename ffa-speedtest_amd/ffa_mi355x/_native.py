@@ -19,7 +19,7 @@ LAYOUT_CONTIG, LAYOUT_PAGED = 0, 1
 SCALE_CHANNEL, SCALE_G32 = 0, 1
 
 EXPORTS = (
-    "ffa_q2fp8_decode_nchunks",
+    "ffa_q2fp8_decode_nparts",
     "ffa_q2fp8_decode",
     "ffa_q2_quantize_nsplit",
     "ffa_q2_quantize_channel",
@@ -78,7 +78,7 @@ class DecodeArgs(ctypes.Structure):
         ("m_buf", ctypes.c_void_p),
         ("l_buf", ctypes.c_void_p),
         ("o_buf", ctypes.c_void_p),
-        ("nchunks", ctypes.c_int),
+        ("nparts", ctypes.c_int),
         ("mask", ctypes.c_void_p),
         ("ntbs", ctypes.c_int),
     ]
@@ -105,8 +105,8 @@ def lib() -> ctypes.CDLL:
         vp, ci, cf = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
         L.ffa_last_error.restype = ctypes.c_char_p
         L.ffa_version.restype = ctypes.c_char_p
-        L.ffa_q2fp8_decode_nchunks.argtypes = [ci, ci, ci]
-        L.ffa_q2fp8_decode_nchunks.restype = ci
+        L.ffa_q2fp8_decode_nparts.argtypes = [ci, ci, ci]
+        L.ffa_q2fp8_decode_nparts.restype = ci
         L.ffa_q2fp8_decode.argtypes = [ctypes.POINTER(DecodeArgs), vp]
         L.ffa_q2fp8_decode.restype = ci
         L.ffa_q2_quantize_nsplit.argtypes = [ci]

@@ -21,8 +21,9 @@ def _cdiv(a: int, b: int) -> int:
     return -(-a // b)
 
 
-def decode_nchunks(T: int, BS: int, SBS: int) -> int:
-    return int(N.lib().ffa_q2fp8_decode_nchunks(int(T), int(BS), int(SBS)))
+def decode_nparts(T: int, BS: int, SBS: int) -> int:
+    """Partial slots per query row (one per 512-token workgroup of the decode kernel)."""
+    return int(N.lib().ffa_q2fp8_decode_nparts(int(T), int(BS), int(SBS)))
 
 
 def decode_ntbs(T: int, BS: int, SBS: int) -> int:
@@ -34,7 +35,7 @@ class DecodeWorkspace:
 
     Mirrors Q2FP8DecodeWorkspace (ffa-q2fp8-h100/attn_kernel/attn_kernel_v1210_fused_bsz_q2fp8.py:232-257):
     o, m_buf, l_buf, o_buf, mask_buf, threshold_buf.  Partials are kept per
-    64-token chunk (m_buf/l_buf [B, HQ, nchunks], o_buf [B, HQ, nchunks, 128]),
+    512-token span (m_buf/l_buf [B, HQ, nparts], o_buf [B, HQ, nparts, 128]),
     mask_buf holds one byte per prune block [B, HKV, NTBS].
     """
 
@@ -44,12 +45,12 @@ class DecodeWorkspace:
         self.V = HEAD_DIM
         self.device = torch.device(device)
         self.dtype = dtype
-        self.nchunks = decode_nchunks(T, BS, SBS)
+        self.nparts = decode_nparts(T, BS, SBS)
         self.NTBS = decode_ntbs(T, BS, SBS)
         self.o = torch.empty((B, HQ, HEAD_DIM), device=device, dtype=dtype)
-        self.m_buf = torch.empty((B, HQ, self.nchunks), device=device, dtype=torch.float32)
-        self.l_buf = torch.empty((B, HQ, self.nchunks), device=device, dtype=torch.float32)
-        self.o_buf = torch.empty((B, HQ, self.nchunks, HEAD_DIM), device=device, dtype=torch.float32)
+        self.m_buf = torch.empty((B, HQ, self.nparts), device=device, dtype=torch.float32)
+        self.l_buf = torch.empty((B, HQ, self.nparts), device=device, dtype=torch.float32)
+        self.o_buf = torch.empty((B, HQ, self.nparts, HEAD_DIM), device=device, dtype=torch.float32)
         self.mask_buf = torch.empty((B, HKV, self.NTBS), device=device, dtype=torch.int8)
         self.threshold_buf = torch.empty((B, HQ), device=device, dtype=torch.float32)
 
@@ -58,7 +59,7 @@ class DecodeWorkspace:
             self.B == int(B)
             and self.HQ == int(HQ)
             and self.HKV == int(HKV)
-            and self.nchunks >= decode_nchunks(T, BS, SBS)
+            and self.nparts >= decode_nparts(T, BS, SBS)
             and self.NTBS == decode_ntbs(T, BS, SBS)
             and self.device == torch.device(device)
             and self.dtype == dtype
@@ -135,7 +136,7 @@ def run_decode(
     a.m_buf = workspace.m_buf.data_ptr()
     a.l_buf = workspace.l_buf.data_ptr()
     a.o_buf = workspace.o_buf.data_ptr()
-    a.nchunks = workspace.nchunks
+    a.nparts = workspace.nparts
     a.mask = workspace.mask_buf.data_ptr()
     a.ntbs = workspace.NTBS
     rc = N.lib().ffa_q2fp8_decode(ctypes.byref(a), ctypes.c_void_p(N.stream_of(q.device)))

@@ -6,13 +6,15 @@ build adds a page pool shared by all sequences, laid out for the gfx950
 kernels (all per (page, KV head) blocks contiguous):
 
     k_q      [P, HKV, 4, 64, 8]  u8    2-bit codes, group-major (32 codes/8 bytes per token and group)
-    k_scale  [P, HKV, 4, 64]     f16   g32 scale per token and group
-    k_zero   [P, HKV, 4, 64]     f16   g32 zero point
+    k_scale  [P, HKV, 4, 64]     f16   g32 scale per token and group (slot order below)
+    k_zero   [P, HKV, 4, 64]     f16   g32 zero point (slot order below)
     k_res    [P, HKV, 64, 128]   fp8   residual (e4m3fn by default)
     v        [P, HKV, 128, 64]   bf16  V^T pages (token-minor)
 
 block_table[b, i] is the pool page of tokens [64 i, 64 i + 64) of sequence b;
-seq_lens[b] is its length.
+seq_lens[b] is its length.  Token t of a page keeps its scale/zero in slot
+scale_pos(t) = 16*(t//16) + 4*(t%4) + (t//4)%4 (the order the decode kernel's
+MFMA tiles consume them in); codes, residual and V use plain token order.
 """
 from __future__ import annotations
 
@@ -24,6 +26,11 @@ from . import _native as N
 from .decode import HEAD_DIM, DecodeWorkspace, run_decode
 
 PAGE = 64
+
+
+def scale_pos(t):
+    """Slot of token t (0..63) in a page row of g32 scales / zeros (an involution)."""
+    return 16 * (t // 16) + 4 * (t % 4) + (t // 4) % 4
 
 
 def check_append_fits(pos: torch.Tensor, Tn: int, block_table: torch.Tensor, num_pages: int) -> None:

@@ -51,8 +51,9 @@ enum {
   FFA_LAYOUT_CONTIG = 0,
   /* paged layout, 64-token pages from a pool of P pages:
      k_q        [P, HKV, 4 groups, 64 tokens, 8 bytes]   (group-major codes)
-     k_scale    [P, HKV, 4 groups, 64 tokens] fp16       (g32 mode)
-     k_zero     [P, HKV, 4 groups, 64 tokens] fp16       (g32 mode)
+     k_scale    [P, HKV, 4 groups, 64 slots] fp16        (g32 mode)
+     k_zero     [P, HKV, 4 groups, 64 slots] fp16        (g32 mode)
+                token t of a page sits in slot 16*(t/16) + 4*(t%4) + (t/4)%4
      k_residual [P, HKV, 64 tokens, 128] fp8
      v          [P, HKV, 128, 64 tokens]                 (V^T pages)
      block_table[b, i] = pool page holding tokens [64i, 64i+64) of sequence b */
@@ -76,8 +77,9 @@ enum {
  * Arguments of one pruned decode step.  Shapes use B sequences, HQ query
  * heads, HKV KV heads (G = HQ/HKV <= 4), head dim D = DV = 128.
  *
- * Scratch (caller-owned, see ffa_q2fp8_decode_nchunks):
- *   m_buf, l_buf [B, HQ, nchunks] f32; o_buf [B, HQ, nchunks, 128] f32;
+ * Scratch (caller-owned, see ffa_q2fp8_decode_nparts): one partial per query
+ * row and 512-token span,
+ *   m_buf, l_buf [B, HQ, nparts] f32; o_buf [B, HQ, nparts, 128] f32;
  *   mask [B, HKV, ntbs] i8 (1 = block kept, written for every block).
  * Two launches on `stream`: score + prune + exact pass, then the log-sum-exp
  * merge.  Calls that share scratch must be ordered on one stream.
@@ -107,13 +109,13 @@ typedef struct ffa_q2fp8_decode_args {
   void *out;                  /* [B, HQ, 128], dtype out_dtype */
   int out_dtype;
   float *m_buf, *l_buf, *o_buf;
-  int nchunks;
+  int nparts;
   int8_t *mask;
   int ntbs;
 } ffa_q2fp8_decode_args;
 
-/* Number of 64-token chunks the scratch buffers must hold for max length T. */
-int ffa_q2fp8_decode_nchunks(int T, int BS, int SBS);
+/* Number of partial slots per query row the scratch buffers must hold for max length T. */
+int ffa_q2fp8_decode_nparts(int T, int BS, int SBS);
 
 int ffa_q2fp8_decode(const ffa_q2fp8_decode_args *args, void *stream);
 

@@ -5,6 +5,7 @@ import numpy as np
 import torch
 
 from ffa_mi355x import synth
+from ffa_mi355x.paged import scale_pos
 from oracle import q2fp8 as O
 
 TORCH_DT = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}
@@ -62,6 +63,7 @@ def paged_case(B=1, T=2048, HQ=32, HKV=8, seed=0, n_heavy=16, res="e4m3fn", seq_
         r_pool = np.zeros((P, HKV, 64, 128), np.uint8)
         v_pool = np.zeros((P, HKV, 128, 64), np.uint16)
     vb = v.view(torch.int16).numpy().view(np.uint16)  # bf16 bits [B,T,HKV,128]
+    spos = np.array([scale_pos(t) for t in range(64)])
     s16 = s.astype(np.float16).view(np.uint16)
     z16 = z.astype(np.float16).view(np.uint16)
     for b in range(B):
@@ -70,8 +72,8 @@ def paged_case(B=1, T=2048, HQ=32, HKV=8, seed=0, n_heavy=16, res="e4m3fn", seq_
             t1 = min(t0 + 64, lens[b])
             n = t1 - t0
             kq_pool[page, :, :, :n, :] = pk[b, t0:t1].reshape(n, HKV, 4, 8).transpose(1, 2, 0, 3)
-            s_pool[page, :, :, :n] = s16[b, t0:t1].transpose(1, 2, 0)
-            z_pool[page, :, :, :n] = z16[b, t0:t1].transpose(1, 2, 0)
+            s_pool[page][:, :, spos[:n]] = s16[b, t0:t1].transpose(1, 2, 0)
+            z_pool[page][:, :, spos[:n]] = z16[b, t0:t1].transpose(1, 2, 0)
             r_pool[page, :, :n, :] = r[b, t0:t1].transpose(1, 0, 2)
             v_pool[page, :, :, :n] = vb[b, t0:t1].transpose(1, 2, 0)
     return dict(q=q, k=k, v=v, k_q=pk, k_scale=s, k_zero=z, k_res=r, res=res, lens=lens, block_table=bt,

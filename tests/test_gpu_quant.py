@@ -11,6 +11,7 @@ import torch
 
 from helpers import FP8_DT, TORCH_DT, f32
 from oracle import producer as OP
+from ffa_mi355x.paged import scale_pos
 from oracle import q2fp8 as O
 
 pytestmark = pytest.mark.gpu
@@ -59,8 +60,9 @@ def test_g32_append_bit_exact(gpu):
     torch.cuda.synchronize()
     pk, s, z, r = O.quantize_g32(f32(k), "e4m3fn")
     kq_pool = cache.k_q.cpu().numpy()
-    s_pool = cache.k_scale.float().cpu().numpy()
-    z_pool = cache.k_zero.float().cpu().numpy()
+    spos = np.array([scale_pos(t) for t in range(64)])
+    s_pool = cache.k_scale.float().cpu().numpy()[..., spos]  # back to token order
+    z_pool = cache.k_zero.float().cpu().numpy()[..., spos]
     r_pool = cache.k_res.view(torch.uint8).cpu().numpy()
     v_pool = cache.v.view(torch.int16).cpu().numpy()
     vb = v.view(torch.int16).numpy()
@@ -133,7 +135,7 @@ def test_kproj_append_config5_small(gpu):
     k_ref = OP.kproj_rope_rows(f32(h), f32(w).T, f32(cos), f32(sin), HKV)
     pk, s, z, r = O.quantize_g32(k_ref, "e4m3fn")
     kq_pool = cache.k_q.cpu().numpy()
-    s_pool = cache.k_scale.float().cpu().numpy()
+    s_pool = cache.k_scale.float().cpu().numpy()[..., [scale_pos(t) for t in range(64)]]
     r_pool = cache.k_res.view(torch.uint8).cpu().numpy()
     mism = 0
     for b in range(B):

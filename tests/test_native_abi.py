@@ -34,9 +34,10 @@ def test_host_only_helpers():
 
     L = N.lib()
     assert L.ffa_version().startswith(b"ffa_mi355x")
-    # 32K tokens, 64-token chunks, 4 chunks per workgroup
-    assert L.ffa_q2fp8_decode_nchunks(32768, 64, 64) == 512
-    assert L.ffa_q2fp8_decode_nchunks(100, 128, 128) == 8  # 8 chunks per workgroup
+    # one partial slot per 512-token workgroup
+    assert L.ffa_q2fp8_decode_nparts(32768, 64, 64) == 64
+    assert L.ffa_q2fp8_decode_nparts(100, 128, 128) == 1
+    assert L.ffa_q2fp8_decode_nparts(1000, 64, 64) == 2
     assert L.ffa_q2_quantize_nsplit(32768) == 64
 
 
