@@ -36,6 +36,8 @@
 
 #include <stdio.h>
 
+#include <type_traits>
+
 namespace ffa {
 
 constexpr int kD = 128;
@@ -232,6 +234,11 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
   __shared__ float s_po[kChunksPerWG][4][128];
   __shared__ uint8_t s_vstage[LAYOUT == kContig ? kWaves * kPage * kVRow : 4];
 
+  // Workgroup barrier for LDS traffic only: __syncthreads() would also wait for every
+  // outstanding global load of the wave (s_waitcnt vmcnt(0)), serialising the page loads
+  // issued ahead of it.
+  auto lds_barrier = []() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+
   // ------------------------------------------------ phase 1: loads
   // q of this lane's (row, group): every wave builds one of the four MFMA operands
   Raw32 qraw, sraw, zraw;
@@ -365,7 +372,7 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
     s_qa[w][lane] = make_uint4(a4[0], a4[1], a4[2], a4[3]);
     s_qr[w][lane] = make_uint4(r4[0], r4[1], r4[2], r4[3]);
   }
-  __syncthreads();
+  lds_barrier();
   f16x8 qa[4], qr[4];
   uint32_t spair[16], zpair[16];
   float zq = 0.f;
@@ -424,7 +431,15 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
   };
   const float cs1 = SMODE == kG32 ? p.scale * 16777216.f : p.scale;  // (R * cs1) * log2e = log2-scaled score
 
-  // ------------------------------------------------ phase 2b: scores
+  // ------------------------------------------------ phase 2b: probe, scores, prune, exact pass
+  // Pages are decided one by one: the residual/V loads of a kept page are issued before the
+  // next page is scored, so its latency hides behind that work.
+  float R[kPPW][16];
+  uint64_t bal[kPPW] = {0, 0};
+  bool keep16[kPPW] = {false, false};
+  float th = INFINITY;
+
+  // probe windows (waves 0 and 1)
   if (do_probe) {
     float r4[4];
     score_tile(px, pgs.x, pgs.y, pgz.x, pgz.y, r4);
@@ -438,10 +453,10 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
     mx = xor_max(mx, 32);
     if (lane < 4) s_probe[wv][lane] = mx;  // lane == ir here
   }
+
   // R[j][k] = raw score of token (c0+j)*64 + 16kc + k (k = 4u + tau)
-  float R[kPPW][16];
-#pragma unroll
-  for (int j = 0; j < kPPW; ++j) {
+  auto score_page = [&](auto J) {
+    constexpr int j = decltype(J)::value;
     const int t0 = (c0 + j) * kPage;
     if (t0 < Tb) {
       const uint32_t sw[8] = {gs[j][0].x, gs[j][0].y, gs[j][0].z, gs[j][0].w,
@@ -464,48 +479,29 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
 #pragma unroll
       for (int k = 0; k < 16; ++k) R[j][k] = -INFINITY;
     }
-  }
-
-  // ------------------------------------------------ prune
-  float mxp[kPPW];
-#pragma unroll
-  for (int j = 0; j < kPPW; ++j) {
+  };
+  // block maximum (log2-scaled) of the prune block holding the lane's 16 tokens, SBS <= 64
+  auto page_max = [&](auto J) -> float {
+    constexpr int j = decltype(J)::value;
     float m = R[j][0];
 #pragma unroll
     for (int k = 1; k < 16; ++k) m = fmaxf(m, R[j][k]);
     m = (m * cs1) * kLog2e;
     if (SBS >= 32) m = xor_max(m, 16);
     if (SBS >= 64) m = xor_max(m, 32);
-    mxp[j] = m;
-  }
-  if (SBS >= 128) {
-    const float m = fmaxf(mxp[0], mxp[1]);
-    mxp[0] = m;
-    mxp[1] = m;
-  }
-  if (SBS > 128 && lane < 4) s_wmax[wv][lane] = mxp[0];
-  __syncthreads();
-  float th;
-  if (p.th_in != nullptr) {
-    th = row_ok ? p.th_in[(size_t)b * p.HQ + hq] : INFINITY;
-  } else {
-    th = row_ok ? fmaxf(s_probe[0][ir], s_probe[1][ir]) - p.delta : INFINITY;
-  }
-  if (p.th_out != nullptr && cg == 0 && threadIdx.x < G) p.th_out[(size_t)b * p.HQ + hkv * G + threadIdx.x] = th;
-  if (SBS > 128) {
-    const int wpb = SBS / (kPage * kPPW);
-    const int w0 = (wv / wpb) * wpb;
-    float m2 = -INFINITY;
-    for (int w = w0; w < w0 + wpb; ++w) m2 = fmaxf(m2, s_wmax[w][ir]);
-    mxp[0] = m2;
-    mxp[1] = m2;
-  }
+    return m;
+  };
+  auto load_threshold = [&]() {
+    if (p.th_in != nullptr) {
+      th = row_ok ? p.th_in[(size_t)b * p.HQ + hq] : INFINITY;
+    } else {
+      th = row_ok ? fmaxf(s_probe[0][ir], s_probe[1][ir]) - p.delta : INFINITY;
+    }
+  };
   // prune iff every row of the group is below its threshold (strict <); rows >= G do not vote
-  uint64_t bal[kPPW];
-  bool keep16[kPPW];
-#pragma unroll
-  for (int j = 0; j < kPPW; ++j) {
-    bal[j] = __ballot(row_ok && !(mxp[j] < th));
+  auto decide = [&](auto J, float mxj) {
+    constexpr int j = decltype(J)::value;
+    bal[j] = __ballot(row_ok && !(mxj < th));
     if (SBS == 16) keep16[j] = ((bal[j] >> (16 * kc)) & 0xffffull) != 0;
     else if (SBS == 32) keep16[j] = ((bal[j] >> (32 * (kc >> 1))) & 0xffffffffull) != 0;
     else keep16[j] = bal[j] != 0;
@@ -525,25 +521,25 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
       const int jb = t0 / SBS;
       if (jb < p.ntbs) mrow_ptr[jb] = (jb < NTBS_b && bal[j] != 0) ? 1 : 0;
     }
-  }
-
-  // ------------------------------------------------ phase 3: exact pass of kept chunks -> LDS partials
-#pragma unroll
-  for (int j = 0; j < kPPW; ++j) {
-    const int pslot = wv * kPPW + j;
-    const int t0 = (c0 + j) * kPage;
-    if (t0 >= Tb || bal[j] == 0) {
-      if (lane < 4) {
-        s_pm[pslot][lane] = -INFINITY;
-        s_pl[pslot][lane] = 0.f;
-      }
-      continue;
+  };
+  auto is_kept = [&](auto J) -> bool {
+    constexpr int j = decltype(J)::value;
+    return (c0 + j) * kPage < Tb && bal[j] != 0;
+  };
+  auto empty_partial = [&](auto J) {
+    constexpr int j = decltype(J)::value;
+    if (lane < 4) {
+      s_pm[wv * kPPW + j][lane] = -INFINITY;
+      s_pl[wv * kPPW + j][lane] = 0.f;
     }
-    float Rj[16];
-#pragma unroll
-    for (int k = 0; k < 16; ++k) Rj[k] = R[j][k];
-    // residual and V loads issued together
-    uint4 rr[4][2];
+  };
+
+  // exact pass of one kept page: residual + V loads, then refined scores, softmax and P.V
+  uint4 rr[4][2];
+  uint4 vv[8][2];
+  auto issue_exact = [&](auto J) {
+    constexpr int j = decltype(J)::value;
+    const int t0 = (c0 + j) * kPage;
     if constexpr (RES != kResNone) {
 #pragma unroll
       for (int tau = 0; tau < 4; ++tau) {
@@ -559,8 +555,6 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
         rr[tau][1] = *(const uint4 *)(p.kr + off + 16);
       }
     }
-    uint4 vv[8][2];
-    uint8_t *st = s_vstage + (LAYOUT == kContig ? wv * kPage * kVRow : 0);
     if constexpr (LAYOUT == kPaged) {
       const uint16_t *vp = (const uint16_t *)p.v + (((size_t)pg[j] * p.HKV + hkv) * 128) * kPage;
 #pragma unroll
@@ -577,7 +571,14 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
         vv[r >> 1][r & 1] = *(const uint4 *)((const uint16_t *)p.v + (((size_t)b * p.T + t) * p.HKV + hkv) * 128 + 8 * vc);
       }
     }
-
+  };
+  auto exact_compute = [&](auto J) {
+    constexpr int j = decltype(J)::value;
+    const int pslot = wv * kPPW + j;
+    const int t0 = (c0 + j) * kPage;
+    float Rj[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) Rj[k] = R[j][k];
     if constexpr (RES != kResNone) {
 #pragma unroll
       for (int tau = 0; tau < 4; ++tau) {
@@ -609,7 +610,6 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
         }
       }
     }
-
     // softmax partial over the active tokens (valid and in a kept sub-block)
     float P[16];
     float mrow_max = -INFINITY;
@@ -631,7 +631,6 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
     }
     lsum = xor_sum(lsum, 16);
     lsum = xor_sum(lsum, 32);
-
     // P operand (A) of P.V for K-chunk kap: element e <-> token 16*kc + 8*kap + e
     typename VTr::vec pa2[2];
 #pragma unroll
@@ -641,7 +640,6 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
       for (int e = 0; e < 4; ++e) w[e] = VTr::pack2(P[8 * kap + 2 * e], P[8 * kap + 2 * e + 1]);
       pa2[kap] = __builtin_bit_cast(typename VTr::vec, w);
     }
-
     const bool partial = (t0 + kPage) > Tb;
     f32x4 oacc[8];
 #pragma unroll
@@ -670,6 +668,7 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
       }
     } else {
       // contiguous layout: stage the V tile [64 tokens][128] through LDS, then read columns
+      uint8_t *st = s_vstage + wv * kPage * kVRow;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int idx = r * 64 + lane;
@@ -706,7 +705,6 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-
     // chunk partial into LDS: lanes 0..15 hold rows 0..3 of columns 16*nu + n
     if (lane < 16) {
 #pragma unroll
@@ -718,7 +716,67 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
       s_pm[pslot][lane] = row_ok ? mrow_max : -INFINITY;
       s_pl[pslot][lane] = row_ok ? lsum : 0.f;
     }
+  };
+
+  const std::integral_constant<int, 0> J0;
+  const std::integral_constant<int, 1> J1;
+  score_page(J0);
+  if (SBS <= kPage) {
+    lds_barrier();  // probe maxima
+    load_threshold();
+    decide(J0, page_max(J0));
+    const bool k0 = is_kept(J0);
+    if (k0) issue_exact(J0);
+    score_page(J1);
+    decide(J1, page_max(J1));
+    const bool k1 = is_kept(J1);
+    if (k0) exact_compute(J0);
+    else empty_partial(J0);
+    if (k1) {
+      issue_exact(J1);
+      exact_compute(J1);
+    } else {
+      empty_partial(J1);
+    }
+  } else {
+    // prune blocks span both pages of the wave (SBS = 128) or several waves (256, 512)
+    score_page(J1);
+    float m0 = R[0][0], m1 = R[1][0];
+#pragma unroll
+    for (int k = 1; k < 16; ++k) {
+      m0 = fmaxf(m0, R[0][k]);
+      m1 = fmaxf(m1, R[1][k]);
+    }
+    float m = (fmaxf(m0, m1) * cs1) * kLog2e;
+    m = xor_max(m, 16);
+    m = xor_max(m, 32);
+    if (SBS > 128 && lane < 4) s_wmax[wv][lane] = m;
+    lds_barrier();  // probe maxima and per-wave block maxima
+    load_threshold();
+    if (SBS > 128) {
+      const int wpb = SBS / (kPage * kPPW);
+      const int w0 = (wv / wpb) * wpb;
+      float m2 = -INFINITY;
+      for (int w = w0; w < w0 + wpb; ++w) m2 = fmaxf(m2, s_wmax[w][ir]);
+      m = m2;
+    }
+    decide(J0, m);
+    decide(J1, m);
+    if (is_kept(J0)) {
+      issue_exact(J0);
+      exact_compute(J0);
+    } else {
+      empty_partial(J0);
+    }
+    if (is_kept(J1)) {
+      issue_exact(J1);
+      exact_compute(J1);
+    } else {
+      empty_partial(J1);
+    }
   }
+  if (p.th_out != nullptr && cg == 0 && threadIdx.x < G) p.th_out[(size_t)b * p.HQ + hkv * G + threadIdx.x] = th;
+
 
   // ------------------------------------------------ phase 4: workgroup partial (8 chunks) -> global
   __syncthreads();
