@@ -121,4 +121,25 @@ constexpr int kRowRor8 = 0x128;
 __device__ __forceinline__ float xor_max(float x, int m) { return fmaxf(x, __shfl_xor(x, m)); }
 __device__ __forceinline__ float xor_sum(float x, int m) { return x + __shfl_xor(x, m); }
 
+// Raw buffer resource over [base, base + bytes) (gfx9 word 3: 32-bit data format, no
+// swizzle).  A load at an offset past `bytes` returns zeros without a memory access, so a
+// load group can be issued on every path with its validity carried by the size; the
+// compiler then counts outstanding loads exactly and waits for one group at a time.
+typedef __amdgpu_buffer_rsrc_t brsrc;
+__device__ __forceinline__ brsrc make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 bload16(brsrc r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint2 bload8(brsrc r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+  return make_uint2(v[0], v[1]);
+}
+__device__ __forceinline__ uint64_t bload8u(brsrc r, uint32_t off) {
+  const uint2 v = bload8(r, off);
+  return ((uint64_t)v.y << 32) | v.x;
+}
+
 }  // namespace ffa

@@ -68,6 +68,7 @@ struct DecodeParams {
   int BS, SBS;
   float delta;
   int nparts, ntbs;
+  int nwg;  // decode workgroups per (sequence, KV head)
 };
 
 enum { kContig = 0, kPaged = 1 };
@@ -134,26 +135,19 @@ struct VTraits<kVF16> {
   }
 };
 
-// 32 consecutive elements of a float tensor (dtype 0=f16, 1=bf16, 2=f32): raw 16-byte loads
-// first (all issued back to back), conversion afterwards.
-struct Raw32 {
-  uint4 v[8];
+// 16 consecutive elements of a float tensor (dtype 0=f16, 1=bf16, 2=f32): four raw 16-byte
+// loads whatever the dtype (16-bit data uses the first two), conversion afterwards.
+struct Raw16 {
+  uint4 v[4];
 };
-__device__ __forceinline__ void raw32_load(Raw32 &r, const void *ptr, size_t off, int dt) {
-  if (dt == 2) {
-    const uint4 *q = (const uint4 *)((const float *)ptr + off);
+__device__ __forceinline__ void raw16_load(Raw16 &r, brsrc rs, uint32_t off) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) r.v[i] = q[i];
-  } else {
-    const uint4 *q = (const uint4 *)((const uint16_t *)ptr + off);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r.v[i] = q[i];
-  }
+  for (int i = 0; i < 4; ++i) r.v[i] = bload16(rs, off + 16 * i);
 }
-__device__ __forceinline__ void raw32_to_f32(const Raw32 &r, int dt, float *out) {
+__device__ __forceinline__ void raw16_to_f32(const Raw16 &r, int dt, float *out) {
   if (dt == 2) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 4; ++i) {
       out[4 * i + 0] = __uint_as_float(r.v[i].x);
       out[4 * i + 1] = __uint_as_float(r.v[i].y);
       out[4 * i + 2] = __uint_as_float(r.v[i].z);
@@ -161,7 +155,7 @@ __device__ __forceinline__ void raw32_to_f32(const Raw32 &r, int dt, float *out)
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 2; ++i) {
       const uint32_t w[4] = {r.v[i].x, r.v[i].y, r.v[i].z, r.v[i].w};
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
@@ -202,17 +196,19 @@ __host__ __device__ constexpr int scale_pos(int t) { return 16 * (t >> 4) + 4 * 
 template <int LAYOUT, int SMODE, int RES, int VT>
 __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p) {
   typedef VTraits<VT> VTr;
+  constexpr bool kG = SMODE == kG32;
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // 1-D grid, unit u = (b, hkv) fastest: with B*HKV a multiple of 8 the workgroups of a
-  // unit land on one XCD (dispatch is round-robin over the 8 XCDs) and share its L2.
-  const int U = p.B * p.HKV;
-  const int u = blockIdx.x % U;
-  const int cg = blockIdx.x / U;  // workgroup index along the sequence = partial slot
+  // 1-D grid, workgroup index along the sequence fastest: consecutive workgroups land on
+  // different XCDs (dispatch is round-robin over the 8 XCDs), so the residual/V traffic of a
+  // (sequence, KV head) unit with many kept chunks is spread over every XCD's memory path.
+  const int u = blockIdx.x / p.nwg;
+  const int cg = blockIdx.x - u * p.nwg;  // workgroup index along the sequence = partial slot
   const int b = u / p.HKV;
   const int hkv = u - b * p.HKV;
   const int G = p.G;
-  const int c0 = cg * kChunksPerWG + wv * kPPW;  // first chunk of this wave
+  const int cw = cg * kChunksPerWG;  // first chunk of the workgroup
+  const int c0 = cw + wv * kPPW;     // first chunk scored by this wave
   const int SBS = p.SBS;
 
   const int mrow = lane & 15;  // MFMA row (A) / column (B) index
@@ -223,13 +219,18 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
   const bool row_ok = ir < G;
   const int hq = hkv * G + (row_ok ? ir : 0);
 
-  __shared__ uint4 s_qa[4][64];  // B operands of the 4 score MFMAs, per lane
-  __shared__ uint4 s_qr[4][64];  // B operands of the 4 residual MFMAs (g32)
-  __shared__ uint4 s_sp[4][64];  // channel mode: fp16 (scale, scale) pairs of 8 channels
-  __shared__ uint4 s_zp2[4][64]; // channel mode: fp16 (zero, zero) pairs
-  __shared__ float s_zs[4][64];  // g32: partial sums of q16 over 8 channels
+  __shared__ uint4 s_qa[4][64];                    // B operands of the 4 score MFMAs, per lane
+  __shared__ uint4 s_qr[4][64];                    // B operands of the 4 residual MFMAs (g32)
+  __shared__ uint4 s_sp[kG ? 1 : 4][64];           // channel scales: fp16 (scale, scale) pairs of 8 channels
+  __shared__ uint4 s_zp2[kG ? 1 : 4][64];          // channel scales: fp16 (zero, zero) pairs
+  __shared__ float s_zs[4][64];                    // g32: partial sums of q16 over 8 channels
   __shared__ float s_probe[2][4];
   __shared__ float s_wmax[kWaves][4];
+  __shared__ int s_kept[kChunksPerWG];             // chunk kept (some prune block survives)
+  __shared__ int s_pgid[kChunksPerWG];             // pool page of the chunk
+  __shared__ uint32_t s_bal[kChunksPerWG][2];      // survivor ballot of the chunk
+  __shared__ float4 s_R[kG ? kChunksPerWG : 1][4][64];        // g32: coarse scores of kept chunks
+  __shared__ uint64_t s_x[kG ? 1 : kChunksPerWG][4][64];       // channel: codes of kept chunks
   __shared__ float s_pm[kChunksPerWG][4], s_pl[kChunksPerWG][4];
   __shared__ float s_po[kChunksPerWG][4][128];
   __shared__ uint8_t s_vstage[LAYOUT == kContig ? kWaves * kPage * kVRow : 4];
@@ -240,18 +241,34 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
   auto lds_barrier = []() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
 
   // ------------------------------------------------ phase 1: loads
-  // q of this lane's (row, group): every wave builds one of the four MFMA operands
-  Raw32 qraw, sraw, zraw;
-  raw32_load(qraw, p.q, ((size_t)b * p.HQ + hq) * kD + 32 * kc, p.q_dtype);
-  if constexpr (SMODE == kChannel) {
-    raw32_load(sraw, p.ks, ((size_t)b * p.HKV + hkv) * kD + 32 * kc, p.s_dtype);
-    raw32_load(zraw, p.kz, ((size_t)b * p.HKV + hkv) * kD + 32 * kc, p.s_dtype);
+  // Every vector load is issued on every path; validity (sequence end, kept or pruned) is
+  // the size of the buffer resource, so the compiler waits for one load group at a time.
+  // Groups are issued in the order they are consumed: q window (and channel scales), the
+  // caller's threshold, probe windows, page 0, page 1.
+  // The q window is channels [32kc + 16h, +16) of the lane's row, h = wave / 2: it holds
+  // every element of the operand this wave builds.
+  const uint32_t es_q = p.q_dtype == 2 ? 4u : 2u;
+  const int hwin = wv >> 1;
+  Raw16 qraw, sraw, zraw;
+  raw16_load(qraw, make_rsrc((const char *)p.q + (size_t)b * p.HQ * kD * es_q, p.HQ * kD * es_q),
+             (hq * kD + 32 * kc + 16 * hwin) * es_q);
+  if constexpr (!kG) {
+    const uint32_t es_s = p.s_dtype == 2 ? 4u : 2u;
+    const size_t so = ((size_t)b * p.HKV + hkv) * kD * es_s;
+    raw16_load(sraw, make_rsrc((const char *)p.ks + so, kD * es_s), (32 * kc + 16 * hwin) * es_s);
+    raw16_load(zraw, make_rsrc((const char *)p.kz + so, kD * es_s), (32 * kc + 16 * hwin) * es_s);
   }
+  // caller's threshold of the lane's query row (zeros when none is given)
+  const float th_pre = __uint_as_float(
+      bload8(make_rsrc(p.th_in + (p.th_in ? (size_t)b * p.HQ : 0), p.th_in ? p.HQ * 4 : 0), hq * 4).x);
   const int Tb = p.seq_lens ? p.seq_lens[b] : p.T;
   const int NTB = (Tb + p.BS - 1) / p.BS;
   const int NTBS_b = NTB * (p.BS / p.SBS);
   const bool do_probe = (p.th_in == nullptr) && wv < 2;
-  const int pa = wv == 0 ? 0 : (NTB - 1) * 16;  // probe window (attn_kernel...q2fp8.py:58-73)
+  const int pa = wv == 0 ? 0 : max(NTB - 1, 0) * 16;  // probe window (attn_kernel...q2fp8.py:58-73)
+  int nv[kPPW];                                       // valid tokens of the wave's chunks
+#pragma unroll
+  for (int j = 0; j < kPPW; ++j) nv[j] = min(max(Tb - (c0 + j) * kPage, 0), kPage);
 
   int pg[kPPW] = {0, 0};
   int ppg = 0;
@@ -259,8 +276,29 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
     const int32_t *btr = p.bt + (size_t)b * p.bt_stride;
 #pragma unroll
     for (int j = 0; j < kPPW; ++j)
-      if ((c0 + j) * kPage < Tb) pg[j] = btr[c0 + j];
-    if (do_probe) ppg = btr[pa >> 6];
+      if (nv[j] > 0) pg[j] = btr[c0 + j];
+    if (do_probe && pa < Tb) ppg = btr[pa >> 6];
+  }
+  // probe tile: MFMA row m <-> token pa + 4(m & 3) + (m >> 2), so that the output rows
+  // 4kc + u hold tokens pa + 4u + kc, whose g32 scales are contiguous (scale_pos)
+  uint64_t px;
+  uint2 pgs = make_uint2(0, 0), pgz = make_uint2(0, 0);
+  {
+    const int tok = pa + 4 * (mrow & 3) + (mrow >> 2);
+    const bool pv = do_probe && pa < Tb;
+    if constexpr (LAYOUT == kPaged) {
+      const size_t blk = (size_t)ppg * p.HKV + hkv;
+      px = bload8u(make_rsrc(p.kq + blk * (4 * kPage * 8), pv ? 4 * kPage * 8 : 0), (kc * kPage + (tok & (kPage - 1))) * 8);
+      if constexpr (kG) {
+        const uint32_t so = (jg * kPage + (pa & (kPage - 1)) + 4 * kc) * 2;
+        pgs = bload8(make_rsrc((const uint16_t *)p.ks + blk * (4 * kPage), pv ? 4 * kPage * 2 : 0), so);
+        pgz = bload8(make_rsrc((const uint16_t *)p.kz + blk * (4 * kPage), pv ? 4 * kPage * 2 : 0), so);
+      }
+    } else {
+      const int nt = pv ? min(16, Tb - pa) : 0;
+      const size_t base = (((size_t)b * p.T + pa) * p.HKV + hkv) * 32;
+      px = bload8u(make_rsrc(p.kq + base, nt > 0 ? ((nt - 1) * p.HKV + 1) * 32 : 0), (tok - pa) * p.HKV * 32 + 8 * kc);
+    }
   }
   // own chunks: the token of MFMA row m in tile tau is 4m + tau
   uint64_t x[kPPW][4];
@@ -268,129 +306,113 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
 #pragma unroll
   for (int j = 0; j < kPPW; ++j) {
     const int t0 = (c0 + j) * kPage;
-#pragma unroll
-    for (int tau = 0; tau < 4; ++tau) x[j][tau] = 0;
-    if (t0 < Tb) {
-      if constexpr (LAYOUT == kPaged) {
-        const uint4 *cp = (const uint4 *)(p.kq + ((((size_t)pg[j] * p.HKV + hkv) * 4 + kc) * kPage + 4 * mrow) * 8);
-        const uint4 q0 = cp[0], q1 = cp[1];
-        x[j][0] = ((uint64_t)q0.y << 32) | q0.x;
-        x[j][1] = ((uint64_t)q0.w << 32) | q0.z;
-        x[j][2] = ((uint64_t)q1.y << 32) | q1.x;
-        x[j][3] = ((uint64_t)q1.w << 32) | q1.z;
-        if constexpr (SMODE == kG32) {
-          const size_t so = (((size_t)pg[j] * p.HKV + hkv) * 4 + jg) * kPage + 16 * kc;
-          gs[j][0] = ((const uint4 *)((const uint16_t *)p.ks + so))[0];
-          gs[j][1] = ((const uint4 *)((const uint16_t *)p.ks + so))[1];
-          gz[j][0] = ((const uint4 *)((const uint16_t *)p.kz + so))[0];
-          gz[j][1] = ((const uint4 *)((const uint16_t *)p.kz + so))[1];
-        }
-      } else {
-#pragma unroll
-        for (int tau = 0; tau < 4; ++tau) {
-          const int t = min(t0 + 4 * mrow + tau, Tb - 1);
-          x[j][tau] = *(const uint64_t *)(p.kq + (((size_t)b * p.T + t) * p.HKV + hkv) * 32 + 8 * kc);
-        }
-      }
-    }
-  }
-  // probe tile: MFMA row m <-> token pa + 4(m & 3) + (m >> 2), so that the output rows
-  // 4kc + u hold tokens pa + 4u + kc, whose g32 scales are contiguous (scale_pos)
-  uint64_t px = 0;
-  uint2 pgs = make_uint2(0, 0), pgz = make_uint2(0, 0);
-  if (do_probe) {
-    const int tok = pa + 4 * (mrow & 3) + (mrow >> 2);
     if constexpr (LAYOUT == kPaged) {
-      px = *(const uint64_t *)(p.kq + ((((size_t)ppg * p.HKV + hkv) * 4 + kc) * kPage + (tok & (kPage - 1))) * 8);
-      if constexpr (SMODE == kG32) {
-        const size_t so = (((size_t)ppg * p.HKV + hkv) * 4 + jg) * kPage + ((pa & (kPage - 1)) + 4 * kc);
-        pgs = *(const uint2 *)((const uint16_t *)p.ks + so);
-        pgz = *(const uint2 *)((const uint16_t *)p.kz + so);
+      const size_t blk = (size_t)pg[j] * p.HKV + hkv;
+      const brsrc rc = make_rsrc(p.kq + blk * (4 * kPage * 8), nv[j] > 0 ? 4 * kPage * 8 : 0);
+      const uint32_t co = (kc * kPage + 4 * mrow) * 8;
+      const uint4 q0 = bload16(rc, co), q1 = bload16(rc, co + 16);
+      x[j][0] = ((uint64_t)q0.y << 32) | q0.x;
+      x[j][1] = ((uint64_t)q0.w << 32) | q0.z;
+      x[j][2] = ((uint64_t)q1.y << 32) | q1.x;
+      x[j][3] = ((uint64_t)q1.w << 32) | q1.z;
+      if constexpr (kG) {
+        const brsrc rs = make_rsrc((const uint16_t *)p.ks + blk * (4 * kPage), nv[j] > 0 ? 4 * kPage * 2 : 0);
+        const brsrc rz = make_rsrc((const uint16_t *)p.kz + blk * (4 * kPage), nv[j] > 0 ? 4 * kPage * 2 : 0);
+        const uint32_t so = (jg * kPage + 16 * kc) * 2;
+        gs[j][0] = bload16(rs, so);
+        gs[j][1] = bload16(rs, so + 16);
+        gz[j][0] = bload16(rz, so);
+        gz[j][1] = bload16(rz, so + 16);
       }
     } else {
-      const int t = min(tok, Tb - 1);
-      px = *(const uint64_t *)(p.kq + (((size_t)b * p.T + t) * p.HKV + hkv) * 32 + 8 * kc);
+      const size_t base = (((size_t)b * p.T + t0) * p.HKV + hkv) * 32;
+      const brsrc rc = make_rsrc(p.kq + base, nv[j] > 0 ? ((nv[j] - 1) * p.HKV + 1) * 32 : 0);
+#pragma unroll
+      for (int tau = 0; tau < 4; ++tau) x[j][tau] = bload8u(rc, (4 * mrow + tau) * p.HKV * 32 + 8 * kc);
     }
   }
 
   // ------------------------------------------------ phase 2a: B operands, built once per workgroup
-  // wave w builds, for every lane, the operand of MFMA m' = w:
-  //   g32 score:    element 2q+half <-> channel 32kc + 16h + 4s + q + 8half (m' = 2h+s), times 4^-q
-  //   channel score: element e <-> channel 32kc + 8m' + e
-  //   residual:     element e <-> channel 32kc + 8m' + e (every column)
+  // wave w = 2h + s builds, for every lane, the operand of MFMA m' = w (channels relative to
+  // the lane's group 32kc):
+  //   g32 score:     element 2q+half <-> channel 16h + 4s + q + 8half, times 4^-q
+  //   channel score: element e <-> channel 8w + e
+  //   residual:      element e <-> channel 8w + e (every column)
   // Score operands are nonzero only on the column's own group (kc == j).
-  {
-    float qv[32];
-    raw32_to_f32(qraw, p.q_dtype, qv);
-    const int w = wv;
+  auto build_operands = [&](auto W) {
+    constexpr int w = decltype(W)::value;  // compile-time: only the needed elements are converted
+    constexpr int s = w & 1;
+    float qv[16];  // channels 32kc + 16h + (0..15)
+    raw16_to_f32(qraw, p.q_dtype, qv);
     u32x4 a4, r4;
-    if constexpr (SMODE == kG32) {
-      const int h = w >> 1, s = w & 1;
+    if constexpr (kG) {
 #pragma unroll
       for (int qq = 0; qq < 4; ++qq) {
         const float inv = qq == 0 ? 1.f : (qq == 1 ? 0.25f : (qq == 2 ? 0.0625f : 0.015625f));
         float e2[2];
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
-          const float q16 = (float)(_Float16)qv[16 * h + 4 * s + qq + 8 * half];
+          const float q16 = (float)(_Float16)qv[4 * s + qq + 8 * half];
           e2[half] = (row_ok && kc == jg) ? q16 * inv : 0.f;
         }
         a4[qq] = f32_to_f16_bits(e2[0]) | (f32_to_f16_bits(e2[1]) << 16);
       }
       float zs = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) zs += (float)(_Float16)qv[8 * w + e];
+      for (int e = 0; e < 8; ++e) zs += (float)(_Float16)qv[8 * s + e];
       s_zs[w][lane] = row_ok ? zs : 0.f;
     } else {
 #pragma unroll
       for (int qq = 0; qq < 4; ++qq) {
-        const float e0 = (row_ok && kc == jg) ? (float)(_Float16)qv[8 * w + 2 * qq] : 0.f;
-        const float e1 = (row_ok && kc == jg) ? (float)(_Float16)qv[8 * w + 2 * qq + 1] : 0.f;
+        const float e0 = (row_ok && kc == jg) ? (float)(_Float16)qv[8 * s + 2 * qq] : 0.f;
+        const float e1 = (row_ok && kc == jg) ? (float)(_Float16)qv[8 * s + 2 * qq + 1] : 0.f;
         a4[qq] = f32_to_f16_bits(e0) | (f32_to_f16_bits(e1) << 16);
       }
-      float sv[32], zv[32];
-      raw32_to_f32(sraw, p.s_dtype, sv);
-      raw32_to_f32(zraw, p.s_dtype, zv);
+      float sv[16], zv[16];
+      raw16_to_f32(sraw, p.s_dtype, sv);
+      raw16_to_f32(zraw, p.s_dtype, zv);
       uint4 sp, zp;
-      sp.x = f32_to_f16_bits(sv[8 * w + 0]) | (f32_to_f16_bits(sv[8 * w + 1]) << 16);
-      sp.y = f32_to_f16_bits(sv[8 * w + 2]) | (f32_to_f16_bits(sv[8 * w + 3]) << 16);
-      sp.z = f32_to_f16_bits(sv[8 * w + 4]) | (f32_to_f16_bits(sv[8 * w + 5]) << 16);
-      sp.w = f32_to_f16_bits(sv[8 * w + 6]) | (f32_to_f16_bits(sv[8 * w + 7]) << 16);
-      zp.x = f32_to_f16_bits(zv[8 * w + 0]) | (f32_to_f16_bits(zv[8 * w + 1]) << 16);
-      zp.y = f32_to_f16_bits(zv[8 * w + 2]) | (f32_to_f16_bits(zv[8 * w + 3]) << 16);
-      zp.z = f32_to_f16_bits(zv[8 * w + 4]) | (f32_to_f16_bits(zv[8 * w + 5]) << 16);
-      zp.w = f32_to_f16_bits(zv[8 * w + 6]) | (f32_to_f16_bits(zv[8 * w + 7]) << 16);
+      sp.x = f32_to_f16_bits(sv[8 * s + 0]) | (f32_to_f16_bits(sv[8 * s + 1]) << 16);
+      sp.y = f32_to_f16_bits(sv[8 * s + 2]) | (f32_to_f16_bits(sv[8 * s + 3]) << 16);
+      sp.z = f32_to_f16_bits(sv[8 * s + 4]) | (f32_to_f16_bits(sv[8 * s + 5]) << 16);
+      sp.w = f32_to_f16_bits(sv[8 * s + 6]) | (f32_to_f16_bits(sv[8 * s + 7]) << 16);
+      zp.x = f32_to_f16_bits(zv[8 * s + 0]) | (f32_to_f16_bits(zv[8 * s + 1]) << 16);
+      zp.y = f32_to_f16_bits(zv[8 * s + 2]) | (f32_to_f16_bits(zv[8 * s + 3]) << 16);
+      zp.z = f32_to_f16_bits(zv[8 * s + 4]) | (f32_to_f16_bits(zv[8 * s + 5]) << 16);
+      zp.w = f32_to_f16_bits(zv[8 * s + 6]) | (f32_to_f16_bits(zv[8 * s + 7]) << 16);
       s_sp[w][lane] = sp;
       s_zp2[w][lane] = zp;
     }
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq) {
-      const float e0 = row_ok ? (float)(_Float16)qv[8 * w + 2 * qq] : 0.f;
-      const float e1 = row_ok ? (float)(_Float16)qv[8 * w + 2 * qq + 1] : 0.f;
+      const float e0 = row_ok ? (float)(_Float16)qv[8 * s + 2 * qq] : 0.f;
+      const float e1 = row_ok ? (float)(_Float16)qv[8 * s + 2 * qq + 1] : 0.f;
       r4[qq] = f32_to_f16_bits(e0) | (f32_to_f16_bits(e1) << 16);
     }
     s_qa[w][lane] = make_uint4(a4[0], a4[1], a4[2], a4[3]);
     s_qr[w][lane] = make_uint4(r4[0], r4[1], r4[2], r4[3]);
+  };
+  switch (wv) {
+    case 0: build_operands(std::integral_constant<int, 0>()); break;
+    case 1: build_operands(std::integral_constant<int, 1>()); break;
+    case 2: build_operands(std::integral_constant<int, 2>()); break;
+    default: build_operands(std::integral_constant<int, 3>()); break;
   }
   lds_barrier();
-  f16x8 qa[4], qr[4];
+  f16x8 qa[4];
   uint32_t spair[16], zpair[16];
   float zq = 0.f;
 #pragma unroll
   for (int mp = 0; mp < 4; ++mp) {
     const uint4 a = s_qa[mp][lane];
     qa[mp] = __builtin_bit_cast(f16x8, u32x4{a.x, a.y, a.z, a.w});
-    if constexpr (SMODE == kG32 && RES != kResNone) {
-      const uint4 r = s_qr[mp][lane];
-      qr[mp] = __builtin_bit_cast(f16x8, u32x4{r.x, r.y, r.z, r.w});
-    }
-    if constexpr (SMODE == kChannel) {
+    if constexpr (!kG) {
       const uint4 sp = s_sp[mp][lane], zp = s_zp2[mp][lane];
       spair[4 * mp + 0] = sp.x; spair[4 * mp + 1] = sp.y; spair[4 * mp + 2] = sp.z; spair[4 * mp + 3] = sp.w;
       zpair[4 * mp + 0] = zp.x; zpair[4 * mp + 1] = zp.y; zpair[4 * mp + 2] = zp.z; zpair[4 * mp + 3] = zp.w;
     }
   }
-  if constexpr (SMODE == kG32) {
+  if constexpr (kG) {
     const int src = (jg << 4) | n;  // lane of the column's own group, same query row
     zq = ((s_zs[0][src] + s_zs[1][src]) + (s_zs[2][src] + s_zs[3][src])) * (1.0f / 16777216.f);
   }
@@ -402,7 +424,7 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
   auto score_tile = [&](uint64_t xx, uint32_t s2lo, uint32_t s2hi, uint32_t z2lo, uint32_t z2hi, float *out) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     const uint32_t wlo = (uint32_t)xx, whi = (uint32_t)(xx >> 32);
-    if constexpr (SMODE == kG32) {
+    if constexpr (kG) {
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes_to_f16x8(wlo, 0), qa[0], acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes_to_f16x8(wlo, 1), qa[1], acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes_to_f16x8(whi, 0), qa[2], acc, 0, 0, 0);
@@ -416,7 +438,7 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
 #pragma unroll
     for (int uu = 0; uu < 4; ++uu) {
       float r;
-      if constexpr (SMODE == kG32) {
+      if constexpr (kG) {
         const uint32_t sw = uu < 2 ? s2lo : s2hi, zw = uu < 2 ? z2lo : z2hi;
         const float su = f16_bits_to_f32((sw >> (16 * (uu & 1))) & 0xffffu);
         const float zu = f16_bits_to_f32((zw >> (16 * (uu & 1))) & 0xffffu);
@@ -429,14 +451,11 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
       out[uu] = r;
     }
   };
-  const float cs1 = SMODE == kG32 ? p.scale * 16777216.f : p.scale;  // (R * cs1) * log2e = log2-scaled score
+  const float cs1 = kG ? p.scale * 16777216.f : p.scale;  // (R * cs1) * log2e = log2-scaled score
 
-  // ------------------------------------------------ phase 2b: probe, scores, prune, exact pass
-  // Pages are decided one by one: the residual/V loads of a kept page are issued before the
-  // next page is scored, so its latency hides behind that work.
+  // ------------------------------------------------ phase 2b: probe, scores, prune
   float R[kPPW][16];
   uint64_t bal[kPPW] = {0, 0};
-  bool keep16[kPPW] = {false, false};
   float th = INFINITY;
 
   // probe windows (waves 0 and 1)
@@ -470,7 +489,7 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
 #pragma unroll
         for (int uu = 0; uu < 4; ++uu) R[j][4 * uu + tau] = r4[uu];
       }
-      if (t0 + kPage > Tb) {
+      if (t0 + kPage > Tb) {  // tokens past the sequence end (page slots hold no data)
 #pragma unroll
         for (int k = 0; k < 16; ++k)
           if (t0 + 16 * kc + k >= Tb) R[j][k] = -INFINITY;
@@ -480,110 +499,152 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
       for (int k = 0; k < 16; ++k) R[j][k] = -INFINITY;
     }
   };
-  // block maximum (log2-scaled) of the prune block holding the lane's 16 tokens, SBS <= 64
-  auto page_max = [&](auto J) -> float {
+  // maximum (log2-scaled) of the lane's 16 tokens, reduced over the lanes of one prune block
+  // when the block spans several 16-token sub-blocks
+  auto lane_max = [&](auto J) -> float {
     constexpr int j = decltype(J)::value;
     float m = R[j][0];
 #pragma unroll
     for (int k = 1; k < 16; ++k) m = fmaxf(m, R[j][k]);
-    m = (m * cs1) * kLog2e;
-    if (SBS >= 32) m = xor_max(m, 16);
-    if (SBS >= 64) m = xor_max(m, 32);
-    return m;
+    return (m * cs1) * kLog2e;
   };
-  auto load_threshold = [&]() {
-    if (p.th_in != nullptr) {
-      th = row_ok ? p.th_in[(size_t)b * p.HQ + hq] : INFINITY;
-    } else {
-      th = row_ok ? fmaxf(s_probe[0][ir], s_probe[1][ir]) - p.delta : INFINITY;
-    }
-  };
+  const std::integral_constant<int, 0> J0;
+  const std::integral_constant<int, 1> J1;
+  score_page(J0);
+  score_page(J1);
+  float mb[kPPW];  // max of the prune block holding the lane's tokens, per chunk
+  mb[0] = lane_max(J0);
+  mb[1] = lane_max(J1);
+  if (SBS >= 32) {
+    mb[0] = xor_max(mb[0], 16);
+    mb[1] = xor_max(mb[1], 16);
+  }
+  if (SBS >= 64) {
+    mb[0] = xor_max(mb[0], 32);
+    mb[1] = xor_max(mb[1], 32);
+  }
+  if (SBS >= 128) mb[0] = mb[1] = fmaxf(mb[0], mb[1]);
+  if (SBS > 128 && lane < 4) s_wmax[wv][lane] = mb[0];
+  lds_barrier();  // probe maxima (and per-wave block maxima)
+  if (p.th_in != nullptr) {
+    th = row_ok ? th_pre : INFINITY;
+  } else {
+    th = row_ok ? fmaxf(s_probe[0][ir], s_probe[1][ir]) - p.delta : INFINITY;
+  }
+  if (SBS > 128) {
+    const int wpb = SBS / (kPage * kPPW);
+    const int w0 = (wv / wpb) * wpb;
+    float m2 = -INFINITY;
+    for (int w = w0; w < w0 + wpb; ++w) m2 = fmaxf(m2, s_wmax[w][ir]);
+    mb[0] = mb[1] = m2;
+  }
   // prune iff every row of the group is below its threshold (strict <); rows >= G do not vote
-  auto decide = [&](auto J, float mxj) {
-    constexpr int j = decltype(J)::value;
-    bal[j] = __ballot(row_ok && !(mxj < th));
-    if (SBS == 16) keep16[j] = ((bal[j] >> (16 * kc)) & 0xffffull) != 0;
-    else if (SBS == 32) keep16[j] = ((bal[j] >> (32 * (kc >> 1))) & 0xffffffffull) != 0;
-    else keep16[j] = bal[j] != 0;
-    const int t0 = (c0 + j) * kPage;
-    int8_t *mrow_ptr = p.mask + ((size_t)b * p.HKV + hkv) * p.ntbs;
-    if (SBS <= kPage) {
-      const int per = kPage / SBS;
-      const int jb = t0 / SBS;
-      if (lane < per && jb + lane < p.ntbs) {
-        const int sh = lane * SBS;
-        const bool kk = SBS == 16   ? ((bal[j] >> sh) & 0xffffull) != 0
-                        : SBS == 32 ? ((bal[j] >> sh) & 0xffffffffull) != 0
-                                    : bal[j] != 0;
-        mrow_ptr[jb + lane] = (jb + lane < NTBS_b && kk) ? 1 : 0;
-      }
-    } else if ((t0 % SBS) == 0 && lane == 0) {
-      const int jb = t0 / SBS;
-      if (jb < p.ntbs) mrow_ptr[jb] = (jb < NTBS_b && bal[j] != 0) ? 1 : 0;
-    }
-  };
-  auto is_kept = [&](auto J) -> bool {
-    constexpr int j = decltype(J)::value;
-    return (c0 + j) * kPage < Tb && bal[j] != 0;
-  };
-  auto empty_partial = [&](auto J) {
-    constexpr int j = decltype(J)::value;
-    if (lane < 4) {
-      s_pm[wv * kPPW + j][lane] = -INFINITY;
-      s_pl[wv * kPPW + j][lane] = 0.f;
-    }
-  };
+#pragma unroll
+  for (int j = 0; j < kPPW; ++j) bal[j] = __ballot(row_ok && !(mb[j] < th));
 
-  // exact pass of one kept page: residual + V loads, then refined scores, softmax and P.V
-  uint4 rr[4][2];
-  uint4 vv[8][2];
-  auto issue_exact = [&](auto J) {
-    constexpr int j = decltype(J)::value;
-    const int t0 = (c0 + j) * kPage;
+  // publish the kept chunks: coarse scores (g32) or codes (channel scales), page, ballot
+#pragma unroll
+  for (int j = 0; j < kPPW; ++j) {
+    const int slot = wv * kPPW + j;
+    const bool kept = (c0 + j) * kPage < Tb && bal[j] != 0;
+    if (lane == 0) {
+      s_kept[slot] = kept ? 1 : 0;
+      s_pgid[slot] = pg[j];
+      s_bal[slot][0] = (uint32_t)bal[j];
+      s_bal[slot][1] = (uint32_t)(bal[j] >> 32);
+    }
+    if (kept) {
+      if constexpr (kG) {
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4)
+          s_R[slot][q4][lane] = make_float4(R[j][4 * q4], R[j][4 * q4 + 1], R[j][4 * q4 + 2], R[j][4 * q4 + 3]);
+      } else {
+#pragma unroll
+        for (int tau = 0; tau < 4; ++tau) s_x[slot][tau][lane] = x[j][tau];
+      }
+    } else if (lane < 4) {
+      s_pm[slot][lane] = -INFINITY;
+      s_pl[slot][lane] = 0.f;
+    }
+  }
+  lds_barrier();
+
+  // ------------------------------------------------ phase 3: exact pass over the kept chunks
+  // The i-th kept chunk of the workgroup (in chunk order) goes to wave i % 4, so a
+  // workgroup's kept chunks are spread over its waves whichever wave scored them.
+  uint32_t km = 0;
+#pragma unroll
+  for (int sl = 0; sl < kChunksPerWG; ++sl) km |= (s_kept[sl] != 0 ? 1u : 0u) << sl;
+  km = __builtin_amdgcn_readfirstlane(km);
+
+  auto exact_chunk = [&](int slot) {
+    const int t0 = (cw + slot) * kPage;
+    const int nvs = min(Tb - t0, kPage);
+    const int pgs_ = __builtin_amdgcn_readfirstlane(s_pgid[slot]);
+    const uint64_t bl = ((uint64_t)s_bal[slot][1] << 32) | s_bal[slot][0];
+    const bool keep16 = SBS == 16   ? ((bl >> (16 * kc)) & 0xffffull) != 0
+                        : SBS == 32 ? ((bl >> (32 * (kc >> 1))) & 0xffffffffull) != 0
+                                    : bl != 0;
+    // residual + V loads (the chunk is kept: whole resource)
+    uint4 rr[4][2];
+    uint4 vv[8][2];
     if constexpr (RES != kResNone) {
+      brsrc rr_s;
+      uint32_t ro[4];
+      if constexpr (LAYOUT == kPaged) {
+        rr_s = make_rsrc(p.kr + ((size_t)pgs_ * p.HKV + hkv) * (kPage * kD), kPage * kD);
+#pragma unroll
+        for (int tau = 0; tau < 4; ++tau) ro[tau] = (4 * mrow + tau) * kD + 32 * kc;
+      } else {
+        rr_s = make_rsrc(p.kr + (((size_t)b * p.T + t0) * p.HKV + hkv) * kD, ((nvs - 1) * p.HKV + 1) * kD);
+#pragma unroll
+        for (int tau = 0; tau < 4; ++tau) ro[tau] = (4 * mrow + tau) * p.HKV * kD + 32 * kc;
+      }
 #pragma unroll
       for (int tau = 0; tau < 4; ++tau) {
-        const int tk = 4 * mrow + tau;
-        size_t off;
-        if constexpr (LAYOUT == kPaged) {
-          off = (((size_t)pg[j] * p.HKV + hkv) * kPage + tk) * kD + 32 * kc;
-        } else {
-          const int t = min(t0 + tk, Tb - 1);
-          off = (((size_t)b * p.T + t) * p.HKV + hkv) * kD + 32 * kc;
-        }
-        rr[tau][0] = *(const uint4 *)(p.kr + off);
-        rr[tau][1] = *(const uint4 *)(p.kr + off + 16);
+        rr[tau][0] = bload16(rr_s, ro[tau]);
+        rr[tau][1] = bload16(rr_s, ro[tau] + 16);
       }
     }
     if constexpr (LAYOUT == kPaged) {
-      const uint16_t *vp = (const uint16_t *)p.v + (((size_t)pg[j] * p.HKV + hkv) * 128) * kPage;
+      const brsrc vs = make_rsrc((const uint16_t *)p.v + ((size_t)pgs_ * p.HKV + hkv) * (kD * kPage), kD * kPage * 2);
 #pragma unroll
       for (int nu = 0; nu < 8; ++nu)
 #pragma unroll
-        for (int kap = 0; kap < 2; ++kap)
-          vv[nu][kap] = *(const uint4 *)(vp + (size_t)(16 * nu + n) * kPage + 16 * kc + 8 * kap);
+        for (int kap = 0; kap < 2; ++kap) vv[nu][kap] = bload16(vs, ((16 * nu + n) * kPage + 16 * kc + 8 * kap) * 2);
     } else {
+      const brsrc vs = make_rsrc((const uint16_t *)p.v + (((size_t)b * p.T + t0) * p.HKV + hkv) * kD,
+                                 ((nvs - 1) * p.HKV + 1) * kD * 2);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int idx = r * 64 + lane;
         const int tk = idx >> 4, vc = idx & 15;
-        const int t = min(t0 + tk, Tb - 1);
-        vv[r >> 1][r & 1] = *(const uint4 *)((const uint16_t *)p.v + (((size_t)b * p.T + t) * p.HKV + hkv) * 128 + 8 * vc);
+        vv[r >> 1][r & 1] = bload16(vs, tk * p.HKV * kD * 2 + 16 * vc);
       }
     }
-  };
-  auto exact_compute = [&](auto J) {
-    constexpr int j = decltype(J)::value;
-    const int pslot = wv * kPPW + j;
-    const int t0 = (c0 + j) * kPage;
+    // refined scores
     float Rj[16];
+    if constexpr (kG) {
 #pragma unroll
-    for (int k = 0; k < 16; ++k) Rj[k] = R[j][k];
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const float4 r4 = s_R[slot][q4][lane];
+        Rj[4 * q4] = r4.x;
+        Rj[4 * q4 + 1] = r4.y;
+        Rj[4 * q4 + 2] = r4.z;
+        Rj[4 * q4 + 3] = r4.w;
+      }
+    }
     if constexpr (RES != kResNone) {
 #pragma unroll
       for (int tau = 0; tau < 4; ++tau) {
-        if constexpr (SMODE == kG32) {
+        if constexpr (kG) {
           // refined = coarse + q . r   (exact fp16 residual, every column carries q_i)
+          f16x8 qr[4];
+#pragma unroll
+          for (int mp = 0; mp < 4; ++mp) {
+            const uint4 r = s_qr[mp][lane];
+            qr[mp] = __builtin_bit_cast(f16x8, u32x4{r.x, r.y, r.z, r.w});
+          }
           f32x4 acc = {0.f, 0.f, 0.f, 0.f};
           acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16x8<RES>(rr[tau][0].x, rr[tau][0].y), qr[0], acc, 0, 0, 0);
           acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16x8<RES>(rr[tau][0].z, rr[tau][0].w), qr[1], acc, 0, 0, 0);
@@ -593,7 +654,7 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
           for (int uu = 0; uu < 4; ++uu) Rj[4 * uu + tau] = __builtin_fmaf(acc[uu], 1.0f / 16777216.f, Rj[4 * uu + tau]);
         } else {
           // reference: k_tilde = fp16(k_hat + fp16(res)) (attn_kernel...q2fp8.py:109-115), full re-score
-          const uint64_t xx = x[j][tau];
+          const uint64_t xx = s_x[slot][tau][lane];
           const uint32_t wlo = (uint32_t)xx, whi = (uint32_t)(xx >> 32);
           f32x4 acc = {0.f, 0.f, 0.f, 0.f};
           acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(add_f16x8(dequant8_channel(wlo & 0xffffu, spair + 0, zpair + 0), fp8x8_to_f16x8<RES>(rr[tau][0].x, rr[tau][0].y)), qa[0], acc, 0, 0, 0);
@@ -609,6 +670,16 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
           }
         }
       }
+    } else if constexpr (!kG) {
+      // no residual: the coarse scores of the chunk again, from its codes
+      const uint32_t zero8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+      for (int tau = 0; tau < 4; ++tau) {
+        float r4[4];
+        score_tile(s_x[slot][tau][lane], zero8[0], zero8[0], zero8[0], zero8[0], r4);
+#pragma unroll
+        for (int uu = 0; uu < 4; ++uu) Rj[4 * uu + tau] = r4[uu];
+      }
     }
     // softmax partial over the active tokens (valid and in a kept sub-block)
     float P[16];
@@ -616,7 +687,7 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
       const int t = t0 + 16 * kc + k;
-      const bool act = row_ok && t < Tb && keep16[j];
+      const bool act = row_ok && t < Tb && keep16;
       P[k] = act ? (Rj[k] * cs1) * kLog2e : -INFINITY;
       mrow_max = fmaxf(mrow_max, P[k]);
     }
@@ -640,7 +711,7 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
       for (int e = 0; e < 4; ++e) w[e] = VTr::pack2(P[8 * kap + 2 * e], P[8 * kap + 2 * e + 1]);
       pa2[kap] = __builtin_bit_cast(typename VTr::vec, w);
     }
-    const bool partial = (t0 + kPage) > Tb;
+    const bool partial = nvs < kPage;
     f32x4 oacc[8];
 #pragma unroll
     for (int nu = 0; nu < 8; ++nu) oacc[nu] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -656,9 +727,8 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
             uint32_t w4[4] = {v4.x, v4.y, v4.z, v4.w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              const int ta = t0 + tk + 2 * e;
-              if (ta >= Tb) w4[e] &= 0xffff0000u;
-              if (ta + 1 >= Tb) w4[e] &= 0x0000ffffu;
+              if (tk + 2 * e >= nvs) w4[e] &= 0xffff0000u;
+              if (tk + 2 * e + 1 >= nvs) w4[e] &= 0x0000ffffu;
             }
             v4 = make_uint4(w4[0], w4[1], w4[2], w4[3]);
           }
@@ -668,6 +738,7 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
       }
     } else {
       // contiguous layout: stage the V tile [64 tokens][128] through LDS, then read columns
+      // (rows past the sequence end were loaded as zeros)
       uint8_t *st = s_vstage + wv * kPage * kVRow;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -675,11 +746,10 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
         const int tk = idx >> 4, vc = idx & 15;
         const uint4 v4 = vv[r >> 1][r & 1];
         uint32_t *d = (uint32_t *)(st + tk * kVRow + 16 * vc);
-        const bool ok = (t0 + tk) < Tb;
-        d[0] = ok ? v4.x : 0u;
-        d[1] = ok ? v4.y : 0u;
-        d[2] = ok ? v4.z : 0u;
-        d[3] = ok ? v4.w : 0u;
+        d[0] = v4.x;
+        d[1] = v4.y;
+        d[2] = v4.z;
+        d[3] = v4.w;
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
@@ -710,76 +780,49 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
 #pragma unroll
       for (int uu = 0; uu < 4; ++uu)
 #pragma unroll
-        for (int nu = 0; nu < 8; ++nu) s_po[pslot][uu][16 * nu + n] = oacc[nu][uu];
+        for (int nu = 0; nu < 8; ++nu) s_po[slot][uu][16 * nu + n] = oacc[nu][uu];
     }
     if (lane < 4) {  // lane == ir, kc == 0, jg == 0
-      s_pm[pslot][lane] = row_ok ? mrow_max : -INFINITY;
-      s_pl[pslot][lane] = row_ok ? lsum : 0.f;
+      s_pm[slot][lane] = row_ok ? mrow_max : -INFINITY;
+      s_pl[slot][lane] = row_ok ? lsum : 0.f;
     }
   };
+  // this wave's kept chunks: the (wv + 4a)-th set bit of km
+  int rank = 0;
+#pragma unroll 1
+  for (int sl = 0; sl < kChunksPerWG; ++sl) {
+    if ((km >> sl) & 1u) {
+      if ((rank & (kWaves - 1)) == wv) exact_chunk(sl);
+      ++rank;
+    }
+  }
 
-  const std::integral_constant<int, 0> J0;
-  const std::integral_constant<int, 1> J1;
-  score_page(J0);
-  if (SBS <= kPage) {
-    lds_barrier();  // probe maxima
-    load_threshold();
-    decide(J0, page_max(J0));
-    const bool k0 = is_kept(J0);
-    if (k0) issue_exact(J0);
-    score_page(J1);
-    decide(J1, page_max(J1));
-    const bool k1 = is_kept(J1);
-    if (k0) exact_compute(J0);
-    else empty_partial(J0);
-    if (k1) {
-      issue_exact(J1);
-      exact_compute(J1);
-    } else {
-      empty_partial(J1);
-    }
-  } else {
-    // prune blocks span both pages of the wave (SBS = 128) or several waves (256, 512)
-    score_page(J1);
-    float m0 = R[0][0], m1 = R[1][0];
-#pragma unroll
-    for (int k = 1; k < 16; ++k) {
-      m0 = fmaxf(m0, R[0][k]);
-      m1 = fmaxf(m1, R[1][k]);
-    }
-    float m = (fmaxf(m0, m1) * cs1) * kLog2e;
-    m = xor_max(m, 16);
-    m = xor_max(m, 32);
-    if (SBS > 128 && lane < 4) s_wmax[wv][lane] = m;
-    lds_barrier();  // probe maxima and per-wave block maxima
-    load_threshold();
-    if (SBS > 128) {
-      const int wpb = SBS / (kPage * kPPW);
-      const int w0 = (wv / wpb) * wpb;
-      float m2 = -INFINITY;
-      for (int w = w0; w < w0 + wpb; ++w) m2 = fmaxf(m2, s_wmax[w][ir]);
-      m = m2;
-    }
-    decide(J0, m);
-    decide(J1, m);
-    if (is_kept(J0)) {
-      issue_exact(J0);
-      exact_compute(J0);
-    } else {
-      empty_partial(J0);
-    }
-    if (is_kept(J1)) {
-      issue_exact(J1);
-      exact_compute(J1);
-    } else {
-      empty_partial(J1);
+  // ------------------------------------------------ phase 4: workgroup partial (8 chunks) -> global
+  // Global stores come last: on gfx9 stores share the vector memory counter with loads, and a
+  // pending store would make every later load wait a full write round trip.
+  __syncthreads();
+  {
+    // survivor mask, one byte per prune block (attn_kernel...q2fp8.py:99-104)
+    int8_t *mrow_ptr = p.mask + ((size_t)b * p.HKV + hkv) * p.ntbs;
+    const int t = threadIdx.x;
+    if (SBS <= kPage) {
+      const int per = kPage / SBS;
+      if (t < kChunksPerWG * per) {
+        const int slot = t / per, k = t - slot * per;
+        const uint64_t bl = ((uint64_t)s_bal[slot][1] << 32) | s_bal[slot][0];
+        const int jb = (cw + slot) * per + k;
+        const bool kk = SBS == 16   ? ((bl >> (16 * k)) & 0xffffull) != 0
+                        : SBS == 32 ? ((bl >> (32 * k)) & 0xffffffffull) != 0
+                                    : bl != 0;
+        if (jb < p.ntbs) mrow_ptr[jb] = (jb < NTBS_b && kk) ? 1 : 0;
+      }
+    } else if (t < kChunksPerWG && ((cw + t) * kPage) % SBS == 0) {
+      const int jb = (cw + t) * kPage / SBS;
+      const bool kk = (s_bal[t][0] | s_bal[t][1]) != 0;
+      if (jb < p.ntbs) mrow_ptr[jb] = (jb < NTBS_b && kk) ? 1 : 0;
     }
   }
   if (p.th_out != nullptr && cg == 0 && threadIdx.x < G) p.th_out[(size_t)b * p.HQ + hkv * G + threadIdx.x] = th;
-
-
-  // ------------------------------------------------ phase 4: workgroup partial (8 chunks) -> global
-  __syncthreads();
   {
     const int i = wv;         // query row handled by this wave
     const int c2 = 2 * lane;  // columns c2, c2 + 1
@@ -1004,6 +1047,7 @@ extern "C" int ffa_q2fp8_decode(const ffa_q2fp8_decode_args *a, void *stream) {
   p.delta = a->delta;
   p.nparts = a->nparts;
   p.ntbs = a->ntbs;
+  p.nwg = need;
 
   hipStream_t st = (hipStream_t)stream;
   dim3 grid(need * a->B * a->HKV);
