@@ -54,6 +54,17 @@ def kept_token_heads(mask, T, SBS):
     return int((mask.to(torch.int64) * valid).sum().item())
 
 
+def measured_traffic():
+    """HBM bytes per stage-1 launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (or None)."""
+    import re
+
+    f = ROOT / "profiles" / "q2fp8_decode_kernel_config2_traffic.md"
+    if not f.exists():
+        return None
+    m = re.search(r"^traffic_bytes_per_dispatch\s*=\s*(\d+)", f.read_text(), flags=re.M)
+    return {"bytes": int(m.group(1)), "source": f"profiles/{f.name}"} if m else None
+
+
 def cpu_baseline(q, k, v, BS, SBS, delta, seconds):
     """The numpy oracle on this host (1 thread) on the same workload: microseconds per layer-step."""
     import numpy as np
@@ -89,6 +100,7 @@ def main():
     ap.add_argument("--SBS", type=int, default=64)
     ap.add_argument("--delta", type=float, default=5.0)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--kernel-launches", type=int, default=480, help="timed stage-1 launches (roofline)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run 5 device copies of 256 MiB (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -176,10 +188,35 @@ def main():
     ms_total = start.elapsed_time(end)
     us_per_step = ms_total * 1e3 / steps
 
+    # dominant kernel (stage 1, q2fp8_decode_kernel) alone: a HIP graph of R back-to-back stage-1 launches
+    # (the same rotations), hipEvents on the replay stream around the replays
+    def stage1(r):
+        cache.decode(qd, bts[r], None, T=T, BS=args.BS, SBS=args.SBS, delta=args.delta, workspace=ws,
+                     stage="stage1")
+
+    g1 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g1, stream=stream):
+        for r in range(R):
+            stage1(r)
+    torch.cuda.synchronize()
+    n_k = max(1, math.ceil(args.kernel_launches / R))
+    g1.replay()
+    torch.cuda.synchronize()
+    k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    k0.record(cur)
+    for _ in range(n_k):
+        g1.replay()
+    k1.record(cur)
+    torch.cuda.synchronize()
+    kernel_us = k0.elapsed_time(k1) * 1e3 / (n_k * R)
+    n_k *= R
+
     kept_th = kept_token_heads(mask, T, args.SBS)
     keep_frac = float(mask.float().mean().item())
     nbytes = algorithmic_bytes([T] * B, HKV, HQ, kept_th, D)
     achieved_gbs = nbytes / (us_per_step * 1e-6) / 1e9
+    kernel_gbs = nbytes / (kernel_us * 1e-6) / 1e9
+    traffic = measured_traffic()
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -211,12 +248,16 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "achieved": round(achieved_gbs, 1),
+            "achieved": round(kernel_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "decode step = q2fp8_decode_kernel + q2fp8_merge_kernel (back to back in the graph)",
+            "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic["bytes"] if traffic else None,
+            "kernel": "q2fp8_decode_kernel (stage 1: scores, prune, exact pass over kept pages)",
+            "kernel_us": round(kernel_us, 3),
+            "kernel_timing": f"HIP graph of {R} back-to-back stage-1 launches, hipEvents around {n_k} launches",
+            "algorithmic_bytes_per_launch": nbytes,
+            "traffic_source": traffic["source"] if traffic else None,
         },
         "cpu_baseline": cpu,
         "setup_s": round(setup_s, 1),

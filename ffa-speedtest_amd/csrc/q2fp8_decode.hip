@@ -991,7 +991,8 @@ static hipError_t dispatch_rv(const ffa::DecodeParams &p, int res, int vdt, dim3
   return hipErrorInvalidValue;
 }
 
-extern "C" int ffa_q2fp8_decode(const ffa_q2fp8_decode_args *a, void *stream) {
+// Validates the arguments and fills the kernel parameters; returns FFA_OK or an error code.
+static int decode_params(const ffa_q2fp8_decode_args *a, ffa::DecodeParams &p) {
   if (!a) return set_err(FFA_E_INVALID, "null args");
   if (a->B <= 0 || a->T <= 0 || a->HQ <= 0 || a->HKV <= 0) return set_err(FFA_E_INVALID, "bad dims");
   if (a->HQ % a->HKV) return set_err(FFA_E_INVALID, "HQ must be a multiple of HKV");
@@ -1016,7 +1017,6 @@ extern "C" int ffa_q2fp8_decode(const ffa_q2fp8_decode_args *a, void *stream) {
   const int ntbs = ((a->T + a->BS - 1) / a->BS) * (a->BS / a->SBS);
   if (a->ntbs < ntbs) return set_err(FFA_E_INVALID, "mask holds too few blocks");
 
-  ffa::DecodeParams p;
   p.q = a->q;
   p.kq = a->k_q;
   p.ks = a->k_scale;
@@ -1048,9 +1048,11 @@ extern "C" int ffa_q2fp8_decode(const ffa_q2fp8_decode_args *a, void *stream) {
   p.nparts = a->nparts;
   p.ntbs = a->ntbs;
   p.nwg = need;
+  return FFA_OK;
+}
 
-  hipStream_t st = (hipStream_t)stream;
-  dim3 grid(need * a->B * a->HKV);
+static int launch_stage1(const ffa_q2fp8_decode_args *a, const ffa::DecodeParams &p, hipStream_t st) {
+  dim3 grid(p.nwg * a->B * a->HKV);
   hipError_t e;
   if (a->layout == FFA_LAYOUT_PAGED) {
     if (a->scale_mode == FFA_SCALE_G32)
@@ -1061,8 +1063,32 @@ extern "C" int ffa_q2fp8_decode(const ffa_q2fp8_decode_args *a, void *stream) {
     e = dispatch_rv<ffa::kContig, ffa::kChannel>(p, a->res_dtype, a->v_dtype, grid, st);
   }
   if (e != hipSuccess) return set_err(FFA_E_LAUNCH, hipGetErrorString(e));
+  return FFA_OK;
+}
+
+static int launch_stage2(const ffa_q2fp8_decode_args *a, const ffa::DecodeParams &p, hipStream_t st) {
   hipLaunchKernelGGL(ffa::q2fp8_merge_kernel, dim3(a->B * a->HQ), dim3(256), 0, st, p);
-  e = hipGetLastError();
+  const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_err(FFA_E_LAUNCH, hipGetErrorString(e));
   return FFA_OK;
+}
+
+extern "C" int ffa_q2fp8_decode_stage1(const ffa_q2fp8_decode_args *a, void *stream) {
+  ffa::DecodeParams p;
+  const int rc = decode_params(a, p);
+  return rc != FFA_OK ? rc : launch_stage1(a, p, (hipStream_t)stream);
+}
+
+extern "C" int ffa_q2fp8_decode_stage2(const ffa_q2fp8_decode_args *a, void *stream) {
+  ffa::DecodeParams p;
+  const int rc = decode_params(a, p);
+  return rc != FFA_OK ? rc : launch_stage2(a, p, (hipStream_t)stream);
+}
+
+extern "C" int ffa_q2fp8_decode(const ffa_q2fp8_decode_args *a, void *stream) {
+  ffa::DecodeParams p;
+  int rc = decode_params(a, p);
+  if (rc != FFA_OK) return rc;
+  rc = launch_stage1(a, p, (hipStream_t)stream);
+  return rc != FFA_OK ? rc : launch_stage2(a, p, (hipStream_t)stream);
 }

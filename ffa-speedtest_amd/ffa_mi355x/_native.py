@@ -21,6 +21,8 @@ SCALE_CHANNEL, SCALE_G32 = 0, 1
 EXPORTS = (
     "ffa_q2fp8_decode_nparts",
     "ffa_q2fp8_decode",
+    "ffa_q2fp8_decode_stage1",
+    "ffa_q2fp8_decode_stage2",
     "ffa_q2_quantize_nsplit",
     "ffa_q2_quantize_channel",
     "ffa_kproj_rope_q2_channel",
@@ -107,8 +109,9 @@ def lib() -> ctypes.CDLL:
         L.ffa_version.restype = ctypes.c_char_p
         L.ffa_q2fp8_decode_nparts.argtypes = [ci, ci, ci]
         L.ffa_q2fp8_decode_nparts.restype = ci
-        L.ffa_q2fp8_decode.argtypes = [ctypes.POINTER(DecodeArgs), vp]
-        L.ffa_q2fp8_decode.restype = ci
+        for name in ("ffa_q2fp8_decode", "ffa_q2fp8_decode_stage1", "ffa_q2fp8_decode_stage2"):
+            getattr(L, name).argtypes = [ctypes.POINTER(DecodeArgs), vp]
+            getattr(L, name).restype = ci
         L.ffa_q2_quantize_nsplit.argtypes = [ci]
         L.ffa_q2_quantize_nsplit.restype = ci
         L.ffa_q2_quantize_channel.argtypes = [vp, ci, ci, ci, ci, ci, vp, vp, vp, vp, ci, vp, vp]

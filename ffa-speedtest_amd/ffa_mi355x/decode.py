@@ -15,6 +15,7 @@ import torch
 from . import _native as N
 
 HEAD_DIM = 128
+_STAGE_FN = {"both": "ffa_q2fp8_decode", "stage1": "ffa_q2fp8_decode_stage1", "stage2": "ffa_q2fp8_decode_stage2"}
 
 
 def _cdiv(a: int, b: int) -> int:
@@ -95,8 +96,15 @@ def run_decode(
     block_table=None,
     seq_lens=None,
     workspace: DecodeWorkspace | None = None,
+    stage: str = "both",
 ) -> DecodeWorkspace:
-    """Launch one decode step; returns the workspace holding o / mask / thresholds."""
+    """Launch one decode step; returns the workspace holding o / mask / thresholds.
+
+    stage: "both" (stage 1 + stage 2), or "stage1" / "stage2" alone, the two launches of
+    attn_forward_decode_quantized (attn_kernel...q2fp8.py:283-304).
+    """
+    if stage not in _STAGE_FN:
+        raise ValueError(f"stage must be one of {sorted(_STAGE_FN)}")
     B, HQ, D = q.shape
     if D != HEAD_DIM:
         raise NotImplementedError(f"head_dim {D} is not supported (this build implements {HEAD_DIM})")
@@ -139,8 +147,9 @@ def run_decode(
     a.nparts = workspace.nparts
     a.mask = workspace.mask_buf.data_ptr()
     a.ntbs = workspace.NTBS
-    rc = N.lib().ffa_q2fp8_decode(ctypes.byref(a), ctypes.c_void_p(N.stream_of(q.device)))
-    N.check(rc, "ffa_q2fp8_decode")
+    fn = _STAGE_FN[stage]
+    rc = getattr(N.lib(), fn)(ctypes.byref(a), ctypes.c_void_p(N.stream_of(q.device)))
+    N.check(rc, fn)
     return workspace
 
 

@@ -83,8 +83,12 @@ class PagedQ2Cache:
 
     # ------------------------------------------------------------------ decode
     def decode(self, q, block_table, seq_lens=None, *, T=None, scale=None, BS=64, SBS=None, delta=5.0,
-               precomputed_threshold=None, use_fp8_residual=True, workspace: DecodeWorkspace | None = None):
-        """Pruned decode of q [B, HQ, 128] (or [B, 1, HQ, 128]) over the paged cache."""
+               precomputed_threshold=None, use_fp8_residual=True, workspace: DecodeWorkspace | None = None,
+               stage="both"):
+        """Pruned decode of q [B, HQ, 128] (or [B, 1, HQ, 128]) over the paged cache.
+
+        stage: "both", or "stage1" (scores, prune, exact partials) / "stage2" (merge) alone.
+        """
         if q.ndim == 4:
             if q.shape[1] != 1:
                 raise AssertionError("decode takes one query token per sequence")
@@ -106,4 +110,4 @@ class PagedQ2Cache:
             q=q, k_q=self.k_q, k_scale=self.k_scale, k_zero=self.k_zero, v=self.v, k_residual=self.k_res,
             layout=N.LAYOUT_PAGED, scale_mode=N.SCALE_G32, T=T, HKV=self.HKV, scale=scale, BS=BS, SBS=SBS,
             delta=delta, use_res=use_fp8_residual, precomputed_threshold=precomputed_threshold,
-            block_table=block_table, seq_lens=seq_lens, workspace=workspace)
+            block_table=block_table, seq_lens=seq_lens, workspace=workspace, stage=stage)

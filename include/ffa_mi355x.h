@@ -12,6 +12,10 @@
  *   ffa_q2fp8_decode          ffa-q2fp8/attn_kernel/attn_kernel_v1210_fused_bsz_q2fp8.py:283-304
  *                             (stage-1 launch :283-291 + stage-2 launch :299-304 of
  *                              attn_forward_decode_quantized :191-309)
+ *   ffa_q2fp8_decode_stage1   the stage-1 launch alone (:283-297, kernel
+ *                             attn_forward_stage1_fused_threshold_qbits :10-139)
+ *   ffa_q2fp8_decode_stage2   the stage-2 launch alone (:299-304, kernel
+ *                             attn_forward_stage2_masked :142-171)
  *   ffa_q2_quantize_channel   ffa-q2fp8/run_attn_bench_q2.py:78-105
  *                             (quantize_k_2bit_fp8_residual; same as
  *                              ffa-q2fp8/fused_kproj_rope_q2fp8.py:40-68)
@@ -117,7 +121,13 @@ typedef struct ffa_q2fp8_decode_args {
 /* Number of partial slots per query row the scratch buffers must hold for max length T. */
 int ffa_q2fp8_decode_nparts(int T, int BS, int SBS);
 
+/* Both stages back to back on `stream`. */
 int ffa_q2fp8_decode(const ffa_q2fp8_decode_args *args, void *stream);
+/* Stage 1: coarse scores, threshold, prune (mask, threshold_out) and the exact pass over
+ * kept blocks, writing the partials m_buf/l_buf/o_buf. */
+int ffa_q2fp8_decode_stage1(const ffa_q2fp8_decode_args *args, void *stream);
+/* Stage 2: log-sum-exp merge of the partials into `out` (same arguments as stage 1). */
+int ffa_q2fp8_decode_stage2(const ffa_q2fp8_decode_args *args, void *stream);
 
 /*
  * Reference quantizer (per-channel scale/zero over T, tau = k_dtype):

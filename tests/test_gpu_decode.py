@@ -132,3 +132,20 @@ def test_extreme_deltas(gpu):
     assert ws.mask_buf.sum().item() == ws.mask_buf.numel()
     o_ref, _ = oracle_paged(case, BS=64, delta=math.inf)
     assert_out_close(f32(ws.o), o_ref, "delta=inf")
+
+
+def test_stage1_then_stage2_equals_both(gpu):
+    """The two entry points ffa_q2fp8_decode_stage1 / _stage2 in sequence give the combined call's results."""
+    c = paged_case(B=2, T=1500, HQ=32, HKV=8, seed=11, n_heavy=16, seq_lens=[1500, 900])
+    cache = to_gpu_paged(c, gpu)
+    q, bt = c["q"].to(gpu), c["block_table"].to(gpu)
+    lens = torch.tensor(c["lens"], dtype=torch.int32, device=gpu)
+    ws = cache.decode(q, bt, lens, BS=64, delta=5.0)
+    torch.cuda.synchronize()
+    ref = (ws.o.clone(), ws.mask_buf.clone(), ws.threshold_buf.clone())
+    ws.o.zero_()
+    ws.mask_buf.fill_(-1)
+    cache.decode(q, bt, lens, BS=64, delta=5.0, workspace=ws, stage="stage1")
+    cache.decode(q, bt, lens, BS=64, delta=5.0, workspace=ws, stage="stage2")
+    torch.cuda.synchronize()
+    assert torch.equal(ws.o, ref[0]) and torch.equal(ws.mask_buf, ref[1]) and torch.equal(ws.threshold_buf, ref[2])
