@@ -261,7 +261,7 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
   // caller's threshold of the lane's query row (zeros when none is given)
   const float th_pre = __uint_as_float(
       bload8(make_rsrc(p.th_in + (p.th_in ? (size_t)b * p.HQ : 0), p.th_in ? p.HQ * 4 : 0), hq * 4).x);
-  const int Tb = p.seq_lens ? p.seq_lens[b] : p.T;
+  const int Tb = p.seq_lens ? min(max(p.seq_lens[b], 0), p.T) : p.T;  // lengths beyond T are clamped to T
   const int NTB = (Tb + p.BS - 1) / p.BS;
   const int NTBS_b = NTB * (p.BS / p.SBS);
   const bool do_probe = (p.th_in == nullptr) && wv < 2;
@@ -864,7 +864,7 @@ __global__ __launch_bounds__(256) void q2fp8_merge_kernel(const DecodeParams p) 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wv = tid >> 6;
   const int k0 = tid >> 2, q4 = tid & 3;
-  const int Tb = p.seq_lens ? p.seq_lens[b] : p.T;
+  const int Tb = p.seq_lens ? min(max(p.seq_lens[b], 0), p.T) : p.T;  // lengths beyond T are clamped to T
   const int nparts = min((Tb + kChunksPerWG * kPage - 1) / (kChunksPerWG * kPage), p.nparts);
   const float *mr = p.m_buf + (size_t)row * p.nparts;
   const float *lr = p.l_buf + (size_t)row * p.nparts;

@@ -34,7 +34,7 @@ __all__ = [
 
 class Q2FP8DecodeWorkspace(DecodeWorkspace):
     """Reusable scratch (ffa-q2fp8-h100 ...q2fp8.py:232-257); attributes o, m_buf, l_buf,
-    o_buf, mask_buf, threshold_buf.  Partials are per 64-token chunk here."""
+    o_buf, mask_buf, threshold_buf.  Partials are kept per 512-token span here."""
 
     def __init__(self, B, HQ, HKV, V, T, BS, SBS, device, dtype):
         if V != 128:
@@ -158,7 +158,7 @@ def attn_forward_decode_quantized(
         scale_mode=smode, T=T, HKV=HKV, scale=scale, BS=BS, SBS=SBS, delta=delta, use_res=use_res,
         precomputed_threshold=precomputed_threshold, block_table=block_table, seq_lens=seq_lens,
         workspace=workspace)
-    o = ws.o if workspace is not None else ws.o
+    o = ws.o
 
     if return_skip_ratio:
         mask_buf = ws.mask_buf

@@ -103,7 +103,7 @@ typedef struct ffa_q2fp8_decode_args {
   int layout;
   const int32_t *block_table; /* [B, bt_stride] (paged only) */
   int bt_stride;
-  const int32_t *seq_lens; /* [B] or NULL (all sequences have length T) */
+  const int32_t *seq_lens; /* [B] or NULL (all sequences have length T); clamped to [0, T] */
   int B, T, HQ, HKV;
   float scale;                /* softmax scale (1/sqrt(D) by default) */
   int BS, SBS;                /* threshold block size / prune block size */

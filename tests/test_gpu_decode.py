@@ -149,3 +149,55 @@ def test_stage1_then_stage2_equals_both(gpu):
     cache.decode(q, bt, lens, BS=64, delta=5.0, workspace=ws, stage="stage2")
     torch.cuda.synchronize()
     assert torch.equal(ws.o, ref[0]) and torch.equal(ws.mask_buf, ref[1]) and torch.equal(ws.threshold_buf, ref[2])
+
+
+def test_cudagraph_runner_replays_match_eager(gpu):
+    """CUDAGraphDecodeRunnerQ2FP8: every replay (new inputs, eager work in between) equals an eager call."""
+    import attn_kernel.attn_kernel_v1210_fused_bsz_q2fp8 as K
+    from attn_kernel.attn_kernel_v1210_fused_bsz_q2fp8_cudagraph import CUDAGraphDecodeRunnerQ2FP8
+
+    cases = [to_gpu_contig(contig_case(B=2, T=1024, tau="bf16", res="e5m2", seed=s, n_heavy=8), gpu) for s in (0, 1, 2)]
+    c0 = cases[0]
+    runner = CUDAGraphDecodeRunnerQ2FP8(c0["q"], c0["k_q"], c0["k_scale"], c0["k_zero"], c0["v"],
+                                        k_residual=c0["k_residual"], BS=64, delta=5.0)
+    for rep in range(2):
+        for c in cases:
+            got = runner(c["q"], c["k_q"], c["k_scale"], c["k_zero"], c["v"], k_residual=c["k_residual"]).clone()
+            torch.cuda.synchronize()
+            _ = torch.randn(4096, device=gpu).sum()  # unrelated eager work between replays
+            ref, sr = K.attn_forward_decode_quantized(c["q"], c["k_q"], c["k_scale"], c["k_zero"], c["v"],
+                                                      k_residual=c["k_residual"], BS=64, delta=5.0,
+                                                      return_skip_ratio=True)
+            torch.cuda.synchronize()
+            assert torch.equal(got, ref), f"replay {rep} differs from eager"
+    c = cases[1]
+    out, sr_g = runner(c["q"], c["k_q"], c["k_scale"], c["k_zero"], c["v"], k_residual=c["k_residual"],
+                       return_skip_ratio=True)
+    _, sr_e = K.attn_forward_decode_quantized(c["q"], c["k_q"], c["k_scale"], c["k_zero"], c["v"],
+                                              k_residual=c["k_residual"], BS=64, delta=5.0, return_skip_ratio=True)
+    assert sr_g == sr_e
+    assert torch.equal(runner.replay_only(), out)
+
+
+def test_cudagraph_runner_paged(gpu):
+    """The runner over a paged g32 cache with a page table and ragged lengths (passed through **kwargs)."""
+    import attn_kernel.attn_kernel_v1210_fused_bsz_q2fp8 as K
+    from attn_kernel.attn_kernel_v1210_fused_bsz_q2fp8_cudagraph import CUDAGraphDecodeRunnerQ2FP8
+
+    c = paged_case(B=2, T=1500, HQ=32, HKV=8, seed=21, n_heavy=16, seq_lens=[1500, 700])
+    cache = to_gpu_paged(c, gpu)
+    q = c["q"].to(gpu).unsqueeze(1).contiguous()
+    bt = c["block_table"].to(gpu)
+    lens = torch.tensor(c["lens"], dtype=torch.int32, device=gpu)
+    args = (q, cache.k_q, cache.k_scale, cache.k_zero, cache.v)
+    runner = CUDAGraphDecodeRunnerQ2FP8(*args, k_residual=cache.k_res, BS=64, delta=5.0, block_table=bt,
+                                        seq_lens=lens)
+    for _ in range(3):
+        got = runner(*args, k_residual=cache.k_res).clone()
+        torch.cuda.synchronize()
+        ref = K.attn_forward_decode_quantized(*args, k_residual=cache.k_res, BS=64, delta=5.0, block_table=bt,
+                                              seq_lens=lens)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref)
+    o_ref, _ = oracle_paged(c, BS=64, SBS=64, delta=5.0)
+    assert_out_close(f32(got), o_ref, "paged runner")

@@ -79,3 +79,17 @@ def test_drop_in_rejects_cpu_tensors():
     with pytest.raises(AssertionError):
         K.attn_forward_decode_quantized(q, torch.zeros(1, 8, 1, 32, dtype=torch.uint8), torch.zeros(1, 1, 128),
                                         torch.zeros(1, 1, 128), torch.zeros(1, 8, 1, 128))
+
+
+def test_graph_runner_interface_matches_reference():
+    """CUDAGraphDecodeRunnerQ2FP8 keeps the reference constructor and methods (..._cudagraph.py:19-183)."""
+    from attn_kernel.attn_kernel_v1210_fused_bsz_q2fp8_cudagraph import CUDAGraphDecodeRunnerQ2FP8 as R
+
+    params = inspect.signature(R.__init__).parameters
+    assert list(params)[1:6] == ["q", "k_q", "k_scale", "k_zero", "v"]
+    for name, default in [("k_residual", None), ("precomputed_threshold", None), ("k_bits", 2), ("scale", None),
+                          ("BS", 128), ("SBS", None), ("delta", 5.0), ("use_fp8_residual", True), ("warmup", 2)]:
+        assert params[name].default == default and params[name].kind == inspect.Parameter.KEYWORD_ONLY
+    assert R.__call__ is R.replay and callable(R.replay_only) and isinstance(R.output, property)
+    rp = inspect.signature(R.replay).parameters
+    assert list(rp)[1:6] == ["q", "k_q", "k_scale", "k_zero", "v"] and rp["return_skip_ratio"].default is False
