@@ -133,6 +133,9 @@ __device__ __forceinline__ uint4 bload16(brsrc r, uint32_t off) {
   const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
+__device__ __forceinline__ uint32_t bload4(brsrc r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
 __device__ __forceinline__ uint2 bload8(brsrc r, uint32_t off) {
   const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
   return make_uint2(v[0], v[1]);

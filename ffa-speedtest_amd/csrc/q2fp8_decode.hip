@@ -243,10 +243,29 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
   // ------------------------------------------------ phase 1: loads
   // Every vector load is issued on every path; validity (sequence end, kept or pruned) is
   // the size of the buffer resource, so the compiler waits for one load group at a time.
-  // Groups are issued in the order they are consumed: q window (and channel scales), the
-  // caller's threshold, probe windows, page 0, page 1.
+  // Groups are issued in the order they are consumed: page ids (paged layout), q window (and
+  // channel scales), the caller's threshold, probe windows, page 0, page 1.
   // The q window is channels [32kc + 16h, +16) of the lane's row, h = wave / 2: it holds
   // every element of the operand this wave builds.
+  const int Tb = p.seq_lens ? min(max(p.seq_lens[b], 0), p.T) : p.T;  // lengths beyond T are clamped to T
+  const int NTB = (Tb + p.BS - 1) / p.BS;
+  const int NTBS_b = NTB * (p.BS / p.SBS);
+  const bool do_probe = (p.th_in == nullptr) && wv < 2;
+  const int pa = wv == 0 ? 0 : max(NTB - 1, 0) * 16;  // probe window (attn_kernel...q2fp8.py:58-73)
+  int nv[kPPW];                                       // valid tokens of the wave's chunks
+#pragma unroll
+  for (int j = 0; j < kPPW; ++j) nv[j] = min(max(Tb - (c0 + j) * kPage, 0), kPage);
+
+  int pg[kPPW] = {0, 0};
+  int ppg = 0;
+  uint32_t pg_lane = 0;
+  if constexpr (LAYOUT == kPaged) {
+    // page ids: one vector load per wave, issued first (lanes 0, 1: the wave's chunks, lane 2: its
+    // probe window; the other lanes read past the resource and get 0)
+    const bool need = lane < kPPW ? nv[lane & 1] > 0 : (lane == kPPW && do_probe && pa < Tb);
+    const int idx = lane < kPPW ? c0 + lane : (pa >> 6);
+    pg_lane = bload4(make_rsrc(p.bt + (size_t)b * p.bt_stride, p.bt_stride * 4), need ? idx * 4 : p.bt_stride * 4);
+  }
   const uint32_t es_q = p.q_dtype == 2 ? 4u : 2u;
   const int hwin = wv >> 1;
   Raw16 qraw, sraw, zraw;
@@ -261,23 +280,11 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
   // caller's threshold of the lane's query row (zeros when none is given)
   const float th_pre = __uint_as_float(
       bload8(make_rsrc(p.th_in + (p.th_in ? (size_t)b * p.HQ : 0), p.th_in ? p.HQ * 4 : 0), hq * 4).x);
-  const int Tb = p.seq_lens ? min(max(p.seq_lens[b], 0), p.T) : p.T;  // lengths beyond T are clamped to T
-  const int NTB = (Tb + p.BS - 1) / p.BS;
-  const int NTBS_b = NTB * (p.BS / p.SBS);
-  const bool do_probe = (p.th_in == nullptr) && wv < 2;
-  const int pa = wv == 0 ? 0 : max(NTB - 1, 0) * 16;  // probe window (attn_kernel...q2fp8.py:58-73)
-  int nv[kPPW];                                       // valid tokens of the wave's chunks
-#pragma unroll
-  for (int j = 0; j < kPPW; ++j) nv[j] = min(max(Tb - (c0 + j) * kPage, 0), kPage);
-
-  int pg[kPPW] = {0, 0};
-  int ppg = 0;
   if constexpr (LAYOUT == kPaged) {
-    const int32_t *btr = p.bt + (size_t)b * p.bt_stride;
+    __builtin_amdgcn_sched_barrier(0);  // the q loads go out before the wait for the page ids
 #pragma unroll
-    for (int j = 0; j < kPPW; ++j)
-      if (nv[j] > 0) pg[j] = btr[c0 + j];
-    if (do_probe && pa < Tb) ppg = btr[pa >> 6];
+    for (int j = 0; j < kPPW; ++j) pg[j] = __builtin_amdgcn_readlane(pg_lane, j);
+    ppg = __builtin_amdgcn_readlane(pg_lane, kPPW);
   }
   // probe tile: MFMA row m <-> token pa + 4(m & 3) + (m >> 2), so that the output rows
   // 4kc + u hold tokens pa + 4u + kc, whose g32 scales are contiguous (scale_pos)
@@ -858,42 +865,37 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
 // (+64 r) and a 32-column quarter.  m, l and the first 64 partials' o are
 // loaded in one batch; the weighted sums are reduced in a fixed order in LDS.
 // --------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void q2fp8_merge_kernel(const DecodeParams p) {
-  const int row = blockIdx.x;  // b * HQ + hq
+__global__ __launch_bounds__(64) void q2fp8_merge_kernel(const DecodeParams p) {
+  // one wave per (sequence, query head, 32-column slab): lane k owns partials k, k + 64, ...
+  const int row = blockIdx.x >> 2;  // b * HQ + hq
+  const int slab = blockIdx.x & 3;
   const int b = row / p.HQ;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wv = tid >> 6;
-  const int k0 = tid >> 2, q4 = tid & 3;
+  const int lane = threadIdx.x;
   const int Tb = p.seq_lens ? min(max(p.seq_lens[b], 0), p.T) : p.T;  // lengths beyond T are clamped to T
   const int nparts = min((Tb + kChunksPerWG * kPage - 1) / (kChunksPerWG * kPage), p.nparts);
   const float *mr = p.m_buf + (size_t)row * p.nparts;
   const float *lr = p.l_buf + (size_t)row * p.nparts;
-  const float *orow = p.o_buf + (size_t)row * p.nparts * 128;
-  __shared__ float s_red[4];
-  __shared__ float s_o[64][129];
-  __shared__ float s_half[2][128];
+  const float *orow = p.o_buf + (size_t)row * p.nparts * 128 + 32 * slab;
+  __shared__ float s_o[64][33];
 
-  // batch 0: m, l and o of partial k0 (o selected by l > 0, so stale slots are never used)
+  // first partial of the lane: m, l and its 32 columns in one batch of loads (o is used only
+  // where l > 0, so slots of empty spans are never read as data)
   float m0 = -INFINITY, l0 = 0.f;
   float4 o0[8];
-  if (k0 < nparts) {
-    m0 = mr[k0];
-    l0 = lr[k0];
-    const float4 *op = (const float4 *)(orow + (size_t)k0 * 128 + 32 * q4);
+  if (lane < nparts) {
+    m0 = mr[lane];
+    l0 = lr[lane];
+    const float4 *op = (const float4 *)(orow + (size_t)lane * 128);
 #pragma unroll
     for (int e = 0; e < 8; ++e) o0[e] = op[e];
   }
   float M = l0 > 0.f ? m0 : -INFINITY;
-  for (int k = k0 + 64; k < nparts; k += 64)
+  for (int k = lane + 64; k < nparts; k += 64)
     if (lr[k] > 0.f) M = fmaxf(M, mr[k]);
   for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
-  if (lane == 0) s_red[wv] = M;
-  __syncthreads();
-  M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-  __syncthreads();
 
-  float A = 0.f;
   float acc[32];
+  float A;
   {
     const bool keep = l0 > 0.f;
     const float wgt = keep ? exp2f(m0 - M) : 0.f;
@@ -906,12 +908,12 @@ __global__ __launch_bounds__(256) void q2fp8_merge_kernel(const DecodeParams p) 
       acc[4 * e + 3] = keep ? o0[e].w * wgt : 0.f;
     }
   }
-  for (int k = k0 + 64; k < nparts; k += 64) {
+  for (int k = lane + 64; k < nparts; k += 64) {
     const float l = lr[k];
     if (l > 0.f) {
       const float wgt = exp2f(mr[k] - M);
       A = __builtin_fmaf(l, wgt, A);
-      const float4 *op = (const float4 *)(orow + (size_t)k * 128 + 32 * q4);
+      const float4 *op = (const float4 *)(orow + (size_t)k * 128);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float4 v = op[e];
@@ -922,26 +924,21 @@ __global__ __launch_bounds__(256) void q2fp8_merge_kernel(const DecodeParams p) 
       }
     }
   }
-  // A: one count per partial (quarter 0 threads)
-  float a = q4 == 0 ? A : 0.f;
-  for (int o = 32; o >= 1; o >>= 1) a += __shfl_xor(a, o);
-  if (lane == 0) s_red[wv] = a;
+  for (int o = 32; o >= 1; o >>= 1) A += __shfl_xor(A, o);
+  // column sums over the 64 lanes through LDS: lane c < 32 sums column c of lanes 0..31,
+  // lane 32 + c of lanes 32..63
 #pragma unroll
-  for (int e = 0; e < 32; ++e) s_o[k0][32 * q4 + e] = acc[e];
-  __syncthreads();
-  const float Atot = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
-  {
-    const int c = tid & 127, h = tid >> 7;
-    float s = 0.f;
+  for (int e = 0; e < 32; ++e) s_o[lane][e] = acc[e];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  const int c = lane & 31, h = lane >> 5;
+  float sum = 0.f;
 #pragma unroll 8
-    for (int k = 32 * h; k < 32 * h + 32; ++k) s += s_o[k][c];
-    s_half[h][c] = s;
-  }
-  __syncthreads();
-  if (tid < 128) {
-    const float o = s_half[0][tid] + s_half[1][tid];
-    store_any(p.out, (size_t)row * 128 + tid, p.out_dtype, Atot == 0.f ? 0.f : o / Atot);
-  }
+  for (int k = 32 * h; k < 32 * h + 32; ++k) sum += s_o[k][c];
+  sum += __shfl_xor(sum, 32);
+  if (lane < 32)
+    store_any(p.out, (size_t)row * 128 + 32 * slab + c, p.out_dtype, A == 0.f ? 0.f : sum / A);
 }
 
 }  // namespace ffa
@@ -1067,7 +1064,7 @@ static int launch_stage1(const ffa_q2fp8_decode_args *a, const ffa::DecodeParams
 }
 
 static int launch_stage2(const ffa_q2fp8_decode_args *a, const ffa::DecodeParams &p, hipStream_t st) {
-  hipLaunchKernelGGL(ffa::q2fp8_merge_kernel, dim3(a->B * a->HQ), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(ffa::q2fp8_merge_kernel, dim3(a->B * a->HQ * 4), dim3(64), 0, st, p);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_err(FFA_E_LAUNCH, hipGetErrorString(e));
   return FFA_OK;
