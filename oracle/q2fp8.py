@@ -209,8 +209,15 @@ def decode(
     seq_lens=None,
     out_dtype: str = "fp16",
     force_mask=None,
+    khat=None,
+    khat_probe1=None,
 ):
     """Appendix-A decode semantics over the contiguous layout.
+
+    khat [B,T,HKV,D] (optional) replaces the 2-bit dequantization with another format's
+    fp16 K (the other formats share the decode, oracle/formats.py); khat_probe1 (optional)
+    is the K used for the second probe window (nvfp4 takes the last block's scale there).
+    With khat, the refined K is fp16(khat + fp16(res)) as in per_channel mode.
 
     q [B,HQ,D]; k_q [B,T,HKV,ceil(D/4)] u8; k_scale/k_zero per_channel
     [B,HKV,D] or g32 [B,T,HKV,D/32]; v [B,T,HKV,DV]; k_residual [B,T,HKV,D]
@@ -257,18 +264,21 @@ def decode(
         blocks_total += HKV * NTBS
         w0, w1 = _probe_windows(Tb, NTB)
         for h in range(HKV):
-            if scale_mode == "per_channel":
-                khat = dequant(k_q[b:b + 1, :Tb, h:h + 1], k_scale[b:b + 1, h:h + 1], k_zero[b:b + 1, h:h + 1], D,
-                               "per_channel")[0, :, 0]
+            if khat is not None:
+                kh = np.asarray(khat[b, :Tb, h], F32)
+            elif scale_mode == "per_channel":
+                kh = dequant(k_q[b:b + 1, :Tb, h:h + 1], k_scale[b:b + 1, h:h + 1], k_zero[b:b + 1, h:h + 1], D,
+                             "per_channel")[0, :, 0]
             else:
-                khat = dequant(k_q[b, :Tb, h], k_scale[b, :Tb, h], k_zero[b, :Tb, h], D, "g32")
+                kh = dequant(k_q[b, :Tb, h], k_scale[b, :Tb, h], k_zero[b, :Tb, h], D, "g32")
             q16 = round_f16(q[b, h * G:(h + 1) * G])  # [G, D]  (:47)
-            Sq = _score(q16, khat, scale)  # [Tb, G] (:94)
+            Sq = _score(q16, kh, scale)  # [Tb, G] (:94)
             if precomputed_threshold is not None:
                 th = np.asarray(precomputed_threshold, F32)[b, h * G:(h + 1) * G]
             else:
+                Sp1 = Sq if khat_probe1 is None else _score(q16, np.asarray(khat_probe1[b, :Tb, h], F32), scale)
                 m0 = Sq[w0].max(axis=0) if len(w0) else np.full(G, -np.inf, F32)
-                m1 = Sq[w1].max(axis=0) if len(w1) else np.full(G, -np.inf, F32)
+                m1 = Sp1[w1].max(axis=0) if len(w1) else np.full(G, -np.inf, F32)
                 th = (np.maximum(m0, m1) - F32(delta)).astype(F32)  # :82
             thr[b, h * G:(h + 1) * G] = th
             Sb = np.where(valid[:, :, None], Sq[idx], -np.inf)  # [NTBS, SBS, G]
@@ -285,10 +295,10 @@ def decode(
                 continue
             if use_res:
                 r16 = fp8_decode(k_residual[b, :Tb, h], res_fmt)  # exact in fp16
-                if scale_mode == "per_channel":
-                    ktil = round_f16(khat + r16)  # (:109-115)
+                if khat is not None or scale_mode == "per_channel":
+                    ktil = round_f16(kh + r16)  # (:109-115)
                 else:
-                    ktil = khat + r16.astype(np.float64)  # g32: exact
+                    ktil = kh + r16.astype(np.float64)  # g32: exact
                 S = _score(q16, ktil, scale)
             else:
                 S = Sq
