@@ -1,0 +1,644 @@
+// Pruned decode attention for the other K formats of the reference, on gfx950:
+//   fp8 base + fp8 residual   ffa-fp8fp8/attn_kernel/attn_kernel_v1210_fused_bsz_fp8fp8.py:10-136
+//   nvfp4 (e2m1 x block scale) ffa-nvfp4fp8/attn_kernel/attn_kernel_v1210_fused_bsz_nvfp4fp8.py:10-169
+//   nf4 (codebook x channel)  ffa-nf4fp8/attn_kernel/attn_kernel_v1210_fused_bsz_nf4fp8.py:41-167
+// and the BASELINE config-1 variant of the fp8 base with one fp16 scale per token and KV head.
+//
+// Every format dequantizes to the fp16 K the reference feeds its dot products,
+// k_hat = fp16(f32(value) * f32(scale)), and then follows the q2fp8 path: the probe
+// threshold (nvfp4 scores its second probe window with the scale of block NTB-1,
+// :96-97), group prune, refined K fp16(k_hat + fp16(res)), exp2 softmax, P.V, and the
+// shared log-sum-exp merge kernel.  Contiguous token-major layouts as in the reference
+// ([B, T, HKV, row]); one workgroup = 4 waves = 8 chunks of 64 tokens of one
+// (sequence, KV head), the partial layout of the q2fp8 kernel.
+//
+// MFMA layout (as the q2fp8 kernel's per-channel mode): rows of a 16x16x32 f16 MFMA are
+// tokens (row m of tile tau = token 4m + tau), the lane of k-chunk kc holds channels
+// [32kc, 32kc + 32) of its token, and MFMA m' takes channels 32kc + 8m' + e; the q operand
+// of column (group j, query row i) is nonzero only for kc == j, so the four groups come out
+// in separate columns and are summed with DPP row rotations.
+#include "decode_common.h"
+#include "ffa_mi355x.h"
+
+#include <type_traits>
+
+extern "C" int ffa_set_error_internal(int code, const char *msg);
+
+namespace ffa {
+
+enum { kF8E4M3 = 0, kF8E5M2 = 1, kFP4 = 2, kNF4 = 3 };
+enum { kSclNone = 0, kSclToken = 1, kSclBlock = 2, kSclChannel = 3 };
+
+// QLoRA NF4 levels (the published 16 normal-float values), as fp32
+__constant__ float kNF4Levels[16] = {
+    -1.0f, -0.6961928009986877f, -0.5229921340942383f, -0.39491748809814453f, -0.28444138169288635f,
+    -0.18477343022823334f, -0.09105003625154495f, 0.0f, 0.07958029955625534f, 0.16093020141124725f,
+    0.24611230194568634f, 0.33791524171829224f, 0.44070982933044434f, 0.5626170039176941f,
+    0.7229568362236023f, 1.0f};
+
+// two fp8 values (bytes 2*HI, 2*HI+1 of w) -> f32, exact
+template <bool E4M3, bool HI>
+__device__ __forceinline__ f32x2 fp8pair_f32(uint32_t w) {
+  if constexpr (E4M3) return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, 1.0f, HI);
+  else return __builtin_amdgcn_cvt_scalef32_pk_f32_bf8(w, 1.0f, HI);
+}
+
+__device__ __forceinline__ uint32_t pack_f16(float a, float b) {  // two RNE conversions
+  return f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16);
+}
+
+// one scale value of a float tensor of dtype dt (0=f16, 1=bf16, 2=f32) at element index i
+__device__ __forceinline__ float load_scale(brsrc rs, uint32_t i, int dt) {
+  const uint32_t es = dt == 2 ? 4u : 2u;
+  const uint32_t off = i * es;
+  const uint32_t w = bload4(rs, off & ~3u);
+  const uint32_t bits = dt == 2 ? w : ((off & 2u) ? (w >> 16) : (w & 0xffffu));
+  return dt == 2 ? __uint_as_float(bits) : (dt == 1 ? bf16_bits_to_f32(bits) : f16_bits_to_f32(bits));
+}
+
+template <int FMT, int SCL, int RES, int VT>
+__global__ __launch_bounds__(256) void kfmt_decode_kernel(const DecodeParams p) {
+  typedef VTraits<VT> VTr;
+  constexpr bool k4 = FMT == kFP4 || FMT == kNF4;
+  constexpr int kRow = k4 ? 64 : 128;  // K bytes of one token and KV head
+  constexpr int kLane = kRow / 4;      // bytes of one lane's 32 channels
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int u = blockIdx.x / p.nwg;
+  const int cg = blockIdx.x - u * p.nwg;  // workgroup index along the sequence = partial slot
+  const int b = u / p.HKV;
+  const int hkv = u - b * p.HKV;
+  const int G = p.G;
+  const int cw = cg * kChunksPerWG;
+  const int c0 = cw + wv * kPPW;
+  const int SBS = p.SBS;
+
+  const int mrow = lane & 15;
+  const int kc = lane >> 4;
+  const int n = mrow;
+  const int jg = n >> 2;
+  const int ir = n & 3;
+  const bool row_ok = ir < G;
+  const int hq = hkv * G + (row_ok ? ir : 0);
+
+  __shared__ uint4 s_qa[4][64];
+  __shared__ float s_probe[2][4];
+  __shared__ float s_wmax[kWaves][4];
+  __shared__ uint32_t s_bal[kChunksPerWG][2];
+  __shared__ float s_pm[kChunksPerWG][4], s_pl[kChunksPerWG][4];
+  __shared__ float s_po[kChunksPerWG][4][128];
+  __shared__ float s_cb[16];
+  __shared__ uint8_t s_vstage[kWaves * kPage * kVRow];
+
+  auto lds_barrier = []() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+
+  // ------------------------------------------------ phase 1: loads (issued on every path)
+  const int Tb = p.seq_lens ? min(max(p.seq_lens[b], 0), p.T) : p.T;  // lengths beyond T are clamped to T
+  const int NTB = (Tb + p.BS - 1) / p.BS;
+  const int NTBS_b = NTB * (p.BS / p.SBS);
+  const int NTBk = (p.T + p.BS - 1) / p.BS;  // blocks of the block-scale tensor
+  const bool do_probe = (p.th_in == nullptr) && wv < 2;
+  const int pa = wv == 0 ? 0 : max(NTB - 1, 0) * 16;  // probe window (attn_kernel...q2fp8.py:58-73)
+  int nv[kPPW];
+#pragma unroll
+  for (int j = 0; j < kPPW; ++j) nv[j] = min(max(Tb - (c0 + j) * kPage, 0), kPage);
+
+  const uint32_t es_q = p.q_dtype == 2 ? 4u : 2u;
+  const int hwin = wv >> 1;
+  Raw16 qraw;
+  raw16_load(qraw, make_rsrc((const char *)p.q + (size_t)b * p.HQ * kD * es_q, p.HQ * kD * es_q),
+             (hq * kD + 32 * kc + 16 * hwin) * es_q);
+  const float th_pre = __uint_as_float(
+      bload8(make_rsrc(p.th_in + (p.th_in ? (size_t)b * p.HQ : 0), p.th_in ? p.HQ * 4 : 0), hq * 4).x);
+  // per-channel scales of the lane's 32 channels (nf4): eight 16-byte loads whatever the dtype
+  float sch[32];
+  if constexpr (SCL == kSclChannel) {
+    const uint32_t es = p.s_dtype == 2 ? 4u : 2u;
+    const brsrc rs = make_rsrc((const char *)p.ks + ((size_t)b * p.HKV + hkv) * kD * es, kD * es);
+    uint4 raw[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) raw[i] = bload16(rs, 32 * kc * es + 16 * i);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t w[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (p.s_dtype == 2) {
+          sch[4 * i + k] = __uint_as_float(w[k]);
+        } else if (i < 4) {
+          const uint32_t lo = w[k] & 0xffffu, hi = w[k] >> 16;
+          sch[8 * i + 2 * k] = p.s_dtype == 1 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
+          sch[8 * i + 2 * k + 1] = p.s_dtype == 1 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
+        }
+      }
+    }
+  }
+  const brsrc rsc = make_rsrc(p.ks, SCL == kSclToken ? (uint32_t)(p.B * p.T * p.HKV) * (p.s_dtype == 2 ? 4u : 2u)
+                                   : SCL == kSclBlock ? (uint32_t)(p.B * NTBk * p.HKV) * (p.s_dtype == 2 ? 4u : 2u)
+                                                      : 0u);
+  // scale of token t for the token / block modes
+  auto tok_scale = [&](int t, int blk) -> float {
+    if constexpr (SCL == kSclToken) return load_scale(rsc, ((uint32_t)b * p.T + (uint32_t)min(t, p.T - 1)) * p.HKV + hkv, p.s_dtype);
+    else if constexpr (SCL == kSclBlock) return load_scale(rsc, ((uint32_t)b * NTBk + (uint32_t)blk) * p.HKV + hkv, p.s_dtype);
+    else return 1.f;
+  };
+  // probe tile: MFMA row m <-> token pa + m
+  uint4 pxa, pxb = make_uint4(0, 0, 0, 0);
+  float psc;
+  {
+    const bool pv = do_probe && pa < Tb;
+    const int nt = pv ? min(16, Tb - pa) : 0;
+    const brsrc rc = make_rsrc(p.kq + (((size_t)b * p.T + pa) * p.HKV + hkv) * kRow, nt > 0 ? ((nt - 1) * p.HKV + 1) * kRow : 0);
+    const uint32_t off = mrow * p.HKV * kRow + kLane * kc;
+    pxa = bload16(rc, off);
+    if constexpr (!k4) pxb = bload16(rc, off + 16);
+    // nvfp4: window 0 uses block 0's scale, window 1 block NTB-1's (attn_kernel...nvfp4fp8.py:86-97)
+    psc = tok_scale(pa + mrow, wv == 0 ? 0 : max(NTB - 1, 0));
+  }
+  uint4 xa[kPPW][4], xb[kPPW][4];
+  float xs[kPPW][4];
+#pragma unroll
+  for (int j = 0; j < kPPW; ++j) {
+    const int t0 = (c0 + j) * kPage;
+    const brsrc rc = make_rsrc(p.kq + (((size_t)b * p.T + t0) * p.HKV + hkv) * kRow,
+                               nv[j] > 0 ? ((nv[j] - 1) * p.HKV + 1) * kRow : 0);
+#pragma unroll
+    for (int tau = 0; tau < 4; ++tau) {
+      const uint32_t off = (4 * mrow + tau) * p.HKV * kRow + kLane * kc;
+      xa[j][tau] = bload16(rc, off);
+      xb[j][tau] = make_uint4(0, 0, 0, 0);
+      if constexpr (!k4) xb[j][tau] = bload16(rc, off + 16);
+      const int t = t0 + 4 * mrow + tau;
+      xs[j][tau] = tok_scale(t, min(t, max(Tb - 1, 0)) / p.BS);
+    }
+  }
+  if constexpr (FMT == kNF4) {
+    if (threadIdx.x < 16) s_cb[threadIdx.x] = kNF4Levels[threadIdx.x];
+  }
+
+  // ------------------------------------------------ phase 2a: q operands (one per wave)
+  auto build_operands = [&](auto W) {
+    constexpr int w = decltype(W)::value;
+    constexpr int s = w & 1;
+    float qv[16];  // channels 32kc + 16h + (0..15)
+    raw16_to_f32(qraw, p.q_dtype, qv);
+    u32x4 a4;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      const float e0 = (row_ok && kc == jg) ? (float)(_Float16)qv[8 * s + 2 * qq] : 0.f;
+      const float e1 = (row_ok && kc == jg) ? (float)(_Float16)qv[8 * s + 2 * qq + 1] : 0.f;
+      a4[qq] = f32_to_f16_bits(e0) | (f32_to_f16_bits(e1) << 16);
+    }
+    s_qa[w][lane] = make_uint4(a4[0], a4[1], a4[2], a4[3]);
+  };
+  switch (wv) {
+    case 0: build_operands(std::integral_constant<int, 0>()); break;
+    case 1: build_operands(std::integral_constant<int, 1>()); break;
+    case 2: build_operands(std::integral_constant<int, 2>()); break;
+    default: build_operands(std::integral_constant<int, 3>()); break;
+  }
+  lds_barrier();
+  f16x8 qa[4];
+#pragma unroll
+  for (int mp = 0; mp < 4; ++mp) {
+    const uint4 a = s_qa[mp][lane];
+    qa[mp] = __builtin_bit_cast(f16x8, u32x4{a.x, a.y, a.z, a.w});
+  }
+
+  // fp16 K of MFMA m' (channels 32kc + 8m' + e) from the lane's row bytes
+  auto dequant = [&](const uint4 &a, const uint4 &bq, int mp, float sc) -> f16x8 {
+    u32x4 r;
+    if constexpr (!k4) {
+      const uint4 &src = mp < 2 ? a : bq;
+      const uint32_t lo = (mp & 1) ? src.z : src.x, hi = (mp & 1) ? src.w : src.y;
+      if constexpr (SCL == kSclNone) {
+        return fp8x8_to_f16x8<FMT == kF8E4M3 ? kResE4M3 : kResE5M2>(lo, hi);
+      } else {
+        const f32x2 v0 = fp8pair_f32<FMT == kF8E4M3, false>(lo), v1 = fp8pair_f32<FMT == kF8E4M3, true>(lo);
+        const f32x2 v2 = fp8pair_f32<FMT == kF8E4M3, false>(hi), v3 = fp8pair_f32<FMT == kF8E4M3, true>(hi);
+        r[0] = pack_f16(v0[0] * sc, v0[1] * sc);
+        r[1] = pack_f16(v1[0] * sc, v1[1] * sc);
+        r[2] = pack_f16(v2[0] * sc, v2[1] * sc);
+        r[3] = pack_f16(v3[0] * sc, v3[1] * sc);
+      }
+    } else {
+      const uint32_t w = mp == 0 ? a.x : mp == 1 ? a.y : mp == 2 ? a.z : a.w;
+      if constexpr (FMT == kFP4) {
+        // e2m1 pairs of each byte (low nibble first), exact in f32, times the scale, RNE to fp16
+        const f32x2 v0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 0);
+        const f32x2 v1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 1);
+        const f32x2 v2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 2);
+        const f32x2 v3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 3);
+        r[0] = pack_f16(v0[0] * sc, v0[1] * sc);
+        r[1] = pack_f16(v1[0] * sc, v1[1] * sc);
+        r[2] = pack_f16(v2[0] * sc, v2[1] * sc);
+        r[3] = pack_f16(v3[0] * sc, v3[1] * sc);
+      }
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        if constexpr (FMT == kNF4) {
+          const uint32_t byte = (w >> (8 * h)) & 0xffu;
+          const float v0 = s_cb[byte & 15u] * sch[8 * mp + 2 * h];
+          const float v1 = s_cb[byte >> 4] * sch[8 * mp + 2 * h + 1];
+          r[h] = pack_f16(v0, v1);
+        }
+      }
+    }
+    return __builtin_bit_cast(f16x8, r);
+  };
+  // dot products of one 16-token tile with the lane's column, summed over the four groups
+  auto score_tile = [&](const uint4 &a, const uint4 &bq, float sc, float *out) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int mp = 0; mp < 4; ++mp) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant(a, bq, mp, sc), qa[mp], acc, 0, 0, 0);
+#pragma unroll
+    for (int uu = 0; uu < 4; ++uu) {
+      float r = acc[uu];
+      r += dpp<kRowRor4>(r);
+      r += dpp<kRowRor8>(r);
+      out[uu] = r;
+    }
+  };
+  const float cs1 = p.scale;
+
+  // ------------------------------------------------ phase 2b: probe, scores, prune
+  float R[kPPW][16];
+  uint64_t bal[kPPW] = {0, 0};
+  float th = INFINITY;
+  if (do_probe) {
+    float r4[4];
+    score_tile(pxa, pxb, psc, r4);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int uu = 0; uu < 4; ++uu) {
+      const int t = pa + 4 * kc + uu;  // output row 4kc + uu
+      mx = fmaxf(mx, t < Tb ? (r4[uu] * cs1) * kLog2e : -INFINITY);
+    }
+    mx = xor_max(mx, 16);
+    mx = xor_max(mx, 32);
+    if (lane < 4) s_probe[wv][lane] = mx;
+  }
+  // R[j][k] = raw score of token (c0+j)*64 + 16kc + k (k = 4u + tau)
+  auto score_page = [&](auto J) {
+    constexpr int j = decltype(J)::value;
+    const int t0 = (c0 + j) * kPage;
+    if (t0 < Tb) {
+#pragma unroll
+      for (int tau = 0; tau < 4; ++tau) {
+        float r4[4];
+        score_tile(xa[j][tau], xb[j][tau], xs[j][tau], r4);
+#pragma unroll
+        for (int uu = 0; uu < 4; ++uu) R[j][4 * uu + tau] = r4[uu];
+      }
+      if (t0 + kPage > Tb) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+          if (t0 + 16 * kc + k >= Tb) R[j][k] = -INFINITY;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) R[j][k] = -INFINITY;
+    }
+  };
+  auto lane_max = [&](int j) -> float {
+    float m = R[j][0];
+#pragma unroll
+    for (int k = 1; k < 16; ++k) m = fmaxf(m, R[j][k]);
+    return (m * cs1) * kLog2e;
+  };
+  score_page(std::integral_constant<int, 0>());
+  score_page(std::integral_constant<int, 1>());
+  float mb[kPPW] = {lane_max(0), lane_max(1)};
+  if (SBS >= 32) {
+    mb[0] = xor_max(mb[0], 16);
+    mb[1] = xor_max(mb[1], 16);
+  }
+  if (SBS >= 64) {
+    mb[0] = xor_max(mb[0], 32);
+    mb[1] = xor_max(mb[1], 32);
+  }
+  if (SBS >= 128) mb[0] = mb[1] = fmaxf(mb[0], mb[1]);
+  if (SBS > 128 && lane < 4) s_wmax[wv][lane] = mb[0];
+  lds_barrier();  // probe maxima (and per-wave block maxima)
+  if (p.th_in != nullptr) th = row_ok ? th_pre : INFINITY;
+  else th = row_ok ? fmaxf(s_probe[0][ir], s_probe[1][ir]) - p.delta : INFINITY;
+  if (SBS > 128) {
+    const int wpb = SBS / (kPage * kPPW);
+    const int w0 = (wv / wpb) * wpb;
+    float m2 = -INFINITY;
+    for (int w = w0; w < w0 + wpb; ++w) m2 = fmaxf(m2, s_wmax[w][ir]);
+    mb[0] = mb[1] = m2;
+  }
+  // prune iff every row of the group is below its threshold (strict <); rows >= G do not vote
+#pragma unroll
+  for (int j = 0; j < kPPW; ++j) {
+    bal[j] = __ballot(row_ok && !(mb[j] < th));
+    const int slot = wv * kPPW + j;
+    if (lane == 0) {
+      s_bal[slot][0] = (uint32_t)bal[j];
+      s_bal[slot][1] = (uint32_t)(bal[j] >> 32);
+    }
+  }
+
+  // ------------------------------------------------ phase 3: exact pass over this wave's kept chunks
+  auto exact_chunk = [&](auto J) {
+    constexpr int j = decltype(J)::value;
+    const int slot = wv * kPPW + j;
+    const int t0 = (c0 + j) * kPage;
+    const int nvs = min(Tb - t0, kPage);
+    const uint64_t bl = bal[j];
+    const bool keep16 = SBS == 16   ? ((bl >> (16 * kc)) & 0xffffull) != 0
+                        : SBS == 32 ? ((bl >> (32 * (kc >> 1))) & 0xffffffffull) != 0
+                                    : bl != 0;
+    uint4 rr[4][2];
+    uint4 vv[8][2];
+    if constexpr (RES != kResNone) {
+      const brsrc rs = make_rsrc(p.kr + (((size_t)b * p.T + t0) * p.HKV + hkv) * kD, ((nvs - 1) * p.HKV + 1) * kD);
+#pragma unroll
+      for (int tau = 0; tau < 4; ++tau) {
+        const uint32_t off = (4 * mrow + tau) * p.HKV * kD + 32 * kc;
+        rr[tau][0] = bload16(rs, off);
+        rr[tau][1] = bload16(rs, off + 16);
+      }
+    }
+    {
+      const brsrc vs = make_rsrc((const uint16_t *)p.v + (((size_t)b * p.T + t0) * p.HKV + hkv) * kD,
+                                 ((nvs - 1) * p.HKV + 1) * kD * 2);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int idx = r * 64 + lane;
+        const int tk = idx >> 4, vc = idx & 15;
+        vv[r >> 1][r & 1] = bload16(vs, tk * p.HKV * kD * 2 + 16 * vc);
+      }
+    }
+    float Rj[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) Rj[k] = R[j][k];
+    if constexpr (RES != kResNone) {
+      // reference: k_tilde = fp16(k_hat + fp16(res)), full re-score (attn_kernel...fp8fp8.py:109-116)
+#pragma unroll
+      for (int tau = 0; tau < 4; ++tau) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int mp = 0; mp < 4; ++mp) {
+          const uint4 &rs4 = rr[tau][mp >> 1];
+          const uint32_t lo = (mp & 1) ? rs4.z : rs4.x, hi = (mp & 1) ? rs4.w : rs4.y;
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              add_f16x8(dequant(xa[j][tau], xb[j][tau], mp, xs[j][tau]), fp8x8_to_f16x8<RES>(lo, hi)), qa[mp], acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int uu = 0; uu < 4; ++uu) {
+          float r = acc[uu];
+          r += dpp<kRowRor4>(r);
+          r += dpp<kRowRor8>(r);
+          Rj[4 * uu + tau] = r;
+        }
+      }
+    }
+    float P[16];
+    float mrow_max = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int t = t0 + 16 * kc + k;
+      const bool act = row_ok && t < Tb && keep16;
+      P[k] = act ? (Rj[k] * cs1) * kLog2e : -INFINITY;
+      mrow_max = fmaxf(mrow_max, P[k]);
+    }
+    mrow_max = xor_max(mrow_max, 16);
+    mrow_max = xor_max(mrow_max, 32);
+    float lsum = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const float e = (P[k] == -INFINITY) ? 0.f : exp2f(P[k] - mrow_max);
+      P[k] = e;
+      lsum += e;
+    }
+    lsum = xor_sum(lsum, 16);
+    lsum = xor_sum(lsum, 32);
+    typename VTr::vec pa2[2];
+#pragma unroll
+    for (int kap = 0; kap < 2; ++kap) {
+      u32x4 w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[e] = VTr::pack2(P[8 * kap + 2 * e], P[8 * kap + 2 * e + 1]);
+      pa2[kap] = __builtin_bit_cast(typename VTr::vec, w);
+    }
+    f32x4 oacc[8];
+#pragma unroll
+    for (int nu = 0; nu < 8; ++nu) oacc[nu] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // stage the V tile [64 tokens][128] through LDS (rows past the sequence end were loaded as zeros)
+    uint8_t *st = s_vstage + wv * kPage * kVRow;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int idx = r * 64 + lane;
+      const int tk = idx >> 4, vc = idx & 15;
+      const uint4 v4 = vv[r >> 1][r & 1];
+      uint32_t *d = (uint32_t *)(st + tk * kVRow + 16 * vc);
+      d[0] = v4.x;
+      d[1] = v4.y;
+      d[2] = v4.z;
+      d[3] = v4.w;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int nu = 0; nu < 8; ++nu) {
+#pragma unroll
+      for (int kap = 0; kap < 2; ++kap) {
+        const int vcol = 16 * nu + n;
+        const int tk = 16 * kc + 8 * kap;
+        u32x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t lo = *(const uint16_t *)(st + (tk + 2 * e) * kVRow + 2 * vcol);
+          const uint32_t hi = *(const uint16_t *)(st + (tk + 2 * e + 1) * kVRow + 2 * vcol);
+          w[e] = lo | (hi << 16);
+        }
+        oacc[nu] = VTr::mfma(pa2[kap], __builtin_bit_cast(typename VTr::vec, w), oacc[nu]);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < 16) {
+#pragma unroll
+      for (int uu = 0; uu < 4; ++uu)
+#pragma unroll
+        for (int nu = 0; nu < 8; ++nu) s_po[slot][uu][16 * nu + n] = oacc[nu][uu];
+    }
+    if (lane < 4) {
+      s_pm[slot][lane] = row_ok ? mrow_max : -INFINITY;
+      s_pl[slot][lane] = row_ok ? lsum : 0.f;
+    }
+  };
+  auto empty_chunk = [&](int slot) {
+    if (lane < 4) {
+      s_pm[slot][lane] = -INFINITY;
+      s_pl[slot][lane] = 0.f;
+    }
+  };
+  if ((c0 + 0) * kPage < Tb && bal[0] != 0) exact_chunk(std::integral_constant<int, 0>());
+  else empty_chunk(wv * kPPW);
+  if ((c0 + 1) * kPage < Tb && bal[1] != 0) exact_chunk(std::integral_constant<int, 1>());
+  else empty_chunk(wv * kPPW + 1);
+
+  // ------------------------------------------------ phase 4: mask, threshold, workgroup partial
+  __syncthreads();
+  {
+    int8_t *mrow_ptr = p.mask + ((size_t)b * p.HKV + hkv) * p.ntbs;
+    const int t = threadIdx.x;
+    if (SBS <= kPage) {
+      const int per = kPage / SBS;
+      if (t < kChunksPerWG * per) {
+        const int slot = t / per, k = t - slot * per;
+        const uint64_t bl = ((uint64_t)s_bal[slot][1] << 32) | s_bal[slot][0];
+        const int jb = (cw + slot) * per + k;
+        const bool kk = SBS == 16   ? ((bl >> (16 * k)) & 0xffffull) != 0
+                        : SBS == 32 ? ((bl >> (32 * k)) & 0xffffffffull) != 0
+                                    : bl != 0;
+        if (jb < p.ntbs) mrow_ptr[jb] = (jb < NTBS_b && kk) ? 1 : 0;
+      }
+    } else if (t < kChunksPerWG && ((cw + t) * kPage) % SBS == 0) {
+      const int jb = (cw + t) * kPage / SBS;
+      const bool kk = (s_bal[t][0] | s_bal[t][1]) != 0;
+      if (jb < p.ntbs) mrow_ptr[jb] = (jb < NTBS_b && kk) ? 1 : 0;
+    }
+  }
+  if (p.th_out != nullptr && cg == 0 && threadIdx.x < G) p.th_out[(size_t)b * p.HQ + hkv * G + threadIdx.x] = th;
+  {
+    const int i = wv;
+    const int c2 = 2 * lane;
+    if (i < G) {
+      float M = -INFINITY;
+#pragma unroll
+      for (int ps = 0; ps < kChunksPerWG; ++ps)
+        if (s_pl[ps][i] > 0.f) M = fmaxf(M, s_pm[ps][i]);
+      float A = 0.f, ox = 0.f, oy = 0.f;
+#pragma unroll
+      for (int ps = 0; ps < kChunksPerWG; ++ps) {
+        const float l = s_pl[ps][i];
+        if (l > 0.f) {
+          const float wgt = exp2f(s_pm[ps][i] - M);
+          A = __builtin_fmaf(l, wgt, A);
+          ox = __builtin_fmaf(s_po[ps][i][c2], wgt, ox);
+          oy = __builtin_fmaf(s_po[ps][i][c2 + 1], wgt, oy);
+        }
+      }
+      const size_t row = (size_t)b * p.HQ + hkv * G + i;
+      if (lane == 0) {
+        p.m_buf[row * p.nparts + cg] = A > 0.f ? M : -INFINITY;
+        p.l_buf[row * p.nparts + cg] = A;
+      }
+      if (A > 0.f) *(float2 *)(p.o_buf + (row * p.nparts + cg) * 128 + c2) = make_float2(ox, oy);
+    }
+  }
+}
+
+}  // namespace ffa
+
+// --------------------------------------------------------------------------
+// C ABI
+// --------------------------------------------------------------------------
+template <int F, int S, int R, int V>
+static hipError_t kfmt_launch(const ffa::DecodeParams &p, dim3 grid, hipStream_t st) {
+  hipLaunchKernelGGL((ffa::kfmt_decode_kernel<F, S, R, V>), grid, dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+
+template <int F, int S>
+static hipError_t kfmt_dispatch_rv(const ffa::DecodeParams &p, int res, int vdt, dim3 grid, hipStream_t st) {
+  const int r = res == FFA_DT_FP8_E4M3 ? ffa::kResE4M3 : (res == FFA_DT_FP8_E5M2 ? ffa::kResE5M2 : ffa::kResNone);
+  const int v = vdt == FFA_DT_BF16 ? ffa::kVBF16 : ffa::kVF16;
+#define FFA_CASE(RR, VV) \
+  if (r == RR && v == VV) return kfmt_launch<F, S, RR, VV>(p, grid, st);
+  FFA_CASE(ffa::kResE4M3, ffa::kVBF16)
+  FFA_CASE(ffa::kResE4M3, ffa::kVF16)
+  FFA_CASE(ffa::kResE5M2, ffa::kVBF16)
+  FFA_CASE(ffa::kResE5M2, ffa::kVF16)
+  FFA_CASE(ffa::kResNone, ffa::kVBF16)
+  FFA_CASE(ffa::kResNone, ffa::kVF16)
+#undef FFA_CASE
+  return hipErrorInvalidValue;
+}
+
+extern "C" int ffa_kfmt_decode(const ffa_kfmt_decode_args *a, void *stream) {
+  if (!a) return ffa_set_error_internal(FFA_E_INVALID, "null args");
+  if (a->B <= 0 || a->T <= 0 || a->HQ <= 0 || a->HKV <= 0) return ffa_set_error_internal(FFA_E_INVALID, "bad dims");
+  if (a->HQ % a->HKV) return ffa_set_error_internal(FFA_E_INVALID, "HQ must be a multiple of HKV");
+  const int G = a->HQ / a->HKV;
+  if (G > 4) return ffa_set_error_internal(FFA_E_UNSUPPORTED, "GQA group size > 4 is not implemented");
+  if (a->SBS <= 0 || a->BS <= 0 || a->BS % a->SBS)
+    return ffa_set_error_internal(FFA_E_UNSUPPORTED, "BS must be a multiple of SBS");
+  if (!(a->SBS == 16 || a->SBS == 32 || a->SBS == 64 || a->SBS == 128 || a->SBS == 256))
+    return ffa_set_error_internal(FFA_E_UNSUPPORTED, "SBS must be one of 16, 32, 64, 128, 256");
+  if (!(a->q_dtype >= FFA_DT_F16 && a->q_dtype <= FFA_DT_F32)) return ffa_set_error_internal(FFA_E_INVALID, "q dtype");
+  if (!(a->out_dtype >= FFA_DT_F16 && a->out_dtype <= FFA_DT_F32))
+    return ffa_set_error_internal(FFA_E_INVALID, "out dtype");
+  if (!(a->v_dtype == FFA_DT_F16 || a->v_dtype == FFA_DT_BF16)) return ffa_set_error_internal(FFA_E_INVALID, "v dtype");
+  if (!(a->res_dtype == FFA_DT_FP8_E4M3 || a->res_dtype == FFA_DT_FP8_E5M2 || a->res_dtype == FFA_DT_NONE))
+    return ffa_set_error_internal(FFA_E_INVALID, "residual dtype");
+  if (a->res_dtype != FFA_DT_NONE && !a->k_residual) return ffa_set_error_internal(FFA_E_INVALID, "residual pointer is null");
+  const bool scaled = a->scale_kind != FFA_KSCALE_NONE;
+  if (scaled && !(a->scale_dtype >= FFA_DT_F16 && a->scale_dtype <= FFA_DT_F32))
+    return ffa_set_error_internal(FFA_E_INVALID, "scale dtype");
+  if (scaled && !a->k_scale) return ffa_set_error_internal(FFA_E_INVALID, "scale pointer is null");
+  const int need = ffa_q2fp8_decode_nparts(a->T, a->BS, a->SBS);
+  if (a->nparts < need) return ffa_set_error_internal(FFA_E_INVALID, "scratch holds too few partial slots");
+  const int ntbs = ((a->T + a->BS - 1) / a->BS) * (a->BS / a->SBS);
+  if (a->ntbs < ntbs) return ffa_set_error_internal(FFA_E_INVALID, "mask holds too few blocks");
+
+  ffa::DecodeParams p = {};
+  p.q = a->q;
+  p.kq = a->k;
+  p.ks = a->k_scale;
+  p.kr = a->k_residual;
+  p.v = a->v;
+  p.seq_lens = a->seq_lens;
+  p.th_in = a->threshold_in;
+  p.th_out = a->threshold_out;
+  p.out = a->out;
+  p.m_buf = a->m_buf;
+  p.l_buf = a->l_buf;
+  p.o_buf = a->o_buf;
+  p.mask = a->mask;
+  p.q_dtype = a->q_dtype;
+  p.s_dtype = a->scale_dtype;
+  p.out_dtype = a->out_dtype;
+  p.B = a->B;
+  p.T = a->T;
+  p.HQ = a->HQ;
+  p.HKV = a->HKV;
+  p.G = G;
+  p.scale = a->scale;
+  p.BS = a->BS;
+  p.SBS = a->SBS;
+  p.delta = a->delta;
+  p.nparts = a->nparts;
+  p.ntbs = a->ntbs;
+  p.nwg = need;
+
+  hipStream_t st = (hipStream_t)stream;
+  dim3 grid(need * a->B * a->HKV);
+  hipError_t e = hipErrorInvalidValue;
+  const int fmt = a->k_format, sk = a->scale_kind;
+  if (fmt == FFA_KFMT_FP8_E4M3 && sk == FFA_KSCALE_NONE)
+    e = kfmt_dispatch_rv<ffa::kF8E4M3, ffa::kSclNone>(p, a->res_dtype, a->v_dtype, grid, st);
+  else if (fmt == FFA_KFMT_FP8_E4M3 && sk == FFA_KSCALE_TOKEN)
+    e = kfmt_dispatch_rv<ffa::kF8E4M3, ffa::kSclToken>(p, a->res_dtype, a->v_dtype, grid, st);
+  else if (fmt == FFA_KFMT_FP8_E5M2 && sk == FFA_KSCALE_NONE)
+    e = kfmt_dispatch_rv<ffa::kF8E5M2, ffa::kSclNone>(p, a->res_dtype, a->v_dtype, grid, st);
+  else if (fmt == FFA_KFMT_FP8_E5M2 && sk == FFA_KSCALE_TOKEN)
+    e = kfmt_dispatch_rv<ffa::kF8E5M2, ffa::kSclToken>(p, a->res_dtype, a->v_dtype, grid, st);
+  else if (fmt == FFA_KFMT_NVFP4 && sk == FFA_KSCALE_BLOCK)
+    e = kfmt_dispatch_rv<ffa::kFP4, ffa::kSclBlock>(p, a->res_dtype, a->v_dtype, grid, st);
+  else if (fmt == FFA_KFMT_NF4 && sk == FFA_KSCALE_CHANNEL)
+    e = kfmt_dispatch_rv<ffa::kNF4, ffa::kSclChannel>(p, a->res_dtype, a->v_dtype, grid, st);
+  else
+    return ffa_set_error_internal(FFA_E_UNSUPPORTED, "unsupported K format / scale granularity combination");
+  if (e != hipSuccess) return ffa_set_error_internal(FFA_E_LAUNCH, hipGetErrorString(e));
+  hipLaunchKernelGGL(ffa::q2fp8_merge_kernel, dim3(a->B * a->HQ * 4), dim3(64), 0, st, p);
+  e = hipGetLastError();
+  if (e != hipSuccess) return ffa_set_error_internal(FFA_E_LAUNCH, hipGetErrorString(e));
+  return FFA_OK;
+}

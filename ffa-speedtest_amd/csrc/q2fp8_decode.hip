@@ -31,7 +31,7 @@
 //   * each wave owns two consecutive chunks; the grid is 1-D with the
 //     (sequence, KV head) unit fastest, so with B*HKV a multiple of 8 a unit's
 //     workgroups share one XCD and its L2.
-#include "ffa_common.h"
+#include "decode_common.h"
 #include "ffa_mi355x.h"
 
 #include <stdio.h>
@@ -39,65 +39,6 @@
 #include <type_traits>
 
 namespace ffa {
-
-constexpr int kD = 128;
-constexpr int kPage = 64;
-constexpr int kWaves = 4;
-constexpr int kPPW = 2;                      // 64-token chunks (pages) per wave
-constexpr int kChunksPerWG = kWaves * kPPW;  // 512 tokens per workgroup
-constexpr int kVRow = 260;  // LDS row pitch (bytes) of the staged V tile: 256 + 4 keeps banks apart
-
-struct DecodeParams {
-  const void *q;
-  const uint8_t *kq;
-  const void *ks;
-  const void *kz;
-  const uint8_t *kr;
-  const void *v;
-  const int32_t *bt;
-  const int32_t *seq_lens;
-  const float *th_in;
-  float *th_out;
-  void *out;
-  float *m_buf, *l_buf, *o_buf;
-  int8_t *mask;
-  int q_dtype, s_dtype, out_dtype;
-  int bt_stride;
-  int B, T, HQ, HKV, G;
-  float scale;
-  int BS, SBS;
-  float delta;
-  int nparts, ntbs;
-  int nwg;  // decode workgroups per (sequence, KV head)
-};
-
-enum { kContig = 0, kPaged = 1 };
-enum { kChannel = 0, kG32 = 1 };
-enum { kResNone = 0, kResE4M3 = 1, kResE5M2 = 2 };
-enum { kVF16 = 0, kVBF16 = 1 };
-
-// 8 fp8 residual bytes -> 8 fp16 (exact)
-template <int RES>
-__device__ __forceinline__ f16x8 fp8x8_to_f16x8(uint32_t lo, uint32_t hi) {
-  u32x4 r;
-  if constexpr (RES == kResE5M2) {
-    // e5m2 is the high byte of the fp16 with the same value
-    r[0] = __builtin_amdgcn_perm(lo, lo, 0x010c000cu);
-    r[1] = __builtin_amdgcn_perm(lo, lo, 0x030c020cu);
-    r[2] = __builtin_amdgcn_perm(hi, hi, 0x010c000cu);
-    r[3] = __builtin_amdgcn_perm(hi, hi, 0x030c020cu);
-  } else {
-    f16x2 a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, false);
-    f16x2 b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, true);
-    f16x2 c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, false);
-    f16x2 d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, true);
-    r[0] = __builtin_bit_cast(uint32_t, a);
-    r[1] = __builtin_bit_cast(uint32_t, b);
-    r[2] = __builtin_bit_cast(uint32_t, c);
-    r[3] = __builtin_bit_cast(uint32_t, d);
-  }
-  return __builtin_bit_cast(f16x8, r);
-}
 
 // A-operand words of the score MFMAs from 16 packed codes (one 32-bit word).
 // s = 0: codes (q, q+8) at bits (2q, 16+2q) -> value c * 4^q * 2^-24
@@ -111,64 +52,6 @@ __device__ __forceinline__ f16x8 codes_to_f16x8(uint32_t w, int s) {
   r[3] = y & 0x00c000c0u;
   return __builtin_bit_cast(f16x8, r);
 }
-
-template <int VT>
-struct VTraits;
-template <>
-struct VTraits<kVBF16> {
-  typedef bf16x8 vec;
-  __device__ static __forceinline__ f32x4 mfma(vec a, vec b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
-  __device__ static __forceinline__ uint32_t pack2(float x, float y) {
-    return f32_to_bf16_bits(x) | (f32_to_bf16_bits(y) << 16);
-  }
-};
-template <>
-struct VTraits<kVF16> {
-  typedef f16x8 vec;
-  __device__ static __forceinline__ f32x4 mfma(vec a, vec b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-  }
-  __device__ static __forceinline__ uint32_t pack2(float x, float y) {
-    return f32_to_f16_bits(x) | (f32_to_f16_bits(y) << 16);
-  }
-};
-
-// 16 consecutive elements of a float tensor (dtype 0=f16, 1=bf16, 2=f32): four raw 16-byte
-// loads whatever the dtype (16-bit data uses the first two), conversion afterwards.
-struct Raw16 {
-  uint4 v[4];
-};
-__device__ __forceinline__ void raw16_load(Raw16 &r, brsrc rs, uint32_t off) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) r.v[i] = bload16(rs, off + 16 * i);
-}
-__device__ __forceinline__ void raw16_to_f32(const Raw16 &r, int dt, float *out) {
-  if (dt == 2) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      out[4 * i + 0] = __uint_as_float(r.v[i].x);
-      out[4 * i + 1] = __uint_as_float(r.v[i].y);
-      out[4 * i + 2] = __uint_as_float(r.v[i].z);
-      out[4 * i + 3] = __uint_as_float(r.v[i].w);
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint32_t w[4] = {r.v[i].x, r.v[i].y, r.v[i].z, r.v[i].w};
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const uint32_t lo = w[k] & 0xffffu, hi = w[k] >> 16;
-        out[8 * i + 2 * k] = dt == 1 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
-        out[8 * i + 2 * k + 1] = dt == 1 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
-      }
-    }
-  }
-}
-
-__device__ __forceinline__ uint32_t f16x2_bits(f16x2 v) { return __builtin_bit_cast(uint32_t, v); }
-__device__ __forceinline__ f16x2 bits_f16x2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
 
 // Reference-layout dequantization of 8 channels: k_hat = fp16(c * s + z) with one rounding
 // (c*s is exact in fp32, so this equals the reference's fp16(fp32(fp32(c*s) + z))).
@@ -185,8 +68,6 @@ __device__ __forceinline__ f16x8 dequant8_channel(uint32_t h, const uint32_t *sp
   }
   return __builtin_bit_cast(f16x8, r);
 }
-
-__device__ __forceinline__ f16x8 add_f16x8(f16x8 a, f16x8 b) { return a + b; }
 
 // Position of token t (0..63) inside a page row of g32 scales / zeros.  Tile-major:
 // the scores of MFMA tile tau hold tokens 16k + 4u + tau (u = 0..3), whose scales

@@ -1,0 +1,109 @@
+# attn_kernel_v1210_fused_bsz_nvfp4fp8.py -- MI355X drop-in.
+# NVFP4 K (block-scaled FP4) with fp8 residual refinement; the kernels are hand-written
+# HIP for gfx950 in libffa_mi355x.so (no Triton).
+"""Drop-in for ffa-nvfp4fp8/attn_kernel/attn_kernel_v1210_fused_bsz_nvfp4fp8.py.
+
+`attn_forward_decode_nvfp4fp8` keeps the reference signature, defaults, scale-shape
+normalisation and exception types (reference :213-367).  K is packed e2m1 nibbles (low
+nibble first) with one scale per (sequence, BS-token block, KV head).  Extension through
+**kwargs: seq_lens=[B] int32.
+"""
+import math
+import sys
+from pathlib import Path
+
+import torch
+
+sys.path.insert(0, str(Path(__file__).resolve().parents[2]))  # ffa-speedtest_amd/
+from ffa_mi355x import _native as _N  # noqa: E402
+from ffa_mi355x.decode import DecodeWorkspace, decode_ntbs  # noqa: E402
+from ffa_mi355x.kfmt import run_kfmt_decode  # noqa: E402
+
+__all__ = ["attn_forward_decode_nvfp4fp8"]
+
+
+def _normalize_k_scale(k_scale: torch.Tensor, expect_shape: tuple[int, int, int]) -> torch.Tensor:
+    """[B, 1, NTB, HKV] or [B, HKV, NTB] are accepted for [B, NTB, HKV] (reference :213-222)."""
+    if k_scale.ndim == 4 and k_scale.shape[1] == 1:
+        k_scale = k_scale.squeeze(1)
+    if k_scale.shape == (expect_shape[0], expect_shape[2], expect_shape[1]):
+        k_scale = k_scale.permute(0, 2, 1)
+    if k_scale.shape != expect_shape:
+        raise ValueError(f"Unsupported k_scale shape: {k_scale.shape=} expected {expect_shape}")
+    return k_scale.contiguous()
+
+
+def attn_forward_decode_nvfp4fp8(
+    q: torch.Tensor,  # [B, 1, HQ, K]
+    k_fp4: torch.Tensor,  # [B, T, HKV, ceil(K / (8 / k_bits))], packed FP4 nibbles (E2M1)
+    k_scale: torch.Tensor,  # [B, NTB, HKV], block scales (page size = BS)
+    v: torch.Tensor,  # [B, T, HKV, V]
+    *,
+    k_residual: torch.Tensor | None = None,  # [B, T, HKV, K], fp8 residual
+    k_bits: int = 4,
+    scale: float = None,
+    BS: int = 128,
+    SBS: int | None = None,
+    delta: float = 5.0,
+    return_skip_ratio: bool = False,
+    precomputed_threshold: torch.Tensor | None = None,
+    use_fp8_residual: bool = True,
+    **kwargs,
+):
+    assert q.is_cuda and k_fp4.is_cuda and k_scale.is_cuda and v.is_cuda
+    if k_residual is not None and not k_residual.is_cuda:
+        raise ValueError("k_residual must be a CUDA tensor when provided")
+    if k_bits != 4:
+        raise ValueError(f"attn_forward_decode_nvfp4fp8 supports 4-bit keys, got k_bits={k_bits}")
+    if k_fp4.is_floating_point():
+        raise ValueError("k_fp4 must contain packed FP4 (E2M1) nibbles in an integer tensor (e.g., uint8)")
+    if not k_scale.is_floating_point():
+        raise ValueError("k_scale must be a floating point tensor")
+    if k_residual is not None and not k_residual.is_floating_point():
+        raise ValueError("k_residual must be a floating point tensor (e.g., fp8/fp16/bf16)")
+
+    B, Tq, HQ, K = q.shape
+    Bk, T, HKV, K_packed = k_fp4.shape
+    Bv, Tv, HKVv, V = v.shape
+    vals_per_byte = 8 // k_bits
+    expected_k_packed = (K + vals_per_byte - 1) // vals_per_byte
+    if K_packed != expected_k_packed:
+        raise ValueError(
+            f"k_fp4 packed dim mismatch: got {K_packed}, expected {expected_k_packed} for K={K}, k_bits={k_bits}")
+    if k_residual is not None:
+        Bk_r, T_r, HKV_r, K_r = k_residual.shape
+        assert (B == Bk == Bv == Bk_r and Tq == 1 and Tv == T == T_r and HKVv == HKV == HKV_r
+                and K == K_r), "K/V layouts must be [B, T, HKV, D]"
+    else:
+        assert B == Bk == Bv and Tq == 1 and Tv == T and HKVv == HKV, "K/V layouts must be [B, T, HKV, D]"
+    if scale is None:
+        scale = 1.0 / math.sqrt(K)
+    if SBS is None:
+        SBS = BS
+    NTB = -(-T // BS)
+    k_scale = _normalize_k_scale(k_scale, (B, NTB, HKV))
+    assert q.is_contiguous() and k_fp4.is_contiguous() and v.is_contiguous()
+    if use_fp8_residual and k_residual is None:
+        raise ValueError("use_fp8_residual=True requires k_residual")
+    if k_residual is not None:
+        assert k_residual.is_contiguous()
+    use_res = bool(use_fp8_residual and k_residual is not None)
+    if precomputed_threshold is not None:
+        assert precomputed_threshold.is_cuda and precomputed_threshold.shape == (B, HQ)
+    seq_lens = kwargs.get("seq_lens")
+    if seq_lens is not None:
+        seq_lens = seq_lens.to(device=q.device, dtype=torch.int32).contiguous()
+    workspace = kwargs.get("workspace")
+    if workspace is not None and not isinstance(workspace, DecodeWorkspace):
+        raise TypeError("workspace must be a DecodeWorkspace")
+
+    ws = run_kfmt_decode(
+        q=q[:, 0], k=k_fp4, k_format=_N.KFMT_NVFP4, k_scale=k_scale, scale_kind=_N.KSCALE_BLOCK, v=v,
+        k_residual=k_residual, use_res=use_res, T=T, HKV=HKV, scale=scale, BS=BS, SBS=SBS, delta=delta,
+        precomputed_threshold=precomputed_threshold, seq_lens=seq_lens, workspace=workspace)
+    if return_skip_ratio:
+        kept = ws.mask_buf.to(torch.int32).sum()
+        total = ws.mask_buf.numel() if seq_lens is None else \
+            sum(decode_ntbs(int(t), BS, SBS) for t in seq_lens.tolist()) * HKV
+        return ws.o, float((1.0 - (kept.float() / float(total))).item())
+    return ws.o

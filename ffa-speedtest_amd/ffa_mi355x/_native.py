@@ -17,12 +17,15 @@ LIB_PATH = Path(__file__).resolve().parent / "libffa_mi355x.so"
 DT_F16, DT_BF16, DT_F32, DT_FP8_E4M3, DT_FP8_E5M2, DT_NONE = range(6)
 LAYOUT_CONTIG, LAYOUT_PAGED = 0, 1
 SCALE_CHANNEL, SCALE_G32 = 0, 1
+KFMT_FP8_E4M3, KFMT_FP8_E5M2, KFMT_NVFP4, KFMT_NF4 = range(4)
+KSCALE_NONE, KSCALE_TOKEN, KSCALE_BLOCK, KSCALE_CHANNEL = range(4)
 
 EXPORTS = (
     "ffa_q2fp8_decode_nparts",
     "ffa_q2fp8_decode",
     "ffa_q2fp8_decode_stage1",
     "ffa_q2fp8_decode_stage2",
+    "ffa_kfmt_decode",
     "ffa_q2_quantize_nsplit",
     "ffa_q2_quantize_channel",
     "ffa_kproj_rope_q2_channel",
@@ -86,6 +89,41 @@ class DecodeArgs(ctypes.Structure):
     ]
 
 
+class KfmtArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("q_dtype", ctypes.c_int),
+        ("k", ctypes.c_void_p),
+        ("k_format", ctypes.c_int),
+        ("k_scale", ctypes.c_void_p),
+        ("scale_dtype", ctypes.c_int),
+        ("scale_kind", ctypes.c_int),
+        ("k_residual", ctypes.c_void_p),
+        ("res_dtype", ctypes.c_int),
+        ("v", ctypes.c_void_p),
+        ("v_dtype", ctypes.c_int),
+        ("seq_lens", ctypes.c_void_p),
+        ("B", ctypes.c_int),
+        ("T", ctypes.c_int),
+        ("HQ", ctypes.c_int),
+        ("HKV", ctypes.c_int),
+        ("scale", ctypes.c_float),
+        ("BS", ctypes.c_int),
+        ("SBS", ctypes.c_int),
+        ("delta", ctypes.c_float),
+        ("threshold_in", ctypes.c_void_p),
+        ("threshold_out", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("out_dtype", ctypes.c_int),
+        ("m_buf", ctypes.c_void_p),
+        ("l_buf", ctypes.c_void_p),
+        ("o_buf", ctypes.c_void_p),
+        ("nparts", ctypes.c_int),
+        ("mask", ctypes.c_void_p),
+        ("ntbs", ctypes.c_int),
+    ]
+
+
 _lib = None
 _lock = threading.Lock()
 
@@ -112,6 +150,8 @@ def lib() -> ctypes.CDLL:
         for name in ("ffa_q2fp8_decode", "ffa_q2fp8_decode_stage1", "ffa_q2fp8_decode_stage2"):
             getattr(L, name).argtypes = [ctypes.POINTER(DecodeArgs), vp]
             getattr(L, name).restype = ci
+        L.ffa_kfmt_decode.argtypes = [ctypes.POINTER(KfmtArgs), vp]
+        L.ffa_kfmt_decode.restype = ci
         L.ffa_q2_quantize_nsplit.argtypes = [ci]
         L.ffa_q2_quantize_nsplit.restype = ci
         L.ffa_q2_quantize_channel.argtypes = [vp, ci, ci, ci, ci, ci, vp, vp, vp, vp, ci, vp, vp]

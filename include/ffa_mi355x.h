@@ -176,6 +176,53 @@ int ffa_q2_quantize_g32_append(const void *k, int k_dtype, int B, int Tn, int HK
                                void *zero_pages, uint8_t *res_pages, int res_dtype, const void *v_new, void *v_pages,
                                void *stream);
 
+/*
+ * Pruned decode for the other K formats of the reference (contiguous [B, T, HKV, row]
+ * layouts as in the reference), same prune / refine / merge as ffa_q2fp8_decode:
+ *   FFA_KFMT_FP8_E4M3/E5M2 + FFA_KSCALE_NONE   fp8 base, k_hat = fp16(base)
+ *       (ffa-fp8fp8/attn_kernel/attn_kernel_v1210_fused_bsz_fp8fp8.py:10-177, launches :263-309)
+ *   FFA_KFMT_FP8_E4M3/E5M2 + FFA_KSCALE_TOKEN  k_hat = fp16(base * scale[b, t, h]) (
+ *       no reference counterpart)
+ *   FFA_KFMT_NVFP4 + FFA_KSCALE_BLOCK          packed e2m1 nibbles (low nibble first) times
+ *       scale[b, t / BS, h] ([B, ceil(T/BS), HKV])
+ *       (ffa-nvfp4fp8/attn_kernel/attn_kernel_v1210_fused_bsz_nvfp4fp8.py:24-210, launches :316-363)
+ *   FFA_KFMT_NF4 + FFA_KSCALE_CHANNEL          NF4 codebook times scale[b, h, d] ([B, HKV, 128])
+ *       (ffa-nf4fp8/attn_kernel/attn_kernel_v1210_fused_bsz_nf4fp8.py:41-199, launches :300-326)
+ * k is [B, T, HKV, 128] fp8 bytes or [B, T, HKV, 64] packed nibbles; residual [B, T, HKV, 128] fp8;
+ * v [B, T, HKV, 128]; scratch as ffa_q2fp8_decode (nparts from ffa_q2fp8_decode_nparts).
+ */
+enum { FFA_KFMT_FP8_E4M3 = 0, FFA_KFMT_FP8_E5M2 = 1, FFA_KFMT_NVFP4 = 2, FFA_KFMT_NF4 = 3 };
+enum { FFA_KSCALE_NONE = 0, FFA_KSCALE_TOKEN = 1, FFA_KSCALE_BLOCK = 2, FFA_KSCALE_CHANNEL = 3 };
+
+typedef struct ffa_kfmt_decode_args {
+  const void *q; /* [B, HQ, 128] */
+  int q_dtype;
+  const uint8_t *k;
+  int k_format;
+  const void *k_scale; /* NULL with FFA_KSCALE_NONE */
+  int scale_dtype;     /* F16/BF16/F32 */
+  int scale_kind;
+  const uint8_t *k_residual; /* may be NULL when res_dtype == FFA_DT_NONE */
+  int res_dtype;
+  const void *v;
+  int v_dtype;
+  const int32_t *seq_lens; /* [B] or NULL; clamped to [0, T] */
+  int B, T, HQ, HKV;
+  float scale;
+  int BS, SBS;
+  float delta;
+  const float *threshold_in;
+  float *threshold_out;
+  void *out;
+  int out_dtype;
+  float *m_buf, *l_buf, *o_buf;
+  int nparts;
+  int8_t *mask;
+  int ntbs;
+} ffa_kfmt_decode_args;
+
+int ffa_kfmt_decode(const ffa_kfmt_decode_args *args, void *stream);
+
 const char *ffa_last_error(void);
 const char *ffa_version(void);
 

@@ -1,0 +1,143 @@
+"""GPU parity of the fp8 / nvfp4 / nf4 decoders (drop-in modules -> C ABI -> HIP) against the oracle."""
+import importlib.util
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import FP8_DT, TORCH_DT, assert_out_close, compare_masks, f32
+from ffa_mi355x import synth
+from oracle import formats as OF
+from oracle import numerics as NM
+from oracle import q2fp8 as O
+
+pytestmark = pytest.mark.gpu
+PKG = Path(__file__).resolve().parents[1] / "ffa-speedtest_amd"
+
+
+def _load(rel, name):
+    spec = importlib.util.spec_from_file_location(name, PKG / rel)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+F8K = _load("ffa-fp8fp8/attn_kernel/attn_kernel_v1210_fused_bsz_fp8fp8.py", "kfmt_fp8fp8")
+NVK = _load("ffa-nvfp4fp8/attn_kernel/attn_kernel_v1210_fused_bsz_nvfp4fp8.py", "kfmt_nvfp4fp8")
+NFK = _load("ffa-nf4fp8/attn_kernel/attn_kernel_v1210_fused_bsz_nf4fp8.py", "kfmt_nf4fp8")
+
+
+def _inputs(B, T, tau, seed, n_heavy, seq_lens=None):
+    q, k, v = synth.attention_inputs(B=B, T=T, HQ=32, HKV=8, seed=seed, n_heavy=n_heavy, dtype=TORCH_DT[tau],
+                                     seq_lens=seq_lens)
+    return q, k, v
+
+
+def _check(o_gpu, ws, o_ref, diag, what):
+    torch.cuda.synchronize()
+    far, near, n_near = compare_masks(ws.mask_buf.cpu().numpy(), diag)
+    print(f"[mask] {what} keep={ws.mask_buf.float().mean().item():.3f} far={far} near={near}/{n_near}")
+    assert far == 0, f"{what}: {far} mask mismatches away from the threshold"
+    th = ws.threshold_buf.cpu().numpy()
+    assert np.abs(th - diag["threshold"]).max() < 1e-4, f"{what}: threshold"
+    mx, mean = assert_out_close(f32(o_gpu), o_ref, what)
+    print(f"[out] {what} max_abs={mx:.3e} mean_abs={mean:.3e}")
+
+
+@pytest.mark.parametrize("fmt,tau,vdt,T,BS,SBS,delta", [
+    ("e5m2", "fp16", "fp16", 1000, 128, None, 5.0),
+    ("e4m3fn", "bf16", "bf16", 4096, 64, 64, 5.0),
+    ("e5m2", "bf16", "bf16", 2048, 64, 32, 3.0),
+    ("e4m3fn", "fp16", "fp16", 777, 64, 16, 2.0),
+])
+def test_fp8fp8_decoder(gpu, fmt, tau, vdt, T, BS, SBS, delta):
+    q, k, v = _inputs(1, T, tau, 1, 16)
+    base, res = OF.quantize_fp8fp8(f32(k), fmt)
+    kh = OF.khat_fp8(base, fmt)
+    o_ref, diag = O.decode(f32(q), base, None, None, f32(v), res, res_fmt=fmt, BS=BS, SBS=SBS, delta=delta,
+                           khat=kh, out_dtype=tau)
+    ws = F8K.__dict__["DecodeWorkspace"](1, 32, 8, T, BS, SBS or BS, gpu, TORCH_DT[tau])
+    o = F8K.attn_forward_decode_fp8fp8(
+        q.to(gpu).unsqueeze(1).contiguous(), torch.from_numpy(base).view(FP8_DT[fmt]).to(gpu),
+        v.to(TORCH_DT[vdt]).to(gpu), k_residual=torch.from_numpy(res).view(FP8_DT[fmt]).to(gpu), BS=BS, SBS=SBS,
+        delta=delta, workspace=ws)
+    _check(o, ws, o_ref, diag, f"fp8fp8 {fmt} T={T}")
+
+
+def test_fp8_scaled_decoder_baseline_config1(gpu):
+    """e4m3 + one fp16 scale per token and KV head + e4m3 residual, 4 outlier channels."""
+    T = 4096
+    q, k, v = _inputs(1, T, "bf16", 0, 0)
+    kf = f32(k)
+    kf[..., :4] *= 10.0
+    base, s, res = OF.quantize_fp8_scaled(kf, "e4m3fn")
+    kh = OF.khat_fp8_scaled(base, s, "e4m3fn")
+    o_ref, diag = O.decode(f32(q), base, None, None, f32(v), res, res_fmt="e4m3fn", BS=64, SBS=64, delta=5.0,
+                           khat=kh, out_dtype="bf16")
+    ws = F8K.__dict__["DecodeWorkspace"](1, 32, 8, T, 64, 64, gpu, torch.bfloat16)
+    o = F8K.attn_forward_decode_fp8fp8(
+        q.to(gpu).unsqueeze(1).contiguous(), torch.from_numpy(base).view(torch.float8_e4m3fn).to(gpu), v.to(gpu),
+        k_residual=torch.from_numpy(res).view(torch.float8_e4m3fn).to(gpu), BS=64, delta=5.0,
+        k_scale=torch.from_numpy(s).to(torch.float16).to(gpu), workspace=ws)
+    _check(o, ws, o_ref, diag, "fp8 scaled (config 1)")
+
+
+@pytest.mark.parametrize("tau,T,BS,SBS,delta", [
+    ("bf16", 2048, 64, 64, 5.0),
+    ("fp16", 1100, 128, 64, 4.0),  # NTB = 9 != HKV: see test_nvfp4_scale_normalisation_quirk
+    ("bf16", 3000, 128, 128, 5.0),
+    ("fp32", 700, 64, 32, 3.0),
+])
+def test_nvfp4_decoder(gpu, tau, T, BS, SBS, delta):
+    q, k, v = _inputs(1, T, "bf16" if tau == "fp32" else tau, 2, 16)
+    kt = NM.round_to(f32(k), tau)
+    pk, sc, res = OF.quantize_nvfp4(kt, tau, "e5m2", BS)
+    kh, kp1 = OF.khat_nvfp4(pk, sc, BS, 128)
+    o_ref, diag = O.decode(f32(q), pk, None, None, f32(v), res, res_fmt="e5m2", BS=BS, SBS=SBS, delta=delta,
+                           khat=kh, khat_probe1=kp1, out_dtype="bf16" if tau == "fp32" else tau)
+    qd = q.to(gpu).unsqueeze(1).contiguous()
+    o, sr = NVK.attn_forward_decode_nvfp4fp8(
+        qd, torch.from_numpy(pk).to(gpu), torch.from_numpy(sc).to(TORCH_DT[tau]).to(gpu), v.to(gpu),
+        k_residual=torch.from_numpy(res).view(torch.float8_e5m2).to(gpu), BS=BS, SBS=SBS, delta=delta,
+        return_skip_ratio=True)
+    ws = NVK.__dict__["DecodeWorkspace"](1, 32, 8, T, BS, SBS, gpu, qd.dtype)
+    o = NVK.attn_forward_decode_nvfp4fp8(
+        qd, torch.from_numpy(pk).to(gpu), torch.from_numpy(sc).to(TORCH_DT[tau]).to(gpu), v.to(gpu),
+        k_residual=torch.from_numpy(res).view(torch.float8_e5m2).to(gpu), BS=BS, SBS=SBS, delta=delta, workspace=ws)
+    _check(o, ws, o_ref, diag, f"nvfp4 {tau} T={T} BS={BS}")
+    assert abs(sr - (1.0 - ws.mask_buf.float().mean().item())) < 1e-6  # return_skip_ratio of the first call
+
+
+@pytest.mark.parametrize("tau,T,BS,SBS,delta,res_fmt", [
+    ("bf16", 2048, 64, 64, 5.0, "e4m3fn"),
+    ("fp16", 1300, 128, 32, 4.0, "e5m2"),
+])
+def test_nf4_decoder(gpu, tau, T, BS, SBS, delta, res_fmt):
+    q, k, v = _inputs(1, T, tau, 3, 16)
+    pk, sc, res = OF.quantize_nf4(f32(k), tau, res_fmt)
+    kh = OF.khat_nf4(pk, sc, 128)
+    o_ref, diag = O.decode(f32(q), pk, None, None, f32(v), res, res_fmt=res_fmt, BS=BS, SBS=SBS, delta=delta,
+                           khat=kh, out_dtype=tau)
+    ws = NFK.__dict__["DecodeWorkspace"](1, 32, 8, T, BS, SBS, gpu, TORCH_DT[tau])
+    o = NFK.attn_forward_decode_nf4(
+        q.to(gpu).unsqueeze(1).contiguous(), torch.from_numpy(pk).to(gpu), torch.from_numpy(sc).to(TORCH_DT[tau]).to(gpu),
+        v.to(gpu), torch.from_numpy(res).view(FP8_DT[res_fmt]).to(gpu), BS=BS, SBS=SBS, delta=delta, workspace=ws)
+    _check(o, ws, o_ref, diag, f"nf4 {tau} T={T}")
+
+
+def test_kfmt_ragged_and_no_residual(gpu):
+    """Ragged lengths (seq_lens) and use_fp8_residual=False on the nf4 decoder."""
+    lens = [1500, 640]
+    q, k, v = _inputs(2, 1500, "bf16", 4, 16, seq_lens=lens)
+    pk, sc, res = OF.quantize_nf4(f32(k), "bf16", "e4m3fn")
+    kh = OF.khat_nf4(pk, sc, 128)
+    o_ref, diag = O.decode(f32(q), pk, None, None, f32(v), res, res_fmt="e4m3fn", BS=64, SBS=64, delta=5.0,
+                           khat=kh, use_fp8_residual=False, seq_lens=lens, out_dtype="bf16")
+    ws = NFK.__dict__["DecodeWorkspace"](2, 32, 8, 1500, 64, 64, gpu, torch.bfloat16)
+    o = NFK.attn_forward_decode_nf4(
+        q.to(gpu).unsqueeze(1).contiguous(), torch.from_numpy(pk).to(gpu), torch.from_numpy(sc).to(torch.bfloat16).to(gpu),
+        v.to(gpu), torch.from_numpy(res).view(torch.float8_e4m3fn).to(gpu), BS=64, delta=5.0, use_fp8_residual=False,
+        seq_lens=torch.tensor(lens, dtype=torch.int32, device=gpu), workspace=ws)
+    _check(o, ws, o_ref, diag, "nf4 ragged no-residual")

@@ -93,3 +93,50 @@ def test_graph_runner_interface_matches_reference():
     assert R.__call__ is R.replay and callable(R.replay_only) and isinstance(R.output, property)
     rp = inspect.signature(R.replay).parameters
     assert list(rp)[1:6] == ["q", "k_q", "k_scale", "k_zero", "v"] and rp["return_skip_ratio"].default is False
+
+
+def test_other_format_drop_in_signatures():
+    """fp8fp8 / nvfp4 / nf4 decoders keep the reference parameter order and defaults
+    (F8K:180-194, NVK:225-241, NFK:212-227)."""
+    import importlib.util
+
+    pkg = ROOT / "ffa-speedtest_amd"
+
+    def load(rel, name):
+        spec = importlib.util.spec_from_file_location(name, pkg / rel)
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        return mod
+
+    f8 = load("ffa-fp8fp8/attn_kernel/attn_kernel_v1210_fused_bsz_fp8fp8.py", "sig_fp8fp8").attn_forward_decode_fp8fp8
+    nv = load("ffa-nvfp4fp8/attn_kernel/attn_kernel_v1210_fused_bsz_nvfp4fp8.py", "sig_nvfp4").attn_forward_decode_nvfp4fp8
+    nf = load("ffa-nf4fp8/attn_kernel/attn_kernel_v1210_fused_bsz_nf4fp8.py", "sig_nf4").attn_forward_decode_nf4
+    tail = ["scale", "BS", "SBS", "delta", "return_skip_ratio", "precomputed_threshold", "use_fp8_residual"]
+    assert list(inspect.signature(f8).parameters)[:-1] == ["q", "k_fp8", "v", "k_residual"] + tail
+    assert list(inspect.signature(nv).parameters)[:-1] == ["q", "k_fp4", "k_scale", "v", "k_residual", "k_bits"] + tail
+    assert list(inspect.signature(nf).parameters)[:-1] == ["q", "k_nf4", "k_scale", "v", "k_residual", "k_bits"] + tail
+    for fn in (f8, nv, nf):
+        ps = inspect.signature(fn).parameters
+        assert ps["BS"].default == 128 and ps["delta"].default == 5.0 and ps["use_fp8_residual"].default is True
+    assert inspect.signature(nv).parameters["k_bits"].default == 4
+    assert inspect.signature(f8).parameters["k_residual"].kind == inspect.Parameter.KEYWORD_ONLY
+    assert inspect.signature(nf).parameters["k_residual"].kind == inspect.Parameter.POSITIONAL_OR_KEYWORD
+
+
+def test_nvfp4_scale_normalisation_quirk():
+    """The nvfp4 drop-in normalises k_scale as the reference does (NVK:213-222): a [B, HKV, NTB]
+    tensor is transposed to [B, NTB, HKV], so when NTB == HKV a correctly shaped [B, NTB, HKV]
+    tensor is transposed too.  Kept on purpose: the drop-in computes what the reference computes."""
+    import importlib.util
+
+    import torch
+
+    spec = importlib.util.spec_from_file_location(
+        "quirk_nvfp4", ROOT / "ffa-speedtest_amd/ffa-nvfp4fp8/attn_kernel/attn_kernel_v1210_fused_bsz_nvfp4fp8.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    s = torch.arange(2 * 9 * 8, dtype=torch.float32).reshape(2, 9, 8)  # NTB = 9, HKV = 8
+    assert torch.equal(mod._normalize_k_scale(s, (2, 9, 8)), s)
+    assert torch.equal(mod._normalize_k_scale(s.permute(0, 2, 1).contiguous(), (2, 9, 8)), s)
+    sq = torch.arange(2 * 8 * 8, dtype=torch.float32).reshape(2, 8, 8)  # NTB == HKV == 8
+    assert torch.equal(mod._normalize_k_scale(sq, (2, 8, 8)), sq.permute(0, 2, 1))
