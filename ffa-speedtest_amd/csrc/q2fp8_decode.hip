@@ -24,13 +24,18 @@
 //     contiguous reference layout.
 //   * the 8 chunk partials (m, l, o) of a workgroup are merged in LDS into one
 //     partial per 512 tokens; a second kernel merges those with one batch of
-//     loads (back to back in a HIP graph; a device-wide completion flag in the
-//     first kernel would need an L2 write-back per wave, which costs more).
+//     loads (back to back in a HIP graph).  Merging in the last-arriving
+//     workgroup of each (sequence, KV head) instead was measured slower: the
+//     release needs an L2 write-back per workgroup (__threadfence), or, with
+//     device-scope stores and loads, the arrival atomic and the device-scope
+//     loads of one workgroup take longer than the kernel boundary plus a
+//     128-workgroup merge launch.
 //   * the q operands of the MFMAs are built once per workgroup (one per wave)
 //     and shared through LDS.
 //   * each wave owns two consecutive chunks; the grid is 1-D with the
-//     (sequence, KV head) unit fastest, so with B*HKV a multiple of 8 a unit's
-//     workgroups share one XCD and its L2.
+//     workgroup index along the sequence fastest, so consecutive workgroups of
+//     one (sequence, KV head) go to different XCDs and its kept chunks'
+//     residual/V traffic spreads over every XCD's memory path.
 #include "decode_common.h"
 #include "ffa_mi355x.h"
 

@@ -29,6 +29,43 @@ def test_library_exports_every_declared_symbol():
     assert set(N.EXPORTS) == declared
 
 
+@pytest.mark.parametrize("cname,pyname", [("ffa_q2fp8_decode_args", "DecodeArgs"),
+                                           ("ffa_kfmt_decode_args", "KfmtArgs")])
+def test_ctypes_argument_structs_match_header(tmp_path, cname, pyname):
+    """Field names, offsets and size of the ctypes mirrors equal the C compiler's layout."""
+    import shutil
+    import subprocess
+
+    from ffa_mi355x import _native as N
+
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc not available")
+    py = getattr(N, pyname)
+    fields = [f[0] for f in py._fields_]
+    body = "\n".join(f'  printf("%s %zu\\n", "{f}", offsetof({cname}, {f}));' for f in fields)
+    src = tmp_path / "layout.c"
+    src.write_text(f'#include <stddef.h>\n#include <stdio.h>\n#include "ffa_mi355x.h"\nint main(void) {{\n{body}\n'
+                   f'  printf("sizeof %zu\\n", sizeof({cname}));\n  return 0;\n}}\n')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)], check=True)
+    out = dict(line.split() for line in subprocess.run([str(exe)], check=True, capture_output=True,
+                                                        text=True).stdout.splitlines())
+    for f in fields:
+        assert int(out[f]) == getattr(py, f).offset, f"{cname}.{f}"
+    assert int(out["sizeof"]) == ctypes.sizeof(py)
+    # every member of the C struct is mirrored
+    text = re.sub(r"/\*.*?\*/", "", (ROOT / "include" / "ffa_mi355x.h").read_text(), flags=re.S)
+    decl = re.search(r"typedef struct %s \{(.*?)\} %s;" % (cname, cname), text, flags=re.S).group(1)
+    members = []
+    for d in decl.split(";"):
+        d = d.strip()
+        if d:
+            head, *rest = d.split(",")
+            members.append(re.findall(r"(\w+)\s*$", head)[0])
+            members += [r.strip().lstrip("*").strip() for r in rest]
+    assert members == fields
+
+
 def test_host_only_helpers():
     from ffa_mi355x import _native as N
 
