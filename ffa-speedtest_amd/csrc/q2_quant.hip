@@ -332,10 +332,10 @@ extern "C" int ffa_q2_quantize_channel(const void *k, int k_dtype, int B, int T,
                               (hipStream_t)stream);
 }
 
-extern "C" int ffa_kproj_rope_q2_channel(const void *h, const void *w_k, const void *bias, int h_dtype, const void *cos,
-                                         const void *sin, int cs_dtype, int B, int T, int H, int HKV, int D,
-                                         void *k_scratch, uint8_t *k_q, void *scale, void *zero, uint8_t *residual,
-                                         int res_dtype, float *minmax, void *stream) {
+extern "C" int ffa_kproj_rope(const void *h, const void *w_k, const void *bias, int h_dtype, const void *cos,
+                              const void *sin, int cs_dtype, int B, int T, int H, int HKV, int D, void *k_out,
+                              void *stream) {
+  if (B <= 0 || T <= 0 || H <= 0 || HKV <= 0 || D <= 0) return ffa_set_error_internal(FFA_E_INVALID, "bad dims");
   if (!(h_dtype == FFA_DT_F16 || h_dtype == FFA_DT_BF16))
     return ffa_set_error_internal(FFA_E_UNSUPPORTED, "h must be fp16 or bf16");
   if (!(cs_dtype == FFA_DT_F32 || cs_dtype == h_dtype))
@@ -347,13 +347,26 @@ extern "C" int ffa_kproj_rope_q2_channel(const void *h, const void *w_k, const v
   dim3 grid(N / 128, (M + 15) / 16);
   if (h_dtype == FFA_DT_BF16)
     hipLaunchKernelGGL(ffa::kproj_rope_kernel<FFA_DT_BF16>, grid, dim3(256), 0, st, h, w_k, bias, cos, sin, cs_dtype, M,
-                       T, H, N, D, k_scratch, odt);
+                       T, H, N, D, k_out, odt);
   else
     hipLaunchKernelGGL(ffa::kproj_rope_kernel<FFA_DT_F16>, grid, dim3(256), 0, st, h, w_k, bias, cos, sin, cs_dtype, M,
-                       T, H, N, D, k_scratch, odt);
+                       T, H, N, D, k_out, odt);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return ffa_set_error_internal(FFA_E_LAUNCH, hipGetErrorString(e));
-  return launch_quant_channel(k_scratch, odt, B, T, HKV, D, k_q, scale, zero, residual, res_dtype, minmax, st);
+  return FFA_OK;
+}
+
+extern "C" int ffa_kproj_rope_q2_channel(const void *h, const void *w_k, const void *bias, int h_dtype, const void *cos,
+                                         const void *sin, int cs_dtype, int B, int T, int H, int HKV, int D,
+                                         void *k_scratch, uint8_t *k_q, void *scale, void *zero, uint8_t *residual,
+                                         int res_dtype, float *minmax, void *stream) {
+  if (!(res_dtype == FFA_DT_FP8_E4M3 || res_dtype == FFA_DT_FP8_E5M2))
+    return ffa_set_error_internal(FFA_E_INVALID, "residual dtype must be fp8");
+  const int rc = ffa_kproj_rope(h, w_k, bias, h_dtype, cos, sin, cs_dtype, B, T, H, HKV, D, k_scratch, stream);
+  if (rc != FFA_OK) return rc;
+  const int odt = cs_dtype == FFA_DT_F32 ? FFA_DT_F32 : h_dtype;
+  return launch_quant_channel(k_scratch, odt, B, T, HKV, D, k_q, scale, zero, residual, res_dtype, minmax,
+                              (hipStream_t)stream);
 }
 
 extern "C" int ffa_kproj_rope_q2_append(const void *h, const void *w_k, const void *bias, int h_dtype, const float *cos,

@@ -31,6 +31,11 @@ EXPORTS = (
     "ffa_kproj_rope_q2_channel",
     "ffa_kproj_rope_q2_append",
     "ffa_q2_quantize_g32_append",
+    "ffa_kproj_rope",
+    "ffa_fp8fp8_quantize",
+    "ffa_nvfp4_quantize",
+    "ffa_nf4_quantize_nsplit",
+    "ffa_nf4_quantize",
     "ffa_last_error",
     "ffa_version",
 )
@@ -164,6 +169,16 @@ def lib() -> ctypes.CDLL:
         L.ffa_kproj_rope_q2_append.restype = ci
         L.ffa_q2_quantize_g32_append.argtypes = [vp, ci, ci, ci, ci, vp, vp, ci, vp, vp, vp, vp, ci, vp, vp, vp]
         L.ffa_q2_quantize_g32_append.restype = ci
+        L.ffa_kproj_rope.argtypes = [vp, vp, vp, ci, vp, vp, ci, ci, ci, ci, ci, ci, vp, vp]
+        L.ffa_kproj_rope.restype = ci
+        L.ffa_fp8fp8_quantize.argtypes = [vp, ci, ctypes.c_size_t, vp, vp, ci, vp]
+        L.ffa_fp8fp8_quantize.restype = ci
+        L.ffa_nvfp4_quantize.argtypes = [vp, ci, ci, ci, ci, ci, ci, vp, vp, vp, ci, vp]
+        L.ffa_nvfp4_quantize.restype = ci
+        L.ffa_nf4_quantize_nsplit.argtypes = [ci]
+        L.ffa_nf4_quantize_nsplit.restype = ci
+        L.ffa_nf4_quantize.argtypes = [vp, ci, ci, ci, ci, ci, vp, vp, vp, ci, vp, vp]
+        L.ffa_nf4_quantize.restype = ci
         _lib = L
         return _lib
 

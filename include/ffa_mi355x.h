@@ -27,10 +27,22 @@
  *                             K-proj + RoPE + g32 quantize into the paged cache
  *                             (incremental quantisation is a TODO in the reference,
  *                              ffa-q2fp8/OPTIMIZATION_NOTES.md:23-26)
+ *   ffa_kproj_rope            F.linear + apply_rope of every reference producer, e.g.
+ *                             ffa-fp8fp8/fused_kproj_rope_fp8fp8.py:80-88,
+ *                             ffa-nvfp4fp8/fused_kproj_rope_nvfp4fp8.py:131-139,
+ *                             ffa-nf4fp8/fused_kproj_rope_nf4fp8.py:428-436
+ *   ffa_fp8fp8_quantize       ffa-fp8fp8/fused_kproj_rope_fp8fp8.py:58-64
+ *                             (quantize_k_fp8_fp8_residual)
+ *   ffa_nvfp4_quantize        ffa-nvfp4fp8/fused_kproj_rope_nvfp4fp8.py:62-114
+ *                             (encode_k_nvfp4_fp8_residual)
+ *   ffa_nf4_quantize          ffa-nf4fp8/fused_kproj_rope_nf4fp8.py:72-96
+ *                             (encode_k_nf4_fp8_residual; the Triton producer
+ *                              kproj_rope_nf4_triton :440-558 is ffa_kproj_rope + this)
  */
 #ifndef FFA_MI355X_H
 #define FFA_MI355X_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -175,6 +187,32 @@ int ffa_q2_quantize_g32_append(const void *k, int k_dtype, int B, int Tn, int HK
                                const int32_t *block_table, int bt_stride, uint8_t *k_q_pages, void *scale_pages,
                                void *zero_pages, uint8_t *res_pages, int res_dtype, const void *v_new, void *v_pages,
                                void *stream);
+
+/*
+ * K projection + RoPE without quantization (the first half of every producer):
+ *   k_out [B, T, HKV, D] in the promoted dtype of h and cos (F32 when cs_dtype is F32,
+ *   else h_dtype); same arithmetic as ffa_kproj_rope_q2_channel's k_scratch.
+ */
+int ffa_kproj_rope(const void *h, const void *w_k, const void *bias, int h_dtype, const void *cos, const void *sin,
+                   int cs_dtype, int B, int T, int H, int HKV, int D, void *k_out, void *stream);
+
+/*
+ * Quantizers of the other K formats (reference layouts), bit-exact with the reference's
+ * torch op sequences; k has dtype k_dtype (F16/BF16/F32), contiguous.
+ *   fp8fp8: n elements -> base, residual (fp8_dtype FP8_E4M3/E5M2), same shape as k.
+ *   nvfp4:  k [B, T, HKV, D] -> k_packed [B, T, HKV, ceil(D/2)] (low nibble first),
+ *           scale [B, ceil(T/page_size), HKV] (k_dtype), residual [B, T, HKV, D] fp8.
+ *   nf4:    k [B, T, HKV, D] -> k_packed [B, T, HKV, ceil(D/2)], scale [B, HKV, D]
+ *           (k_dtype), residual; scratch absmax f32 [B, nsplit, HKV*D] with
+ *           nsplit = ffa_nf4_quantize_nsplit(T).
+ */
+int ffa_fp8fp8_quantize(const void *k, int k_dtype, size_t n, uint8_t *base, uint8_t *residual, int fp8_dtype,
+                        void *stream);
+int ffa_nvfp4_quantize(const void *k, int k_dtype, int B, int T, int HKV, int D, int page_size, uint8_t *k_packed,
+                       void *scale, uint8_t *residual, int res_dtype, void *stream);
+int ffa_nf4_quantize_nsplit(int T);
+int ffa_nf4_quantize(const void *k, int k_dtype, int B, int T, int HKV, int D, uint8_t *k_packed, void *scale,
+                     uint8_t *residual, int res_dtype, float *absmax, void *stream);
 
 /*
  * Pruned decode for the other K formats of the reference (contiguous [B, T, HKV, row]

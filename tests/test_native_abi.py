@@ -4,6 +4,7 @@ import inspect
 import re
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
@@ -177,3 +178,61 @@ def test_nvfp4_scale_normalisation_quirk():
     assert torch.equal(mod._normalize_k_scale(s.permute(0, 2, 1).contiguous(), (2, 9, 8)), s)
     sq = torch.arange(2 * 8 * 8, dtype=torch.float32).reshape(2, 8, 8)  # NTB == HKV == 8
     assert torch.equal(mod._normalize_k_scale(sq, (2, 8, 8)), sq.permute(0, 2, 1))
+
+
+def _load_dropin(rel, name):
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location(name, ROOT / "ffa-speedtest_amd" / rel)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_other_format_producer_signatures():
+    """Producer drop-ins keep the reference names, parameter order and defaults
+    (F8F:58-135, NVF:62-190, NFF:72-96, 415-580)."""
+    f8 = _load_dropin("ffa-fp8fp8/fused_kproj_rope_fp8fp8.py", "prod_fp8fp8")
+    nv = _load_dropin("ffa-nvfp4fp8/fused_kproj_rope_nvfp4fp8.py", "prod_nvfp4")
+    nf = _load_dropin("ffa-nf4fp8/fused_kproj_rope_nf4fp8.py", "prod_nf4")
+    head = ["h", "w_k", "cos", "sin", "num_kv_heads", "head_dim"]
+    for fn in (f8.kproj_rope_quantize_reference, f8.kproj_rope_quantize_fused, nf.kproj_rope_nf4_reference,
+               nf.kproj_rope_nf4_fused):
+        assert list(inspect.signature(fn).parameters) == head + ["bias", "fp8_dtype"]
+    for fn in (nv.kproj_rope_quantize_reference, nv.kproj_rope_quantize_fused):
+        assert list(inspect.signature(fn).parameters) == head + ["page_size", "bias", "fp8_dtype"]
+    assert list(inspect.signature(nf.kproj_rope_nf4_triton).parameters) == head + [
+        "bias", "fp8_dtype", "block_t", "block_h", "block_pair", "num_warps", "num_stages"]
+    assert list(inspect.signature(f8.quantize_k_fp8_fp8_residual).parameters) == ["k", "fp8_dtype"]
+    assert list(inspect.signature(nv.encode_k_nvfp4_fp8_residual).parameters) == ["k", "fp8_dtype", "page_size"]
+    assert list(inspect.signature(nf.encode_k_nf4_fp8_residual).parameters) == ["k", "fp8_dtype"]
+    # the codebook literal is the published NF4 table: 16 increasing levels from -1 to 1 with 0 at index 7
+    cb = nf.NF4_CODEBOOK_VALUES
+    assert len(cb) == 16 and cb[0] == -1.0 and cb[7] == 0.0 and cb[15] == 1.0
+    assert all(a < b for a, b in zip(cb, cb[1:]))
+    from oracle import formats as OF
+
+    assert np.array_equal(np.array(cb, np.float32), OF.NF4_CODEBOOK)
+
+
+def test_rope_helpers_closed_form():
+    """build_rope_cache / rotate_half / apply_rope: angle t * base^(-2i/D) for channels i and i + D/2,
+    interleaved pair rotation, and a rotation preserves each pair's norm."""
+    import torch
+
+    from ffa_mi355x import rope
+
+    T, D = 7, 8
+    cos, sin = rope.build_rope_cache(T, D, base=500000.0)
+    i = np.arange(D) % (D // 2)
+    ang = np.arange(T)[:, None] * (1.0 / 500000.0 ** (2.0 * i / D))[None, :]
+    assert np.allclose(cos.numpy(), np.cos(ang), atol=1e-6) and np.allclose(sin.numpy(), np.sin(ang), atol=1e-6)
+    x = torch.arange(1, 9, dtype=torch.float32).view(1, 1, 1, 8)
+    assert rope.rotate_half(x).flatten().tolist() == [-2, 1, -4, 3, -6, 5, -8, 7]
+    xr = torch.randn(2, T, 3, D)
+    y = rope.apply_rope(xr, cos, sin)
+    # pairs (2j, 2j+1) use angles of channels 2j and 2j+1; with equal angles a pair keeps its norm
+    c2, s2 = rope.build_rope_cache(T, 2)
+    y2 = rope.apply_rope(xr[..., :2], c2, s2)
+    assert torch.allclose(y2.norm(dim=-1), xr[..., :2].norm(dim=-1), atol=1e-5)
+    assert y.shape == xr.shape
