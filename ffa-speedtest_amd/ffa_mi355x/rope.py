@@ -4,6 +4,8 @@ All four reference producers define the same three functions
 (ffa-q2fp8/fused_kproj_rope_q2fp8.py:10-37, ffa-fp8fp8/fused_kproj_rope_fp8fp8.py:8-35,
 ffa-nvfp4fp8/fused_kproj_rope_nvfp4fp8.py:12-39, ffa-nf4fp8/fused_kproj_rope_nf4fp8.py:42-69);
 they are part of each module's interface, so the drop-ins re-export these.
+`rope_rows` gives the same angles for arbitrary positions in fp32 (the paged append's
+cos/sin rows), so positions above 65504 (fp16's range) stay exact.
 """
 from __future__ import annotations
 
@@ -42,3 +44,11 @@ def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.T
         cos = cos[None, :, None, :]
         sin = sin[None, :, None, :]
     return (x * cos) + (rotate_half(x) * sin)
+
+
+def rope_rows(positions: torch.Tensor, head_dim: int = 128, base: float = 10000.0):
+    """positions [...] int -> (cos, sin) [..., head_dim] fp32 (same frequencies as build_rope_cache)."""
+    inv = 1.0 / (base ** (torch.arange(0, head_dim, 2, dtype=torch.float32, device=positions.device) / head_dim))
+    ang = positions.to(torch.float32)[..., None] * inv
+    emb = torch.cat([ang, ang], dim=-1)
+    return emb.cos(), emb.sin()

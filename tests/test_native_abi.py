@@ -236,3 +236,6 @@ def test_rope_helpers_closed_form():
     y2 = rope.apply_rope(xr[..., :2], c2, s2)
     assert torch.allclose(y2.norm(dim=-1), xr[..., :2].norm(dim=-1), atol=1e-5)
     assert y.shape == xr.shape
+    # rope_rows: the rows of build_rope_cache's table at the given positions (fp32 angles)
+    cr, sr = rope.rope_rows(torch.tensor([0, 3, 6]), head_dim=D, base=500000.0)
+    assert torch.allclose(cr, cos[[0, 3, 6]], atol=1e-6) and torch.allclose(sr, sin[[0, 3, 6]], atol=1e-6)
