@@ -2,15 +2,19 @@
 //   fp8 base + fp8 residual   ffa-fp8fp8/attn_kernel/attn_kernel_v1210_fused_bsz_fp8fp8.py:10-136
 //   nvfp4 (e2m1 x block scale) ffa-nvfp4fp8/attn_kernel/attn_kernel_v1210_fused_bsz_nvfp4fp8.py:10-169
 //   nf4 (codebook x channel)  ffa-nf4fp8/attn_kernel/attn_kernel_v1210_fused_bsz_nf4fp8.py:41-167
-// and the BASELINE config-1 variant of the fp8 base with one fp16 scale per token and KV head.
+// and the BASELINE config-1 variant of the fp8 base with one fp16 scale per token and KV head,
+// plus the BASELINE paged modes of configs 3 and 4 (no reference counterpart): nvfp4 with one
+// e4m3 scale per 16 channels of each token, nf4 with one fp16 scale per 64 channels, in
+// 64-token pages (codes [P, HKV, 64, 64], scales [P, HKV, 64, 8 | 2], residual [P, HKV, 64, 128],
+// V^T [P, HKV, 128, 64]) read through a block table.
 //
 // Every format dequantizes to the fp16 K the reference feeds its dot products,
 // k_hat = fp16(f32(value) * f32(scale)), and then follows the q2fp8 path: the probe
 // threshold (nvfp4 scores its second probe window with the scale of block NTB-1,
 // :96-97), group prune, refined K fp16(k_hat + fp16(res)), exp2 softmax, P.V, and the
 // shared log-sum-exp merge kernel.  Contiguous token-major layouts as in the reference
-// ([B, T, HKV, row]); one workgroup = 4 waves = 8 chunks of 64 tokens of one
-// (sequence, KV head), the partial layout of the q2fp8 kernel.
+// ([B, T, HKV, row]) or the pages above; one workgroup = 4 waves = 8 chunks of 64 tokens
+// of one (sequence, KV head), the partial layout of the q2fp8 kernel.
 //
 // MFMA layout (as the q2fp8 kernel's per-channel mode): rows of a 16x16x32 f16 MFMA are
 // tokens (row m of tile tau = token 4m + tau), the lane of k-chunk kc holds channels
@@ -27,7 +31,7 @@ extern "C" int ffa_set_error_internal(int code, const char *msg);
 namespace ffa {
 
 enum { kF8E4M3 = 0, kF8E5M2 = 1, kFP4 = 2, kNF4 = 3 };
-enum { kSclNone = 0, kSclToken = 1, kSclBlock = 2, kSclChannel = 3 };
+enum { kSclNone = 0, kSclToken = 1, kSclBlock = 2, kSclChannel = 3, kSclG16 = 4, kSclG64 = 5 };
 
 // QLoRA NF4 levels (the published 16 normal-float values), as fp32
 __constant__ float kNF4Levels[16] = {
@@ -56,10 +60,14 @@ __device__ __forceinline__ float load_scale(brsrc rs, uint32_t i, int dt) {
   return dt == 2 ? __uint_as_float(bits) : (dt == 1 ? bf16_bits_to_f32(bits) : f16_bits_to_f32(bits));
 }
 
-template <int FMT, int SCL, int RES, int VT>
+template <int LAYOUT, int FMT, int SCL, int RES, int VT>
 __global__ __launch_bounds__(256) void kfmt_decode_kernel(const DecodeParams p) {
   typedef VTraits<VT> VTr;
   constexpr bool k4 = FMT == kFP4 || FMT == kNF4;
+  constexpr bool kGrp = SCL == kSclG16 || SCL == kSclG64;  // per-token group scales (paged modes)
+  static_assert(kGrp == (LAYOUT == kPaged), "group scales go with the paged layout");
+  static_assert(SCL != kSclG16 || FMT == kFP4, "g16 scales are nvfp4's");
+  static_assert(SCL != kSclG64 || FMT == kNF4, "g64 scales are nf4's");
   constexpr int kRow = k4 ? 64 : 128;  // K bytes of one token and KV head
   constexpr int kLane = kRow / 4;      // bytes of one lane's 32 channels
   const int lane = threadIdx.x & 63;
@@ -88,7 +96,7 @@ __global__ __launch_bounds__(256) void kfmt_decode_kernel(const DecodeParams p) 
   __shared__ float s_pm[kChunksPerWG][4], s_pl[kChunksPerWG][4];
   __shared__ float s_po[kChunksPerWG][4][128];
   __shared__ float s_cb[16];
-  __shared__ uint8_t s_vstage[kWaves * kPage * kVRow];
+  __shared__ uint8_t s_vstage[LAYOUT == kContig ? kWaves * kPage * kVRow : 4];
 
   auto lds_barrier = []() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
 
@@ -103,6 +111,14 @@ __global__ __launch_bounds__(256) void kfmt_decode_kernel(const DecodeParams p) 
 #pragma unroll
   for (int j = 0; j < kPPW; ++j) nv[j] = min(max(Tb - (c0 + j) * kPage, 0), kPage);
 
+  uint32_t pg_lane = 0;
+  if constexpr (LAYOUT == kPaged) {
+    // page ids: one vector load per wave, issued first (lanes 0, 1: the wave's chunks, lane 2: its
+    // probe window; the other lanes read past the resource and get 0)
+    const bool need = lane < kPPW ? nv[lane & 1] > 0 : (lane == kPPW && do_probe && pa < Tb);
+    const int idx = lane < kPPW ? c0 + lane : (pa >> 6);
+    pg_lane = bload4(make_rsrc(p.bt + (size_t)b * p.bt_stride, p.bt_stride * 4), need ? idx * 4 : p.bt_stride * 4);
+  }
   const uint32_t es_q = p.q_dtype == 2 ? 4u : 2u;
   const int hwin = wv >> 1;
   Raw16 qraw;
@@ -110,6 +126,30 @@ __global__ __launch_bounds__(256) void kfmt_decode_kernel(const DecodeParams p) 
              (hq * kD + 32 * kc + 16 * hwin) * es_q);
   const float th_pre = __uint_as_float(
       bload8(make_rsrc(p.th_in + (p.th_in ? (size_t)b * p.HQ : 0), p.th_in ? p.HQ * 4 : 0), hq * 4).x);
+  int pg[kPPW] = {0, 0};
+  int ppg = 0;
+  if constexpr (LAYOUT == kPaged) {
+    __builtin_amdgcn_sched_barrier(0);  // the q loads go out before the wait for the page ids
+#pragma unroll
+    for (int j = 0; j < kPPW; ++j) pg[j] = __builtin_amdgcn_readlane(pg_lane, j);
+    ppg = __builtin_amdgcn_readlane(pg_lane, kPPW);
+  }
+  // pool block (page, head) of the paged layout: kPage rows of kRow bytes
+  auto page_rows = [&](const uint8_t *pool, int page, int row_bytes, bool valid) -> brsrc {
+    return make_rsrc(pool + ((size_t)page * p.HKV + hkv) * kPage * row_bytes, valid ? kPage * row_bytes : 0);
+  };
+  // group scales of the lane's 32 channels for one token of a page: (scale of channels
+  // [32kc, 32kc + 16), scale of [32kc + 16, 32kc + 32)) -- e4m3 per 16 channels, or fp16 per 64
+  auto group_scales = [&](const brsrc &rs, int tok) -> f32x2 {
+    if constexpr (SCL == kSclG16) {
+      const uint32_t w = bload4(rs, tok * 8 + 4 * (kc >> 1));
+      return fp8pair_f32<true, false>((kc & 1) ? (w >> 16) : w);
+    } else {
+      const uint32_t w = bload4(rs, tok * 4);
+      const float sc = f16_bits_to_f32((kc >> 1) ? (w >> 16) : (w & 0xffffu));
+      return f32x2{sc, sc};
+    }
+  };
   // per-channel scales of the lane's 32 channels (nf4): eight 16-byte loads whatever the dtype
   float sch[32];
   if constexpr (SCL == kSclChannel) {
@@ -144,32 +184,55 @@ __global__ __launch_bounds__(256) void kfmt_decode_kernel(const DecodeParams p) 
   };
   // probe tile: MFMA row m <-> token pa + m
   uint4 pxa, pxb = make_uint4(0, 0, 0, 0);
-  float psc;
+  float psc = 1.f;
+  f32x2 pgs = {1.f, 1.f};
   {
     const bool pv = do_probe && pa < Tb;
-    const int nt = pv ? min(16, Tb - pa) : 0;
-    const brsrc rc = make_rsrc(p.kq + (((size_t)b * p.T + pa) * p.HKV + hkv) * kRow, nt > 0 ? ((nt - 1) * p.HKV + 1) * kRow : 0);
-    const uint32_t off = mrow * p.HKV * kRow + kLane * kc;
-    pxa = bload16(rc, off);
-    if constexpr (!k4) pxb = bload16(rc, off + 16);
-    // nvfp4: window 0 uses block 0's scale, window 1 block NTB-1's (attn_kernel...nvfp4fp8.py:86-97)
-    psc = tok_scale(pa + mrow, wv == 0 ? 0 : max(NTB - 1, 0));
+    if constexpr (LAYOUT == kPaged) {
+      // the 16 window tokens lie in one page (pa is a multiple of 16); rows past the sequence
+      // end hold no data, their scores are masked below
+      const int tok = (pa & (kPage - 1)) + mrow;
+      pxa = bload16(page_rows(p.kq, ppg, kRow, pv), tok * kRow + kLane * kc);
+      pgs = group_scales(page_rows((const uint8_t *)p.ks, ppg, SCL == kSclG16 ? 8 : 4, pv), tok);
+    } else {
+      const int nt = pv ? min(16, Tb - pa) : 0;
+      const brsrc rc = make_rsrc(p.kq + (((size_t)b * p.T + pa) * p.HKV + hkv) * kRow, nt > 0 ? ((nt - 1) * p.HKV + 1) * kRow : 0);
+      const uint32_t off = mrow * p.HKV * kRow + kLane * kc;
+      pxa = bload16(rc, off);
+      if constexpr (!k4) pxb = bload16(rc, off + 16);
+      // nvfp4: window 0 uses block 0's scale, window 1 block NTB-1's (attn_kernel...nvfp4fp8.py:86-97)
+      psc = tok_scale(pa + mrow, wv == 0 ? 0 : max(NTB - 1, 0));
+    }
   }
   uint4 xa[kPPW][4], xb[kPPW][4];
   float xs[kPPW][4];
+  f32x2 xg[kPPW][4];  // group scales (paged modes)
 #pragma unroll
   for (int j = 0; j < kPPW; ++j) {
     const int t0 = (c0 + j) * kPage;
-    const brsrc rc = make_rsrc(p.kq + (((size_t)b * p.T + t0) * p.HKV + hkv) * kRow,
-                               nv[j] > 0 ? ((nv[j] - 1) * p.HKV + 1) * kRow : 0);
+    if constexpr (LAYOUT == kPaged) {
+      const brsrc rc = page_rows(p.kq, pg[j], kRow, nv[j] > 0);
+      const brsrc rs = page_rows((const uint8_t *)p.ks, pg[j], SCL == kSclG16 ? 8 : 4, nv[j] > 0);
 #pragma unroll
-    for (int tau = 0; tau < 4; ++tau) {
-      const uint32_t off = (4 * mrow + tau) * p.HKV * kRow + kLane * kc;
-      xa[j][tau] = bload16(rc, off);
-      xb[j][tau] = make_uint4(0, 0, 0, 0);
-      if constexpr (!k4) xb[j][tau] = bload16(rc, off + 16);
-      const int t = t0 + 4 * mrow + tau;
-      xs[j][tau] = tok_scale(t, min(t, max(Tb - 1, 0)) / p.BS);
+      for (int tau = 0; tau < 4; ++tau) {
+        xa[j][tau] = bload16(rc, (4 * mrow + tau) * kRow + kLane * kc);
+        xb[j][tau] = make_uint4(0, 0, 0, 0);
+        xs[j][tau] = 1.f;
+        xg[j][tau] = group_scales(rs, 4 * mrow + tau);
+      }
+    } else {
+      const brsrc rc = make_rsrc(p.kq + (((size_t)b * p.T + t0) * p.HKV + hkv) * kRow,
+                                 nv[j] > 0 ? ((nv[j] - 1) * p.HKV + 1) * kRow : 0);
+#pragma unroll
+      for (int tau = 0; tau < 4; ++tau) {
+        const uint32_t off = (4 * mrow + tau) * p.HKV * kRow + kLane * kc;
+        xa[j][tau] = bload16(rc, off);
+        xb[j][tau] = make_uint4(0, 0, 0, 0);
+        if constexpr (!k4) xb[j][tau] = bload16(rc, off + 16);
+        const int t = t0 + 4 * mrow + tau;
+        xs[j][tau] = tok_scale(t, min(t, max(Tb - 1, 0)) / p.BS);
+        xg[j][tau] = f32x2{1.f, 1.f};
+      }
     }
   }
   if constexpr (FMT == kNF4) {
@@ -206,8 +269,9 @@ __global__ __launch_bounds__(256) void kfmt_decode_kernel(const DecodeParams p) 
   }
 
   // fp16 K of MFMA m' (channels 32kc + 8m' + e) from the lane's row bytes
-  auto dequant = [&](const uint4 &a, const uint4 &bq, int mp, float sc) -> f16x8 {
+  auto dequant = [&](const uint4 &a, const uint4 &bq, int mp, float sc, f32x2 gs) -> f16x8 {
     u32x4 r;
+    if constexpr (kGrp) sc = mp < 2 ? gs[0] : gs[1];  // channels 32kc + 8mp + e lie in the first or second half
     if constexpr (!k4) {
       const uint4 &src = mp < 2 ? a : bq;
       const uint32_t lo = (mp & 1) ? src.z : src.x, hi = (mp & 1) ? src.w : src.y;
@@ -238,19 +302,18 @@ __global__ __launch_bounds__(256) void kfmt_decode_kernel(const DecodeParams p) 
       for (int h = 0; h < 4; ++h) {
         if constexpr (FMT == kNF4) {
           const uint32_t byte = (w >> (8 * h)) & 0xffu;
-          const float v0 = s_cb[byte & 15u] * sch[8 * mp + 2 * h];
-          const float v1 = s_cb[byte >> 4] * sch[8 * mp + 2 * h + 1];
-          r[h] = pack_f16(v0, v1);
+          const float s0 = kGrp ? sc : sch[8 * mp + 2 * h], s1 = kGrp ? sc : sch[8 * mp + 2 * h + 1];
+          r[h] = pack_f16(s_cb[byte & 15u] * s0, s_cb[byte >> 4] * s1);
         }
       }
     }
     return __builtin_bit_cast(f16x8, r);
   };
   // dot products of one 16-token tile with the lane's column, summed over the four groups
-  auto score_tile = [&](const uint4 &a, const uint4 &bq, float sc, float *out) {
+  auto score_tile = [&](const uint4 &a, const uint4 &bq, float sc, f32x2 gs, float *out) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int mp = 0; mp < 4; ++mp) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant(a, bq, mp, sc), qa[mp], acc, 0, 0, 0);
+    for (int mp = 0; mp < 4; ++mp) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant(a, bq, mp, sc, gs), qa[mp], acc, 0, 0, 0);
 #pragma unroll
     for (int uu = 0; uu < 4; ++uu) {
       float r = acc[uu];
@@ -267,7 +330,7 @@ __global__ __launch_bounds__(256) void kfmt_decode_kernel(const DecodeParams p) 
   float th = INFINITY;
   if (do_probe) {
     float r4[4];
-    score_tile(pxa, pxb, psc, r4);
+    score_tile(pxa, pxb, psc, pgs, r4);
     float mx = -INFINITY;
 #pragma unroll
     for (int uu = 0; uu < 4; ++uu) {
@@ -286,7 +349,7 @@ __global__ __launch_bounds__(256) void kfmt_decode_kernel(const DecodeParams p) 
 #pragma unroll
       for (int tau = 0; tau < 4; ++tau) {
         float r4[4];
-        score_tile(xa[j][tau], xb[j][tau], xs[j][tau], r4);
+        score_tile(xa[j][tau], xb[j][tau], xs[j][tau], xg[j][tau], r4);
 #pragma unroll
         for (int uu = 0; uu < 4; ++uu) R[j][4 * uu + tau] = r4[uu];
       }
@@ -353,15 +416,25 @@ __global__ __launch_bounds__(256) void kfmt_decode_kernel(const DecodeParams p) 
     uint4 rr[4][2];
     uint4 vv[8][2];
     if constexpr (RES != kResNone) {
-      const brsrc rs = make_rsrc(p.kr + (((size_t)b * p.T + t0) * p.HKV + hkv) * kD, ((nvs - 1) * p.HKV + 1) * kD);
+      const brsrc rs = LAYOUT == kPaged ? page_rows(p.kr, pg[j], kD, true)
+                                        : make_rsrc(p.kr + (((size_t)b * p.T + t0) * p.HKV + hkv) * kD,
+                                                    ((nvs - 1) * p.HKV + 1) * kD);
+      const uint32_t rstride = LAYOUT == kPaged ? kD : p.HKV * kD;
 #pragma unroll
       for (int tau = 0; tau < 4; ++tau) {
-        const uint32_t off = (4 * mrow + tau) * p.HKV * kD + 32 * kc;
+        const uint32_t off = (4 * mrow + tau) * rstride + 32 * kc;
         rr[tau][0] = bload16(rs, off);
         rr[tau][1] = bload16(rs, off + 16);
       }
     }
-    {
+    if constexpr (LAYOUT == kPaged) {
+      // V^T page [128][64]: lane (n, kc) reads column 16 nu + n, tokens 16 kc + 8 kap .. + 8
+      const brsrc vs = make_rsrc((const uint16_t *)p.v + ((size_t)pg[j] * p.HKV + hkv) * (kD * kPage), kD * kPage * 2);
+#pragma unroll
+      for (int nu = 0; nu < 8; ++nu)
+#pragma unroll
+        for (int kap = 0; kap < 2; ++kap) vv[nu][kap] = bload16(vs, ((16 * nu + n) * kPage + 16 * kc + 8 * kap) * 2);
+    } else {
       const brsrc vs = make_rsrc((const uint16_t *)p.v + (((size_t)b * p.T + t0) * p.HKV + hkv) * kD,
                                  ((nvs - 1) * p.HKV + 1) * kD * 2);
 #pragma unroll
@@ -384,7 +457,7 @@ __global__ __launch_bounds__(256) void kfmt_decode_kernel(const DecodeParams p) 
           const uint4 &rs4 = rr[tau][mp >> 1];
           const uint32_t lo = (mp & 1) ? rs4.z : rs4.x, hi = (mp & 1) ? rs4.w : rs4.y;
           acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-              add_f16x8(dequant(xa[j][tau], xb[j][tau], mp, xs[j][tau]), fp8x8_to_f16x8<RES>(lo, hi)), qa[mp], acc, 0, 0, 0);
+              add_f16x8(dequant(xa[j][tau], xb[j][tau], mp, xs[j][tau], xg[j][tau]), fp8x8_to_f16x8<RES>(lo, hi)), qa[mp], acc, 0, 0, 0);
         }
 #pragma unroll
         for (int uu = 0; uu < 4; ++uu) {
@@ -426,6 +499,29 @@ __global__ __launch_bounds__(256) void kfmt_decode_kernel(const DecodeParams p) 
     f32x4 oacc[8];
 #pragma unroll
     for (int nu = 0; nu < 8; ++nu) oacc[nu] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (LAYOUT == kPaged) {
+      const bool partial = nvs < kPage;
+#pragma unroll
+      for (int nu = 0; nu < 8; ++nu) {
+#pragma unroll
+        for (int kap = 0; kap < 2; ++kap) {
+          uint4 v4 = vv[nu][kap];
+          if (partial) {
+            // V of page slots past the sequence end is not data: zero it
+            const int tk = 16 * kc + 8 * kap;
+            uint32_t w4[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              if (tk + 2 * e >= nvs) w4[e] &= 0xffff0000u;
+              if (tk + 2 * e + 1 >= nvs) w4[e] &= 0x0000ffffu;
+            }
+            v4 = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+          }
+          const u32x4 w = {v4.x, v4.y, v4.z, v4.w};
+          oacc[nu] = VTr::mfma(pa2[kap], __builtin_bit_cast(typename VTr::vec, w), oacc[nu]);
+        }
+      }
+    } else {
     // stage the V tile [64 tokens][128] through LDS (rows past the sequence end were loaded as zeros)
     uint8_t *st = s_vstage + wv * kPage * kVRow;
 #pragma unroll
@@ -461,6 +557,7 @@ __global__ __launch_bounds__(256) void kfmt_decode_kernel(const DecodeParams p) 
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
     if (lane < 16) {
 #pragma unroll
       for (int uu = 0; uu < 4; ++uu)
@@ -540,18 +637,18 @@ __global__ __launch_bounds__(256) void kfmt_decode_kernel(const DecodeParams p) 
 // --------------------------------------------------------------------------
 // C ABI
 // --------------------------------------------------------------------------
-template <int F, int S, int R, int V>
+template <int L, int F, int S, int R, int V>
 static hipError_t kfmt_launch(const ffa::DecodeParams &p, dim3 grid, hipStream_t st) {
-  hipLaunchKernelGGL((ffa::kfmt_decode_kernel<F, S, R, V>), grid, dim3(256), 0, st, p);
+  hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V>), grid, dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
-template <int F, int S>
+template <int L, int F, int S>
 static hipError_t kfmt_dispatch_rv(const ffa::DecodeParams &p, int res, int vdt, dim3 grid, hipStream_t st) {
   const int r = res == FFA_DT_FP8_E4M3 ? ffa::kResE4M3 : (res == FFA_DT_FP8_E5M2 ? ffa::kResE5M2 : ffa::kResNone);
   const int v = vdt == FFA_DT_BF16 ? ffa::kVBF16 : ffa::kVF16;
 #define FFA_CASE(RR, VV) \
-  if (r == RR && v == VV) return kfmt_launch<F, S, RR, VV>(p, grid, st);
+  if (r == RR && v == VV) return kfmt_launch<L, F, S, RR, VV>(p, grid, st);
   FFA_CASE(ffa::kResE4M3, ffa::kVBF16)
   FFA_CASE(ffa::kResE4M3, ffa::kVF16)
   FFA_CASE(ffa::kResE5M2, ffa::kVBF16)
@@ -587,6 +684,12 @@ extern "C" int ffa_kfmt_decode(const ffa_kfmt_decode_args *a, void *stream) {
   if (a->nparts < need) return ffa_set_error_internal(FFA_E_INVALID, "scratch holds too few partial slots");
   const int ntbs = ((a->T + a->BS - 1) / a->BS) * (a->BS / a->SBS);
   if (a->ntbs < ntbs) return ffa_set_error_internal(FFA_E_INVALID, "mask holds too few blocks");
+  const bool paged = a->layout == FFA_LAYOUT_PAGED;
+  if (!paged && a->layout != FFA_LAYOUT_CONTIG) return ffa_set_error_internal(FFA_E_INVALID, "layout");
+  if (paged && !a->block_table) return ffa_set_error_internal(FFA_E_INVALID, "paged layout needs a block table");
+  if (paged != (a->scale_kind == FFA_KSCALE_G16 || a->scale_kind == FFA_KSCALE_G64))
+    return ffa_set_error_internal(FFA_E_UNSUPPORTED,
+                                  "the paged layout takes the per-token group scales (G16 / G64) and only it");
 
   ffa::DecodeParams p = {};
   p.q = a->q;
@@ -594,6 +697,8 @@ extern "C" int ffa_kfmt_decode(const ffa_kfmt_decode_args *a, void *stream) {
   p.ks = a->k_scale;
   p.kr = a->k_residual;
   p.v = a->v;
+  p.bt = a->block_table;
+  p.bt_stride = a->bt_stride;
   p.seq_lens = a->seq_lens;
   p.th_in = a->threshold_in;
   p.th_out = a->threshold_out;
@@ -622,18 +727,23 @@ extern "C" int ffa_kfmt_decode(const ffa_kfmt_decode_args *a, void *stream) {
   dim3 grid(need * a->B * a->HKV);
   hipError_t e = hipErrorInvalidValue;
   const int fmt = a->k_format, sk = a->scale_kind;
+  constexpr int C = ffa::kContig, PG = ffa::kPaged;
   if (fmt == FFA_KFMT_FP8_E4M3 && sk == FFA_KSCALE_NONE)
-    e = kfmt_dispatch_rv<ffa::kF8E4M3, ffa::kSclNone>(p, a->res_dtype, a->v_dtype, grid, st);
+    e = kfmt_dispatch_rv<C, ffa::kF8E4M3, ffa::kSclNone>(p, a->res_dtype, a->v_dtype, grid, st);
   else if (fmt == FFA_KFMT_FP8_E4M3 && sk == FFA_KSCALE_TOKEN)
-    e = kfmt_dispatch_rv<ffa::kF8E4M3, ffa::kSclToken>(p, a->res_dtype, a->v_dtype, grid, st);
+    e = kfmt_dispatch_rv<C, ffa::kF8E4M3, ffa::kSclToken>(p, a->res_dtype, a->v_dtype, grid, st);
   else if (fmt == FFA_KFMT_FP8_E5M2 && sk == FFA_KSCALE_NONE)
-    e = kfmt_dispatch_rv<ffa::kF8E5M2, ffa::kSclNone>(p, a->res_dtype, a->v_dtype, grid, st);
+    e = kfmt_dispatch_rv<C, ffa::kF8E5M2, ffa::kSclNone>(p, a->res_dtype, a->v_dtype, grid, st);
   else if (fmt == FFA_KFMT_FP8_E5M2 && sk == FFA_KSCALE_TOKEN)
-    e = kfmt_dispatch_rv<ffa::kF8E5M2, ffa::kSclToken>(p, a->res_dtype, a->v_dtype, grid, st);
+    e = kfmt_dispatch_rv<C, ffa::kF8E5M2, ffa::kSclToken>(p, a->res_dtype, a->v_dtype, grid, st);
   else if (fmt == FFA_KFMT_NVFP4 && sk == FFA_KSCALE_BLOCK)
-    e = kfmt_dispatch_rv<ffa::kFP4, ffa::kSclBlock>(p, a->res_dtype, a->v_dtype, grid, st);
+    e = kfmt_dispatch_rv<C, ffa::kFP4, ffa::kSclBlock>(p, a->res_dtype, a->v_dtype, grid, st);
   else if (fmt == FFA_KFMT_NF4 && sk == FFA_KSCALE_CHANNEL)
-    e = kfmt_dispatch_rv<ffa::kNF4, ffa::kSclChannel>(p, a->res_dtype, a->v_dtype, grid, st);
+    e = kfmt_dispatch_rv<C, ffa::kNF4, ffa::kSclChannel>(p, a->res_dtype, a->v_dtype, grid, st);
+  else if (fmt == FFA_KFMT_NVFP4 && sk == FFA_KSCALE_G16)
+    e = kfmt_dispatch_rv<PG, ffa::kFP4, ffa::kSclG16>(p, a->res_dtype, a->v_dtype, grid, st);
+  else if (fmt == FFA_KFMT_NF4 && sk == FFA_KSCALE_G64)
+    e = kfmt_dispatch_rv<PG, ffa::kNF4, ffa::kSclG64>(p, a->res_dtype, a->v_dtype, grid, st);
   else
     return ffa_set_error_internal(FFA_E_UNSUPPORTED, "unsupported K format / scale granularity combination");
   if (e != hipSuccess) return ffa_set_error_internal(FFA_E_LAUNCH, hipGetErrorString(e));

@@ -186,6 +186,80 @@ __global__ __launch_bounds__(256) void nf4_quant_kernel(const void *k, int kdt, 
   packed[row * DP + byte] = (uint8_t)pk;
 }
 
+// ---------------------------------------------------------------------------
+// BASELINE paged modes (no reference counterpart): quantize K rows and append them,
+// with V, into 64-token pages.  One thread per (token row, KV head, 16 channels);
+// the 8 threads of a row and head are consecutive lanes of one wave.
+//   nvfp4-g16: s = e4m3(min(amax16 / 6, 448)), x = k / s (0 where s == 0),
+//              code = #{e2m1 midpoints <= |x|} | sign << 3, residual = fp8(k - (+-level * s))
+//   nf4-g64:   s = fp16(max(amax64, 1e-6)), x = clamp(k / s, -1, 1),
+//              code = #{codebook midpoints < x}, residual = fp8(k - codebook[code] * s)
+// Pools: codes [P, HKV, 64, 64] u8 (token-major, low nibble first), scales [P, HKV, 64, 8] e4m3
+// (nvfp4) or [P, HKV, 64, 2] fp16 (nf4), residual [P, HKV, 64, 128] fp8, V^T [P, HKV, 128, 64].
+// ---------------------------------------------------------------------------
+template <bool NF4>
+__global__ __launch_bounds__(256) void kfmt_group_append_kernel(const void *k, int kdt, int M, int Tn, int HKV,
+                                                                 const int32_t *pos, const int32_t *bt, int bt_stride,
+                                                                 uint8_t *k_pages, void *s_pages, uint8_t *r_pages,
+                                                                 int res_e4m3, const void *v_new, void *v_pages) {
+  constexpr int D = 128;
+  const size_t id = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const bool live = id < (size_t)M * HKV * 8;  // whole groups of 8 lanes are live or not
+  const size_t idc = live ? id : 0;
+  const int c16 = (int)(idc & 7);
+  const int hkv = (int)((idc >> 3) % HKV);
+  const int m = (int)((idc >> 3) / HKV);
+  const int b = m / Tn, nn = m - b * Tn;
+  const int P = pos[b] + nn;
+  const int page = bt[(size_t)b * bt_stride + (P >> 6)];
+  const int slot = P & 63;
+  const size_t prow = ((size_t)page * HKV + hkv) * 64 + slot;  // (page, head, token) row of the pools
+  float kv[16];
+  float amax = 0.f;
+  for (int e = 0; e < 16; ++e) {
+    kv[e] = load_any(k, ((size_t)m * HKV + hkv) * D + 16 * c16 + e, kdt);
+    amax = fmaxf(amax, fabsf(kv[e]));
+  }
+  uint32_t cw[2] = {0u, 0u};
+  uint32_t rw[4] = {0u, 0u, 0u, 0u};
+  if constexpr (NF4) {
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    const float sc = (float)(_Float16)fmaxf(amax, 1e-6f);
+    for (int e = 0; e < 16; ++e) {
+      const float x = fminf(fmaxf(__fdiv_rn(kv[e], sc), -1.0f), 1.0f);
+      int idx = 0;
+#pragma unroll
+      for (int j = 0; j < 15; ++j) idx += ((kNF4Book[j] + kNF4Book[j + 1]) * 0.5f < x) ? 1 : 0;
+      rw[e >> 2] |= f32_to_fp8(kv[e] - kNF4Book[idx] * sc, res_e4m3) << (8 * (e & 3));
+      cw[e >> 3] |= (uint32_t)idx << (4 * (e & 7));
+    }
+    if (live && (c16 & 3) == 0) ((uint16_t *)s_pages)[prow * 2 + (c16 >> 2)] = (uint16_t)f32_to_f16_bits(sc);
+  } else {
+    const uint32_t sb = f32_to_fp8(fminf(__fdiv_rn(amax, 6.0f), 448.0f), 1);
+    const float sc = fp8_bits_to_f32(sb, 1);
+    for (int e = 0; e < 16; ++e) {
+      const float x = sc > 0.f ? __fdiv_rn(kv[e], sc) : 0.f;
+      const float ax = fabsf(x);
+      const int idx = (ax >= 0.25f) + (ax >= 0.75f) + (ax >= 1.25f) + (ax >= 1.75f) + (ax >= 2.5f) + (ax >= 3.5f) +
+                      (ax >= 5.0f);
+      const bool neg = x < 0.f;
+      const float deq = (neg ? -fp4_level(idx) : fp4_level(idx)) * sc;  // exact
+      rw[e >> 2] |= f32_to_fp8(kv[e] - deq, res_e4m3) << (8 * (e & 3));
+      cw[e >> 3] |= (uint32_t)(idx | (neg ? 8 : 0)) << (4 * (e & 7));
+    }
+    if (live) ((uint8_t *)s_pages)[prow * 8 + c16] = (uint8_t)sb;
+  }
+  if (!live) return;
+  *(uint2 *)(k_pages + prow * 64 + 8 * c16) = make_uint2(cw[0], cw[1]);
+  *(uint4 *)(r_pages + prow * D + 16 * c16) = make_uint4(rw[0], rw[1], rw[2], rw[3]);
+  if (v_new != nullptr) {
+    const uint16_t *vs = (const uint16_t *)v_new + ((size_t)m * HKV + hkv) * D + 16 * c16;
+    uint16_t *vd = (uint16_t *)v_pages + (((size_t)page * HKV + hkv) * D + 16 * c16) * 64 + slot;
+    for (int e = 0; e < 16; ++e) vd[(size_t)e * 64] = vs[e];
+  }
+}
+
 }  // namespace ffa
 
 // ============================================================================
@@ -244,4 +318,36 @@ extern "C" int ffa_nf4_quantize(const void *k, int k_dtype, int B, int T, int HK
   hipLaunchKernelGGL(ffa::nf4_quant_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, k, k_dtype, B, T,
                      HKV, D, (const float *)absmax, nsplit, k_packed, residual, res_dtype == FFA_DT_FP8_E4M3 ? 1 : 0);
   return launch_status();
+}
+
+static int group_append(bool nf4, const void *k, int k_dtype, int B, int Tn, int HKV, const int32_t *pos,
+                        const int32_t *block_table, int bt_stride, uint8_t *k_pages, void *scale_pages,
+                        uint8_t *res_pages, int res_dtype, const void *v_new, void *v_pages, void *stream) {
+  if (B <= 0 || Tn <= 0 || HKV <= 0) return ffa_set_error_internal(FFA_E_INVALID, "bad dims");
+  if (!is_float(k_dtype)) return ffa_set_error_internal(FFA_E_INVALID, "k dtype");
+  if (!is_fp8(res_dtype)) return ffa_set_error_internal(FFA_E_INVALID, "residual dtype must be fp8");
+  const size_t total = (size_t)B * Tn * HKV * 8;
+  const dim3 grid((unsigned)((total + 255) / 256));
+  const int e4 = res_dtype == FFA_DT_FP8_E4M3 ? 1 : 0;
+  if (nf4)
+    hipLaunchKernelGGL(ffa::kfmt_group_append_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, k, k_dtype, B * Tn,
+                       Tn, HKV, pos, block_table, bt_stride, k_pages, scale_pages, res_pages, e4, v_new, v_pages);
+  else
+    hipLaunchKernelGGL(ffa::kfmt_group_append_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, k, k_dtype,
+                       B * Tn, Tn, HKV, pos, block_table, bt_stride, k_pages, scale_pages, res_pages, e4, v_new, v_pages);
+  return launch_status();
+}
+
+extern "C" int ffa_nvfp4_g16_append(const void *k, int k_dtype, int B, int Tn, int HKV, const int32_t *pos,
+                                    const int32_t *block_table, int bt_stride, uint8_t *k_pages, uint8_t *scale_pages,
+                                    uint8_t *res_pages, int res_dtype, const void *v_new, void *v_pages, void *stream) {
+  return group_append(false, k, k_dtype, B, Tn, HKV, pos, block_table, bt_stride, k_pages, scale_pages, res_pages,
+                      res_dtype, v_new, v_pages, stream);
+}
+
+extern "C" int ffa_nf4_g64_append(const void *k, int k_dtype, int B, int Tn, int HKV, const int32_t *pos,
+                                  const int32_t *block_table, int bt_stride, uint8_t *k_pages, void *scale_pages,
+                                  uint8_t *res_pages, int res_dtype, const void *v_new, void *v_pages, void *stream) {
+  return group_append(true, k, k_dtype, B, Tn, HKV, pos, block_table, bt_stride, k_pages, scale_pages, res_pages,
+                      res_dtype, v_new, v_pages, stream);
 }

@@ -6,7 +6,9 @@
 `attn_forward_decode_nvfp4fp8` keeps the reference signature, defaults, scale-shape
 normalisation and exception types (reference :213-367).  K is packed e2m1 nibbles (low
 nibble first) with one scale per (sequence, BS-token block, KV head).  Extension through
-**kwargs: seq_lens=[B] int32.
+**kwargs: seq_lens=[B] int32, workspace=DecodeWorkspace; block_table=[B, n] int32 (with
+T= or seq_lens=) selects the BASELINE paged layout, where k_fp4 / k_scale / k_residual / v are
+the page pools of ffa_mi355x.paged_kfmt.PagedKfmtCache("nvfp4", ...).
 """
 import math
 import sys
@@ -18,6 +20,7 @@ sys.path.insert(0, str(Path(__file__).resolve().parents[2]))  # ffa-speedtest_am
 from ffa_mi355x import _native as _N  # noqa: E402
 from ffa_mi355x.decode import DecodeWorkspace, decode_ntbs  # noqa: E402
 from ffa_mi355x.kfmt import run_kfmt_decode  # noqa: E402
+from ffa_mi355x.paged_kfmt import decode_pools  # noqa: E402
 
 __all__ = ["attn_forward_decode_nvfp4fp8"]
 
@@ -61,6 +64,24 @@ def attn_forward_decode_nvfp4fp8(
         raise ValueError("k_scale must be a floating point tensor")
     if k_residual is not None and not k_residual.is_floating_point():
         raise ValueError("k_residual must be a floating point tensor (e.g., fp8/fp16/bf16)")
+
+    if kwargs.get("block_table") is not None:
+        # BASELINE paged layout (per-token group scales; no reference counterpart)
+        if use_fp8_residual and k_residual is None:
+            raise ValueError("use_fp8_residual=True requires k_residual")
+        workspace = kwargs.get("workspace")
+        if workspace is not None and not isinstance(workspace, DecodeWorkspace):
+            raise TypeError("workspace must be a DecodeWorkspace")
+        seq_lens = kwargs.get("seq_lens")
+        ws = decode_pools("nvfp4", q, k_fp4, k_scale, v, k_residual, kwargs["block_table"], seq_lens, T=kwargs.get("T"),
+                          scale=scale, BS=BS, SBS=SBS, delta=delta, precomputed_threshold=precomputed_threshold,
+                          use_fp8_residual=use_fp8_residual, workspace=workspace)
+        if return_skip_ratio:
+            kept = ws.mask_buf.to(torch.int32).sum()
+            sl = seq_lens.tolist() if seq_lens is not None else [ws.T] * q.shape[0]
+            total = sum(decode_ntbs(int(t), BS, BS if SBS is None else SBS) for t in sl) * k_fp4.shape[1]
+            return ws.o, float((1.0 - (kept.float() / float(total))).item())
+        return ws.o
 
     B, Tq, HQ, K = q.shape
     Bk, T, HKV, K_packed = k_fp4.shape

@@ -18,7 +18,7 @@ DT_F16, DT_BF16, DT_F32, DT_FP8_E4M3, DT_FP8_E5M2, DT_NONE = range(6)
 LAYOUT_CONTIG, LAYOUT_PAGED = 0, 1
 SCALE_CHANNEL, SCALE_G32 = 0, 1
 KFMT_FP8_E4M3, KFMT_FP8_E5M2, KFMT_NVFP4, KFMT_NF4 = range(4)
-KSCALE_NONE, KSCALE_TOKEN, KSCALE_BLOCK, KSCALE_CHANNEL = range(4)
+KSCALE_NONE, KSCALE_TOKEN, KSCALE_BLOCK, KSCALE_CHANNEL, KSCALE_G16, KSCALE_G64 = range(6)
 
 EXPORTS = (
     "ffa_q2fp8_decode_nparts",
@@ -36,6 +36,8 @@ EXPORTS = (
     "ffa_nvfp4_quantize",
     "ffa_nf4_quantize_nsplit",
     "ffa_nf4_quantize",
+    "ffa_nvfp4_g16_append",
+    "ffa_nf4_g64_append",
     "ffa_last_error",
     "ffa_version",
 )
@@ -126,6 +128,9 @@ class KfmtArgs(ctypes.Structure):
         ("nparts", ctypes.c_int),
         ("mask", ctypes.c_void_p),
         ("ntbs", ctypes.c_int),
+        ("layout", ctypes.c_int),
+        ("block_table", ctypes.c_void_p),
+        ("bt_stride", ctypes.c_int),
     ]
 
 
@@ -179,6 +184,9 @@ def lib() -> ctypes.CDLL:
         L.ffa_nf4_quantize_nsplit.restype = ci
         L.ffa_nf4_quantize.argtypes = [vp, ci, ci, ci, ci, ci, vp, vp, vp, ci, vp, vp]
         L.ffa_nf4_quantize.restype = ci
+        for name in ("ffa_nvfp4_g16_append", "ffa_nf4_g64_append"):
+            getattr(L, name).argtypes = [vp, ci, ci, ci, ci, vp, vp, ci, vp, vp, vp, ci, vp, vp, vp]
+            getattr(L, name).restype = ci
         _lib = L
         return _lib
 

@@ -28,7 +28,7 @@ def fp8_format_of(dtype: torch.dtype) -> int:
 def run_kfmt_decode(
     *,
     q: torch.Tensor,  # [B, HQ, 128]
-    k: torch.Tensor,  # [B, T, HKV, 128] fp8 or [B, T, HKV, 64] u8 nibbles
+    k: torch.Tensor,  # [B, T, HKV, 128] fp8 or [B, T, HKV, 64] u8 nibbles (paged: [P, HKV, 64, 64] pool)
     k_format: int,
     k_scale,  # tensor or None
     scale_kind: int,
@@ -44,10 +44,13 @@ def run_kfmt_decode(
     precomputed_threshold=None,
     seq_lens=None,
     workspace: DecodeWorkspace | None = None,
+    layout: int = N.LAYOUT_CONTIG,
+    block_table=None,
 ) -> DecodeWorkspace:
     B, HQ, D = q.shape
-    if D != HEAD_DIM or v.shape[-1] != HEAD_DIM:
-        raise NotImplementedError(f"head_dim {D} / value dim {v.shape[-1]} not supported (this build implements 128)")
+    vdim = v.shape[-2] if layout == N.LAYOUT_PAGED else v.shape[-1]  # V^T pages [P, HKV, 128, 64]
+    if D != HEAD_DIM or vdim != HEAD_DIM:
+        raise NotImplementedError(f"head_dim {D} / value dim {vdim} not supported (this build implements 128)")
     if workspace is None:
         workspace = DecodeWorkspace(B, HQ, HKV, T, BS, SBS, q.device, q.dtype)
     elif not workspace.matches(B, HQ, HKV, T, BS, SBS, q.device, q.dtype):
@@ -73,6 +76,9 @@ def run_kfmt_decode(
     a.m_buf, a.l_buf, a.o_buf = workspace.m_buf.data_ptr(), workspace.l_buf.data_ptr(), workspace.o_buf.data_ptr()
     a.nparts = workspace.nparts
     a.mask, a.ntbs = workspace.mask_buf.data_ptr(), workspace.NTBS
+    a.layout = layout
+    a.block_table = block_table.data_ptr() if block_table is not None else None
+    a.bt_stride = block_table.shape[1] if block_table is not None else 0
     rc = N.lib().ffa_kfmt_decode(ctypes.byref(a), ctypes.c_void_p(N.stream_of(q.device)))
     N.check(rc, "ffa_kfmt_decode")
     return workspace

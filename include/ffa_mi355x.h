@@ -35,6 +35,8 @@
  *                             (quantize_k_fp8_fp8_residual)
  *   ffa_nvfp4_quantize        ffa-nvfp4fp8/fused_kproj_rope_nvfp4fp8.py:62-114
  *                             (encode_k_nvfp4_fp8_residual)
+ *   ffa_nvfp4_g16_append,     no reference counterpart: BASELINE configs 3 / 4 paged layouts
+ *   ffa_nf4_g64_append        (per-token group scales), quantize + append
  *   ffa_nf4_quantize          ffa-nf4fp8/fused_kproj_rope_nf4fp8.py:72-96
  *                             (encode_k_nf4_fp8_residual; the Triton producer
  *                              kproj_rope_nf4_triton :440-558 is ffa_kproj_rope + this)
@@ -211,6 +213,23 @@ int ffa_fp8fp8_quantize(const void *k, int k_dtype, size_t n, uint8_t *base, uin
 int ffa_nvfp4_quantize(const void *k, int k_dtype, int B, int T, int HKV, int D, int page_size, uint8_t *k_packed,
                        void *scale, uint8_t *residual, int res_dtype, void *stream);
 int ffa_nf4_quantize_nsplit(int T);
+
+/*
+ * BASELINE paged modes of configs 3 / 4 (no reference counterpart): quantize K rows
+ * k [B, Tn, HKV, 128] (F16/BF16/F32) and append them, with v_new [B, Tn, HKV, 128] (the
+ * V pool's 2-byte dtype) or NULL, at positions pos[b] + n of the pages block_table[b, :].
+ *   nvfp4-g16: per 16 channels s = e4m3(min(amax / 6, 448)), code = nearest e2m1 level of
+ *              k / s by the midpoint rule (ties up), residual = fp8(k - level * s).
+ *   nf4-g64:   per 64 channels s = fp16(max(amax, 1e-6)), code = nearest NF4 level of
+ *              clamp(k / s, -1, 1) (ties down), residual = fp8(k - codebook[code] * s).
+ * Pools as described at ffa_kfmt_decode.
+ */
+int ffa_nvfp4_g16_append(const void *k, int k_dtype, int B, int Tn, int HKV, const int32_t *pos,
+                         const int32_t *block_table, int bt_stride, uint8_t *k_pages, uint8_t *scale_pages,
+                         uint8_t *res_pages, int res_dtype, const void *v_new, void *v_pages, void *stream);
+int ffa_nf4_g64_append(const void *k, int k_dtype, int B, int Tn, int HKV, const int32_t *pos,
+                       const int32_t *block_table, int bt_stride, uint8_t *k_pages, void *scale_pages,
+                       uint8_t *res_pages, int res_dtype, const void *v_new, void *v_pages, void *stream);
 int ffa_nf4_quantize(const void *k, int k_dtype, int B, int T, int HKV, int D, uint8_t *k_packed, void *scale,
                      uint8_t *residual, int res_dtype, float *absmax, void *stream);
 
@@ -226,11 +245,25 @@ int ffa_nf4_quantize(const void *k, int k_dtype, int B, int T, int HKV, int D, u
  *       (ffa-nvfp4fp8/attn_kernel/attn_kernel_v1210_fused_bsz_nvfp4fp8.py:24-210, launches :316-363)
  *   FFA_KFMT_NF4 + FFA_KSCALE_CHANNEL          NF4 codebook times scale[b, h, d] ([B, HKV, 128])
  *       (ffa-nf4fp8/attn_kernel/attn_kernel_v1210_fused_bsz_nf4fp8.py:41-199, launches :300-326)
- * k is [B, T, HKV, 128] fp8 bytes or [B, T, HKV, 64] packed nibbles; residual [B, T, HKV, 128] fp8;
- * v [B, T, HKV, 128]; scratch as ffa_q2fp8_decode (nparts from ffa_q2fp8_decode_nparts).
+ *   FFA_KFMT_NVFP4 + FFA_KSCALE_G16 / FFA_KFMT_NF4 + FFA_KSCALE_G64, layout FFA_LAYOUT_PAGED
+ *       (BASELINE configs 3 and 4; no reference counterpart): 64-token pages through block_table
+ *       [B, bt_stride]: k [P, HKV, 64, 64] packed nibbles, k_scale [P, HKV, 64, 8] e4m3 (G16) or
+ *       [P, HKV, 64, 2] fp16 (G64), residual [P, HKV, 64, 128] fp8, v [P, HKV, 128, 64] (V^T pages);
+ *       k_hat = fp16(value * scale of the channel's group).  Written by ffa_nvfp4_g16_append /
+ *       ffa_nf4_g64_append.
+ * Contiguous layout: k is [B, T, HKV, 128] fp8 bytes or [B, T, HKV, 64] packed nibbles; residual
+ * [B, T, HKV, 128] fp8; v [B, T, HKV, 128].  Scratch as ffa_q2fp8_decode (nparts from
+ * ffa_q2fp8_decode_nparts).
  */
 enum { FFA_KFMT_FP8_E4M3 = 0, FFA_KFMT_FP8_E5M2 = 1, FFA_KFMT_NVFP4 = 2, FFA_KFMT_NF4 = 3 };
-enum { FFA_KSCALE_NONE = 0, FFA_KSCALE_TOKEN = 1, FFA_KSCALE_BLOCK = 2, FFA_KSCALE_CHANNEL = 3 };
+enum {
+  FFA_KSCALE_NONE = 0,
+  FFA_KSCALE_TOKEN = 1,
+  FFA_KSCALE_BLOCK = 2,
+  FFA_KSCALE_CHANNEL = 3,
+  FFA_KSCALE_G16 = 4, /* paged nvfp4: one e4m3 scale per 16 channels of each token */
+  FFA_KSCALE_G64 = 5  /* paged nf4: one fp16 scale per 64 channels of each token */
+};
 
 typedef struct ffa_kfmt_decode_args {
   const void *q; /* [B, HQ, 128] */
@@ -257,6 +290,9 @@ typedef struct ffa_kfmt_decode_args {
   int nparts;
   int8_t *mask;
   int ntbs;
+  int layout;                 /* FFA_LAYOUT_CONTIG or FFA_LAYOUT_PAGED */
+  const int32_t *block_table; /* [B, bt_stride] (paged only) */
+  int bt_stride;
 } ffa_kfmt_decode_args;
 
 int ffa_kfmt_decode(const ffa_kfmt_decode_args *args, void *stream);

@@ -20,6 +20,15 @@ reference checkout):
 * quantize_nf4      ffa-nf4fp8/fused_kproj_rope_nf4fp8.py:72-96 (fp32 arithmetic; the residual uses
                     the fp32 scale, the decode the scale rounded to k's dtype)
 * khat_nf4          ffa-nf4fp8/attn_kernel/attn_kernel_v1210_fused_bsz_nf4fp8.py:80-81, 93, 121
+* quantize_nvfp4_g16 / khat_nvfp4_g16
+                    BASELINE config 3 (no reference counterpart): e2m1 with one e4m3 scale per
+                    16 channels of each token, s = e4m3(amax / 6); the codes follow the
+                    reference encoder's midpoint rule (bucketize right=True), k_hat = fp16(level * s)
+* quantize_nf4_g64 / khat_nf4_g64
+                    BASELINE config 4 (no reference counterpart): NF4 with one fp16 absmax scale
+                    per 64 channels of each token, s = fp16(max(amax, 1e-6)); codes by the
+                    reference encoder's rule (clamp to [-1, 1], bucketize right=False),
+                    k_hat = fp16(codebook[c] * s)
 """
 from __future__ import annotations
 
@@ -153,3 +162,52 @@ def khat_nf4(packed: np.ndarray, scale: np.ndarray, D: int) -> np.ndarray:
     """k_hat = fp16(f32(codebook[c]) * f32(scale[b, h, d]))."""
     c = unpack_4bit(packed, D).astype(np.int64)
     return round_f16((NF4_CODEBOOK[c] * np.asarray(scale, F32)[:, None]).astype(F32))
+
+
+# ----------------------------------------------------------------------------- BASELINE per-token group scales
+def quantize_nvfp4_g16(k: np.ndarray, fmt: str = "e4m3fn"):
+    """k [..., 128] (values of k's dtype) -> (packed u8 [..., 64], scale bytes u8 [..., 8] (e4m3),
+    residual u8 [..., 128]).  Per 16-channel block: s = e4m3(min(amax / 6, 448)); x = k / s (0 where
+    s == 0); code = #{midpoints <= |x|} | sign(x) << 3; residual = fp8(k - (+-level * s))."""
+    k = np.asarray(k, F32)
+    kb = k.reshape(k.shape[:-1] + (-1, 16))
+    amax = np.abs(kb).max(axis=-1)
+    sbytes = fp8_encode(np.minimum((amax / F32(6.0)).astype(F32), F32(448.0)), "e4m3fn")
+    s = fp8_decode(sbytes, "e4m3fn")[..., None]
+    with np.errstate(divide="ignore", invalid="ignore"):
+        x = np.where(s > 0, (kb / s).astype(F32), F32(0.0))
+    idx = np.searchsorted(FP4_THRESHOLDS, np.abs(x), side="right")
+    neg = x < 0
+    deq = (np.where(neg, -FP4_POS_LEVELS[idx], FP4_POS_LEVELS[idx]) * s).astype(F32)  # exact
+    res = fp8_encode((kb - deq).astype(F32), fmt).reshape(k.shape)
+    codes = (idx | (neg.astype(np.int64) << 3)).astype(np.uint8).reshape(k.shape)
+    return pack_4bit(codes), sbytes.astype(np.uint8), res
+
+
+def khat_nvfp4_g16(packed: np.ndarray, sbytes: np.ndarray) -> np.ndarray:
+    """k_hat = fp16(f32(e2m1) * f32(e4m3 scale of the channel's 16-block)) -- exact (<= 5 significant bits)."""
+    v = fp4_decode(unpack_4bit(packed, 2 * np.asarray(packed).shape[-1]))
+    s = np.repeat(fp8_decode(sbytes, "e4m3fn"), 16, axis=-1)
+    return round_f16((v * s).astype(F32))
+
+
+def quantize_nf4_g64(k: np.ndarray, fmt: str = "e4m3fn"):
+    """k [..., 128] -> (packed u8 [..., 64], scale f32 [..., 2] (fp16 values), residual u8 [..., 128]).
+    Per 64-channel block: s = fp16(max(amax, 1e-6)); x = clamp(k / s, -1, 1);
+    code = #{codebook midpoints < x}; residual = fp8(k - codebook[code] * s)."""
+    k = np.asarray(k, F32)
+    kb = k.reshape(k.shape[:-1] + (-1, 64))
+    s = round_f16(np.maximum(np.abs(kb).max(axis=-1), F32(1e-6)).astype(F32))  # [..., 2]
+    x = np.clip((kb / s[..., None]).astype(F32), F32(-1.0), F32(1.0))
+    bounds = ((NF4_CODEBOOK[:-1] + NF4_CODEBOOK[1:]).astype(F32) * F32(0.5)).astype(F32)
+    idx = np.searchsorted(bounds, x, side="left")
+    deq = (NF4_CODEBOOK[idx] * s[..., None]).astype(F32)
+    res = fp8_encode((kb - deq).astype(F32), fmt).reshape(k.shape)
+    return pack_4bit(idx.astype(np.uint8).reshape(k.shape)), s.astype(F32), res
+
+
+def khat_nf4_g64(packed: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    """k_hat = fp16(f32(codebook[c]) * f32(fp16 scale of the channel's 64-block))."""
+    c = unpack_4bit(packed, 2 * np.asarray(packed).shape[-1]).astype(np.int64)
+    s = np.repeat(np.asarray(scale, F32), 64, axis=-1)
+    return round_f16((NF4_CODEBOOK[c] * s).astype(F32))

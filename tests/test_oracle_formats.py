@@ -196,3 +196,53 @@ def test_nvfp4_second_probe_window_uses_last_block_scale():
              ).astype(np.float32) * O.L2E
     th = np.maximum(sc_w0.max(axis=0), sc_w1.max(axis=0)) - np.float32(2.0)
     assert np.array_equal(diag["threshold"][0], th.astype(np.float32))
+
+
+# ----------------------------------------------------------------------------- BASELINE group-scale modes
+def test_nvfp4_g16_quantizer_pins():
+    """Scales are torch's e4m3 cast of amax/6; codes are the nearest e2m1 level of k/s (ties to the
+    larger level, the encoder's right=True rule); k_hat = level * s exactly; residual = torch's fp8 cast."""
+    k = _k((2, 9, 3, 128), "bf16", 11, outliers=True)
+    k[0, 0, 0, :16] = 0.0  # an all-zero block: scale 0, codes 0
+    pk, sb, res = OF.quantize_nvfp4_g16(k)
+    kb = torch.from_numpy(k).view(2, 9, 3, 8, 16)
+    amax = kb.abs().amax(-1)
+    assert np.array_equal(sb, _bytes((amax / 6.0).clamp(max=448.0).to(torch.float8_e4m3fn)))
+    s = torch.from_numpy(sb).view(torch.float8_e4m3fn).float()[..., None]
+    x = torch.where(s > 0, kb / s, torch.zeros_like(kb))
+    codes = torch.from_numpy(OF.unpack_4bit(pk, 128)).view(2, 9, 3, 8, 16).long()
+    lv = torch.from_numpy(OF.FP4_POS_LEVELS)
+    mag = lv[codes & 7]
+    d = (x.abs()[..., None] - lv).abs()  # brute force over the 8 levels
+    best = d.min(-1).values
+    assert torch.all((x.abs() - mag).abs() <= best + 1e-7)
+    tie_hi = ((d - best[..., None]).abs() <= 1e-7).float().argmax(-1, keepdim=True)  # first (smaller) level
+    n_tie = ((d - best[..., None]).abs() <= 1e-7).sum(-1)
+    assert torch.all((n_tie < 2) | (codes & 7 > tie_hi[..., 0]))  # a tie takes the larger level
+    assert torch.all(((codes >> 3) == 1) == (x < 0))
+    kh = OF.khat_nvfp4_g16(pk, sb)
+    exact = (torch.where(x < 0, -mag, mag) * s).reshape(2, 9, 3, 128).numpy()
+    assert np.array_equal(kh, exact)  # fp16 rounding is a no-op here
+    assert np.array_equal(res, _bytes((torch.from_numpy(k) - torch.from_numpy(exact)).to(torch.float8_e4m3fn)))
+    assert (sb[0, 0, 0, 0] == 0) and (codes[0, 0, 0, 0] == 0).all()
+
+
+def test_nf4_g64_quantizer_pins():
+    """Scales are torch's fp16 cast of max(amax, 1e-6); codes are the nearest NF4 level of
+    clamp(k/s, -1, 1) (ties to the smaller level, right=False); residual = torch's fp8 cast."""
+    k = _k((2, 9, 3, 128), "bf16", 12, outliers=True)
+    k[1, 2, 1, 64:] = 0.0  # zero block: s = fp16(1e-6), code 7 (level 0)
+    pk, s, res = OF.quantize_nf4_g64(k)
+    kb = torch.from_numpy(k).view(2, 9, 3, 2, 64)
+    st = kb.abs().amax(-1).clamp(min=1e-6).to(torch.float16).float()
+    assert np.array_equal(s, st.numpy())
+    x = (kb / st[..., None]).clamp(-1.0, 1.0)
+    codes = torch.from_numpy(OF.unpack_4bit(pk, 128)).view(2, 9, 3, 2, 64).long()
+    cb = torch.from_numpy(OF.NF4_CODEBOOK)
+    d = (x[..., None] - cb).abs()
+    best = d.min(-1).values
+    assert torch.all((x - cb[codes]).abs() <= best + 1e-7)
+    deq = cb[codes] * st[..., None]
+    assert np.array_equal(res, _bytes((kb - deq).reshape(2, 9, 3, 128).to(torch.float8_e4m3fn)))
+    assert np.array_equal(OF.khat_nf4_g64(pk, s), deq.reshape(2, 9, 3, 128).to(torch.float16).float().numpy())
+    assert (codes[1, 2, 1, 1] == 7).all() and s[1, 2, 1, 1] == np.float32(np.float16(1e-6))
