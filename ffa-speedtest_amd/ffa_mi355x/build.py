@@ -26,6 +26,9 @@ HIPCC_FLAGS = [
     "-fPIC",
     # packed fp32 ops are disabled on purpose (see the kernels' build notes)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in arch VGPRs rather than AGPRs: the decode kernel then needs 196 registers
+    # instead of 228 and no v_accvgpr_read copies (measured 2 % faster on the config-2 decode)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wno-unused-command-line-argument",
 ]
 
