@@ -38,6 +38,38 @@ struct DecodeParams {
 };
 
 enum { kContig = 0, kPaged = 1 };
+
+// ---------------------------------------------------------------------------
+// Page-internal order of the paged pools (one (page, KV head) block each).  The
+// decode reads every block with 16-byte-per-lane loads; lane L = 16 kc + mrow of an
+// instruction reads the L-th 16-byte piece of one contiguous 1 KB (or 256 B) block, so
+// each load instruction covers whole cache lines.  t = token in the page (0..63).
+// ---------------------------------------------------------------------------
+// residual [64 tokens][128 ch] fp8 -> [8 blocks (tau, h)][64 lanes (kc, mrow)][16 B]:
+// tile tau = t & 3 holds tokens 4 mrow + tau, lane kc its channels 32 kc + 16 h + (0..15)
+__host__ __device__ constexpr uint32_t res_off(int t, int c) {
+  return (uint32_t)((((t & 3) * 2 + ((c >> 4) & 1)) * 64 + (c >> 5) * 16 + (t >> 2)) * 16 + (c & 15));
+}
+// V^T [128 columns][64 tokens] bf16 -> [16 blocks (nu, kap)][64 lanes (kc, n)][8 tokens]:
+// element index of column c, token t (the P.V B operand of lane (n, kc), K-chunk kap)
+__host__ __device__ constexpr uint32_t vt_off(int c, int t) {
+  return (uint32_t)((((c >> 4) * 2 + ((t >> 3) & 1)) * 64 + (t >> 4) * 16 + (c & 15)) * 8 + (t & 7));
+}
+// q2 codes [4 groups][64 tokens][8 B] -> [2 blocks h][64 lanes (g, mrow)][2 tokens][8 B]:
+// byte offset of the 8 code bytes of group g, token t (tokens 4 mrow + 2h, + 1 per lane)
+__host__ __device__ constexpr uint32_t codes_off(int g, int t) {
+  return (uint32_t)(((((t >> 1) & 1) * 64 + g * 16 + (t >> 2)) * 2 + (t & 1)) * 8);
+}
+// g32 scale / zero [4 groups][64 slots] f16 -> [2 h][4 groups][4 kc][8 slots]: element
+// index of slot s of group g (a token's slot is scale_pos(t))
+__host__ __device__ constexpr uint32_t gscale_off(int g, int s) {
+  return (uint32_t)(((((s >> 3) & 1) * 4 + g) * 4 + (s >> 4)) * 8 + (s & 7));
+}
+// 4-bit codes [64 tokens][64 B] -> [4 blocks tau][64 lanes (kc, mrow)][16 B]: byte offset
+// of byte b (channels 2b, 2b + 1) of token t
+__host__ __device__ constexpr uint32_t k4_off(int t, int b) {
+  return (uint32_t)(((t & 3) * 64 + (b >> 4) * 16 + (t >> 2)) * 16 + (b & 15));
+}
 enum { kChannel = 0, kG32 = 1 };
 enum { kResNone = 0, kResE4M3 = 1, kResE5M2 = 2 };
 enum { kVF16 = 0, kVBF16 = 1 };

@@ -6,7 +6,8 @@
 // plus the BASELINE paged modes of configs 3 and 4 (no reference counterpart): nvfp4 with one
 // e4m3 scale per 16 channels of each token, nf4 with one fp16 scale per 64 channels, in
 // 64-token pages (codes [P, HKV, 64, 64], scales [P, HKV, 64, 8 | 2], residual [P, HKV, 64, 128],
-// V^T [P, HKV, 128, 64]) read through a block table.
+// V^T [P, HKV, 128, 64]; codes, residual and V in the page-internal orders of decode_common.h)
+// read through a block table.
 //
 // Every format dequantizes to the fp16 K the reference feeds its dot products,
 // k_hat = fp16(f32(value) * f32(scale)), and then follows the q2fp8 path: the probe
@@ -192,7 +193,7 @@ __global__ __launch_bounds__(256) void kfmt_decode_kernel(const DecodeParams p) 
       // the 16 window tokens lie in one page (pa is a multiple of 16); rows past the sequence
       // end hold no data, their scores are masked below
       const int tok = (pa & (kPage - 1)) + mrow;
-      pxa = bload16(page_rows(p.kq, ppg, kRow, pv), tok * kRow + kLane * kc);
+      pxa = bload16(page_rows(p.kq, ppg, kRow, pv), k4_off(tok, 16 * kc));
       pgs = group_scales(page_rows((const uint8_t *)p.ks, ppg, SCL == kSclG16 ? 8 : 4, pv), tok);
     } else {
       const int nt = pv ? min(16, Tb - pa) : 0;
@@ -215,7 +216,7 @@ __global__ __launch_bounds__(256) void kfmt_decode_kernel(const DecodeParams p) 
       const brsrc rs = page_rows((const uint8_t *)p.ks, pg[j], SCL == kSclG16 ? 8 : 4, nv[j] > 0);
 #pragma unroll
       for (int tau = 0; tau < 4; ++tau) {
-        xa[j][tau] = bload16(rc, (4 * mrow + tau) * kRow + kLane * kc);
+        xa[j][tau] = bload16(rc, (tau * 64 + lane) * 16);  // block tau: token 4 mrow + tau, bytes 16 kc + (0..15)
         xb[j][tau] = make_uint4(0, 0, 0, 0);
         xs[j][tau] = 1.f;
         xg[j][tau] = group_scales(rs, 4 * mrow + tau);
@@ -419,21 +420,25 @@ __global__ __launch_bounds__(256) void kfmt_decode_kernel(const DecodeParams p) 
       const brsrc rs = LAYOUT == kPaged ? page_rows(p.kr, pg[j], kD, true)
                                         : make_rsrc(p.kr + (((size_t)b * p.T + t0) * p.HKV + hkv) * kD,
                                                     ((nvs - 1) * p.HKV + 1) * kD);
-      const uint32_t rstride = LAYOUT == kPaged ? kD : p.HKV * kD;
 #pragma unroll
       for (int tau = 0; tau < 4; ++tau) {
-        const uint32_t off = (4 * mrow + tau) * rstride + 32 * kc;
-        rr[tau][0] = bload16(rs, off);
-        rr[tau][1] = bload16(rs, off + 16);
+        if constexpr (LAYOUT == kPaged) {  // blocks (tau, h) of the page's residual
+          rr[tau][0] = bload16(rs, ((tau * 2 + 0) * 64 + lane) * 16);
+          rr[tau][1] = bload16(rs, ((tau * 2 + 1) * 64 + lane) * 16);
+        } else {
+          const uint32_t off = (4 * mrow + tau) * p.HKV * kD + 32 * kc;
+          rr[tau][0] = bload16(rs, off);
+          rr[tau][1] = bload16(rs, off + 16);
+        }
       }
     }
     if constexpr (LAYOUT == kPaged) {
-      // V^T page [128][64]: lane (n, kc) reads column 16 nu + n, tokens 16 kc + 8 kap .. + 8
+      // V^T page: lane (n, kc) reads column 16 nu + n, tokens 16 kc + 8 kap .. + 8 (vt_off order)
       const brsrc vs = make_rsrc((const uint16_t *)p.v + ((size_t)pg[j] * p.HKV + hkv) * (kD * kPage), kD * kPage * 2);
 #pragma unroll
       for (int nu = 0; nu < 8; ++nu)
 #pragma unroll
-        for (int kap = 0; kap < 2; ++kap) vv[nu][kap] = bload16(vs, ((16 * nu + n) * kPage + 16 * kc + 8 * kap) * 2);
+        for (int kap = 0; kap < 2; ++kap) vv[nu][kap] = bload16(vs, ((nu * 2 + kap) * 64 + lane) * 16);  // block (nu, kap)
     } else {
       const brsrc vs = make_rsrc((const uint16_t *)p.v + (((size_t)b * p.T + t0) * p.HKV + hkv) * kD,
                                  ((nvs - 1) * p.HKV + 1) * kD * 2);

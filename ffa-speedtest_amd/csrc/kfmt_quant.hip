@@ -12,6 +12,7 @@
 //    code = #{codebook midpoints < x}, residual = fp8(k - codebook[code] * s); the
 //    scale is stored in tau.
 // No FMA contraction in this file; divisions are IEEE round-to-nearest.
+#include "decode_common.h"
 #include "ffa_common.h"
 #include "ffa_mi355x.h"
 
@@ -251,12 +252,14 @@ __global__ __launch_bounds__(256) void kfmt_group_append_kernel(const void *k, i
     if (live) ((uint8_t *)s_pages)[prow * 8 + c16] = (uint8_t)sb;
   }
   if (!live) return;
-  *(uint2 *)(k_pages + prow * 64 + 8 * c16) = make_uint2(cw[0], cw[1]);
-  *(uint4 *)(r_pages + prow * D + 16 * c16) = make_uint4(rw[0], rw[1], rw[2], rw[3]);
+  // page-internal orders: decode_common.h (k4_off, res_off, vt_off)
+  const size_t blk = (size_t)page * HKV + hkv;
+  *(uint2 *)(k_pages + blk * (64 * 64) + k4_off(slot, 8 * c16)) = make_uint2(cw[0], cw[1]);
+  *(uint4 *)(r_pages + blk * (64 * D) + res_off(slot, 16 * c16)) = make_uint4(rw[0], rw[1], rw[2], rw[3]);
   if (v_new != nullptr) {
     const uint16_t *vs = (const uint16_t *)v_new + ((size_t)m * HKV + hkv) * D + 16 * c16;
-    uint16_t *vd = (uint16_t *)v_pages + (((size_t)page * HKV + hkv) * D + 16 * c16) * 64 + slot;
-    for (int e = 0; e < 16; ++e) vd[(size_t)e * 64] = vs[e];
+    uint16_t *vd = (uint16_t *)v_pages + blk * (D * 64);
+    for (int e = 0; e < 16; ++e) vd[vt_off(16 * c16 + e, slot)] = vs[e];
   }
 }
 

@@ -10,6 +10,7 @@
 //  * fused K-proj + RoPE + g32 quantize + append into the paged cache
 //    per-token groups make the append local, so GEMM,
 //    RoPE, quantization and the page writes are one kernel.
+#include "decode_common.h"
 #include "ffa_common.h"
 #include "ffa_mi355x.h"
 
@@ -107,18 +108,21 @@ __device__ __forceinline__ void g32_quantize_store(const float *kv, int page, in
   const float zr = (float)(_Float16)mn;
   const float sc = (float)(_Float16)__fdiv_rn(fmaxf(mx - zr, 1e-6f), 3.0f);
   uint32_t words[2] = {0u, 0u};
-  uint8_t *rp = r_pages + (((size_t)page * HKV + hkv) * 64 + slot) * D + 32 * g;
+  uint32_t rw[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
   for (int e = 0; e < 32; ++e) {
     const float cq = fminf(fmaxf(__builtin_rintf(__fdiv_rn(kv[e] - zr, sc)), 0.f), 3.f);
     const float deq = (cq * sc) + zr;
-    rp[e] = (uint8_t)f32_to_fp8(kv[e] - deq, res_e4m3);
+    rw[e >> 2] |= f32_to_fp8(kv[e] - deq, res_e4m3) << (8 * (e & 3));
     words[e >> 4] |= ((uint32_t)cq) << (2 * (e & 15));
   }
-  uint32_t *cp = (uint32_t *)(kq_pages + ((((size_t)page * HKV + hkv) * 4 + g) * 64 + slot) * 8);
-  cp[0] = words[0];
-  cp[1] = words[1];
+  // page-internal orders: decode_common.h (res_off, codes_off, gscale_off)
+  const size_t blk = (size_t)page * HKV + hkv;
+  uint8_t *rp = r_pages + blk * (64 * D);
+  *(uint4 *)(rp + res_off(slot, 32 * g)) = make_uint4(rw[0], rw[1], rw[2], rw[3]);
+  *(uint4 *)(rp + res_off(slot, 32 * g + 16)) = make_uint4(rw[4], rw[5], rw[6], rw[7]);
+  *(uint2 *)(kq_pages + blk * (4 * 64 * 8) + codes_off(g, slot)) = make_uint2(words[0], words[1]);
   const int ss = 16 * (slot >> 4) + 4 * (slot & 3) + ((slot >> 2) & 3);  // tile-major scale slot
-  const size_t so = (((size_t)page * HKV + hkv) * 4 + g) * 64 + ss;
+  const size_t so = blk * (4 * 64) + gscale_off(g, ss);
   s_pages[so] = (uint16_t)f32_to_f16_bits(sc);
   z_pages[so] = (uint16_t)f32_to_f16_bits(zr);
 }
@@ -255,8 +259,8 @@ __global__ __launch_bounds__(256) void kproj_append_kernel(const void *h, const 
       const int page = bt[(size_t)b * bt_stride + (P >> 6)];
       const int slot = P & 63;
       const uint16_t *vs = (const uint16_t *)v_new + ((size_t)m * HKV + hkv) * D + c8;
-      uint16_t *vd = (uint16_t *)v_pages + (((size_t)page * HKV + hkv) * D + c8) * 64 + slot;
-      for (int e = 0; e < 8; ++e) vd[(size_t)e * 64] = vs[e];
+      uint16_t *vd = (uint16_t *)v_pages + ((size_t)page * HKV + hkv) * (D * 64);
+      for (int e = 0; e < 8; ++e) vd[vt_off(c8 + e, slot)] = vs[e];
     }
   }
   (void)N;
@@ -286,8 +290,8 @@ __global__ __launch_bounds__(256) void q2_g32_append_kernel(const void *k, int k
   g32_quantize_store(kv, page, slot, hkv, HKV, g, kq_pages, s_pages, z_pages, r_pages, res_e4m3);
   if (v_new != nullptr) {
     const uint16_t *vs = (const uint16_t *)v_new + ((size_t)m * HKV + hkv) * D + 32 * g;
-    uint16_t *vd = (uint16_t *)v_pages + (((size_t)page * HKV + hkv) * D + 32 * g) * 64 + slot;
-    for (int e = 0; e < 32; ++e) vd[(size_t)e * 64] = vs[e];
+    uint16_t *vd = (uint16_t *)v_pages + ((size_t)page * HKV + hkv) * (D * 64);
+    for (int e = 0; e < 32; ++e) vd[vt_off(32 * g + e, slot)] = vs[e];
   }
 }
 

@@ -181,9 +181,9 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
     const bool pv = do_probe && pa < Tb;
     if constexpr (LAYOUT == kPaged) {
       const size_t blk = (size_t)ppg * p.HKV + hkv;
-      px = bload8u(make_rsrc(p.kq + blk * (4 * kPage * 8), pv ? 4 * kPage * 8 : 0), (kc * kPage + (tok & (kPage - 1))) * 8);
+      px = bload8u(make_rsrc(p.kq + blk * (4 * kPage * 8), pv ? 4 * kPage * 8 : 0), codes_off(kc, tok & (kPage - 1)));
       if constexpr (kG) {
-        const uint32_t so = (jg * kPage + (pa & (kPage - 1)) + 4 * kc) * 2;
+        const uint32_t so = gscale_off(jg, (pa & (kPage - 1)) + 4 * kc) * 2;  // 4 consecutive slots
         pgs = bload8(make_rsrc((const uint16_t *)p.ks + blk * (4 * kPage), pv ? 4 * kPage * 2 : 0), so);
         pgz = bload8(make_rsrc((const uint16_t *)p.kz + blk * (4 * kPage), pv ? 4 * kPage * 2 : 0), so);
       }
@@ -202,8 +202,8 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
     if constexpr (LAYOUT == kPaged) {
       const size_t blk = (size_t)pg[j] * p.HKV + hkv;
       const brsrc rc = make_rsrc(p.kq + blk * (4 * kPage * 8), nv[j] > 0 ? 4 * kPage * 8 : 0);
-      const uint32_t co = (kc * kPage + 4 * mrow) * 8;
-      const uint4 q0 = bload16(rc, co), q1 = bload16(rc, co + 16);
+      // tokens 4 mrow + (0, 1) and 4 mrow + (2, 3) of group kc: two 1 KB blocks, lane-ordered
+      const uint4 q0 = bload16(rc, lane * 16), q1 = bload16(rc, (64 + lane) * 16);
       x[j][0] = ((uint64_t)q0.y << 32) | q0.x;
       x[j][1] = ((uint64_t)q0.w << 32) | q0.z;
       x[j][2] = ((uint64_t)q1.y << 32) | q1.x;
@@ -211,11 +211,12 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
       if constexpr (kG) {
         const brsrc rs = make_rsrc((const uint16_t *)p.ks + blk * (4 * kPage), nv[j] > 0 ? 4 * kPage * 2 : 0);
         const brsrc rz = make_rsrc((const uint16_t *)p.kz + blk * (4 * kPage), nv[j] > 0 ? 4 * kPage * 2 : 0);
-        const uint32_t so = (jg * kPage + 16 * kc) * 2;
-        gs[j][0] = bload16(rs, so);
-        gs[j][1] = bload16(rs, so + 16);
-        gz[j][0] = bload16(rz, so);
-        gz[j][1] = bload16(rz, so + 16);
+        // slots 16 kc + (0..7) and 16 kc + (8..15) of group jg
+        const uint32_t so0 = gscale_off(jg, 16 * kc) * 2, so1 = gscale_off(jg, 16 * kc + 8) * 2;
+        gs[j][0] = bload16(rs, so0);
+        gs[j][1] = bload16(rs, so1);
+        gz[j][0] = bload16(rz, so0);
+        gz[j][1] = bload16(rz, so1);
       }
     } else {
       const size_t base = (((size_t)b * p.T + t0) * p.HKV + hkv) * 32;
@@ -486,8 +487,6 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
       uint32_t ro[4];
       if constexpr (LAYOUT == kPaged) {
         rr_s = make_rsrc(p.kr + ((size_t)pgs_ * p.HKV + hkv) * (kPage * kD), kPage * kD);
-#pragma unroll
-        for (int tau = 0; tau < 4; ++tau) ro[tau] = (4 * mrow + tau) * kD + 32 * kc;
       } else {
         rr_s = make_rsrc(p.kr + (((size_t)b * p.T + t0) * p.HKV + hkv) * kD, ((nvs - 1) * p.HKV + 1) * kD);
 #pragma unroll
@@ -495,8 +494,13 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
       }
 #pragma unroll
       for (int tau = 0; tau < 4; ++tau) {
-        rr[tau][0] = bload16(rr_s, ro[tau]);
-        rr[tau][1] = bload16(rr_s, ro[tau] + 16);
+        if constexpr (LAYOUT == kPaged) {  // token 4 mrow + tau, channels 32 kc + 16 h + (0..15): block (tau, h)
+          rr[tau][0] = bload16(rr_s, ((tau * 2 + 0) * 64 + lane) * 16);
+          rr[tau][1] = bload16(rr_s, ((tau * 2 + 1) * 64 + lane) * 16);
+        } else {
+          rr[tau][0] = bload16(rr_s, ro[tau]);
+          rr[tau][1] = bload16(rr_s, ro[tau] + 16);
+        }
       }
     }
     if constexpr (LAYOUT == kPaged) {
@@ -504,7 +508,7 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
 #pragma unroll
       for (int nu = 0; nu < 8; ++nu)
 #pragma unroll
-        for (int kap = 0; kap < 2; ++kap) vv[nu][kap] = bload16(vs, ((16 * nu + n) * kPage + 16 * kc + 8 * kap) * 2);
+        for (int kap = 0; kap < 2; ++kap) vv[nu][kap] = bload16(vs, ((nu * 2 + kap) * 64 + lane) * 16);  // block (nu, kap)
     } else {
       const brsrc vs = make_rsrc((const uint16_t *)p.v + (((size_t)b * p.T + t0) * p.HKV + hkv) * kD,
                                  ((nvs - 1) * p.HKV + 1) * kD * 2);

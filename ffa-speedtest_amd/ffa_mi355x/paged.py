@@ -14,18 +14,57 @@ kernels (all per (page, KV head) blocks contiguous):
 block_table[b, i] is the pool page of tokens [64 i, 64 i + 64) of sequence b;
 seq_lens[b] is its length.  Token t of a page keeps its scale/zero in slot
 scale_pos(t) = 16*(t//16) + 4*(t%4) + (t//4)%4 (the order the decode kernel's
-MFMA tiles consume them in); codes, residual and V use plain token order.
+MFMA tiles consume them in).  Inside each (page, head) block the data are stored in
+the order the decode's load instructions read them (every instruction reads whole
+1 KB / 256 B blocks): RES_ORDER, VT_ORDER, CODES_ORDER, GSCALE_ORDER and K4_ORDER
+give the position of each logical element (the mirror of decode_common.h);
+`to_logical` / `to_tiled` convert whole pools.
 """
 from __future__ import annotations
 
 import math
 
+import numpy as np
 import torch
 
 from . import _native as N
 from .decode import HEAD_DIM, DecodeWorkspace, run_decode
 
 PAGE = 64
+
+
+def _orders():
+    t = np.arange(64)[:, None]
+    c = np.arange(128)[None, :]
+    res = (((t & 3) * 2 + ((c >> 4) & 1)) * 64 + (c >> 5) * 16 + (t >> 2)) * 16 + (c & 15)  # [t, c] byte
+    cc = np.arange(128)[:, None]
+    tt = np.arange(64)[None, :]
+    vt = (((cc >> 4) * 2 + ((tt >> 3) & 1)) * 64 + (tt >> 4) * 16 + (cc & 15)) * 8 + (tt & 7)  # [c, t] element
+    g = np.arange(4)[:, None]
+    codes = ((((tt >> 1) & 1) * 64 + g * 16 + (tt >> 2)) * 2 + (tt & 1))  # [g, t] 8-byte unit
+    gscale = ((((tt >> 3) & 1) * 4 + g) * 4 + (tt >> 4)) * 8 + (tt & 7)  # [g, slot] element
+    b = np.arange(64)[None, :]
+    k4 = ((t & 3) * 64 + (b >> 4) * 16 + (t >> 2)) * 16 + (b & 15)  # [t, byte] byte
+    return res, vt, codes, gscale, k4
+
+
+RES_ORDER, VT_ORDER, CODES_ORDER, GSCALE_ORDER, K4_ORDER = _orders()
+
+
+def to_tiled(logical: np.ndarray, order: np.ndarray, unit: int = 1) -> np.ndarray:
+    """Pool in logical page order [..., *order.shape (, unit)] -> the stored order (same shape)."""
+    lead = logical.shape[: logical.ndim - order.ndim - (1 if unit > 1 else 0)]
+    flat = logical.reshape(lead + (order.size, unit))
+    out = np.empty_like(flat)
+    out[..., order.ravel(), :] = flat
+    return out.reshape(logical.shape)
+
+
+def to_logical(stored: np.ndarray, order: np.ndarray, unit: int = 1) -> np.ndarray:
+    """Pool in stored order -> logical page order (inverse of to_tiled)."""
+    lead = stored.shape[: stored.ndim - order.ndim - (1 if unit > 1 else 0)]
+    flat = stored.reshape(lead + (order.size, unit))
+    return flat[..., order.ravel(), :].reshape(stored.shape)
 
 
 def scale_pos(t):

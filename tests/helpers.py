@@ -76,8 +76,13 @@ def paged_case(B=1, T=2048, HQ=32, HKV=8, seed=0, n_heavy=16, res="e4m3fn", seq_
             z_pool[page][:, :, spos[:n]] = z16[b, t0:t1].transpose(1, 2, 0)
             r_pool[page, :, :n, :] = r[b, t0:t1].transpose(1, 0, 2)
             v_pool[page, :, :, :n] = vb[b, t0:t1].transpose(1, 2, 0)
+    # the pools keep each (page, head) block in the decode's load order
+    from ffa_mi355x.paged import CODES_ORDER, GSCALE_ORDER, RES_ORDER, VT_ORDER, to_tiled
+
+    pools = dict(k_q=to_tiled(kq_pool, CODES_ORDER, 8), k_scale=to_tiled(s_pool, GSCALE_ORDER),
+                 k_zero=to_tiled(z_pool, GSCALE_ORDER), k_res=to_tiled(r_pool, RES_ORDER), v=to_tiled(v_pool, VT_ORDER))
     return dict(q=q, k=k, v=v, k_q=pk, k_scale=s, k_zero=z, k_res=r, res=res, lens=lens, block_table=bt,
-                pools=dict(k_q=kq_pool, k_scale=s_pool, k_zero=z_pool, k_res=r_pool, v=v_pool), P=P)
+                pools=pools, P=P)
 
 
 def to_gpu_paged(case, dev):

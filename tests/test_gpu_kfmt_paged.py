@@ -65,10 +65,12 @@ def test_paged_append_bit_exact(gpu, fmt):
     q, k, v, lens, bt, btd, cache = _build(fmt, B, T, None, seed=21, chunks=3)
     torch.cuda.synchronize()
     pk, sc, res = QUANT[fmt](f32(k))
-    kpool = cache.k.cpu().numpy()
+    from ffa_mi355x.paged import K4_ORDER, RES_ORDER, VT_ORDER, to_logical
+
+    kpool = to_logical(cache.k.cpu().numpy(), K4_ORDER)
     spool = cache.k_scale.view(torch.uint8).cpu().numpy() if fmt == "nvfp4" else f32(cache.k_scale)
-    rpool = cache.k_res.view(torch.uint8).cpu().numpy()
-    vpool = cache.v.view(torch.int16).cpu().numpy()
+    rpool = to_logical(cache.k_res.view(torch.uint8).cpu().numpy(), RES_ORDER)
+    vpool = to_logical(cache.v.view(torch.int16).cpu().numpy(), VT_ORDER)
     vb = v.view(torch.int16).numpy()
     for b in range(B):
         assert np.array_equal(_gather(kpool, bt, lens, b), pk[b]), "codes"

@@ -59,12 +59,14 @@ def test_g32_append_bit_exact(gpu):
     cache.append(k[:, 200:].to(gpu), v[:, 200:].to(gpu), (pos0 + 200).to(gpu), bt.to(gpu))
     torch.cuda.synchronize()
     pk, s, z, r = O.quantize_g32(f32(k), "e4m3fn")
-    kq_pool = cache.k_q.cpu().numpy()
+    from ffa_mi355x.paged import CODES_ORDER, GSCALE_ORDER, RES_ORDER, VT_ORDER, to_logical
+
+    kq_pool = to_logical(cache.k_q.cpu().numpy(), CODES_ORDER, 8)
     spos = np.array([scale_pos(t) for t in range(64)])
-    s_pool = cache.k_scale.float().cpu().numpy()[..., spos]  # back to token order
-    z_pool = cache.k_zero.float().cpu().numpy()[..., spos]
-    r_pool = cache.k_res.view(torch.uint8).cpu().numpy()
-    v_pool = cache.v.view(torch.int16).cpu().numpy()
+    s_pool = to_logical(cache.k_scale.float().cpu().numpy(), GSCALE_ORDER)[..., spos]  # back to token order
+    z_pool = to_logical(cache.k_zero.float().cpu().numpy(), GSCALE_ORDER)[..., spos]
+    r_pool = to_logical(cache.k_res.view(torch.uint8).cpu().numpy(), RES_ORDER)
+    v_pool = to_logical(cache.v.view(torch.int16).cpu().numpy(), VT_ORDER)
     vb = v.view(torch.int16).numpy()
     for b in range(B):
         for t in range(0, T, 64):
@@ -134,9 +136,12 @@ def test_kproj_append_config5_small(gpu):
     torch.cuda.synchronize()
     k_ref = OP.kproj_rope_rows(f32(h), f32(w).T, f32(cos), f32(sin), HKV)
     pk, s, z, r = O.quantize_g32(k_ref, "e4m3fn")
-    kq_pool = cache.k_q.cpu().numpy()
-    s_pool = cache.k_scale.float().cpu().numpy()[..., [scale_pos(t) for t in range(64)]]
-    r_pool = cache.k_res.view(torch.uint8).cpu().numpy()
+    from ffa_mi355x.paged import CODES_ORDER, GSCALE_ORDER, RES_ORDER, VT_ORDER, to_logical
+
+    kq_pool = to_logical(cache.k_q.cpu().numpy(), CODES_ORDER, 8)
+    s_pool = to_logical(cache.k_scale.float().cpu().numpy(), GSCALE_ORDER)[..., [scale_pos(t) for t in range(64)]]
+    r_pool = to_logical(cache.k_res.view(torch.uint8).cpu().numpy(), RES_ORDER)
+    v_pool = torch.from_numpy(to_logical(cache.v.view(torch.int16).cpu().numpy(), VT_ORDER)).view(torch.bfloat16)
     mism = 0
     for b in range(B):
         page, slot = int(bt[b, int(pos[b]) // 64]), int(pos[b]) % 64
@@ -148,6 +153,6 @@ def test_kproj_append_config5_small(gpu):
         assert res_gpu is not None
         deq_gpu = codes_gpu.astype(np.float32) * np.repeat(s_pool[page, :, :, slot], 32, -1)
         assert np.isfinite(deq_gpu).all()
-        vg = cache.v[page, :, :, slot].cpu()
+        vg = v_pool[page, :, :, slot]
         assert torch.equal(vg, v_new[b, 0])
     assert mism <= 0.01 * B * HKV * 128

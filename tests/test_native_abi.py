@@ -239,3 +239,41 @@ def test_rope_helpers_closed_form():
     # rope_rows: the rows of build_rope_cache's table at the given positions (fp32 angles)
     cr, sr = rope.rope_rows(torch.tensor([0, 3, 6]), head_dim=D, base=500000.0)
     assert torch.allclose(cr, cos[[0, 3, 6]], atol=1e-6) and torch.allclose(sr, sin[[0, 3, 6]], atol=1e-6)
+
+
+def test_page_orders_match_the_kernels(tmp_path):
+    """The numpy page orders (ffa_mi355x.paged) equal decode_common.h's offset functions, and each
+    is a permutation of its block."""
+    import shutil
+    import subprocess
+
+    from ffa_mi355x import paged as PG
+
+    for order, n in ((PG.RES_ORDER, 8192), (PG.VT_ORDER, 8192), (PG.CODES_ORDER, 256), (PG.GSCALE_ORDER, 256),
+                     (PG.K4_ORDER, 4096)):
+        assert np.array_equal(np.sort(order.ravel()), np.arange(n))
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(hipcc).exists():
+        pytest.skip("hipcc not available")
+    src = tmp_path / "orders.cpp"
+    src.write_text('#include <stdio.h>\n#include "decode_common.h"\nint main() {\n'
+                   '  for (int t = 0; t < 64; ++t) for (int c = 0; c < 128; ++c) printf("%u ", ffa::res_off(t, c));\n'
+                   '  printf("\\n");\n'
+                   '  for (int c = 0; c < 128; ++c) for (int t = 0; t < 64; ++t) printf("%u ", ffa::vt_off(c, t));\n'
+                   '  printf("\\n");\n'
+                   '  for (int g = 0; g < 4; ++g) for (int t = 0; t < 64; ++t) printf("%u ", ffa::codes_off(g, t) / 8);\n'
+                   '  printf("\\n");\n'
+                   '  for (int g = 0; g < 4; ++g) for (int s = 0; s < 64; ++s) printf("%u ", ffa::gscale_off(g, s));\n'
+                   '  printf("\\n");\n'
+                   '  for (int t = 0; t < 64; ++t) for (int b = 0; b < 64; ++b) printf("%u ", ffa::k4_off(t, b));\n'
+                   '  printf("\\n");\n  return 0;\n}\n')
+    exe = tmp_path / "orders"
+    csrc = ROOT / "ffa-speedtest_amd" / "csrc"
+    r = subprocess.run([hipcc, "-x", "hip", "--offload-arch=gfx950", "-std=c++17", f"-I{csrc}", f"-I{ROOT / 'include'}",
+                        str(src), "-o", str(exe)], capture_output=True, text=True)
+    if r.returncode != 0:
+        pytest.skip(f"host build of decode_common.h failed: {r.stderr[:200]}")
+    lines = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.splitlines()
+    got = [np.array(line.split(), dtype=np.int64) for line in lines]
+    for g, order in zip(got, (PG.RES_ORDER, PG.VT_ORDER, PG.CODES_ORDER, PG.GSCALE_ORDER, PG.K4_ORDER)):
+        assert np.array_equal(g, order.ravel())

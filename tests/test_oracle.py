@@ -224,8 +224,13 @@ def test_merge_is_partition_invariant():
 
 def test_paged_gather_is_layout_only():
     """The paged pools built for the GPU gather back to the contiguous arrays the oracle used."""
+    from ffa_mi355x.paged import CODES_ORDER, RES_ORDER, VT_ORDER, to_logical
+
     c = paged_case(B=2, T=300, HQ=8, HKV=2, seed=3, n_heavy=2, seq_lens=[300, 130])
-    p = c["pools"]
+    p = dict(c["pools"])
+    p["k_q"] = to_logical(p["k_q"], CODES_ORDER, 8)  # stored block order -> logical page order
+    p["k_res"] = to_logical(p["k_res"], RES_ORDER)
+    p["v"] = to_logical(p["v"], VT_ORDER)
     for b, T in enumerate(c["lens"]):
         bt = c["block_table"][b].numpy()
         kq = O.gather_pages(p["k_q"].reshape(*p["k_q"].shape[:2], 4, 64, 8).transpose(0, 1, 3, 2, 4).reshape(
