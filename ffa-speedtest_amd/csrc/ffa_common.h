@@ -77,8 +77,8 @@ __device__ __forceinline__ uint32_t f32_to_fp8(float x, int e4m3) {
   const int e = (int)(a >> 23) - 127;  // unbiased exponent of the input (normal inputs)
   uint32_t bits;
   if (a < 0x00800000u || e < emin) {
-    // result is subnormal (or zero) in fp8: quantum 2^(emin - mbits); RNE via float add
-    // (|x| < 2^emin, so x + 2^(emin) * 2^? ... use explicit integer rounding)
+    // result is subnormal (or zero) in fp8: a multiple of the quantum 2^(emin - mbits),
+    // rounded to nearest even in units of the quantum
     const float q = __uint_as_float((uint32_t)(127 + emin - mbits) << 23);  // 2^(emin-mbits)
     const float r = __uint_as_float(a) / q;                                 // exact (power of 2)
     const float ri = __builtin_rintf(r);                                    // RNE
@@ -118,8 +118,69 @@ __device__ __forceinline__ float dpp(float x) {
 constexpr int kRowRor4 = 0x124;
 constexpr int kRowRor8 = 0x128;
 
-__device__ __forceinline__ float xor_max(float x, int m) { return fmaxf(x, __shfl_xor(x, m)); }
-__device__ __forceinline__ float xor_sum(float x, int m) { return x + __shfl_xor(x, m); }
+// Lane i combined with lane i ^ m.  For m = 16 and 32 a single register-to-register exchange:
+// v_permlane16_swap / v_permlane32_swap (gfx950) of x with itself leaves x_i in one result and
+// x_(i^m) in the other; other distances go through __shfl_xor (an LDS-pipe permute).
+template <int M>
+__device__ __forceinline__ void xor_pair(float x, float &a, float &b) {
+  if constexpr (M == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+  } else if constexpr (M == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+  } else {
+    a = x;
+    b = __shfl_xor(x, M);
+  }
+}
+__device__ __forceinline__ float xor_max(float x, int m) {
+  float a, b;
+  if (m == 16) xor_pair<16>(x, a, b);
+  else if (m == 32) xor_pair<32>(x, a, b);
+  else { a = x; b = __shfl_xor(x, m); }
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float xor_sum(float x, int m) {
+  float a, b;
+  if (m == 16) xor_pair<16>(x, a, b);
+  else if (m == 32) xor_pair<32>(x, a, b);
+  else { a = x; b = __shfl_xor(x, m); }
+  return a + b;
+}
+
+// Whole-wave max / sum with register-to-register exchanges: lane i with i ^ 32 and i ^ 16,
+// then DPP row rotations by 8, 4, 2, 1 inside each 16-lane row.  Every lane ends with the
+// result.
+constexpr int kRowRor1 = 0x121;
+constexpr int kRowRor2 = 0x122;
+__device__ __forceinline__ float wave_max(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto c = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(c[0]), __uint_as_float(c[1]));
+  x = fmaxf(x, dpp<kRowRor8>(x));
+  x = fmaxf(x, dpp<kRowRor4>(x));
+  x = fmaxf(x, dpp<kRowRor2>(x));
+  return fmaxf(x, dpp<kRowRor1>(x));
+}
+__device__ __forceinline__ float wave_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto c = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(c[0]) + __uint_as_float(c[1]);
+  x += dpp<kRowRor8>(x);
+  x += dpp<kRowRor4>(x);
+  x += dpp<kRowRor2>(x);
+  return x + dpp<kRowRor1>(x);
+}
+// lane i + lane (i ^ 32), for every lane
+__device__ __forceinline__ float swap32_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(a[0]) + __uint_as_float(a[1]);
+}
 
 // Raw buffer resource over [base, base + bytes) (gfx9 word 3: 32-bit data format, no
 // swizzle).  A load at an offset past `bytes` returns zeros without a memory access, so a

@@ -751,70 +751,67 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
 
 // --------------------------------------------------------------------------
 // Log-sum-exp merge of the workgroup partials (attn_kernel...q2fp8.py:142-171).
-// One workgroup per (sequence, query head); thread t handles partial t/4
-// (+64 r) and a 32-column quarter.  m, l and the first 64 partials' o are
-// loaded in one batch; the weighted sums are reduced in a fixed order in LDS.
+// One wave per (sequence, query head, 32-column slab): lane k owns partials k,
+// k + 64, ...; m, l and the first 64 partials' columns are loaded in one batch of
+// unconditional buffer loads (validity = resource size), the maxima and sums go
+// through register exchanges, the column sums over lanes through LDS.
 // --------------------------------------------------------------------------
 __global__ __launch_bounds__(64) void q2fp8_merge_kernel(const DecodeParams p) {
-  // one wave per (sequence, query head, 32-column slab): lane k owns partials k, k + 64, ...
   const int row = blockIdx.x >> 2;  // b * HQ + hq
   const int slab = blockIdx.x & 3;
   const int b = row / p.HQ;
   const int lane = threadIdx.x;
   const int Tb = p.seq_lens ? min(max(p.seq_lens[b], 0), p.T) : p.T;  // lengths beyond T are clamped to T
   const int nparts = min((Tb + kChunksPerWG * kPage - 1) / (kChunksPerWG * kPage), p.nparts);
-  const float *mr = p.m_buf + (size_t)row * p.nparts;
-  const float *lr = p.l_buf + (size_t)row * p.nparts;
-  const float *orow = p.o_buf + (size_t)row * p.nparts * 128 + 32 * slab;
+  const brsrc rm = make_rsrc(p.m_buf + (size_t)row * p.nparts, nparts * 4);
+  const brsrc rl = make_rsrc(p.l_buf + (size_t)row * p.nparts, nparts * 4);
+  const brsrc ro = make_rsrc(p.o_buf + (size_t)row * p.nparts * 128 + 32 * slab, nparts > 0 ? ((nparts - 1) * 128 + 32) * 4 : 0);
   __shared__ float s_o[64][33];
 
-  // first partial of the lane: m, l and its 32 columns in one batch of loads (o is used only
-  // where l > 0, so slots of empty spans are never read as data)
-  float m0 = -INFINITY, l0 = 0.f;
-  float4 o0[8];
-  if (lane < nparts) {
-    m0 = mr[lane];
-    l0 = lr[lane];
-    const float4 *op = (const float4 *)(orow + (size_t)lane * 128);
+  // first partial of the lane (slots past nparts read as l = 0, o = 0)
+  const float m0 = __uint_as_float(bload4(rm, lane * 4));
+  const float l0 = __uint_as_float(bload4(rl, lane * 4));
+  uint4 o0[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o0[e] = op[e];
-  }
+  for (int e = 0; e < 8; ++e) o0[e] = bload16(ro, (lane * 128 + 4 * e) * 4);
   float M = l0 > 0.f ? m0 : -INFINITY;
-  for (int k = lane + 64; k < nparts; k += 64)
-    if (lr[k] > 0.f) M = fmaxf(M, mr[k]);
-  for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+  for (int k = lane + 64; k < nparts; k += 64) {
+    const float l = __uint_as_float(bload4(rl, k * 4));
+    if (l > 0.f) M = fmaxf(M, __uint_as_float(bload4(rm, k * 4)));
+  }
+  M = wave_max(M);
 
   float acc[32];
   float A;
   {
+    // o is used only where l > 0: a slot whose span kept nothing holds no defined values
     const bool keep = l0 > 0.f;
     const float wgt = keep ? exp2f(m0 - M) : 0.f;
     A = keep ? l0 * wgt : 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      acc[4 * e + 0] = keep ? o0[e].x * wgt : 0.f;
-      acc[4 * e + 1] = keep ? o0[e].y * wgt : 0.f;
-      acc[4 * e + 2] = keep ? o0[e].z * wgt : 0.f;
-      acc[4 * e + 3] = keep ? o0[e].w * wgt : 0.f;
+      acc[4 * e + 0] = keep ? __uint_as_float(o0[e].x) * wgt : 0.f;
+      acc[4 * e + 1] = keep ? __uint_as_float(o0[e].y) * wgt : 0.f;
+      acc[4 * e + 2] = keep ? __uint_as_float(o0[e].z) * wgt : 0.f;
+      acc[4 * e + 3] = keep ? __uint_as_float(o0[e].w) * wgt : 0.f;
     }
   }
   for (int k = lane + 64; k < nparts; k += 64) {
-    const float l = lr[k];
+    const float l = __uint_as_float(bload4(rl, k * 4));
     if (l > 0.f) {
-      const float wgt = exp2f(mr[k] - M);
+      const float wgt = exp2f(__uint_as_float(bload4(rm, k * 4)) - M);
       A = __builtin_fmaf(l, wgt, A);
-      const float4 *op = (const float4 *)(orow + (size_t)k * 128);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float4 v = op[e];
-        acc[4 * e + 0] = __builtin_fmaf(v.x, wgt, acc[4 * e + 0]);
-        acc[4 * e + 1] = __builtin_fmaf(v.y, wgt, acc[4 * e + 1]);
-        acc[4 * e + 2] = __builtin_fmaf(v.z, wgt, acc[4 * e + 2]);
-        acc[4 * e + 3] = __builtin_fmaf(v.w, wgt, acc[4 * e + 3]);
+        const uint4 v = bload16(ro, (k * 128 + 4 * e) * 4);
+        acc[4 * e + 0] = __builtin_fmaf(__uint_as_float(v.x), wgt, acc[4 * e + 0]);
+        acc[4 * e + 1] = __builtin_fmaf(__uint_as_float(v.y), wgt, acc[4 * e + 1]);
+        acc[4 * e + 2] = __builtin_fmaf(__uint_as_float(v.z), wgt, acc[4 * e + 2]);
+        acc[4 * e + 3] = __builtin_fmaf(__uint_as_float(v.w), wgt, acc[4 * e + 3]);
       }
     }
   }
-  for (int o = 32; o >= 1; o >>= 1) A += __shfl_xor(A, o);
+  A = wave_sum(A);
   // column sums over the 64 lanes through LDS: lane c < 32 sums column c of lanes 0..31,
   // lane 32 + c of lanes 32..63
 #pragma unroll
@@ -826,7 +823,7 @@ __global__ __launch_bounds__(64) void q2fp8_merge_kernel(const DecodeParams p) {
   float sum = 0.f;
 #pragma unroll 8
   for (int k = 32 * h; k < 32 * h + 32; ++k) sum += s_o[k][c];
-  sum += __shfl_xor(sum, 32);
+  sum = swap32_sum(sum);
   if (lane < 32)
     store_any(p.out, (size_t)row * 128 + 32 * slab + c, p.out_dtype, A == 0.f ? 0.f : sum / A);
 }
