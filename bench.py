@@ -89,6 +89,171 @@ def cpu_baseline(q, k, v, BS, SBS, delta, seconds):
     return statistics.median(times) * 1e6, len(times)
 
 
+WORKLOADS = {
+    "config3": "BASELINE config 3: nvfp4-g16 + e4m3 residual pruned decode, B=4 x 128K, 32/8/128, 64-token pages "
+               "interleaved across sequences",
+    "config4": "BASELINE config 4: nf4-g64 + e4m3 residual pruned decode, B=16 ragged 8K-64K (seeded), 32/8/128, "
+               "64-token pages interleaved across sequences",
+    "config5": "BASELINE config 5: K-proj (4096 -> 8x128) + RoPE (theta 5e5, positions 65536..65599) + g32 q2 + "
+               "e4m3 quantize, appending token 65536+b to sequence b of 64, then one q2fp8 pruned decode over "
+               "the 65537..65600-token contexts at B=64",
+}
+# bytes of one (token, KV head) that every step reads (codes + scales) and that a kept token adds (residual + V)
+_EVERY = {"config3": 64 + 8, "config4": 64 + 4, "config5": 32 + 16}
+_KEPT = 128 + 256
+
+
+def _graph_time(step, R, reps, stream, per_graph=1):
+    """Microseconds per call of step(r): a HIP graph of `per_graph` rounds of step(0..R-1), replayed `reps`
+    times, hipEvents around the replays (per_graph > 1 amortises the replay launch for short calls)."""
+    import torch
+
+    with torch.cuda.stream(stream):
+        step(0)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for _ in range(per_graph):
+            for r in range(R):
+                step(r)
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    cur = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(cur)
+    for _ in range(reps):
+        g.replay()
+    e1.record(cur)
+    torch.cuda.synchronize()
+    n = reps * R * per_graph
+    return e0.elapsed_time(e1) * 1e3 / n, n
+
+
+def bench_workload(args):
+    """BASELINE configs 3, 4 and 5 at their full sizes: one JSON line with the step time and its bandwidth.
+
+    K and V are drawn on the device per sequence (synth.sequence_inputs_device), quantized and appended by
+    the library's own append kernels, so no host copy of the multi-GB caches exists.
+    """
+    import torch
+
+    from ffa_mi355x import synth
+    from ffa_mi355x.decode import DecodeWorkspace, decode_ntbs
+
+    dev = torch.device("cuda:0")
+    wl = args.workload
+    HQ, HKV, D, BS, SBS, delta = 32, 8, 128, 64, 64, args.delta
+    t_setup = time.perf_counter()
+    if wl == "config3":
+        lens = [131072] * 4
+    elif wl == "config4":
+        lens = [int(x) for x in synth.ragged_lengths(16, 8192, 65536, seed=0)]
+    else:
+        lens = [65536 + b for b in range(64)]  # sequence b holds 65536 + b tokens before its append
+    B = len(lens)
+    final = [t + 1 for t in lens] if wl == "config5" else lens  # config 5 decodes after its append
+    T = max(final)
+    R = 1 if wl == "config5" else 2  # the caches (1.9-15.6 GB) dwarf the 256 MB MALL; 2 copies for 3 and 4
+    bt0, npool = synth.page_tables(final, seed=0, interleave=True)
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(B, HQ, D, generator=g).to(torch.bfloat16)
+    qd = q.to(dev)
+    if wl == "config5":
+        from ffa_mi355x import quant
+        from ffa_mi355x.paged import PagedQ2Cache, check_append_fits
+
+        cache = PagedQ2Cache(npool * R, HKV, dev)
+    else:
+        from ffa_mi355x.paged_kfmt import PagedKfmtCache
+
+        cache = PagedKfmtCache("nvfp4" if wl == "config3" else "nf4", npool * R, HKV, dev)
+    bts = [(bt0 + r * npool).to(dev) for r in range(R)]
+    zero = torch.zeros(1, dtype=torch.int32, device=dev)
+    for b in range(B):
+        k, v = synth.sequence_inputs_device(qd[b], lens[b], HKV=HKV, D=D, seed=1000 + b)
+        for r in range(R):
+            cache.append(k, v, zero, bts[r][b:b + 1])
+        del k, v
+    lens_d = torch.tensor(final, dtype=torch.int32, device=dev)
+    ws = DecodeWorkspace(B, HQ, HKV, T, BS, SBS, dev, torch.bfloat16)
+    extra = {}
+
+    def decode(r):
+        cache.decode(qd, bts[r], lens_d, T=T, BS=BS, SBS=SBS, delta=delta, workspace=ws)
+
+    if wl == "config5":
+        H = 4096
+        # one new token per sequence: token b of the 64 is rotated at, and appended to, position 65536 + b
+        pos = torch.tensor(lens, dtype=torch.int32)
+        h = (torch.randn(B, 1, H, generator=g)).to(torch.bfloat16).to(dev)
+        # W_k [4096, 1024] ~ N(0, 0.02), held once in nn.Linear's [out, in] layout, whose rows the GEMM streams
+        # (an [in, out] tensor would be transposed by the wrapper on every call, as the reference does)
+        w = (torch.randn(H, HKV * D, generator=g) * 0.02).to(torch.bfloat16).t().contiguous().to(dev)
+        inv = 1.0 / (500000.0 ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
+        ang = pos.float()[:, None] * inv[None, :]
+        emb = torch.cat([ang, ang], -1)[:, None, :]
+        cos, sin = emb.cos().to(dev), emb.sin().to(dev)
+        v_new = torch.randn(B, 1, HKV, D, generator=g).to(torch.bfloat16).to(dev)
+        pos_d = pos.to(dev)
+
+        for r in range(R):  # host-side bounds check once, outside graph capture
+            check_append_fits(pos_d, 1, bts[r], cache.P)
+
+        def produce(r):
+            quant.kproj_rope_q2_append(cache, h, w, cos, sin, pos_d, bts[r], v_new=v_new, validate=False)
+
+        def step(r):
+            produce(r)
+            decode(r)
+    else:
+        step = decode
+
+    for r in range(R):
+        step(r)
+    torch.cuda.synchronize()
+    o0, mask = ws.o.clone(), ws.mask_buf.clone()
+    stream = torch.cuda.Stream()
+    setup_s = time.perf_counter() - t_setup
+    reps = max(1, math.ceil(args.steps / R))
+    us, steps = _graph_time(step, R, reps, stream)
+    assert torch.equal(o0, ws.o), "graph replays must match the eager step"
+    if wl == "config5":
+        extra["producer_us"] = round(_graph_time(produce, R, 8, stream, per_graph=32)[0], 3)
+        extra["decode_us"] = round(_graph_time(decode, R, reps, stream)[0], 3)
+
+    valid = torch.zeros_like(mask, dtype=torch.int64)
+    nb = mask.shape[-1]
+    for b in range(B):
+        valid[b] = torch.clamp(final[b] - torch.arange(nb, device=dev) * SBS, min=0, max=SBS)
+    kept_th = int((mask.to(torch.int64) * valid).sum().item())
+    total_blocks = sum(decode_ntbs(t, BS, SBS) for t in final) * HKV
+    keep_frac = float(mask.to(torch.int64).sum().item()) / total_blocks
+    nbytes = sum(final) * HKV * _EVERY[wl] + kept_th * _KEPT + B * HQ * D * 4 + sum(-(-t // PAGE) for t in final) * 4
+    decode_us = extra.get("decode_us", us)
+    gbs = nbytes / (decode_us * 1e-6) / 1e9
+    line = {
+        "metric": f"{wl} decode-attn us/step + HBM TB/s on the algorithmic bytes",
+        "value": round(us, 3), "unit": "us/step", "n_gpus": 1, "steps": steps, "warmup": R,
+        "ms_per_step": round(us / 1e3, 6), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": {"config3": "e2m1 K x e4m3 g16 scale + e4m3 residual, bf16 V",
+                  "config4": "nf4 K x fp16 g64 absmax + e4m3 residual, bf16 V",
+                  "config5": "bf16 K-proj (f32 accumulate); q2 g32 + e4m3 residual K, bf16 V"}[wl]
+                 + "; f16/bf16 MFMA, f32 accumulate",
+        "data": "synthetic (N(0,1) bf16 drawn on the device per sequence, 16 heavy tokens per query head)",
+        "config": {"workload": WORKLOADS[wl], "B": B, "T_max": T, "tokens": sum(final), "HQ": HQ, "HKV": HKV,
+                   "D": D, "BS": BS, "SBS": SBS, "delta": delta, "keep_fraction": round(keep_frac, 4),
+                   "algorithmic_bytes": nbytes, "rotations": R,
+                   "timing": "HIP graph of R steps, hipEvents over the replays"},
+        "decode_hbm_tbps": round(gbs / 1e3, 4),
+        "decode_hbm_pct_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
+        "cpu_baseline": None,
+        "setup_s": round(setup_s, 1),
+    }
+    line.update(extra)
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -104,6 +269,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run 5 device copies of 256 MiB (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--workload", choices=("config2",) + tuple(WORKLOADS), default="config2",
+                    help="config2 (default) is the metric's line; config3/4/5 time the other BASELINE decodes")
     args = ap.parse_args()
     if args.copy_probe:
         import torch
@@ -121,6 +288,10 @@ def main():
         print(json.dumps({"error": "this build runs on one GPU: the decode shards by KV head / sequence without "
                                    "changing the per-GPU kernel (see DESIGN.md); --gpus must be 1"}))
         sys.exit(2)
+
+    if args.workload != "config2":
+        bench_workload(args)
+        return
 
     import torch
 

@@ -127,38 +127,122 @@ __device__ __forceinline__ void g32_quantize_store(const float *kv, int page, in
   z_pages[so] = (uint16_t)f32_to_f16_bits(zr);
 }
 
-// K projection GEMM tile: 16 tokens x 128 output channels per workgroup,
-// 4 waves x 2 MFMA column tiles of 16.  acc[tile][u] = row 4*(lane>>4)+u,
-// column n0 + 32*wave + 16*tile + (lane & 15).
+// K projection GEMM tile: 16 tokens x 32 output channels per 512-thread workgroup.  The 32-wide k
+// steps are dealt round-robin to the 8 waves (wave w takes steps w, w + 8, ...), so even a handful of
+// tokens keeps 8 waves per tile streaming W; each wave accumulates its steps with MFMA 16x16x32 into
+// two 16x16 tiles, and the 8 partial tiles are summed in wave order through LDS, so the result does
+// not depend on timing.  Returns the fp32 product for row threadIdx.x >> 5 (token m0 + row) and
+// column threadIdx.x & 31 (output channel n0 + column).  w is [N, H] (out, in), rows of H elements.
 // ---------------------------------------------------------------------------
+constexpr int kKpWaves = 8;
+
 template <int HDT>
-__device__ __forceinline__ void kproj_tile(const void *h, const void *w, int M, int H, int m0, int n0,
-                                           f32x4 acc[2]) {
+__device__ __forceinline__ f32x4 kp_mfma(uint4 a, uint4 b, f32x4 c) {
+  const u32x4 av = {a.x, a.y, a.z, a.w}, bv = {b.x, b.y, b.z, b.w};
+  if constexpr (HDT == FFA_DT_BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, bv), c,
+                                                   0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av), __builtin_bit_cast(f16x8, bv), c, 0,
+                                                  0, 0);
+}
+
+// NB k steps of one wave: all 3 * NB loads are issued before the first MFMA waits.
+template <int NB, int HDT>
+__device__ __forceinline__ void kp_steps(const uint16_t *hp, const uint16_t *wp0, const uint16_t *wp1, int wv, int i,
+                                         f32x4 &acc0, f32x4 &acc1) {
+  uint4 a[NB], b0[NB], b1[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int k0 = 32 * (wv + kKpWaves * (i + j));
+    a[j] = *(const uint4 *)(hp + k0);
+    b0[j] = *(const uint4 *)(wp0 + k0);
+    b1[j] = *(const uint4 *)(wp1 + k0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    acc0 = kp_mfma<HDT>(a[j], b0[j], acc0);
+    acc1 = kp_mfma<HDT>(a[j], b1[j], acc1);
+  }
+}
+
+template <int HDT>
+__device__ __forceinline__ float kproj_tile32(const void *h, const void *w, int M, int H, int m0, int n0,
+                                              float (*red)[16][33]) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int mrow = min(m0 + (lane & 15), M - 1);
   const int kq = 8 * (lane >> 4);
   const uint16_t *hp = (const uint16_t *)h + (size_t)mrow * H + kq;
-  const uint16_t *wp0 = (const uint16_t *)w + (size_t)(n0 + 32 * wv + (lane & 15)) * H + kq;
+  const uint16_t *wp0 = (const uint16_t *)w + (size_t)(n0 + (lane & 15)) * H + kq;
   const uint16_t *wp1 = wp0 + (size_t)16 * H;
-  acc[0] = f32x4{0.f, 0.f, 0.f, 0.f};
-  acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-  for (int k0 = 0; k0 < H; k0 += 32) {
-    const uint4 a = *(const uint4 *)(hp + k0);
-    const uint4 b0 = *(const uint4 *)(wp0 + k0);
-    const uint4 b1 = *(const uint4 *)(wp1 + k0);
-    const u32x4 av = {a.x, a.y, a.z, a.w}, bv0 = {b0.x, b0.y, b0.z, b0.w}, bv1 = {b1.x, b1.y, b1.z, b1.w};
-    if constexpr (HDT == FFA_DT_BF16) {
-      acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, bv0),
-                                                       acc[0], 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, bv1),
-                                                       acc[1], 0, 0, 0);
-    } else {
-      acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av), __builtin_bit_cast(f16x8, bv0),
-                                                      acc[0], 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av), __builtin_bit_cast(f16x8, bv1),
-                                                      acc[1], 0, 0, 0);
-    }
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  const int nsteps = H / 32;
+  const int mine = (nsteps - wv + kKpWaves - 1) / kKpWaves;  // steps of this wave (16 at H = 4096)
+  int i = 0;
+  for (; i + 16 <= mine; i += 16) kp_steps<16, HDT>(hp, wp0, wp1, wv, i, acc0, acc1);
+  for (; i + 4 <= mine; i += 4) kp_steps<4, HDT>(hp, wp0, wp1, wv, i, acc0, acc1);
+  for (; i < mine; ++i) kp_steps<1, HDT>(hp, wp0, wp1, wv, i, acc0, acc1);
+  // MFMA 16x16 result: acc[u] is row 4 * (lane >> 4) + u, column lane & 15
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    red[wv][4 * (lane >> 4) + u][lane & 15] = acc0[u];
+    red[wv][4 * (lane >> 4) + u][16 + (lane & 15)] = acc1[u];
+  }
+  __syncthreads();
+  const int row = threadIdx.x >> 5, col = threadIdx.x & 31;
+  float sum = red[0][row][col];
+#pragma unroll
+  for (int x = 1; x < kKpWaves; ++x) sum += red[x][row][col];
+  return sum;
+}
+
+// blockIdx.x -> (column tile ct, token tile mt).  Workgroups go to the 8 XCDs round-robin; when the
+// column tiles split evenly over the XCDs, all token tiles of one column tile run on one XCD and share
+// its L2, so each slice of W is read from HBM once.
+__device__ __forceinline__ void kproj_tile_of(int bid, int nct, int &ct, int &mt) {
+  if ((nct & 7) == 0) {
+    const int per = nct >> 3, j = bid >> 3;
+    ct = (bid & 7) + 8 * (j % per);
+    mt = j / per;
+  } else {
+    ct = bid % nct;
+    mt = bid / nct;
+  }
+}
+
+// g32 quantization of one (token, KV head, group) held by the 32 lanes of a half wave (lane e of the
+// half holds channel 32 g + e), with the rules of g32_quantize_store; min / max by shuffles, 2-bit
+// codes OR-reduced over 16 lanes, residual bytes stored by each lane.  All 64 lanes must call it;
+// `store` masks the writes.
+__device__ __forceinline__ void g32_quantize_lanes(float x, bool store, int page, int slot, int hkv, int HKV, int g,
+                                                   uint8_t *kq_pages, uint16_t *s_pages, uint16_t *z_pages,
+                                                   uint8_t *r_pages, int res_e4m3) {
+  constexpr int D = 128;
+  const int e = threadIdx.x & 31;
+  float mn = x, mx = x;
+#pragma unroll
+  for (int m = 1; m < 32; m <<= 1) {
+    mn = fminf(mn, __shfl_xor(mn, m));
+    mx = fmaxf(mx, __shfl_xor(mx, m));
+  }
+  const float zr = (float)(_Float16)mn;
+  const float sc = (float)(_Float16)__fdiv_rn(fmaxf(mx - zr, 1e-6f), 3.0f);
+  const float cq = fminf(fmaxf(__builtin_rintf(__fdiv_rn(x - zr, sc)), 0.f), 3.f);
+  const float deq = (cq * sc) + zr;
+  const uint32_t rb = f32_to_fp8(x - deq, res_e4m3);
+  uint32_t word = ((uint32_t)cq) << (2 * (e & 15));
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) word |= (uint32_t)__shfl_xor((int)word, m);
+  if (!store) return;
+  const size_t blk = (size_t)page * HKV + hkv;
+  r_pages[blk * (64 * D) + res_off(slot, 32 * g + e)] = (uint8_t)rb;
+  if ((e & 15) == 0) *(uint32_t *)(kq_pages + blk * (4 * 64 * 8) + codes_off(g, slot) + 4 * (e >> 4)) = word;
+  if (e == 0) {
+    const int ss = 16 * (slot >> 4) + 4 * (slot & 3) + ((slot >> 2) & 3);  // tile-major scale slot
+    const size_t so = blk * (4 * 64) + gscale_off(g, ss);
+    s_pages[so] = (uint16_t)f32_to_f16_bits(sc);
+    z_pages[so] = (uint16_t)f32_to_f16_bits(zr);
   }
 }
 
@@ -173,98 +257,62 @@ __device__ __forceinline__ float rope_one(float x, float partner, bool odd, floa
   return round_to(t1 + t2, odt);
 }
 
-// Rotated K of the reference producer -> k_scratch [M, N] in dtype odt.
+// Rotated K of the reference producer -> k_scratch [M, N] in dtype odt.  One 512-thread workgroup per
+// (16 tokens, 32 output channels); grid = (N / 32) * ceil(M / 16).
 template <int HDT>
-__global__ __launch_bounds__(256) void kproj_rope_kernel(const void *h, const void *w, const void *bias, const void *cos,
+__global__ __launch_bounds__(512) void kproj_rope_kernel(const void *h, const void *w, const void *bias, const void *cos,
                                                          const void *sin, int csdt, int M, int T, int H, int N, int D,
                                                          void *kout, int odt) {
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int m0 = blockIdx.y * 16, n0 = blockIdx.x * 128;
-  f32x4 acc[2];
-  kproj_tile<HDT>(h, w, M, H, m0, n0, acc);
-#pragma unroll
-  for (int tile = 0; tile < 2; ++tile) {
-    const int col = n0 + 32 * wv + 16 * tile + (lane & 15);
-    const float bv = bias ? load_any(bias, col, HDT) : 0.f;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int m = m0 + 4 * (lane >> 4) + u;
-      // F.linear output in the h dtype
-      const float x = round_to(acc[tile][u] + bv, HDT);
-      const float partner = __shfl_xor(x, 1);
-      const int d = col % D;
-      const int t = m % T;
-      const float c = load_any(cos, (size_t)t * D + d, csdt);
-      const float s = load_any(sin, (size_t)t * D + d, csdt);
-      const float r = rope_one(x, partner, (d & 1) != 0, c, s, odt);
-      if (m < M) store_any(kout, (size_t)m * N + col, odt, r);
-    }
+  __shared__ float red[kKpWaves][16][33];
+  int ct, mt;
+  kproj_tile_of(blockIdx.x, N / 32, ct, mt);
+  const int m0 = mt * 16, n0 = ct * 32;
+  const float acc = kproj_tile32<HDT>(h, w, M, H, m0, n0, red);
+  const int m = m0 + (threadIdx.x >> 5), col = n0 + (threadIdx.x & 31);
+  const float bv = bias ? load_any(bias, col, HDT) : 0.f;
+  const float x = round_to(acc + bv, HDT);  // F.linear output in the h dtype
+  const float partner = __shfl_xor(x, 1);   // channel col ^ 1 (D is even, so the RoPE pair)
+  if (m < M) {
+    const int d = col % D, t = m % T;
+    const float c = load_any(cos, (size_t)t * D + d, csdt);
+    const float s = load_any(sin, (size_t)t * D + d, csdt);
+    store_any(kout, (size_t)m * N + col, odt, rope_one(x, partner, (d & 1) != 0, c, s, odt));
   }
 }
 
-// K-proj + RoPE (fp32 cos/sin rows per token) + g32 quantize + paged append.
+// K-proj + RoPE (fp32 cos/sin rows per token) + g32 quantize + paged append; the 32 channels of a
+// workgroup are one g32 group of one KV head, so quantization needs no other workgroup.
 template <int HDT>
-__global__ __launch_bounds__(256) void kproj_append_kernel(const void *h, const void *w, const void *bias,
+__global__ __launch_bounds__(512) void kproj_append_kernel(const void *h, const void *w, const void *bias,
                                                            const float *cos, const float *sin, int M, int Tn, int H,
                                                            int HKV, const int32_t *pos, const int32_t *bt, int bt_stride,
                                                            uint8_t *kq_pages, uint16_t *s_pages, uint16_t *z_pages,
                                                            uint8_t *r_pages, int res_e4m3, const void *v_new,
-                                                           void *v_pages, int vdt) {
+                                                           void *v_pages) {
   constexpr int D = 128;
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int m0 = blockIdx.y * 16;
-  const int hkv = blockIdx.x;  // one head (128 channels) per workgroup column
-  const int n0 = hkv * D;
-  const int N = HKV * D;
-  __shared__ float s_k[16][D + 1];
-  f32x4 acc[2];
-  kproj_tile<HDT>(h, w, M, H, m0, n0, acc);
-#pragma unroll
-  for (int tile = 0; tile < 2; ++tile) {
-    const int d = 32 * wv + 16 * tile + (lane & 15);
-    const float bv = bias ? load_any(bias, n0 + d, HDT) : 0.f;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int r = 4 * (lane >> 4) + u;
-      const int m = min(m0 + r, M - 1);
-      const float x = round_to(acc[tile][u] + bv, HDT);
-      const float partner = __shfl_xor(x, 1);
-      const float c = cos[(size_t)m * D + d];
-      const float s = sin[(size_t)m * D + d];
-      s_k[r][d] = rope_one(x, partner, (d & 1) != 0, c, s, FFA_DT_F32);  // fp32 cos promotes to fp32
-    }
-  }
-  __syncthreads();
-  // one thread per (token row, group): 16 x 4 = 64 threads
-  if (threadIdx.x < 64) {
-    const int r = threadIdx.x >> 2, g = threadIdx.x & 3;
-    const int m = m0 + r;
-    if (m < M) {
-      const int b = m / Tn, nn = m % Tn;
-      const int P = pos[b] + nn;
-      const int page = bt[(size_t)b * bt_stride + (P >> 6)];
-      const int slot = P & 63;
-      float kv[32];
-      for (int e = 0; e < 32; ++e) kv[e] = s_k[r][32 * g + e];
-      g32_quantize_store(kv, page, slot, hkv, HKV, g, kq_pages, s_pages, z_pages, r_pages, res_e4m3);
-    }
-  }
-  // V append into V^T pages: thread -> (token row, 8 channels)
-  if (v_new != nullptr) {
-    const int r = threadIdx.x >> 4, c8 = (threadIdx.x & 15) * 8;
-    const int m = m0 + r;
-    if (m < M) {
-      const int b = m / Tn, nn = m % Tn;
-      const int P = pos[b] + nn;
-      const int page = bt[(size_t)b * bt_stride + (P >> 6)];
-      const int slot = P & 63;
-      const uint16_t *vs = (const uint16_t *)v_new + ((size_t)m * HKV + hkv) * D + c8;
-      uint16_t *vd = (uint16_t *)v_pages + ((size_t)page * HKV + hkv) * (D * 64);
-      for (int e = 0; e < 8; ++e) vd[vt_off(c8 + e, slot)] = vs[e];
-    }
-  }
-  (void)N;
-  (void)vdt;
+  __shared__ float red[kKpWaves][16][33];
+  int ct, mt;
+  kproj_tile_of(blockIdx.x, HKV * (D / 32), ct, mt);
+  const int m0 = mt * 16, n0 = ct * 32;
+  const int hkv = n0 / D, g = (n0 % D) / 32;
+  const int e = threadIdx.x & 31, d = 32 * g + e;
+  const int m = m0 + (threadIdx.x >> 5), mc = min(m, M - 1);
+  // the epilogue's inputs are fetched before the GEMM so their latency hides behind it
+  const float bv = bias ? load_any(bias, n0 + e, HDT) : 0.f;
+  const float cv = cos[(size_t)mc * D + d], sv = sin[(size_t)mc * D + d];
+  const int b = mc / Tn, nn = mc % Tn;
+  const int P = pos[b] + nn;
+  const uint16_t vv = v_new != nullptr ? ((const uint16_t *)v_new)[((size_t)mc * HKV + hkv) * D + d] : 0;
+  const float acc = kproj_tile32<HDT>(h, w, M, H, m0, n0, red);
+  const float x = round_to(acc + bv, HDT);
+  const float partner = __shfl_xor(x, 1);
+  // fp32 cos / sin promote the rotation to fp32
+  const float k = rope_one(x, partner, (d & 1) != 0, cv, sv, FFA_DT_F32);
+  const int page = bt[(size_t)b * bt_stride + (P >> 6)];
+  const int slot = P & 63;
+  g32_quantize_lanes(k, m < M, page, slot, hkv, HKV, g, kq_pages, s_pages, z_pages, r_pages, res_e4m3);
+  if (v_new != nullptr && m < M)  // V^T pages: this workgroup's 32 channels of each token
+    ((uint16_t *)v_pages)[((size_t)page * HKV + hkv) * (D * 64) + vt_off(d, slot)] = vv;
 }
 
 
@@ -344,16 +392,17 @@ extern "C" int ffa_kproj_rope(const void *h, const void *w_k, const void *bias, 
     return ffa_set_error_internal(FFA_E_UNSUPPORTED, "h must be fp16 or bf16");
   if (!(cs_dtype == FFA_DT_F32 || cs_dtype == h_dtype))
     return ffa_set_error_internal(FFA_E_UNSUPPORTED, "cos/sin must be fp32 or the dtype of h");
-  if (D % 2 || (HKV * D) % 128 || H % 32) return ffa_set_error_internal(FFA_E_UNSUPPORTED, "needs even D, HKV*D % 128 == 0, H % 32 == 0");
+  if (D % 2 || (HKV * D) % 32 || H % 32)
+    return ffa_set_error_internal(FFA_E_UNSUPPORTED, "needs even D, HKV*D % 32 == 0, H % 32 == 0");
   const int M = B * T, N = HKV * D;
   const int odt = cs_dtype == FFA_DT_F32 ? FFA_DT_F32 : h_dtype;
   hipStream_t st = (hipStream_t)stream;
-  dim3 grid(N / 128, (M + 15) / 16);
+  const dim3 grid((unsigned)((N / 32) * ((M + 15) / 16)));
   if (h_dtype == FFA_DT_BF16)
-    hipLaunchKernelGGL(ffa::kproj_rope_kernel<FFA_DT_BF16>, grid, dim3(256), 0, st, h, w_k, bias, cos, sin, cs_dtype, M,
+    hipLaunchKernelGGL(ffa::kproj_rope_kernel<FFA_DT_BF16>, grid, dim3(512), 0, st, h, w_k, bias, cos, sin, cs_dtype, M,
                        T, H, N, D, k_out, odt);
   else
-    hipLaunchKernelGGL(ffa::kproj_rope_kernel<FFA_DT_F16>, grid, dim3(256), 0, st, h, w_k, bias, cos, sin, cs_dtype, M,
+    hipLaunchKernelGGL(ffa::kproj_rope_kernel<FFA_DT_F16>, grid, dim3(512), 0, st, h, w_k, bias, cos, sin, cs_dtype, M,
                        T, H, N, D, k_out, odt);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return ffa_set_error_internal(FFA_E_LAUNCH, hipGetErrorString(e));
@@ -378,22 +427,25 @@ extern "C" int ffa_kproj_rope_q2_append(const void *h, const void *w_k, const vo
                                         const int32_t *block_table, int bt_stride, uint8_t *k_q_pages,
                                         void *scale_pages, void *zero_pages, uint8_t *res_pages, int res_dtype,
                                         const void *v_new, void *v_pages, int v_dtype, void *stream) {
+  if (B <= 0 || Tn <= 0 || H <= 0 || HKV <= 0) return ffa_set_error_internal(FFA_E_INVALID, "bad dims");
   if (!(h_dtype == FFA_DT_F16 || h_dtype == FFA_DT_BF16))
     return ffa_set_error_internal(FFA_E_UNSUPPORTED, "h must be fp16 or bf16");
   if (H % 32) return ffa_set_error_internal(FFA_E_UNSUPPORTED, "H must be a multiple of 32");
   if (!(res_dtype == FFA_DT_FP8_E4M3 || res_dtype == FFA_DT_FP8_E5M2))
     return ffa_set_error_internal(FFA_E_INVALID, "residual dtype must be fp8");
+  if (v_new != nullptr && !(v_dtype == FFA_DT_F16 || v_dtype == FFA_DT_BF16))
+    return ffa_set_error_internal(FFA_E_UNSUPPORTED, "V pages must be fp16 or bf16");
   const int M = B * Tn;
   hipStream_t st = (hipStream_t)stream;
-  dim3 grid(HKV, (M + 15) / 16);
+  const dim3 grid((unsigned)(HKV * 4 * ((M + 15) / 16)));
   if (h_dtype == FFA_DT_BF16)
-    hipLaunchKernelGGL(ffa::kproj_append_kernel<FFA_DT_BF16>, grid, dim3(256), 0, st, h, w_k, bias, cos, sin, M, Tn, H,
+    hipLaunchKernelGGL(ffa::kproj_append_kernel<FFA_DT_BF16>, grid, dim3(512), 0, st, h, w_k, bias, cos, sin, M, Tn, H,
                        HKV, pos, block_table, bt_stride, k_q_pages, (uint16_t *)scale_pages, (uint16_t *)zero_pages,
-                       res_pages, res_dtype == FFA_DT_FP8_E4M3 ? 1 : 0, v_new, v_pages, v_dtype);
+                       res_pages, res_dtype == FFA_DT_FP8_E4M3 ? 1 : 0, v_new, v_pages);
   else
-    hipLaunchKernelGGL(ffa::kproj_append_kernel<FFA_DT_F16>, grid, dim3(256), 0, st, h, w_k, bias, cos, sin, M, Tn, H,
+    hipLaunchKernelGGL(ffa::kproj_append_kernel<FFA_DT_F16>, grid, dim3(512), 0, st, h, w_k, bias, cos, sin, M, Tn, H,
                        HKV, pos, block_table, bt_stride, k_q_pages, (uint16_t *)scale_pages, (uint16_t *)zero_pages,
-                       res_pages, res_dtype == FFA_DT_FP8_E4M3 ? 1 : 0, v_new, v_pages, v_dtype);
+                       res_pages, res_dtype == FFA_DT_FP8_E4M3 ? 1 : 0, v_new, v_pages);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return ffa_set_error_internal(FFA_E_LAUNCH, hipGetErrorString(e));
   return FFA_OK;

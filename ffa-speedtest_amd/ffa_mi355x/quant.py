@@ -85,11 +85,14 @@ def kproj_rope_q2_channel(h, w_k, cos, sin, num_kv_heads, head_dim, bias=None, f
     return (out, k_scr) if return_k else out
 
 
-def kproj_rope_q2_append(cache: PagedQ2Cache, h, w_k, cos_rows, sin_rows, pos, block_table, bias=None, v_new=None):
+def kproj_rope_q2_append(cache: PagedQ2Cache, h, w_k, cos_rows, sin_rows, pos, block_table, bias=None, v_new=None,
+                         validate=True):
     """Project, rotate, g32-quantize and append Tn new tokens per sequence into a paged cache.
 
     h [B, Tn, H]; cos_rows/sin_rows [B, Tn, 128] fp32 (angles of positions pos[b] + n);
-    v_new [B, Tn, HKV, 128] or None.
+    v_new [B, Tn, HKV, 128] or None.  validate=False skips the host-side check that the positions and
+    page ids stay inside the table and the pool (it reads them back, which graph capture forbids): the
+    caller must have checked the same pos / block_table before.
     """
     if not h.is_cuda:
         raise ValueError("kernel requires CUDA tensors.")
@@ -102,7 +105,8 @@ def kproj_rope_q2_append(cache: PagedQ2Cache, h, w_k, cos_rows, sin_rows, pos, b
     sin_rows = sin_rows.float().reshape(B, Tn, 128).contiguous()
     pos = pos.to(device=h.device, dtype=torch.int32).contiguous()
     block_table = block_table.to(device=h.device, dtype=torch.int32).contiguous()
-    check_append_fits(pos, Tn, block_table, cache.P)
+    if validate:
+        check_append_fits(pos, Tn, block_table, cache.P)
     if v_new is not None:
         v_new = v_new.to(cache.v_dtype).contiguous()
     bias = bias.to(h.dtype).contiguous() if bias is not None else None

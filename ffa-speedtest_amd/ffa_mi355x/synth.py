@@ -83,3 +83,33 @@ def page_tables(seq_lens, page=64, seed=0, interleave=True, base=0):
         bt[b, :n] = perm[o:o + n].to(torch.int32) + base
         o += n
     return bt, total
+
+
+def sequence_inputs_device(q_seq, T, HKV=8, D=128, seed=0, n_heavy=16, cos=0.8, dtype=torch.bfloat16):
+    """k, v [1, T, HKV, D] of one sequence, drawn on q_seq's device (for benchmark shapes too large to
+    draw on the host).
+
+    q_seq [HQ, D].  Same construction as `attention_inputs` (N(0, 1) K and V, n_heavy heavy keys per
+    query head at cosine `cos` with it, one inside tokens 0..15) with the device's generator, so the
+    values differ from the host-drawn ones of the same seed.
+    """
+    dev = q_seq.device
+    g = torch.Generator(device=dev).manual_seed(seed)
+    k = torch.randn((T, HKV, D), generator=g, device=dev)
+    v = torch.randn((T, HKV, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
+    HQ = q_seq.shape[0]
+    G = HQ // HKV
+    sin = math.sqrt(max(0.0, 1.0 - cos * cos))
+    if n_heavy and T > 16:
+        qn = q_seq.float() / q_seq.float().norm(dim=-1, keepdim=True)  # [HQ, D]
+        for h in range(HKV):
+            first = torch.randperm(16, generator=g, device=dev)[:G]
+            rest = 16 + torch.randperm(T - 16, generator=g, device=dev)[: G * (n_heavy - 1)]
+            pos = torch.cat([first.view(G, 1), rest.view(G, n_heavy - 1)], 1)  # [G, n_heavy]
+            qh = qn[h * G:(h + 1) * G].unsqueeze(1).expand(G, n_heavy, D)
+            u = torch.randn((G, n_heavy, D), generator=g, device=dev)
+            u = u - (u * qh).sum(-1, keepdim=True) * qh
+            u = u / u.norm(dim=-1, keepdim=True)
+            kn = k[pos, h].norm(dim=-1, keepdim=True)
+            k[pos.reshape(-1), h] = (kn * (cos * qh + sin * u)).reshape(-1, D)
+    return k.to(dtype).unsqueeze(0), v.unsqueeze(0)

@@ -113,6 +113,56 @@ def test_reference_smoke_test(gpu):
     FK.run_smoke_test(gpu, torch.float16, torch.float8_e5m2, B=2, T=32, H=256, HKV=4, K=64)
 
 
+@pytest.mark.parametrize("B,Tn,H,use_bias", [(3, 20, 4096, False), (2, 7, 288, True), (1, 64, 4096, True)])
+def test_kproj_append_multi_token_bit_exact(gpu, B, Tn, H, use_bias):
+    """Appends of several tokens per sequence (token tiles with a ragged last tile, page boundaries,
+    H with whole and partial k batches, bias): every byte equals the oracle's g32 quantization of the
+    rotated K that ffa_kproj_rope (the same GEMM tile) computes; V^T bytes are the new V."""
+    from ffa_mi355x import kfmt_quant as KQ
+    from ffa_mi355x import quant, synth
+    from ffa_mi355x.paged import CODES_ORDER, GSCALE_ORDER, RES_ORDER, VT_ORDER, PagedQ2Cache, to_logical
+
+    HKV = 8
+    g = torch.Generator().manual_seed(B * 100 + Tn)
+    h = torch.randn(B, Tn, H, generator=g).bfloat16()
+    w = (torch.randn(HKV * 128, H, generator=g) * 0.02).bfloat16()  # [out, in] orientation
+    bias = (torch.randn(HKV * 128, generator=g) * 0.1).bfloat16() if use_bias else None
+    pos = torch.tensor([50 + 13 * b for b in range(B)], dtype=torch.int32)
+    inv = 1.0 / (500000.0 ** (torch.arange(0, 128, 2, dtype=torch.float32) / 128))
+    ang = (pos[:, None].float() + torch.arange(Tn, dtype=torch.float32)[None, :])[..., None] * inv
+    emb = torch.cat([ang, ang], -1)  # [B, Tn, 128]
+    cos, sin = emb.cos(), emb.sin()
+    lens = [int(p) + Tn for p in pos]
+    bt, P = synth.page_tables(lens, seed=B)
+    cache = PagedQ2Cache(P, HKV, gpu)
+    v_new = torch.randn(B, Tn, HKV, 128, generator=g).bfloat16()
+    quant.kproj_rope_q2_append(cache, h.to(gpu), w.to(gpu), cos.to(gpu), sin.to(gpu), pos.to(gpu), bt.to(gpu),
+                               bias=None if bias is None else bias.to(gpu), v_new=v_new.to(gpu))
+    M = B * Tn
+    k_own = KQ.kproj_rope(h.view(1, M, H).to(gpu), w.to(gpu), cos.view(M, 128).to(gpu), sin.view(M, 128).to(gpu),
+                          HKV, 128, bias=None if bias is None else bias.to(gpu))
+    torch.cuda.synchronize()
+    k_ref = OP.kproj_rope_rows(f32(h), f32(w), f32(cos), f32(sin), HKV, bias=None if bias is None else f32(bias))
+    assert np.abs(f32(k_own).reshape(B, Tn, HKV, 128) - k_ref).max() < 2e-2 * max(1.0, np.abs(k_ref).max())
+    pk, s, z, r = O.quantize_g32(f32(k_own).reshape(B, Tn, HKV, 128), "e4m3fn")
+    kq_pool = to_logical(cache.k_q.cpu().numpy(), CODES_ORDER, 8)
+    sp = [scale_pos(t) for t in range(64)]
+    s_pool = to_logical(cache.k_scale.float().cpu().numpy(), GSCALE_ORDER)[..., sp]
+    z_pool = to_logical(cache.k_zero.float().cpu().numpy(), GSCALE_ORDER)[..., sp]
+    r_pool = to_logical(cache.k_res.view(torch.uint8).cpu().numpy(), RES_ORDER)
+    v_pool = to_logical(cache.v.view(torch.int16).cpu().numpy(), VT_ORDER)
+    vb = v_new.view(torch.int16).numpy()
+    for b in range(B):
+        for n in range(Tn):
+            t = int(pos[b]) + n
+            page, slot = int(bt[b, t // 64]), t % 64
+            assert np.array_equal(kq_pool[page, :, :, slot].reshape(HKV, 32), pk[b, n]), ("codes", b, n)
+            assert np.array_equal(s_pool[page, :, :, slot], s[b, n]), ("scales", b, n)
+            assert np.array_equal(z_pool[page, :, :, slot], z[b, n]), ("zeros", b, n)
+            assert np.array_equal(r_pool[page, :, slot], r[b, n]), ("residual", b, n)
+            assert np.array_equal(v_pool[page, :, :, slot], vb[b, n]), ("V", b, n)
+
+
 def test_kproj_append_config5_small(gpu):
     """K-proj (theta 5e5, positions 65536+) + g32 quantize + paged append, then decode over the cache."""
     from ffa_mi355x import quant, synth
@@ -156,3 +206,18 @@ def test_kproj_append_config5_small(gpu):
         vg = v_pool[page, :, :, slot]
         assert torch.equal(vg, v_new[b, 0])
     assert mism <= 0.01 * B * HKV * 128
+    # ffa_kproj_rope runs the same GEMM tile (same fp32 sums), so its rotated K, quantized by the oracle,
+    # must give exactly the appended bytes
+    from ffa_mi355x import kfmt_quant as KQ
+
+    k_own = KQ.kproj_rope(h.view(1, B, H).to(gpu), w.to(gpu), cos.view(B, 128).to(gpu), sin.view(B, 128).to(gpu),
+                          HKV, 128)
+    torch.cuda.synchronize()
+    pk2, s2, z2, r2 = O.quantize_g32(f32(k_own).reshape(B, 1, HKV, 128), "e4m3fn")
+    z_pool = to_logical(cache.k_zero.float().cpu().numpy(), GSCALE_ORDER)[..., [scale_pos(t) for t in range(64)]]
+    for b in range(B):
+        page, slot = int(bt[b, int(pos[b]) // 64]), int(pos[b]) % 64
+        assert np.array_equal(kq_pool[page, :, :, slot].reshape(HKV, 32), pk2[b, 0]), "codes"
+        assert np.array_equal(s_pool[page, :, :, slot], s2[b, 0]), "scales"
+        assert np.array_equal(z_pool[page, :, :, slot], z2[b, 0]), "zeros"
+        assert np.array_equal(r_pool[page, :, slot], r2[b, 0]), "residual"
