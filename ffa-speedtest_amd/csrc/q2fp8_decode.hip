@@ -336,7 +336,8 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
         const uint32_t sw = uu < 2 ? s2lo : s2hi, zw = uu < 2 ? z2lo : z2hi;
         const float su = f16_bits_to_f32((sw >> (16 * (uu & 1))) & 0xffffu);
         const float zu = f16_bits_to_f32((zw >> (16 * (uu & 1))) & 0xffffu);
-        r = __builtin_fmaf(su, acc[uu], zu * zq);
+        // z * zq as an fma with a zero addend: one mixed-precision op on the fp16 zero
+        r = __builtin_fmaf(su, acc[uu], __builtin_fmaf(zu, zq, 0.0f));
       } else {
         r = acc[uu];
       }
@@ -383,20 +384,18 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
 #pragma unroll
         for (int uu = 0; uu < 4; ++uu) R[j][4 * uu + tau] = r4[uu];
       }
-      if (t0 + kPage > Tb) {  // tokens past the sequence end (page slots hold no data)
+      if (t0 + kPage > Tb) [[unlikely]] {  // tokens past the sequence end (page slots hold no data)
 #pragma unroll
         for (int k = 0; k < 16; ++k)
           if (t0 + 16 * kc + k >= Tb) R[j][k] = -INFINITY;
       }
-    } else {
-#pragma unroll
-      for (int k = 0; k < 16; ++k) R[j][k] = -INFINITY;
-    }
+    }  // a page past the sequence end leaves R[j] unset: lane_max gives -inf and it is never kept
   };
   // maximum (log2-scaled) of the lane's 16 tokens, reduced over the lanes of one prune block
   // when the block spans several 16-token sub-blocks
   auto lane_max = [&](auto J) -> float {
     constexpr int j = decltype(J)::value;
+    if ((c0 + j) * kPage >= Tb) return -INFINITY;
     float m = R[j][0];
 #pragma unroll
     for (int k = 1; k < 16; ++k) m = fmaxf(m, R[j][k]);
