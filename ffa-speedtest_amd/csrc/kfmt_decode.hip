@@ -61,8 +61,11 @@ __device__ __forceinline__ float load_scale(brsrc rs, uint32_t i, int dt) {
   return dt == 2 ? __uint_as_float(bits) : (dt == 1 ? bf16_bits_to_f32(bits) : f16_bits_to_f32(bits));
 }
 
+// Paged layout: four waves per SIMD (at most 128 registers, one or two spilled), so that four
+// workgroups share a CU; the contiguous layouts stage V through 87 KB of LDS and hold one.
 template <int LAYOUT, int FMT, int SCL, int RES, int VT>
-__global__ __launch_bounds__(256) void kfmt_decode_kernel(const DecodeParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LAYOUT == kPaged ? 4 : 1))) void kfmt_decode_kernel(
+    const DecodeParams p) {
   typedef VTraits<VT> VTr;
   constexpr bool k4 = FMT == kFP4 || FMT == kNF4;
   constexpr bool kGrp = SCL == kSclG16 || SCL == kSclG64;  // per-token group scales (paged modes)
@@ -354,17 +357,15 @@ __global__ __launch_bounds__(256) void kfmt_decode_kernel(const DecodeParams p) 
 #pragma unroll
         for (int uu = 0; uu < 4; ++uu) R[j][4 * uu + tau] = r4[uu];
       }
-      if (t0 + kPage > Tb) {
+      if (t0 + kPage > Tb) [[unlikely]] {  // tokens past the sequence end
 #pragma unroll
         for (int k = 0; k < 16; ++k)
           if (t0 + 16 * kc + k >= Tb) R[j][k] = -INFINITY;
       }
-    } else {
-#pragma unroll
-      for (int k = 0; k < 16; ++k) R[j][k] = -INFINITY;
-    }
+    }  // a page past the sequence end leaves R[j] unset: lane_max gives -inf and it is never kept
   };
   auto lane_max = [&](int j) -> float {
+    if ((c0 + j) * kPage >= Tb) return -INFINITY;
     float m = R[j][0];
 #pragma unroll
     for (int k = 1; k < 16; ++k) m = fmaxf(m, R[j][k]);
@@ -416,6 +417,19 @@ __global__ __launch_bounds__(256) void kfmt_decode_kernel(const DecodeParams p) 
                                     : bl != 0;
     uint4 rr[4][2];
     uint4 vv[8][2];
+    // paged layout: the chunk's codes and group scales again (cache-hot), so that the scoring
+    // registers of the wave's other chunk are not held through this exact pass
+    uint4 ka[4];
+    f32x2 kg[4];
+    if constexpr (LAYOUT == kPaged) {
+      const brsrc rc = page_rows(p.kq, pg[j], kRow, true);
+      const brsrc rs = page_rows((const uint8_t *)p.ks, pg[j], SCL == kSclG16 ? 8 : 4, true);
+#pragma unroll
+      for (int tau = 0; tau < 4; ++tau) {
+        ka[tau] = bload16(rc, (tau * 64 + lane) * 16);
+        kg[tau] = group_scales(rs, 4 * mrow + tau);
+      }
+    }
     if constexpr (RES != kResNone) {
       const brsrc rs = LAYOUT == kPaged ? page_rows(p.kr, pg[j], kD, true)
                                         : make_rsrc(p.kr + (((size_t)b * p.T + t0) * p.HKV + hkv) * kD,
@@ -462,7 +476,10 @@ __global__ __launch_bounds__(256) void kfmt_decode_kernel(const DecodeParams p) 
           const uint4 &rs4 = rr[tau][mp >> 1];
           const uint32_t lo = (mp & 1) ? rs4.z : rs4.x, hi = (mp & 1) ? rs4.w : rs4.y;
           acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-              add_f16x8(dequant(xa[j][tau], xb[j][tau], mp, xs[j][tau], xg[j][tau]), fp8x8_to_f16x8<RES>(lo, hi)), qa[mp], acc, 0, 0, 0);
+              add_f16x8(LAYOUT == kPaged ? dequant(ka[tau], xb[j][tau], mp, xs[j][tau], kg[tau])
+                                         : dequant(xa[j][tau], xb[j][tau], mp, xs[j][tau], xg[j][tau]),
+                        fp8x8_to_f16x8<RES>(lo, hi)),
+              qa[mp], acc, 0, 0, 0);
         }
 #pragma unroll
         for (int uu = 0; uu < 4; ++uu) {

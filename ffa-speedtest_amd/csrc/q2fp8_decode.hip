@@ -79,8 +79,12 @@ __device__ __forceinline__ f16x8 dequant8_channel(uint32_t h, const uint32_t *sp
 // then sit at 16k + 4tau + u, one 8-byte load per lane and tile.
 __host__ __device__ constexpr int scale_pos(int t) { return 16 * (t >> 4) + 4 * (t & 3) + ((t >> 2) & 3); }
 
-template <int LAYOUT, int SMODE, int RES, int VT>
-__global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p) {
+// OCC = 3 asks the compiler for three waves per SIMD (at most 168 registers), so that three
+// workgroups share a CU: used when the grid has more workgroups than two per CU can hold
+// (large batches), where it trades a few spilled registers for a third workgroup in flight.
+template <int LAYOUT, int SMODE, int RES, int VT, int OCC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void q2fp8_decode_kernel(
+    const DecodeParams p) {
   typedef VTraits<VT> VTr;
   constexpr bool kG = SMODE == kG32;
   const int lane = threadIdx.x & 63;
@@ -105,20 +109,23 @@ __global__ __launch_bounds__(256) void q2fp8_decode_kernel(const DecodeParams p)
   const bool row_ok = ir < G;
   const int hq = hkv * G + (row_ok ? ir : 0);
 
-  __shared__ uint4 s_qa[4][64];                    // B operands of the 4 score MFMAs, per lane
   __shared__ uint4 s_qr[4][64];                    // B operands of the 4 residual MFMAs (g32)
-  __shared__ uint4 s_sp[kG ? 1 : 4][64];           // channel scales: fp16 (scale, scale) pairs of 8 channels
-  __shared__ uint4 s_zp2[kG ? 1 : 4][64];          // channel scales: fp16 (zero, zero) pairs
-  __shared__ float s_zs[4][64];                    // g32: partial sums of q16 over 8 channels
+  __shared__ uint4 s_sp[kG ? 1 : 4][kG ? 1 : 64];   // channel scales: fp16 (scale, scale) pairs of 8 channels
+  __shared__ uint4 s_zp2[kG ? 1 : 4][kG ? 1 : 64];  // channel scales: fp16 (zero, zero) pairs
   __shared__ float s_probe[2][4];
   __shared__ float s_wmax[kWaves][4];
   __shared__ int s_kept[kChunksPerWG];             // chunk kept (some prune block survives)
   __shared__ int s_pgid[kChunksPerWG];             // pool page of the chunk
   __shared__ uint32_t s_bal[kChunksPerWG][2];      // survivor ballot of the chunk
   __shared__ float4 s_R[kG ? kChunksPerWG : 1][4][64];        // g32: coarse scores of kept chunks
-  __shared__ uint64_t s_x[kG ? 1 : kChunksPerWG][4][64];       // channel: codes of kept chunks
+  __shared__ uint64_t s_x[kG ? 1 : kChunksPerWG][kG ? 1 : 4][kG ? 1 : 64];  // channel: codes of kept chunks
   __shared__ float s_pm[kChunksPerWG][4], s_pl[kChunksPerWG][4];
-  __shared__ float s_po[kChunksPerWG][4][128];
+  __shared__ __attribute__((aligned(16))) float s_po[kChunksPerWG][4][128];
+  // B operands of the 4 score MFMAs, per lane: read once after the operand barrier, long
+  // before the exact pass writes s_po (two barriers later), so they share its storage
+  uint4(*const s_qa)[64] = reinterpret_cast<uint4(*)[64]>(&s_po[0][0][0]);
+  // g32: partial sums of q16 over 8 channels (read with the operands), after s_qa
+  float(*const s_zs)[64] = reinterpret_cast<float(*)[64]>(&s_po[2][0][0]);
   __shared__ uint8_t s_vstage[LAYOUT == kContig ? kWaves * kPage * kVRow : 4];
 
   // Workgroup barrier for LDS traffic only: __syncthreads() would also wait for every
@@ -852,9 +859,30 @@ extern "C" int ffa_q2fp8_decode_nparts(int T, int BS, int SBS) {
   return (int)((tokens + ffa::kChunksPerWG * ffa::kPage - 1) / (ffa::kChunksPerWG * ffa::kPage));
 }
 
+// CUs of the current device, queried once per device
+static int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 0;
+    cache[dev] = cus;
+  }
+  return cache[dev];
+}
+
 template <int L, int S, int R, int V>
 static hipError_t launch_decode(const ffa::DecodeParams &p, dim3 grid, hipStream_t st) {
-  hipLaunchKernelGGL((ffa::q2fp8_decode_kernel<L, S, R, V>), grid, dim3(256), 0, st, p);
+  // paged g32 with more workgroups than two per CU: the three-per-CU build of the kernel
+  if constexpr (L == ffa::kPaged && S == ffa::kG32) {
+    const int cus = device_cus();
+    if (cus > 0 && grid.x > 2u * (unsigned)cus) {
+      hipLaunchKernelGGL((ffa::q2fp8_decode_kernel<L, S, R, V, 3>), grid, dim3(256), 0, st, p);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((ffa::q2fp8_decode_kernel<L, S, R, V, 1>), grid, dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
