@@ -285,8 +285,8 @@ def main():
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(json.dumps({"error": "this build runs on one GPU: the decode shards by KV head / sequence without "
-                                   "changing the per-GPU kernel (see DESIGN.md); --gpus must be 1"}))
+        print(json.dumps({"error": "this build runs on one GPU (the decode would shard by KV head or sequence "
+                                   "without changing the per-GPU kernel); --gpus must be 1"}))
         sys.exit(2)
 
     if args.workload != "config2":

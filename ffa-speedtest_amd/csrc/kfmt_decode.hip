@@ -2,8 +2,8 @@
 //   fp8 base + fp8 residual   ffa-fp8fp8/attn_kernel/attn_kernel_v1210_fused_bsz_fp8fp8.py:10-136
 //   nvfp4 (e2m1 x block scale) ffa-nvfp4fp8/attn_kernel/attn_kernel_v1210_fused_bsz_nvfp4fp8.py:10-169
 //   nf4 (codebook x channel)  ffa-nf4fp8/attn_kernel/attn_kernel_v1210_fused_bsz_nf4fp8.py:41-167
-// and the BASELINE config-1 variant of the fp8 base with one fp16 scale per token and KV head,
-// plus the BASELINE paged modes of configs 3 and 4 (no reference counterpart): nvfp4 with one
+// and a variant of the fp8 base with one fp16 scale per token and KV head, plus two paged
+// modes (no reference counterpart): nvfp4 with one
 // e4m3 scale per 16 channels of each token, nf4 with one fp16 scale per 64 channels, in
 // 64-token pages (codes [P, HKV, 64, 64], scales [P, HKV, 64, 8 | 2], residual [P, HKV, 64, 128],
 // V^T [P, HKV, 128, 64]; codes, residual and V in the page-internal orders of decode_common.h)

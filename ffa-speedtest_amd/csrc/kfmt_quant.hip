@@ -188,7 +188,7 @@ __global__ __launch_bounds__(256) void nf4_quant_kernel(const void *k, int kdt, 
 }
 
 // ---------------------------------------------------------------------------
-// BASELINE paged modes (no reference counterpart): quantize K rows and append them,
+// Paged group-scale modes (no reference counterpart): quantize K rows and append them,
 // with V, into 64-token pages.  One thread per (token row, KV head, 16 channels);
 // the 8 threads of a row and head are consecutive lanes of one wave.
 //   nvfp4-g16: s = e4m3(min(amax16 / 6, 448)), x = k / s (0 where s == 0),

@@ -8,7 +8,7 @@
 //    runs the GEMM twice): one MFMA GEMM pass writes the rotated K, then the
 //    per-channel quantizer runs on it.
 //  * fused K-proj + RoPE + g32 quantize + append into the paged cache
-//    per-token groups make the append local, so GEMM,
+//    (the decode-time producer): per-token groups make the append local, so GEMM,
 //    RoPE, quantization and the page writes are one kernel.
 #include "decode_common.h"
 #include "ffa_common.h"

@@ -5,7 +5,7 @@
 
 `attn_forward_decode_fp8fp8` keeps the reference signature, defaults and exception
 types (reference :180-312).  Extension through **kwargs: k_scale=[B, T, HKV] (one scale
-per token and KV head, BASELINE config 1), so that k_hat = fp16(k_fp8 * k_scale);
+per token and KV head, no reference counterpart), so that k_hat = fp16(k_fp8 * k_scale);
 seq_lens=[B] int32 (ragged lengths).
 """
 import math

@@ -7,7 +7,7 @@
 normalisation and exception types (reference :202-330).  K is packed NF4 codes (low
 nibble first) with one scale per (sequence, KV head, channel).  Extension through
 **kwargs: seq_lens=[B] int32, workspace=DecodeWorkspace; block_table=[B, n] int32 (with
-T= or seq_lens=) selects the BASELINE paged layout, where k_nf4 / k_scale / k_residual / v are
+T= or seq_lens=) selects the paged layout (64-token page pools, one fp16 absmax per 64 channels), where k_nf4 / k_scale / k_residual / v are
 the page pools of ffa_mi355x.paged_kfmt.PagedKfmtCache("nf4", ...).
 """
 import math
@@ -72,7 +72,7 @@ def attn_forward_decode_nf4(
         raise ValueError("k_residual must be a floating point tensor (e.g., fp8/fp16/bf16)")
 
     if kwargs.get("block_table") is not None:
-        # BASELINE paged layout (per-token group scales; no reference counterpart)
+        # paged layout (per-token group scales; no reference counterpart)
         if use_fp8_residual and k_residual is None:
             raise ValueError("use_fp8_residual=True requires k_residual")
         workspace = kwargs.get("workspace")

@@ -1,10 +1,10 @@
-"""Paged nvfp4 / nf4 KV caches of BASELINE configs 3 and 4 (64-token pages, per-token group scales).
+"""Paged nvfp4 / nf4 KV caches (64-token pages, per-token group scales; no reference counterpart).
 
 The reference keeps one contiguous cache per batch with one nvfp4 scale per
 (sequence, BS-token block, KV head) or one nf4 scale per (sequence, KV head, channel)
 (ffa-nvfp4fp8/attn_kernel/attn_kernel_v1210_fused_bsz_nvfp4fp8.py:225-231,
-ffa-nf4fp8/attn_kernel/attn_kernel_v1210_fused_bsz_nf4fp8.py:212-217).  BASELINE configs
-3 and 4 ask for a page pool shared by all sequences with scales along head_dim instead:
+ffa-nf4fp8/attn_kernel/attn_kernel_v1210_fused_bsz_nf4fp8.py:212-217).  These caches keep
+one page pool shared by all sequences, with scales along head_dim instead:
 
     k        [P, HKV, 64, 64]   u8    packed 4-bit codes, token-major (low nibble first)
     k_scale  [P, HKV, 64, 8]    e4m3  nvfp4: scale of each 16-channel block

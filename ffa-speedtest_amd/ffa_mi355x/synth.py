@@ -1,4 +1,4 @@
-"""Seeded synthetic inputs for the BASELINE configurations (no recorded data).
+"""Seeded synthetic inputs for the benchmark and test workloads (no recorded data).
 
 The reference benchmarks recorded Llama layers (ffa-q2fp8/run_attn_bench_q2.py:26-29),
 which are not available; these generators build inputs of the same shapes.

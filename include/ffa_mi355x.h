@@ -22,8 +22,8 @@
  *   ffa_kproj_rope_q2_channel ffa-q2fp8/fused_kproj_rope_q2fp8.py:492-542
  *                             (the two Triton launches of kproj_rope_quantize_triton)
  *   ffa_q2_quantize_g32_append no reference counterpart: g32 quantize + paged append of
- *                             given K rows (BASELINE configs 2 and 5 cache layout)
- *   ffa_kproj_rope_q2_append  no reference counterpart: BASELINE config 5 append of
+ *                             given K rows (the paged g32 cache layout)
+ *   ffa_kproj_rope_q2_append  no reference counterpart: decode-time append of
  *                             K-proj + RoPE + g32 quantize into the paged cache
  *                             (incremental quantisation is a TODO in the reference,
  *                              ffa-q2fp8/OPTIMIZATION_NOTES.md:23-26)
@@ -35,7 +35,7 @@
  *                             (quantize_k_fp8_fp8_residual)
  *   ffa_nvfp4_quantize        ffa-nvfp4fp8/fused_kproj_rope_nvfp4fp8.py:62-114
  *                             (encode_k_nvfp4_fp8_residual)
- *   ffa_nvfp4_g16_append,     no reference counterpart: BASELINE configs 3 / 4 paged layouts
+ *   ffa_nvfp4_g16_append,     no reference counterpart: paged nvfp4 / nf4 layouts
  *   ffa_nf4_g64_append        (per-token group scales), quantize + append
  *   ffa_nf4_quantize          ffa-nf4fp8/fused_kproj_rope_nf4fp8.py:72-96
  *                             (encode_k_nf4_fp8_residual; the Triton producer
@@ -215,7 +215,7 @@ int ffa_nvfp4_quantize(const void *k, int k_dtype, int B, int T, int HKV, int D,
 int ffa_nf4_quantize_nsplit(int T);
 
 /*
- * BASELINE paged modes of configs 3 / 4 (no reference counterpart): quantize K rows
+ * Paged nvfp4-g16 / nf4-g64 modes (no reference counterpart): quantize K rows
  * k [B, Tn, HKV, 128] (F16/BF16/F32) and append them, with v_new [B, Tn, HKV, 128] (the
  * V pool's 2-byte dtype) or NULL, at positions pos[b] + n of the pages block_table[b, :].
  *   nvfp4-g16: per 16 channels s = e4m3(min(amax / 6, 448)), code = nearest e2m1 level of
@@ -238,7 +238,7 @@ int ffa_nf4_quantize(const void *k, int k_dtype, int B, int T, int HKV, int D, u
  * layouts as in the reference), same prune / refine / merge as ffa_q2fp8_decode:
  *   FFA_KFMT_FP8_E4M3/E5M2 + FFA_KSCALE_NONE   fp8 base, k_hat = fp16(base)
  *       (ffa-fp8fp8/attn_kernel/attn_kernel_v1210_fused_bsz_fp8fp8.py:10-177, launches :263-309)
- *   FFA_KFMT_FP8_E4M3/E5M2 + FFA_KSCALE_TOKEN  k_hat = fp16(base * scale[b, t, h]) (
+ *   FFA_KFMT_FP8_E4M3/E5M2 + FFA_KSCALE_TOKEN  k_hat = fp16(base * scale[b, t, h]) (per-token scales;
  *       no reference counterpart)
  *   FFA_KFMT_NVFP4 + FFA_KSCALE_BLOCK          packed e2m1 nibbles (low nibble first) times
  *       scale[b, t / BS, h] ([B, ceil(T/BS), HKV])
@@ -246,7 +246,7 @@ int ffa_nf4_quantize(const void *k, int k_dtype, int B, int T, int HKV, int D, u
  *   FFA_KFMT_NF4 + FFA_KSCALE_CHANNEL          NF4 codebook times scale[b, h, d] ([B, HKV, 128])
  *       (ffa-nf4fp8/attn_kernel/attn_kernel_v1210_fused_bsz_nf4fp8.py:41-199, launches :300-326)
  *   FFA_KFMT_NVFP4 + FFA_KSCALE_G16 / FFA_KFMT_NF4 + FFA_KSCALE_G64, layout FFA_LAYOUT_PAGED
- *       (BASELINE configs 3 and 4; no reference counterpart): 64-token pages through block_table
+ *       (no reference counterpart): 64-token pages through block_table
  *       [B, bt_stride]: k [P, HKV, 64, 64] packed nibbles, k_scale [P, HKV, 64, 8] e4m3 (G16) or
  *       [P, HKV, 64, 2] fp16 (G64), residual [P, HKV, 64, 128] fp8, v [P, HKV, 128, 64] (V^T pages);
  *       k_hat = fp16(value * scale of the channel's group).  Written by ffa_nvfp4_g16_append /

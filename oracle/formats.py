@@ -12,7 +12,7 @@ reference checkout):
 * quantize_fp8fp8   ffa-fp8fp8/fused_kproj_rope_fp8fp8.py:58-64
 * khat_fp8          ffa-fp8fp8/attn_kernel/attn_kernel_v1210_fused_bsz_fp8fp8.py:87-90 (fp8 -> fp16, exact)
 * quantize_fp8_scaled / khat_fp8_scaled
-                    BASELINE config 1 (no reference counterpart): e4m3 with one fp16
+                    per-token variant (no reference counterpart): e4m3 with one fp16
                     scale per token and KV head, fp16(amax / 448)
 * quantize_nvfp4    ffa-nvfp4fp8/fused_kproj_rope_nvfp4fp8.py:62-114 (all arithmetic in k's dtype)
 * khat_nvfp4        ffa-nvfp4fp8/attn_kernel/attn_kernel_v1210_fused_bsz_nvfp4fp8.py:10-21, 80-81, 123;
@@ -21,11 +21,11 @@ reference checkout):
                     the fp32 scale, the decode the scale rounded to k's dtype)
 * khat_nf4          ffa-nf4fp8/attn_kernel/attn_kernel_v1210_fused_bsz_nf4fp8.py:80-81, 93, 121
 * quantize_nvfp4_g16 / khat_nvfp4_g16
-                    BASELINE config 3 (no reference counterpart): e2m1 with one e4m3 scale per
+                    paged nvfp4 mode (no reference counterpart): e2m1 with one e4m3 scale per
                     16 channels of each token, s = e4m3(amax / 6); the codes follow the
                     reference encoder's midpoint rule (bucketize right=True), k_hat = fp16(level * s)
 * quantize_nf4_g64 / khat_nf4_g64
-                    BASELINE config 4 (no reference counterpart): NF4 with one fp16 absmax scale
+                    paged nf4 mode (no reference counterpart): NF4 with one fp16 absmax scale
                     per 64 channels of each token, s = fp16(max(amax, 1e-6)); codes by the
                     reference encoder's rule (clamp to [-1, 1], bucketize right=False),
                     k_hat = fp16(codebook[c] * s)
@@ -77,7 +77,7 @@ def khat_fp8(base: np.ndarray, fmt: str) -> np.ndarray:
 
 
 def quantize_fp8_scaled(k: np.ndarray, fmt: str = "e4m3fn"):
-    """BASELINE config 1: s = fp16(max(amax_d |k|, 1e-6) / 448) per (b, t, h); base = fp8(k / s);
+    """Per-token-scaled fp8: s = fp16(max(amax_d |k|, 1e-6) / 448) per (b, t, h); base = fp8(k / s);
     residual = fp8(k - base * s).  Returns (base u8 [B,T,HKV,D], scale f32 [B,T,HKV], residual u8)."""
     k = np.asarray(k, F32)
     fmax = 448.0 if fmt == "e4m3fn" else 57344.0
@@ -164,7 +164,7 @@ def khat_nf4(packed: np.ndarray, scale: np.ndarray, D: int) -> np.ndarray:
     return round_f16((NF4_CODEBOOK[c] * np.asarray(scale, F32)[:, None]).astype(F32))
 
 
-# ----------------------------------------------------------------------------- BASELINE per-token group scales
+# ----------------------------------------------------------------------------- per-token group scales (paged modes)
 def quantize_nvfp4_g16(k: np.ndarray, fmt: str = "e4m3fn"):
     """k [..., 128] (values of k's dtype) -> (packed u8 [..., 64], scale bytes u8 [..., 8] (e4m3),
     residual u8 [..., 128]).  Per 16-channel block: s = e4m3(min(amax / 6, 448)); x = k / s (0 where

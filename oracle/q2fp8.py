@@ -9,7 +9,7 @@ checkout):
 
 * quantize_per_channel   ffa-q2fp8/run_attn_bench_q2.py:78-105
                          (== ffa-q2fp8/fused_kproj_rope_q2fp8.py:40-68)
-* quantize_g32           BASELINE layout (2-bit, groups of 32 along D, fp16
+* quantize_g32           paged-cache layout (2-bit, groups of 32 along D, fp16
                          scale/zero per token).  The reference has no such
                          quantizer; the rules mirror the per-channel one.
 * decode                 ffa-q2fp8/attn_kernel/attn_kernel_v1210_fused_bsz_q2fp8.py
@@ -93,7 +93,7 @@ def quantize_per_channel(k: np.ndarray, tau: str, fp8: str = "e5m2"):
 
 
 def quantize_g32(k: np.ndarray, fp8: str = "e4m3fn", group: int = 32):
-    """BASELINE q2 layout: groups of `group` along D, fp16 scale/zero per token.
+    """Paged-cache q2 layout: groups of `group` along D, fp16 scale/zero per token.
 
     k: [..., D] float32 (any tau).  Per group g of one token:
       zero  = fp16(min_g k)
