@@ -90,6 +90,8 @@ def cpu_baseline(q, k, v, BS, SBS, delta, seconds):
 
 
 WORKLOADS = {
+    "config1": "BASELINE config 1: fp8 e4m3 K with one fp16 scale per token and KV head + e4m3 residual, bf16 V, "
+               "B=1, T=4096, 32/8/128, 4 of 128 K channels x10, contiguous cache, BS=SBS=64, delta=5",
     "config3": "BASELINE config 3: nvfp4-g16 + e4m3 residual pruned decode, B=4 x 128K, 32/8/128, 64-token pages "
                "interleaved across sequences",
     "config4": "BASELINE config 4: nf4-g64 + e4m3 residual pruned decode, B=16 ragged 8K-64K (seeded), 32/8/128, "
@@ -128,6 +130,88 @@ def _graph_time(step, R, reps, stream, per_graph=1):
     torch.cuda.synchronize()
     n = reps * R * per_graph
     return e0.elapsed_time(e1) * 1e3 / n, n
+
+
+def bench_config1(args):
+    """BASELINE config 1 on the GPU (the reference runs it on the CPU): HIP quantizer, then the fp8 decode over
+    the contiguous cache; 24 rotated copies defeat the MALL.  cpu_baseline: the numpy oracle, 1 thread."""
+    import numpy as np
+    import torch
+    from threadpoolctl import threadpool_limits
+
+    from ffa_mi355x import _native as N
+    from ffa_mi355x import kfmt_quant as KQ
+    from ffa_mi355x import synth
+    from ffa_mi355x.decode import DecodeWorkspace
+    from ffa_mi355x.kfmt import run_kfmt_decode
+
+    dev = torch.device("cuda:0")
+    B, HQ, HKV, D, T, BS, SBS, R = 1, 32, 8, 128, 4096, 64, 64, args.rotations
+    t_setup = time.perf_counter()
+    q, k, v = synth.attention_inputs(B=B, T=T, HQ=HQ, HKV=HKV, D=D, seed=0, n_heavy=0, outlier_channels=4,
+                                     outlier_scale=10.0)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    base, sc, res = KQ.quantize_fp8_scaled(kd, torch.float8_e4m3fn)
+    copies = [(base.clone(), sc.clone(), res.clone(), vd.clone()) for _ in range(R)]
+    ws = DecodeWorkspace(B, HQ, HKV, T, BS, SBS, dev, torch.bfloat16)
+    scale = 1.0 / math.sqrt(D)
+
+    def step(r):
+        b_, s_, r_, v_ = copies[r]
+        run_kfmt_decode(q=qd, k=b_, k_format=N.KFMT_FP8_E4M3, k_scale=s_, scale_kind=N.KSCALE_TOKEN, v=v_,
+                        k_residual=r_, use_res=True, T=T, HKV=HKV, scale=scale, BS=BS, SBS=SBS, delta=args.delta,
+                        workspace=ws)
+
+    for r in range(R):
+        step(r)
+    torch.cuda.synchronize()
+    o0, mask = ws.o.clone(), ws.mask_buf.clone()
+    stream = torch.cuda.Stream()
+    setup_s = time.perf_counter() - t_setup
+    us, steps = _graph_time(step, R, max(1, math.ceil(args.steps / R)), stream)
+    assert torch.equal(o0, ws.o), "graph replays must match the eager step"
+    kept_th = kept_token_heads(mask, T, SBS)
+    keep_frac = float(mask.float().mean().item())
+    nbytes = T * HKV * (D + 2) + kept_th * _KEPT + B * HQ * D * 4
+    gbs = nbytes / (us * 1e-6) / 1e9
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import formats as OF
+        from oracle import q2fp8 as O
+
+        kf, qf, vf = k.float().numpy(), q.float().numpy(), v.float().numpy()
+        ob, osc, ores = OF.quantize_fp8_scaled(kf, "e4m3fn")  # cache building, not timed
+        kh = OF.khat_fp8_scaled(ob, osc, "e4m3fn")
+        times = []
+        with threadpool_limits(1):
+            t_end = time.perf_counter() + args.cpu_seconds
+            while True:
+                t0 = time.perf_counter()
+                O.decode(qf, ob, None, None, vf, ores, res_fmt="e4m3fn", BS=BS, SBS=SBS, delta=args.delta, khat=kh,
+                         out_dtype="bf16")
+                times.append(time.perf_counter() - t0)
+                if time.perf_counter() > t_end and len(times) >= 3:
+                    break
+        cpu = {"value": round(statistics.median(times) * 1e6, 1), "unit": "us/step", "cores": 1, "kind": "port",
+               "sample": f"full workload (B=1, T={T}, 32/8/128, per-token fp8 + e4m3 residual), numpy oracle, 1 thread, "
+                         f"median of {len(times)} runs; cache quantization not timed"}
+        del np
+    line = {
+        "metric": "config1 decode-attn us/step + HBM TB/s on the algorithmic bytes",
+        "value": round(us, 3), "unit": "us/step", "n_gpus": 1, "steps": steps, "warmup": R,
+        "ms_per_step": round(us / 1e3, 6), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "e4m3 K x fp16 token scale + e4m3 residual, bf16 V; f16/bf16 MFMA, f32 accumulate",
+        "data": "synthetic (seeded N(0,1) bf16, 4 K channels x10)",
+        "config": {"workload": WORKLOADS["config1"], "B": B, "T": T, "HQ": HQ, "HKV": HKV, "D": D, "BS": BS,
+                   "SBS": SBS, "delta": args.delta, "keep_fraction": round(keep_frac, 4), "algorithmic_bytes": nbytes,
+                   "rotations": R, "timing": "HIP graph of R steps (decode + merge), hipEvents over the replays"},
+        "decode_hbm_tbps": round(gbs / 1e3, 4),
+        "decode_hbm_pct_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
+        "cpu_baseline": cpu,
+        "setup_s": round(setup_s, 1),
+    }
+    print(json.dumps(line), flush=True)
 
 
 def bench_workload(args):
@@ -270,7 +354,7 @@ def main():
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run 5 device copies of 256 MiB (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--workload", choices=("config2",) + tuple(WORKLOADS), default="config2",
-                    help="config2 (default) is the metric's line; config3/4/5 time the other BASELINE decodes")
+                    help="config2 (default) is the metric's line; config1/3/4/5 time the other BASELINE decodes")
     args = ap.parse_args()
     if args.copy_probe:
         import torch
@@ -289,6 +373,9 @@ def main():
                                    "without changing the per-GPU kernel); --gpus must be 1"}))
         sys.exit(2)
 
+    if args.workload == "config1":
+        bench_config1(args)
+        return
     if args.workload != "config2":
         bench_workload(args)
         return

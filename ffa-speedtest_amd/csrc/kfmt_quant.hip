@@ -60,6 +60,32 @@ __global__ __launch_bounds__(256) void fp8fp8_quant_kernel(const void *k, int kd
 }
 
 // ---------------------------------------------------------------------------
+// per-token-scaled fp8 (no reference counterpart): for each row of D values (one token and
+// KV head) s = fp16(max(amax |k|, 1e-6) / fmax) (fmax = 448 for e4m3, 57344 for e5m2),
+// base = fp8(k / s), residual = fp8(k - value(base) * s); the product is exact (at most
+// 4 x 11 significant bits).  One wave per row, lane e holds elements e, e + 64, ...
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void fp8_scaled_quant_kernel(const void *k, int kdt, size_t rows, int D,
+                                                               uint8_t *base, uint16_t *scale, uint8_t *res,
+                                                               int e4m3) {
+  const size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // whole waves
+  const int lane = threadIdx.x & 63;
+  const size_t r0 = row * (size_t)D;
+  float amax = 0.f;
+  for (int d = lane; d < D; d += 64) amax = fmaxf(amax, fabsf(load_any(k, r0 + d, kdt)));
+  amax = wave_max(amax);
+  const float s = (float)(_Float16)__fdiv_rn(fmaxf(amax, 1e-6f), e4m3 ? 448.f : 57344.f);
+  for (int d = lane; d < D; d += 64) {
+    const float x = load_any(k, r0 + d, kdt);
+    const uint32_t bb = f32_to_fp8(__fdiv_rn(x, s), e4m3);
+    base[r0 + d] = (uint8_t)bb;
+    res[r0 + d] = (uint8_t)f32_to_fp8(x - fp8_bits_to_f32(bb, e4m3) * s, e4m3);
+  }
+  if (lane == 0) scale[row] = (uint16_t)f32_to_f16_bits(s);
+}
+
+// ---------------------------------------------------------------------------
 // nvfp4: one workgroup per (sequence, page, KV head)
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float fp4_level(int i) {
@@ -286,6 +312,17 @@ extern "C" int ffa_fp8fp8_quantize(const void *k, int k_dtype, size_t n, uint8_t
   const size_t threads = (n + 3) / 4;
   hipLaunchKernelGGL(ffa::fp8fp8_quant_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
                      (hipStream_t)stream, k, k_dtype, n, base, residual, fp8_dtype == FFA_DT_FP8_E4M3 ? 1 : 0);
+  return launch_status();
+}
+
+extern "C" int ffa_fp8_scaled_quantize(const void *k, int k_dtype, size_t rows, int D, uint8_t *base, void *scale,
+                                       uint8_t *residual, int fp8_dtype, void *stream) {
+  if (D <= 0) return ffa_set_error_internal(FFA_E_INVALID, "bad dims");
+  if (!is_float(k_dtype)) return ffa_set_error_internal(FFA_E_INVALID, "k dtype");
+  if (!is_fp8(fp8_dtype)) return ffa_set_error_internal(FFA_E_INVALID, "fp8 dtype");
+  if (rows == 0) return FFA_OK;
+  hipLaunchKernelGGL(ffa::fp8_scaled_quant_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, (hipStream_t)stream,
+                     k, k_dtype, rows, D, base, (uint16_t *)scale, residual, fp8_dtype == FFA_DT_FP8_E4M3 ? 1 : 0);
   return launch_status();
 }
 

@@ -33,6 +33,7 @@ EXPORTS = (
     "ffa_q2_quantize_g32_append",
     "ffa_kproj_rope",
     "ffa_fp8fp8_quantize",
+    "ffa_fp8_scaled_quantize",
     "ffa_nvfp4_quantize",
     "ffa_nf4_quantize_nsplit",
     "ffa_nf4_quantize",
@@ -178,6 +179,8 @@ def lib() -> ctypes.CDLL:
         L.ffa_kproj_rope.restype = ci
         L.ffa_fp8fp8_quantize.argtypes = [vp, ci, ctypes.c_size_t, vp, vp, ci, vp]
         L.ffa_fp8fp8_quantize.restype = ci
+        L.ffa_fp8_scaled_quantize.argtypes = [vp, ci, ctypes.c_size_t, ci, vp, vp, vp, ci, vp]
+        L.ffa_fp8_scaled_quantize.restype = ci
         L.ffa_nvfp4_quantize.argtypes = [vp, ci, ci, ci, ci, ci, ci, vp, vp, vp, ci, vp]
         L.ffa_nvfp4_quantize.restype = ci
         L.ffa_nf4_quantize_nsplit.argtypes = [ci]

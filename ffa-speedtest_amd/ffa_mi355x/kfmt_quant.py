@@ -38,6 +38,22 @@ def quantize_fp8fp8(k: torch.Tensor, fp8_dtype=torch.float8_e5m2):
     return base, res
 
 
+def quantize_fp8_scaled(k: torch.Tensor, fp8_dtype=torch.float8_e4m3fn):
+    """k [..., D] -> (base fp8 [..., D], scale fp16 [...], residual fp8 [..., D]) with one fp16 scale per
+    row (token and KV head): s = fp16(max(amax, 1e-6) / fmax), base = fp8(k / s), residual = fp8(k - base * s)."""
+    k = _check_k(k, fp8_dtype)
+    D = k.shape[-1]
+    rows = k.numel() // D if D else 0
+    base = torch.empty(k.shape, dtype=fp8_dtype, device=k.device)
+    res = torch.empty(k.shape, dtype=fp8_dtype, device=k.device)
+    scale = torch.empty(k.shape[:-1], dtype=torch.float16, device=k.device)
+    rc = N.lib().ffa_fp8_scaled_quantize(k.data_ptr(), N.dtype_code(k.dtype), rows, D, base.data_ptr(),
+                                         scale.data_ptr(), res.data_ptr(), N.dtype_code(fp8_dtype),
+                                         N.stream_of(k.device))
+    N.check(rc, "ffa_fp8_scaled_quantize")
+    return base, scale, res
+
+
 def encode_nvfp4(k: torch.Tensor, fp8_dtype, page_size: int):
     """(packed [B,T,HKV,ceil(D/2)] u8, scale [B,ceil(T/page),HKV] in k.dtype, residual [B,T,HKV,D] fp8)."""
     k = _check_k(k, fp8_dtype)

@@ -33,6 +33,8 @@
  *                             ffa-nf4fp8/fused_kproj_rope_nf4fp8.py:428-436
  *   ffa_fp8fp8_quantize       ffa-fp8fp8/fused_kproj_rope_fp8fp8.py:58-64
  *                             (quantize_k_fp8_fp8_residual)
+ *   ffa_fp8_scaled_quantize   no reference counterpart: fp8 K with one fp16 scale per
+ *                             token and KV head (read by ffa_kfmt_decode)
  *   ffa_nvfp4_quantize        ffa-nvfp4fp8/fused_kproj_rope_nvfp4fp8.py:62-114
  *                             (encode_k_nvfp4_fp8_residual)
  *   ffa_nvfp4_g16_append,     no reference counterpart: paged nvfp4 / nf4 layouts
@@ -210,6 +212,12 @@ int ffa_kproj_rope(const void *h, const void *w_k, const void *bias, int h_dtype
  */
 int ffa_fp8fp8_quantize(const void *k, int k_dtype, size_t n, uint8_t *base, uint8_t *residual, int fp8_dtype,
                         void *stream);
+/* Per-token-scaled fp8 (no reference counterpart; the K layout ffa_kfmt_decode reads with
+ * FFA_KSCALE_TOKEN): k [rows, D] (k_dtype) -> base [rows, D] fp8, scale [rows] fp16,
+ * residual [rows, D] fp8; per row s = fp16(max(amax |k|, 1e-6) / fmax) with fmax 448 (e4m3)
+ * or 57344 (e5m2), base = fp8(k / s), residual = fp8(k - base * s). */
+int ffa_fp8_scaled_quantize(const void *k, int k_dtype, size_t rows, int D, uint8_t *base, void *scale,
+                            uint8_t *residual, int fp8_dtype, void *stream);
 int ffa_nvfp4_quantize(const void *k, int k_dtype, int B, int T, int HKV, int D, int page_size, uint8_t *k_packed,
                        void *scale, uint8_t *residual, int res_dtype, void *stream);
 int ffa_nf4_quantize_nsplit(int T);

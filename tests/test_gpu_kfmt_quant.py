@@ -48,6 +48,30 @@ def _u8(t):
 
 @pytest.mark.parametrize("tau", ["bf16", "fp16", "fp32"])
 @pytest.mark.parametrize("fmt", ["e4m3fn", "e5m2"])
+@pytest.mark.parametrize("D", [128, 77])
+def test_fp8_scaled_quantizer_bit_exact(gpu, tau, fmt, D):
+    """Per-token-scaled fp8 (one fp16 scale per token and KV head): base, scale and residual
+    bytes equal the oracle's, with outlier channels, an all-zero row and a tiny row."""
+    from ffa_mi355x import kfmt_quant as KQ
+
+    k = _k((2, 300, 8, D), tau, 3)
+    k[0, 5, 2] = 0.0  # amax 0: s = fp16(1e-6 / fmax)
+    k[1, 7, 1] = (torch.randn(D) * 1e-7).to(TORCH_DT[tau])
+    base, sc, res = KQ.quantize_fp8_scaled(k.to(gpu), FP8_DT[fmt])
+    torch.cuda.synchronize()
+    ob, osc, orr = OF.quantize_fp8_scaled(f32(k), fmt)
+    assert base.shape == k.shape and sc.shape == k.shape[:-1] and sc.dtype == torch.float16
+    assert np.array_equal(_u8(base), ob)
+    assert np.array_equal(f32(sc), osc)
+    # rows whose scale underflows fp16 to 0 give NaN bases and residuals (NaN sign not specified)
+    nan = (lambda b: (b & 0x7F) == 0x7F) if fmt == "e4m3fn" else (lambda b: ((b & 0x7C) == 0x7C) & ((b & 3) != 0))
+    g = _u8(res)
+    assert np.array_equal(g[~nan(orr)], orr[~nan(orr)]) and nan(g[nan(orr)]).all()
+    assert (osc[0, 5, 2] == 0.0) and nan(orr[0, 5, 2]).all()
+
+
+@pytest.mark.parametrize("tau", ["bf16", "fp16", "fp32"])
+@pytest.mark.parametrize("fmt", ["e4m3fn", "e5m2"])
 def test_fp8fp8_quantizer_bit_exact(gpu, tau, fmt):
     k = _k((2, 77, 3, 128), tau, 1)
     # 1000 / -60000 overflow e4m3 (NaN base), 1e-9 underflows to zero
