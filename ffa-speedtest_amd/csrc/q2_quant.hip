@@ -147,6 +147,19 @@ __device__ __forceinline__ f32x4 kp_mfma(uint4 a, uint4 b, f32x4 c) {
                                                   0, 0);
 }
 
+// Operand loads read 4 lanes per row (lane L: row L >> 2, 16-byte piece L & 3 of the step's
+// 64 bytes), so a 16-lane quarter of the wave touches 4 rows; the MFMA layout (lane L: row
+// L & 15, piece L >> 4) puts 16 rows in each quarter, which the memory pipeline serves about
+// twice as slowly.  A cross-lane permute then moves each piece to its MFMA lane.
+__device__ __forceinline__ uint4 kp_to_mfma_layout(uint4 v) {
+  const int lane = threadIdx.x & 63;
+  const int src = (4 * (lane & 15) + (lane >> 4)) << 2;  // byte address of the source lane
+  return make_uint4((uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)v.x),
+                    (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)v.y),
+                    (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)v.z),
+                    (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)v.w));
+}
+
 // NB k steps of one wave: all 3 * NB loads are issued before the first MFMA waits.
 template <int NB, int HDT>
 __device__ __forceinline__ void kp_steps(const uint16_t *hp, const uint16_t *wp0, const uint16_t *wp1, int wv, int i,
@@ -162,8 +175,9 @@ __device__ __forceinline__ void kp_steps(const uint16_t *hp, const uint16_t *wp0
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int j = 0; j < NB; ++j) {
-    acc0 = kp_mfma<HDT>(a[j], b0[j], acc0);
-    acc1 = kp_mfma<HDT>(a[j], b1[j], acc1);
+    const uint4 aj = kp_to_mfma_layout(a[j]);
+    acc0 = kp_mfma<HDT>(aj, kp_to_mfma_layout(b0[j]), acc0);
+    acc1 = kp_mfma<HDT>(aj, kp_to_mfma_layout(b1[j]), acc1);
   }
 }
 
@@ -171,10 +185,11 @@ template <int HDT>
 __device__ __forceinline__ float kproj_tile32(const void *h, const void *w, int M, int H, int m0, int n0,
                                               float (*red)[16][33]) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int mrow = min(m0 + (lane & 15), M - 1);
-  const int kq = 8 * (lane >> 4);
+  // load layout: lane L reads row L >> 2, elements 8 (L & 3) .. + 8 of each 32-wide k step
+  const int mrow = min(m0 + (lane >> 2), M - 1);
+  const int kq = 8 * (lane & 3);
   const uint16_t *hp = (const uint16_t *)h + (size_t)mrow * H + kq;
-  const uint16_t *wp0 = (const uint16_t *)w + (size_t)(n0 + (lane & 15)) * H + kq;
+  const uint16_t *wp0 = (const uint16_t *)w + (size_t)(n0 + (lane >> 2)) * H + kq;
   const uint16_t *wp1 = wp0 + (size_t)16 * H;
   f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
   const int nsteps = H / 32;
