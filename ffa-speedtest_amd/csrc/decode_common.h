@@ -157,7 +157,8 @@ __device__ __forceinline__ f16x2 bits_f16x2(uint32_t v) { return __builtin_bit_c
 
 __device__ __forceinline__ f16x8 add_f16x8(f16x8 a, f16x8 b) { return a + b; }
 
-// stage 2: log-sum-exp merge of the per-workgroup partials (defined in q2fp8_decode.hip)
-__global__ void q2fp8_merge_kernel(const DecodeParams p);
+// stage 2: log-sum-exp merge of the per-workgroup partials (defined in q2fp8_decode.hip):
+// launches the merge kernel suited to the batch on stream st
+hipError_t launch_merge(const DecodeParams &p, hipStream_t st);
 
 }  // namespace ffa

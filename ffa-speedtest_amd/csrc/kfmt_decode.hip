@@ -769,8 +769,7 @@ extern "C" int ffa_kfmt_decode(const ffa_kfmt_decode_args *a, void *stream) {
   else
     return ffa_set_error_internal(FFA_E_UNSUPPORTED, "unsupported K format / scale granularity combination");
   if (e != hipSuccess) return ffa_set_error_internal(FFA_E_LAUNCH, hipGetErrorString(e));
-  hipLaunchKernelGGL(ffa::q2fp8_merge_kernel, dim3(a->B * a->HQ * 4), dim3(64), 0, st, p);
-  e = hipGetLastError();
+  e = ffa::launch_merge(p, st);
   if (e != hipSuccess) return ffa_set_error_internal(FFA_E_LAUNCH, hipGetErrorString(e));
   return FFA_OK;
 }

@@ -758,11 +758,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
 // --------------------------------------------------------------------------
 // Log-sum-exp merge of the workgroup partials (attn_kernel...q2fp8.py:142-171).
 // One wave per (sequence, query head, 32-column slab): lane k owns partials k,
-// k + 64, ...; m, l and the first 64 partials' columns are loaded in one batch of
-// unconditional buffer loads (validity = resource size), the maxima and sums go
+// k + 64, ...; m, l and (small batches) the first 64 partials' columns are loaded in one
+// batch of unconditional buffer loads (validity = resource size), the maxima and sums go
 // through register exchanges, the column sums over lanes through LDS.
 // --------------------------------------------------------------------------
-__global__ __launch_bounds__(64) void q2fp8_merge_kernel(const DecodeParams p) {
+template <bool LAZY>
+__device__ __forceinline__ void merge_partials(const DecodeParams &p) {
   const int row = blockIdx.x >> 2;  // b * HQ + hq
   const int slab = blockIdx.x & 3;
   const int b = row / p.HQ;
@@ -774,12 +775,24 @@ __global__ __launch_bounds__(64) void q2fp8_merge_kernel(const DecodeParams p) {
   const brsrc ro = make_rsrc(p.o_buf + (size_t)row * p.nparts * 128 + 32 * slab, nparts > 0 ? ((nparts - 1) * 128 + 32) * 4 : 0);
   __shared__ float s_o[64][33];
 
-  // first partial of the lane (slots past nparts read as l = 0, o = 0)
+  // first partial of the lane (slots past nparts read as l = 0, o = 0).  Eager (small
+  // batches): its columns are loaded with m and l in one round trip, kept or not.  LAZY (many
+  // rows): only partials with l > 0 are read, a second round trip, since most slots of long
+  // sequences hold pruned spans and reading them all would dominate the traffic.
   const float m0 = __uint_as_float(bload4(rm, lane * 4));
   const float l0 = __uint_as_float(bload4(rl, lane * 4));
   uint4 o0[8];
+  if constexpr (!LAZY) {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) o0[e] = bload16(ro, (lane * 128 + 4 * e) * 4);
+    for (int e = 0; e < 8; ++e) o0[e] = bload16(ro, (lane * 128 + 4 * e) * 4);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o0[e] = make_uint4(0, 0, 0, 0);
+    if (l0 > 0.f) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o0[e] = bload16(ro, (lane * 128 + 4 * e) * 4);
+    }
+  }
   float M = l0 > 0.f ? m0 : -INFINITY;
   for (int k = lane + 64; k < nparts; k += 64) {
     const float l = __uint_as_float(bload4(rl, k * 4));
@@ -832,6 +845,19 @@ __global__ __launch_bounds__(64) void q2fp8_merge_kernel(const DecodeParams p) {
   sum = swap32_sum(sum);
   if (lane < 32)
     store_any(p.out, (size_t)row * 128 + 32 * slab + c, p.out_dtype, A == 0.f ? 0.f : sum / A);
+}
+
+__global__ __launch_bounds__(64) void q2fp8_merge_kernel(const DecodeParams p) { merge_partials<false>(p); }
+__global__ __launch_bounds__(64) void q2fp8_merge_sparse_kernel(const DecodeParams p) { merge_partials<true>(p); }
+
+// more than 256 query rows (8 sequences of 32 heads): the lazy merge
+hipError_t launch_merge(const DecodeParams &p, hipStream_t st) {
+  const dim3 grid((unsigned)(p.B * p.HQ * 4));
+  if (p.B * p.HQ > 256)
+    hipLaunchKernelGGL(q2fp8_merge_sparse_kernel, grid, dim3(64), 0, st, p);
+  else
+    hipLaunchKernelGGL(q2fp8_merge_kernel, grid, dim3(64), 0, st, p);
+  return hipGetLastError();
 }
 
 }  // namespace ffa
@@ -978,8 +1004,8 @@ static int launch_stage1(const ffa_q2fp8_decode_args *a, const ffa::DecodeParams
 }
 
 static int launch_stage2(const ffa_q2fp8_decode_args *a, const ffa::DecodeParams &p, hipStream_t st) {
-  hipLaunchKernelGGL(ffa::q2fp8_merge_kernel, dim3(a->B * a->HQ * 4), dim3(64), 0, st, p);
-  const hipError_t e = hipGetLastError();
+  (void)a;
+  const hipError_t e = ffa::launch_merge(p, st);
   if (e != hipSuccess) return set_err(FFA_E_LAUNCH, hipGetErrorString(e));
   return FFA_OK;
 }
