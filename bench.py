@@ -90,6 +90,9 @@ def cpu_baseline(q, k, v, BS, SBS, delta, seconds):
 
 
 WORKLOADS = {
+    "config2ref": "BASELINE config 2 in the reference's own layout: per-channel q2 scale/zero over T, e5m2 "
+                  "residual, contiguous [B, T, HKV, D] cache (ffa-q2fp8/run_attn_bench_q2.py:78-105), bs=1, 32K ctx, "
+                  "32/8/128, BS=SBS=64, delta=5",
     "config1": "BASELINE config 1: fp8 e4m3 K with one fp16 scale per token and KV head + e4m3 residual, bf16 V, "
                "B=1, T=4096, 32/8/128, 4 of 128 K channels x10, contiguous cache, BS=SBS=64, delta=5",
     "config3": "BASELINE config 3: nvfp4-g16 + e4m3 residual pruned decode, B=4 x 128K, 32/8/128, 64-token pages "
@@ -130,6 +133,61 @@ def _graph_time(step, R, reps, stream, per_graph=1):
     torch.cuda.synchronize()
     n = reps * R * per_graph
     return e0.elapsed_time(e1) * 1e3 / n, n
+
+
+def bench_config2_reference_layout(args):
+    """Config 2's inputs in the reference's contiguous per-channel layout, quantized by the HIP port of the
+    reference quantizer and decoded through the stage-1 + merge launches; 24 rotated copies."""
+    import torch
+
+    from ffa_mi355x import _native as N
+    from ffa_mi355x import quant, synth
+    from ffa_mi355x.decode import DecodeWorkspace, run_decode
+
+    dev = torch.device("cuda:0")
+    B, HQ, HKV, D, T, BS, SBS, R = 1, 32, 8, 128, args.T, args.BS, args.SBS, args.rotations
+    t_setup = time.perf_counter()
+    q, k, v = synth.attention_inputs(B=B, T=T, HQ=HQ, HKV=HKV, D=D, seed=0, n_heavy=16, cos=0.8)
+    qd, vd = q.to(dev), v.to(dev)
+    kq, ks, kz, kr = quant.quantize_per_channel(k.to(dev), torch.float8_e5m2)
+    copies = [(kq.clone(), kr.clone(), vd.clone()) for _ in range(R)]
+    ws = DecodeWorkspace(B, HQ, HKV, T, BS, SBS, dev, torch.bfloat16)
+    scale = 1.0 / math.sqrt(D)
+
+    def step(r):
+        kq_, kr_, v_ = copies[r]
+        run_decode(q=qd, k_q=kq_, k_scale=ks, k_zero=kz, v=v_, k_residual=kr_, layout=N.LAYOUT_CONTIG,
+                   scale_mode=N.SCALE_CHANNEL, T=T, HKV=HKV, scale=scale, BS=BS, SBS=SBS, delta=args.delta,
+                   use_res=True, workspace=ws)
+
+    for r in range(R):
+        step(r)
+    torch.cuda.synchronize()
+    o0, mask = ws.o.clone(), ws.mask_buf.clone()
+    stream = torch.cuda.Stream()
+    setup_s = time.perf_counter() - t_setup
+    us, steps = _graph_time(step, R, max(1, math.ceil(args.steps / R)), stream)
+    assert torch.equal(o0, ws.o), "graph replays must match the eager step"
+    kept_th = kept_token_heads(mask, T, SBS)
+    keep_frac = float(mask.float().mean().item())
+    # every token's codes, the per-channel scale/zero once, residual + V of kept tokens, q and o
+    nbytes = T * HKV * (D // 4) + B * HKV * D * 2 * 2 + kept_th * _KEPT + B * HQ * D * 4
+    gbs = nbytes / (us * 1e-6) / 1e9
+    line = {
+        "metric": "config2 (reference layout) decode-attn us/step + HBM TB/s on the algorithmic bytes",
+        "value": round(us, 3), "unit": "us/step", "n_gpus": 1, "steps": steps, "warmup": R,
+        "ms_per_step": round(us / 1e3, 6), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q2 per-channel + e5m2 residual K, bf16 V; f16/bf16 MFMA, f32 accumulate",
+        "data": "synthetic (seeded N(0,1) bf16 with planted heavy tokens)",
+        "config": {"workload": WORKLOADS["config2ref"], "B": B, "T": T, "HQ": HQ, "HKV": HKV, "D": D, "BS": BS,
+                   "SBS": SBS, "delta": args.delta, "keep_fraction": round(keep_frac, 4), "algorithmic_bytes": nbytes,
+                   "rotations": R, "timing": "HIP graph of R steps (decode + merge), hipEvents over the replays"},
+        "decode_hbm_tbps": round(gbs / 1e3, 4),
+        "decode_hbm_pct_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
+        "cpu_baseline": None,
+        "setup_s": round(setup_s, 1),
+    }
+    print(json.dumps(line), flush=True)
 
 
 def bench_config1(args):
@@ -354,7 +412,7 @@ def main():
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run 5 device copies of 256 MiB (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--workload", choices=("config2",) + tuple(WORKLOADS), default="config2",
-                    help="config2 (default) is the metric's line; config1/3/4/5 time the other BASELINE decodes")
+                    help="config2 (default) is the metric's line; config2ref, config1/3/4/5 time the other BASELINE decodes")
     args = ap.parse_args()
     if args.copy_probe:
         import torch
@@ -375,6 +433,9 @@ def main():
 
     if args.workload == "config1":
         bench_config1(args)
+        return
+    if args.workload == "config2ref":
+        bench_config2_reference_layout(args)
         return
     if args.workload != "config2":
         bench_workload(args)

@@ -11,7 +11,8 @@ constexpr int kPage = 64;
 constexpr int kWaves = 4;
 constexpr int kPPW = 2;                      // 64-token chunks (pages) per wave
 constexpr int kChunksPerWG = kWaves * kPPW;  // 512 tokens per workgroup
-constexpr int kVRow = 260;  // LDS row pitch (bytes) of the staged V tile: 256 + 4 keeps banks apart
+constexpr int kVRow = 260;      // LDS row pitch (bytes) of a staged V tile: 256 + 4 keeps banks apart
+constexpr int kVRowHalf = 132;  // the same for half a tile (64 columns)
 
 struct DecodeParams {
   const void *q;
@@ -160,5 +161,7 @@ __device__ __forceinline__ f16x8 add_f16x8(f16x8 a, f16x8 b) { return a + b; }
 // stage 2: log-sum-exp merge of the per-workgroup partials (defined in q2fp8_decode.hip):
 // launches the merge kernel suited to the batch on stream st
 hipError_t launch_merge(const DecodeParams &p, hipStream_t st);
+// CUs of the current device (queried once per device; 0 when the query fails)
+int device_cus();
 
 }  // namespace ffa

@@ -61,11 +61,14 @@ __device__ __forceinline__ float load_scale(brsrc rs, uint32_t i, int dt) {
   return dt == 2 ? __uint_as_float(bits) : (dt == 1 ? bf16_bits_to_f32(bits) : f16_bits_to_f32(bits));
 }
 
-// Paged layout: four waves per SIMD (at most 128 registers, one or two spilled), so that four
-// workgroups share a CU; the contiguous layouts stage V through 87 KB of LDS and hold one.
-template <int LAYOUT, int FMT, int SCL, int RES, int VT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LAYOUT == kPaged ? 4 : 1))) void kfmt_decode_kernel(
-    const DecodeParams p) {
+// RELOAD: the exact pass loads a kept chunk's codes and scales again instead of keeping the
+// scoring registers of the wave's other chunk, which roughly halves the registers.  Paged
+// layout: always, with four waves per SIMD (at most 128 registers, one or two spilled).
+// Contiguous layouts (54.7 KB of LDS, two workgroups per CU): when the grid is larger than the
+// CU count; small grids keep the registers, one latency chain per wave being all they have.
+template <int LAYOUT, int FMT, int SCL, int RES, int VT, bool RELOAD>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LAYOUT == kPaged ? 4 : (RELOAD ? 2 : 1))))
+void kfmt_decode_kernel(const DecodeParams p) {
   typedef VTraits<VT> VTr;
   constexpr bool k4 = FMT == kFP4 || FMT == kNF4;
   constexpr bool kGrp = SCL == kSclG16 || SCL == kSclG64;  // per-token group scales (paged modes)
@@ -100,7 +103,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LAYOUT == k
   __shared__ float s_pm[kChunksPerWG][4], s_pl[kChunksPerWG][4];
   __shared__ float s_po[kChunksPerWG][4][128];
   __shared__ float s_cb[16];
-  __shared__ uint8_t s_vstage[LAYOUT == kContig ? kWaves * kPage * kVRow : 4];
+  __shared__ uint8_t s_vstage[LAYOUT == kContig ? kWaves * kPage * (RELOAD ? kVRowHalf : kVRow) : 4];
 
   auto lds_barrier = []() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
 
@@ -417,9 +420,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LAYOUT == k
                                     : bl != 0;
     uint4 rr[4][2];
     uint4 vv[8][2];
-    // paged layout: the chunk's codes and group scales again (cache-hot), so that the scoring
-    // registers of the wave's other chunk are not held through this exact pass
-    uint4 ka[4];
+    // the chunk's codes and scales again (cache-hot), so that the scoring registers of the
+    // wave's other chunk are not held through this exact pass
+    uint4 ka[4], kb[4];
+    float ksc[4];
     f32x2 kg[4];
     if constexpr (LAYOUT == kPaged) {
       const brsrc rc = page_rows(p.kq, pg[j], kRow, true);
@@ -427,7 +431,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LAYOUT == k
 #pragma unroll
       for (int tau = 0; tau < 4; ++tau) {
         ka[tau] = bload16(rc, (tau * 64 + lane) * 16);
+        kb[tau] = make_uint4(0, 0, 0, 0);
+        ksc[tau] = 1.f;
         kg[tau] = group_scales(rs, 4 * mrow + tau);
+      }
+    } else if constexpr (!RELOAD) {
+#pragma unroll
+      for (int tau = 0; tau < 4; ++tau) {
+        ka[tau] = xa[j][tau];
+        kb[tau] = xb[j][tau];
+        ksc[tau] = xs[j][tau];
+        kg[tau] = xg[j][tau];
+      }
+    } else {
+      const brsrc rc = make_rsrc(p.kq + (((size_t)b * p.T + t0) * p.HKV + hkv) * kRow, ((nvs - 1) * p.HKV + 1) * kRow);
+#pragma unroll
+      for (int tau = 0; tau < 4; ++tau) {
+        const uint32_t off = (4 * mrow + tau) * p.HKV * kRow + kLane * kc;
+        ka[tau] = bload16(rc, off);
+        kb[tau] = make_uint4(0, 0, 0, 0);
+        if constexpr (!k4) kb[tau] = bload16(rc, off + 16);
+        const int t = t0 + 4 * mrow + tau;
+        ksc[tau] = tok_scale(t, min(t, max(Tb - 1, 0)) / p.BS);
+        kg[tau] = f32x2{1.f, 1.f};
       }
     }
     if constexpr (RES != kResNone) {
@@ -476,9 +502,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LAYOUT == k
           const uint4 &rs4 = rr[tau][mp >> 1];
           const uint32_t lo = (mp & 1) ? rs4.z : rs4.x, hi = (mp & 1) ? rs4.w : rs4.y;
           acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-              add_f16x8(LAYOUT == kPaged ? dequant(ka[tau], xb[j][tau], mp, xs[j][tau], kg[tau])
-                                         : dequant(xa[j][tau], xb[j][tau], mp, xs[j][tau], xg[j][tau]),
-                        fp8x8_to_f16x8<RES>(lo, hi)),
+              add_f16x8(dequant(ka[tau], kb[tau], mp, ksc[tau], kg[tau]), fp8x8_to_f16x8<RES>(lo, hi)),
               qa[mp], acc, 0, 0, 0);
         }
 #pragma unroll
@@ -544,41 +568,52 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LAYOUT == k
         }
       }
     } else {
-    // stage the V tile [64 tokens][128] through LDS (rows past the sequence end were loaded as zeros)
-    uint8_t *st = s_vstage + wv * kPage * kVRow;
+    // stage the V tile [64 tokens][128] through LDS (rows past the sequence end were loaded as
+    // zeros): whole in the register-holding build (one workgroup per CU anyway), one half of the
+    // columns at a time in the RELOAD build, so that two workgroups fit in a CU's LDS
+    constexpr int kHalves = RELOAD ? 2 : 1;
+    constexpr int kPitch = RELOAD ? kVRowHalf : kVRow;
+    constexpr int kPieces = 16 / kHalves;  // 16-byte column pieces of a row staged per pass
+    uint8_t *st = s_vstage + wv * kPage * kPitch;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int idx = r * 64 + lane;
-      const int tk = idx >> 4, vc = idx & 15;
-      const uint4 v4 = vv[r >> 1][r & 1];
-      uint32_t *d = (uint32_t *)(st + tk * kVRow + 16 * vc);
-      d[0] = v4.x;
-      d[1] = v4.y;
-      d[2] = v4.z;
-      d[3] = v4.w;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int hf = 0; hf < kHalves; ++hf) {
 #pragma unroll
-    for (int nu = 0; nu < 8; ++nu) {
-#pragma unroll
-      for (int kap = 0; kap < 2; ++kap) {
-        const int vcol = 16 * nu + n;
-        const int tk = 16 * kc + 8 * kap;
-        u32x4 w;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t lo = *(const uint16_t *)(st + (tk + 2 * e) * kVRow + 2 * vcol);
-          const uint32_t hi = *(const uint16_t *)(st + (tk + 2 * e + 1) * kVRow + 2 * vcol);
-          w[e] = lo | (hi << 16);
+      for (int r = 0; r < 16; ++r) {
+        const int idx = r * 64 + lane;
+        const int tk = idx >> 4, vc = idx & 15;
+        if (kHalves == 1 || (vc >> 3) == hf) {
+          const uint4 v4 = vv[r >> 1][r & 1];
+          uint32_t *d = (uint32_t *)(st + tk * kPitch + 16 * (vc % kPieces));
+          d[0] = v4.x;
+          d[1] = v4.y;
+          d[2] = v4.z;
+          d[3] = v4.w;
         }
-        oacc[nu] = VTr::mfma(pa2[kap], __builtin_bit_cast(typename VTr::vec, w), oacc[nu]);
       }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int nl = 0; nl < 8 / kHalves; ++nl) {
+        const int nu = (8 / kHalves) * hf + nl;
+#pragma unroll
+        for (int kap = 0; kap < 2; ++kap) {
+          const int vcol = 16 * nl + n;  // column within the staged part
+          const int tk = 16 * kc + 8 * kap;
+          u32x4 w;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t lo = *(const uint16_t *)(st + (tk + 2 * e) * kPitch + 2 * vcol);
+            const uint32_t hi = *(const uint16_t *)(st + (tk + 2 * e + 1) * kPitch + 2 * vcol);
+            w[e] = lo | (hi << 16);
+          }
+          oacc[nu] = VTr::mfma(pa2[kap], __builtin_bit_cast(typename VTr::vec, w), oacc[nu]);
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
     if (lane < 16) {
 #pragma unroll
@@ -661,7 +696,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LAYOUT == k
 // --------------------------------------------------------------------------
 template <int L, int F, int S, int R, int V>
 static hipError_t kfmt_launch(const ffa::DecodeParams &p, dim3 grid, hipStream_t st) {
-  hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V>), grid, dim3(256), 0, st, p);
+  if constexpr (L == ffa::kPaged) {
+    hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, true>), grid, dim3(256), 0, st, p);
+  } else {
+    const int cus = ffa::device_cus();
+    if (cus > 0 && grid.x > (unsigned)cus)
+      hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, true>), grid, dim3(256), 0, st, p);
+    else
+      hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, false>), grid, dim3(256), 0, st, p);
+  }
   return hipGetLastError();
 }
 

@@ -126,7 +126,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   uint4(*const s_qa)[64] = reinterpret_cast<uint4(*)[64]>(&s_po[0][0][0]);
   // g32: partial sums of q16 over 8 channels (read with the operands), after s_qa
   float(*const s_zs)[64] = reinterpret_cast<float(*)[64]>(&s_po[2][0][0]);
-  __shared__ uint8_t s_vstage[LAYOUT == kContig ? kWaves * kPage * kVRow : 4];
+  __shared__ uint8_t s_vstage[LAYOUT == kContig ? kWaves * kPage * kVRowHalf : 4];
 
   // Workgroup barrier for LDS traffic only: __syncthreads() would also wait for every
   // outstanding global load of the wave (s_waitcnt vmcnt(0)), serialising the page loads
@@ -640,43 +640,50 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
         }
       }
     } else {
-      // contiguous layout: stage the V tile [64 tokens][128] through LDS, then read columns
-      // (rows past the sequence end were loaded as zeros)
-      uint8_t *st = s_vstage + wv * kPage * kVRow;
+      // contiguous layout: stage the V tile through LDS one half at a time ([64 tokens][64
+      // columns], a 132-byte row pitch keeps banks apart), then read columns (rows past the
+      // sequence end were loaded as zeros).  Half tiles keep two workgroups per CU in LDS.
+      uint8_t *st = s_vstage + wv * kPage * kVRowHalf;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int idx = r * 64 + lane;
-        const int tk = idx >> 4, vc = idx & 15;
-        const uint4 v4 = vv[r >> 1][r & 1];
-        uint32_t *d = (uint32_t *)(st + tk * kVRow + 16 * vc);
-        d[0] = v4.x;
-        d[1] = v4.y;
-        d[2] = v4.z;
-        d[3] = v4.w;
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      for (int hf = 0; hf < 2; ++hf) {
 #pragma unroll
-      for (int nu = 0; nu < 8; ++nu) {
-#pragma unroll
-        for (int kap = 0; kap < 2; ++kap) {
-          const int vcol = 16 * nu + n;
-          const int tk = 16 * kc + 8 * kap;
-          u32x4 w;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t lo = *(const uint16_t *)(st + (tk + 2 * e) * kVRow + 2 * vcol);
-            const uint32_t hi = *(const uint16_t *)(st + (tk + 2 * e + 1) * kVRow + 2 * vcol);
-            w[e] = lo | (hi << 16);
+        for (int r = 0; r < 16; ++r) {
+          const int idx = r * 64 + lane;
+          const int tk = idx >> 4, vc = idx & 15;
+          if ((vc >> 3) == hf) {
+            const uint4 v4 = vv[r >> 1][r & 1];
+            uint32_t *d = (uint32_t *)(st + tk * kVRowHalf + 16 * (vc & 7));
+            d[0] = v4.x;
+            d[1] = v4.y;
+            d[2] = v4.z;
+            d[3] = v4.w;
           }
-          oacc[nu] = VTr::mfma(pa2[kap], __builtin_bit_cast(typename VTr::vec, w), oacc[nu]);
         }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int nl = 0; nl < 4; ++nl) {
+          const int nu = 4 * hf + nl;
+#pragma unroll
+          for (int kap = 0; kap < 2; ++kap) {
+            const int vcol = 16 * nl + n;  // column within the half
+            const int tk = 16 * kc + 8 * kap;
+            u32x4 w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const uint32_t lo = *(const uint16_t *)(st + (tk + 2 * e) * kVRowHalf + 2 * vcol);
+              const uint32_t hi = *(const uint16_t *)(st + (tk + 2 * e + 1) * kVRowHalf + 2 * vcol);
+              w[e] = lo | (hi << 16);
+            }
+            oacc[nu] = VTr::mfma(pa2[kap], __builtin_bit_cast(typename VTr::vec, w), oacc[nu]);
+          }
+        }
+        // the other half (and the next kept chunk) reuses the staging buffer
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       }
-      // the tile of the next kept chunk reuses the staging buffer
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
     // chunk partial into LDS: lanes 0..15 hold rows 0..3 of columns 16*nu + n
     if (lane < 16) {
@@ -885,8 +892,8 @@ extern "C" int ffa_q2fp8_decode_nparts(int T, int BS, int SBS) {
   return (int)((tokens + ffa::kChunksPerWG * ffa::kPage - 1) / (ffa::kChunksPerWG * ffa::kPage));
 }
 
-// CUs of the current device, queried once per device
-static int device_cus() {
+namespace ffa {
+int device_cus() {
   static int cache[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
@@ -897,12 +904,13 @@ static int device_cus() {
   }
   return cache[dev];
 }
+}  // namespace ffa
 
 template <int L, int S, int R, int V>
 static hipError_t launch_decode(const ffa::DecodeParams &p, dim3 grid, hipStream_t st) {
   // paged g32 with more workgroups than two per CU: the three-per-CU build of the kernel
   if constexpr (L == ffa::kPaged && S == ffa::kG32) {
-    const int cus = device_cus();
+    const int cus = ffa::device_cus();
     if (cus > 0 && grid.x > 2u * (unsigned)cus) {
       hipLaunchKernelGGL((ffa::q2fp8_decode_kernel<L, S, R, V, 3>), grid, dim3(256), 0, st, p);
       return hipGetLastError();

@@ -141,3 +141,41 @@ def test_kfmt_ragged_and_no_residual(gpu):
         v.to(gpu), torch.from_numpy(res).view(torch.float8_e4m3fn).to(gpu), BS=64, delta=5.0, use_fp8_residual=False,
         seq_lens=torch.tensor(lens, dtype=torch.int32, device=gpu), workspace=ws)
     _check(o, ws, o_ref, diag, "nf4 ragged no-residual")
+
+
+@pytest.mark.parametrize("fmt", ["fp8_scaled", "nvfp4", "nf4"])
+def test_contiguous_large_grid_reload_build(gpu, fmt):
+    """More workgroups than CUs (B=6, T=3000: 6 x 8 x 6 = 288) selects the contiguous decoders' build that
+    reloads a kept chunk's codes and scales in the exact pass; it must match the oracle as the other does."""
+    B, T = 6, 3000
+    q, k, v = _inputs(B, T, "bf16", 11, 16)
+    qd = q.to(gpu).unsqueeze(1).contiguous()
+    if fmt == "fp8_scaled":
+        base, s, res = OF.quantize_fp8_scaled(f32(k), "e4m3fn")
+        kh = OF.khat_fp8_scaled(base, s, "e4m3fn")
+        o_ref, diag = O.decode(f32(q), base, None, None, f32(v), res, res_fmt="e4m3fn", BS=64, SBS=64, delta=5.0,
+                               khat=kh, out_dtype="bf16")
+        ws = F8K.__dict__["DecodeWorkspace"](B, 32, 8, T, 64, 64, gpu, torch.bfloat16)
+        o = F8K.attn_forward_decode_fp8fp8(
+            qd, torch.from_numpy(base).view(torch.float8_e4m3fn).to(gpu), v.to(gpu),
+            k_residual=torch.from_numpy(res).view(torch.float8_e4m3fn).to(gpu), BS=64, delta=5.0,
+            k_scale=torch.from_numpy(s).to(torch.float16).to(gpu), workspace=ws)
+    elif fmt == "nvfp4":
+        pk, sc, res = OF.quantize_nvfp4(f32(k), "bf16", "e5m2", 64)
+        kh, kp1 = OF.khat_nvfp4(pk, sc, 64, 128)
+        o_ref, diag = O.decode(f32(q), pk, None, None, f32(v), res, res_fmt="e5m2", BS=64, SBS=64, delta=5.0,
+                               khat=kh, khat_probe1=kp1, out_dtype="bf16")
+        ws = NVK.__dict__["DecodeWorkspace"](B, 32, 8, T, 64, 64, gpu, torch.bfloat16)
+        o = NVK.attn_forward_decode_nvfp4fp8(
+            qd, torch.from_numpy(pk).to(gpu), torch.from_numpy(sc).to(torch.bfloat16).to(gpu), v.to(gpu),
+            k_residual=torch.from_numpy(res).view(torch.float8_e5m2).to(gpu), BS=64, delta=5.0, workspace=ws)
+    else:
+        pk, sc, res = OF.quantize_nf4(f32(k), "bf16", "e5m2")
+        kh = OF.khat_nf4(pk, sc, 128)
+        o_ref, diag = O.decode(f32(q), pk, None, None, f32(v), res, res_fmt="e5m2", BS=64, SBS=64, delta=5.0,
+                               khat=kh, out_dtype="bf16")
+        ws = NFK.__dict__["DecodeWorkspace"](B, 32, 8, T, 64, 64, gpu, torch.bfloat16)
+        o = NFK.attn_forward_decode_nf4(
+            qd, torch.from_numpy(pk).to(gpu), torch.from_numpy(sc).to(torch.bfloat16).to(gpu), v.to(gpu),
+            k_residual=torch.from_numpy(res).view(torch.float8_e5m2).to(gpu), BS=64, delta=5.0, workspace=ws)
+    _check(o, ws, o_ref, diag, f"{fmt} contiguous, large grid")
