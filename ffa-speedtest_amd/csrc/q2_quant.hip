@@ -92,41 +92,6 @@ __global__ __launch_bounds__(256) void q2_quant_channel_kernel(const void *k, in
   kq[row * DP + byte] = (uint8_t)packed;
 }
 
-// ---------------------------------------------------------------------------
-// g32 quantization of one (token, KV head, group) and its page writes.
-// zero = fp16(min), scale = fp16(max(max - zero, 1e-6) / 3), c = clamp(rne((k - zero)/scale), 0, 3),
-// residual = fp8(k - (c*scale + zero)) with two fp32 roundings.
-__device__ __forceinline__ void g32_quantize_store(const float *kv, int page, int slot, int hkv, int HKV, int g,
-                                                   uint8_t *kq_pages, uint16_t *s_pages, uint16_t *z_pages,
-                                                   uint8_t *r_pages, int res_e4m3) {
-  constexpr int D = 128;
-  float mn = INFINITY, mx = -INFINITY;
-  for (int e = 0; e < 32; ++e) {
-    mn = fminf(mn, kv[e]);
-    mx = fmaxf(mx, kv[e]);
-  }
-  const float zr = (float)(_Float16)mn;
-  const float sc = (float)(_Float16)__fdiv_rn(fmaxf(mx - zr, 1e-6f), 3.0f);
-  uint32_t words[2] = {0u, 0u};
-  uint32_t rw[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
-  for (int e = 0; e < 32; ++e) {
-    const float cq = fminf(fmaxf(__builtin_rintf(__fdiv_rn(kv[e] - zr, sc)), 0.f), 3.f);
-    const float deq = (cq * sc) + zr;
-    rw[e >> 2] |= f32_to_fp8(kv[e] - deq, res_e4m3) << (8 * (e & 3));
-    words[e >> 4] |= ((uint32_t)cq) << (2 * (e & 15));
-  }
-  // page-internal orders: decode_common.h (res_off, codes_off, gscale_off)
-  const size_t blk = (size_t)page * HKV + hkv;
-  uint8_t *rp = r_pages + blk * (64 * D);
-  *(uint4 *)(rp + res_off(slot, 32 * g)) = make_uint4(rw[0], rw[1], rw[2], rw[3]);
-  *(uint4 *)(rp + res_off(slot, 32 * g + 16)) = make_uint4(rw[4], rw[5], rw[6], rw[7]);
-  *(uint2 *)(kq_pages + blk * (4 * 64 * 8) + codes_off(g, slot)) = make_uint2(words[0], words[1]);
-  const int ss = 16 * (slot >> 4) + 4 * (slot & 3) + ((slot >> 2) & 3);  // tile-major scale slot
-  const size_t so = blk * (4 * 64) + gscale_off(g, ss);
-  s_pages[so] = (uint16_t)f32_to_f16_bits(sc);
-  z_pages[so] = (uint16_t)f32_to_f16_bits(zr);
-}
-
 // K projection GEMM tile: 16 tokens x 32 output channels per 512-thread workgroup.  The 32-wide k
 // steps are dealt round-robin to the 8 waves (wave w takes steps w, w + 8, ...), so even a handful of
 // tokens keeps 8 waves per tile streaming W; each wave accumulates its steps with MFMA 16x16x32 into
@@ -227,9 +192,11 @@ __device__ __forceinline__ void kproj_tile_of(int bid, int nct, int &ct, int &mt
 }
 
 // g32 quantization of one (token, KV head, group) held by the 32 lanes of a half wave (lane e of the
-// half holds channel 32 g + e), with the rules of g32_quantize_store; min / max by shuffles, 2-bit
-// codes OR-reduced over 16 lanes, residual bytes stored by each lane.  All 64 lanes must call it;
-// `store` masks the writes.
+// half holds channel 32 g + e), and its page writes:
+//   zero = fp16(min), scale = fp16(max(max - zero, 1e-6) / 3), c = clamp(rne((k - zero)/scale), 0, 3),
+//   residual = fp8(k - (c*scale + zero)) with two fp32 roundings;
+// min / max by shuffles, 2-bit codes OR-reduced over 16 lanes, residual bytes stored by each lane.
+// All 64 lanes must call it; `store` masks the writes.
 __device__ __forceinline__ void g32_quantize_lanes(float x, bool store, int page, int slot, int hkv, int HKV, int g,
                                                    uint8_t *kq_pages, uint16_t *s_pages, uint16_t *z_pages,
                                                    uint8_t *r_pages, int res_e4m3) {
@@ -331,31 +298,28 @@ __global__ __launch_bounds__(512) void kproj_append_kernel(const void *h, const 
 }
 
 
-// g32 quantize + append of given K rows (no projection): one thread per
-// (token row, KV head, group).  k [B, Tn, HKV, 128] (dtype kdt).
+// g32 quantize + append of given K rows (no projection): 128 threads per (token row, KV head),
+// one channel each (coalesced loads; the quantization of a 32-channel group runs across the 32
+// lanes of a half wave, g32_quantize_lanes).  k [B, Tn, HKV, 128] (dtype kdt).
 __global__ __launch_bounds__(256) void q2_g32_append_kernel(const void *k, int kdt, int M, int Tn, int HKV,
                                                              const int32_t *pos, const int32_t *bt, int bt_stride,
                                                              uint8_t *kq_pages, uint16_t *s_pages, uint16_t *z_pages,
                                                              uint8_t *r_pages, int res_e4m3, const void *v_new,
                                                              void *v_pages) {
   constexpr int D = 128;
-  const size_t id = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (id >= (size_t)M * HKV * 4) return;
-  const int g = (int)(id & 3);
-  const int hkv = (int)((id >> 2) % HKV);
-  const int m = (int)((id >> 2) / HKV);
+  const size_t rowid = (size_t)blockIdx.x * 2 + (threadIdx.x >> 7);  // (token row, head)
+  if (rowid >= (size_t)M * HKV) return;  // whole waves (a row is two waves)
+  const int c = threadIdx.x & 127, g = c >> 5;
+  const int hkv = (int)(rowid % HKV);
+  const int m = (int)(rowid / HKV);
   const int b = m / Tn, nn = m % Tn;
   const int P = pos[b] + nn;
   const int page = bt[(size_t)b * bt_stride + (P >> 6)];
   const int slot = P & 63;
-  float kv[32];
-  for (int e = 0; e < 32; ++e) kv[e] = load_any(k, ((size_t)m * HKV + hkv) * D + 32 * g + e, kdt);
-  g32_quantize_store(kv, page, slot, hkv, HKV, g, kq_pages, s_pages, z_pages, r_pages, res_e4m3);
-  if (v_new != nullptr) {
-    const uint16_t *vs = (const uint16_t *)v_new + ((size_t)m * HKV + hkv) * D + 32 * g;
-    uint16_t *vd = (uint16_t *)v_pages + ((size_t)page * HKV + hkv) * (D * 64);
-    for (int e = 0; e < 32; ++e) vd[vt_off(32 * g + e, slot)] = vs[e];
-  }
+  const float x = load_any(k, rowid * D + c, kdt);
+  g32_quantize_lanes(x, true, page, slot, hkv, HKV, g, kq_pages, s_pages, z_pages, r_pages, res_e4m3);
+  if (v_new != nullptr)
+    ((uint16_t *)v_pages)[((size_t)page * HKV + hkv) * (D * 64) + vt_off(c, slot)] = ((const uint16_t *)v_new)[rowid * D + c];
 }
 
 }  // namespace ffa
@@ -474,8 +438,8 @@ extern "C" int ffa_q2_quantize_g32_append(const void *k, int k_dtype, int B, int
   if (!(k_dtype >= FFA_DT_F16 && k_dtype <= FFA_DT_F32)) return ffa_set_error_internal(FFA_E_INVALID, "k dtype");
   if (!(res_dtype == FFA_DT_FP8_E4M3 || res_dtype == FFA_DT_FP8_E5M2))
     return ffa_set_error_internal(FFA_E_INVALID, "residual dtype must be fp8");
-  const size_t total = (size_t)B * Tn * HKV * 4;
-  hipLaunchKernelGGL(ffa::q2_g32_append_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+  const size_t rows = (size_t)B * Tn * HKV;
+  hipLaunchKernelGGL(ffa::q2_g32_append_kernel, dim3((unsigned)((rows + 1) / 2)), dim3(256), 0,
                      (hipStream_t)stream, k, k_dtype, B * Tn, Tn, HKV, pos, block_table, bt_stride, k_q_pages,
                      (uint16_t *)scale_pages, (uint16_t *)zero_pages, res_pages, res_dtype == FFA_DT_FP8_E4M3 ? 1 : 0,
                      v_new, v_pages);
