@@ -139,15 +139,24 @@ __device__ __forceinline__ void raw16_to_f32(const Raw16 &r, int dt, float *out)
       out[4 * i + 2] = __uint_as_float(r.v[i].z);
       out[4 * i + 3] = __uint_as_float(r.v[i].w);
     }
+  } else if (dt == 1) {  // one uniform branch per dtype, not a select per element
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t w[4] = {r.v[i].x, r.v[i].y, r.v[i].z, r.v[i].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        out[8 * i + 2 * k] = __uint_as_float(w[k] << 16);
+        out[8 * i + 2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+      }
+    }
   } else {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const uint32_t w[4] = {r.v[i].x, r.v[i].y, r.v[i].z, r.v[i].w};
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const uint32_t lo = w[k] & 0xffffu, hi = w[k] >> 16;
-        out[8 * i + 2 * k] = dt == 1 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
-        out[8 * i + 2 * k + 1] = dt == 1 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
+        out[8 * i + 2 * k] = f16_bits_to_f32(w[k] & 0xffffu);
+        out[8 * i + 2 * k + 1] = f16_bits_to_f32(w[k] >> 16);
       }
     }
   }

@@ -737,13 +737,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     const int i = wv;         // query row handled by this wave
     const int c2 = 2 * lane;  // columns c2, c2 + 1
     if (i < G) {
+      // only kept chunks hold partials (km, uniform): the others are skipped by scalar branches
       float M = -INFINITY;
 #pragma unroll
       for (int ps = 0; ps < kChunksPerWG; ++ps)
-        if (s_pl[ps][i] > 0.f) M = fmaxf(M, s_pm[ps][i]);
+        if (((km >> ps) & 1u) && s_pl[ps][i] > 0.f) M = fmaxf(M, s_pm[ps][i]);
       float A = 0.f, ox = 0.f, oy = 0.f;
 #pragma unroll
       for (int ps = 0; ps < kChunksPerWG; ++ps) {
+        if (!((km >> ps) & 1u)) continue;
         const float l = s_pl[ps][i];
         if (l > 0.f) {
           const float wgt = exp2f(s_pm[ps][i] - M);
