@@ -664,13 +664,19 @@ void kfmt_decode_kernel(const DecodeParams p) {
     const int i = wv;
     const int c2 = 2 * lane;
     if (i < G) {
+      // slots whose ballot is empty hold no partial: skipped by scalar branches
+      uint32_t km = 0;
+#pragma unroll
+      for (int sl = 0; sl < kChunksPerWG; ++sl) km |= ((s_bal[sl][0] | s_bal[sl][1]) != 0u ? 1u : 0u) << sl;
+      km = __builtin_amdgcn_readfirstlane(km);
       float M = -INFINITY;
 #pragma unroll
       for (int ps = 0; ps < kChunksPerWG; ++ps)
-        if (s_pl[ps][i] > 0.f) M = fmaxf(M, s_pm[ps][i]);
+        if (((km >> ps) & 1u) && s_pl[ps][i] > 0.f) M = fmaxf(M, s_pm[ps][i]);
       float A = 0.f, ox = 0.f, oy = 0.f;
 #pragma unroll
       for (int ps = 0; ps < kChunksPerWG; ++ps) {
+        if (!((km >> ps) & 1u)) continue;
         const float l = s_pl[ps][i];
         if (l > 0.f) {
           const float wgt = exp2f(s_pm[ps][i] - M);
