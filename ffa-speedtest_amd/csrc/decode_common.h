@@ -30,6 +30,7 @@ struct DecodeParams {
   int8_t *mask;
   int q_dtype, s_dtype, out_dtype;
   int bt_stride;
+  int num_pages;  // paged: pages in each pool; block-table entries outside [0, num_pages) read page 0
   int B, T, HQ, HKV, G;
   float scale;
   int BS, SBS;
@@ -70,6 +71,13 @@ __host__ __device__ constexpr uint32_t gscale_off(int g, int s) {
 // of byte b (channels 2b, 2b + 1) of token t
 __host__ __device__ constexpr uint32_t k4_off(int t, int b) {
   return (uint32_t)(((t & 3) * 64 + (b >> 4) * 16 + (t >> 2)) * 16 + (b & 15));
+}
+// Pool page of position P of sequence b for the append kernels, or -1 (nothing is written) when
+// P lies outside the block table's row or the table names a page outside [0, num_pages).
+__device__ __forceinline__ int append_page(const int32_t *bt, int bt_stride, int num_pages, int b, int P) {
+  if (P < 0 || (P >> 6) >= bt_stride) return -1;
+  const int page = bt[(size_t)b * bt_stride + (P >> 6)];
+  return (unsigned)page < (unsigned)num_pages ? page : -1;
 }
 enum { kChannel = 0, kG32 = 1 };
 enum { kResNone = 0, kResE4M3 = 1, kResE5M2 = 2 };

@@ -125,6 +125,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
     const bool need = lane < kPPW ? nv[lane & 1] > 0 : (lane == kPPW && do_probe && pa < Tb);
     const int idx = lane < kPPW ? c0 + lane : (pa >> 6);
     pg_lane = bload4(make_rsrc(p.bt + (size_t)b * p.bt_stride, p.bt_stride * 4), need ? idx * 4 : p.bt_stride * 4);
+    pg_lane = pg_lane < (uint32_t)p.num_pages ? pg_lane : 0u;  // ids outside the pools read page 0
   }
   const uint32_t es_q = p.q_dtype == 2 ? 4u : 2u;
   const int hwin = wv >> 1;
@@ -758,6 +759,10 @@ extern "C" int ffa_kfmt_decode(const ffa_kfmt_decode_args *a, void *stream) {
   const bool paged = a->layout == FFA_LAYOUT_PAGED;
   if (!paged && a->layout != FFA_LAYOUT_CONTIG) return ffa_set_error_internal(FFA_E_INVALID, "layout");
   if (paged && !a->block_table) return ffa_set_error_internal(FFA_E_INVALID, "paged layout needs a block table");
+  if (paged && a->num_pages <= 0)
+    return ffa_set_error_internal(FFA_E_INVALID, "paged layout needs num_pages > 0 (pages in each pool)");
+  if (paged && (long)a->bt_stride * ffa::kPage < a->T)
+    return ffa_set_error_internal(FFA_E_INVALID, "block table has fewer than ceil(T/64) columns");
   if (paged != (a->scale_kind == FFA_KSCALE_G16 || a->scale_kind == FFA_KSCALE_G64))
     return ffa_set_error_internal(FFA_E_UNSUPPORTED,
                                   "the paged layout takes the per-token group scales (G16 / G64) and only it");
@@ -770,6 +775,7 @@ extern "C" int ffa_kfmt_decode(const ffa_kfmt_decode_args *a, void *stream) {
   p.v = a->v;
   p.bt = a->block_table;
   p.bt_stride = a->bt_stride;
+  p.num_pages = paged ? a->num_pages : 0;
   p.seq_lens = a->seq_lens;
   p.th_in = a->threshold_in;
   p.th_out = a->threshold_out;

@@ -227,8 +227,9 @@ __global__ __launch_bounds__(256) void nf4_quant_kernel(const void *k, int kdt, 
 template <bool NF4>
 __global__ __launch_bounds__(256) void kfmt_group_append_kernel(const void *k, int kdt, int M, int Tn, int HKV,
                                                                  const int32_t *pos, const int32_t *bt, int bt_stride,
-                                                                 uint8_t *k_pages, void *s_pages, uint8_t *r_pages,
-                                                                 int res_e4m3, const void *v_new, void *v_pages) {
+                                                                 int num_pages, uint8_t *k_pages, void *s_pages,
+                                                                 uint8_t *r_pages, int res_e4m3, const void *v_new,
+                                                                 void *v_pages) {
   constexpr int D = 128;
   const size_t id = (size_t)blockIdx.x * 256 + threadIdx.x;
   const bool live = id < (size_t)M * HKV * 8;  // whole groups of 8 lanes are live or not
@@ -238,7 +239,8 @@ __global__ __launch_bounds__(256) void kfmt_group_append_kernel(const void *k, i
   const int m = (int)((idc >> 3) / HKV);
   const int b = m / Tn, nn = m - b * Tn;
   const int P = pos[b] + nn;
-  const int page = bt[(size_t)b * bt_stride + (P >> 6)];
+  const int page = append_page(bt, bt_stride, num_pages, b, P);
+  const bool wr = live && page >= 0;  // whole groups of 8 lanes (one token and head) write or not
   const int slot = P & 63;
   const size_t prow = ((size_t)page * HKV + hkv) * 64 + slot;  // (page, head, token) row of the pools
   float kv[16];
@@ -261,7 +263,7 @@ __global__ __launch_bounds__(256) void kfmt_group_append_kernel(const void *k, i
       rw[e >> 2] |= f32_to_fp8(kv[e] - kNF4Book[idx] * sc, res_e4m3) << (8 * (e & 3));
       cw[e >> 3] |= (uint32_t)idx << (4 * (e & 7));
     }
-    if (live && (c16 & 3) == 0) ((uint16_t *)s_pages)[prow * 2 + (c16 >> 2)] = (uint16_t)f32_to_f16_bits(sc);
+    if (wr && (c16 & 3) == 0) ((uint16_t *)s_pages)[prow * 2 + (c16 >> 2)] = (uint16_t)f32_to_f16_bits(sc);
   } else {
     const uint32_t sb = f32_to_fp8(fminf(__fdiv_rn(amax, 6.0f), 448.0f), 1);
     const float sc = fp8_bits_to_f32(sb, 1);
@@ -275,9 +277,9 @@ __global__ __launch_bounds__(256) void kfmt_group_append_kernel(const void *k, i
       rw[e >> 2] |= f32_to_fp8(kv[e] - deq, res_e4m3) << (8 * (e & 3));
       cw[e >> 3] |= (uint32_t)(idx | (neg ? 8 : 0)) << (4 * (e & 7));
     }
-    if (live) ((uint8_t *)s_pages)[prow * 8 + c16] = (uint8_t)sb;
+    if (wr) ((uint8_t *)s_pages)[prow * 8 + c16] = (uint8_t)sb;
   }
-  if (!live) return;
+  if (!wr) return;
   // page-internal orders: decode_common.h (k4_off, res_off, vt_off)
   const size_t blk = (size_t)page * HKV + hkv;
   *(uint2 *)(k_pages + blk * (64 * 64) + k4_off(slot, 8 * c16)) = make_uint2(cw[0], cw[1]);
@@ -361,9 +363,11 @@ extern "C" int ffa_nf4_quantize(const void *k, int k_dtype, int B, int T, int HK
 }
 
 static int group_append(bool nf4, const void *k, int k_dtype, int B, int Tn, int HKV, const int32_t *pos,
-                        const int32_t *block_table, int bt_stride, uint8_t *k_pages, void *scale_pages,
-                        uint8_t *res_pages, int res_dtype, const void *v_new, void *v_pages, void *stream) {
+                        const int32_t *block_table, int bt_stride, int num_pages, uint8_t *k_pages,
+                        void *scale_pages, uint8_t *res_pages, int res_dtype, const void *v_new, void *v_pages,
+                        void *stream) {
   if (B <= 0 || Tn <= 0 || HKV <= 0) return ffa_set_error_internal(FFA_E_INVALID, "bad dims");
+  if (bt_stride <= 0 || num_pages <= 0) return ffa_set_error_internal(FFA_E_INVALID, "empty block table or pool");
   if (!is_float(k_dtype)) return ffa_set_error_internal(FFA_E_INVALID, "k dtype");
   if (!is_fp8(res_dtype)) return ffa_set_error_internal(FFA_E_INVALID, "residual dtype must be fp8");
   const size_t total = (size_t)B * Tn * HKV * 8;
@@ -371,23 +375,27 @@ static int group_append(bool nf4, const void *k, int k_dtype, int B, int Tn, int
   const int e4 = res_dtype == FFA_DT_FP8_E4M3 ? 1 : 0;
   if (nf4)
     hipLaunchKernelGGL(ffa::kfmt_group_append_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, k, k_dtype, B * Tn,
-                       Tn, HKV, pos, block_table, bt_stride, k_pages, scale_pages, res_pages, e4, v_new, v_pages);
+                       Tn, HKV, pos, block_table, bt_stride, num_pages, k_pages, scale_pages, res_pages, e4, v_new,
+                       v_pages);
   else
     hipLaunchKernelGGL(ffa::kfmt_group_append_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, k, k_dtype,
-                       B * Tn, Tn, HKV, pos, block_table, bt_stride, k_pages, scale_pages, res_pages, e4, v_new, v_pages);
+                       B * Tn, Tn, HKV, pos, block_table, bt_stride, num_pages, k_pages, scale_pages, res_pages, e4,
+                       v_new, v_pages);
   return launch_status();
 }
 
 extern "C" int ffa_nvfp4_g16_append(const void *k, int k_dtype, int B, int Tn, int HKV, const int32_t *pos,
-                                    const int32_t *block_table, int bt_stride, uint8_t *k_pages, uint8_t *scale_pages,
-                                    uint8_t *res_pages, int res_dtype, const void *v_new, void *v_pages, void *stream) {
-  return group_append(false, k, k_dtype, B, Tn, HKV, pos, block_table, bt_stride, k_pages, scale_pages, res_pages,
-                      res_dtype, v_new, v_pages, stream);
+                                    const int32_t *block_table, int bt_stride, int num_pages, uint8_t *k_pages,
+                                    uint8_t *scale_pages, uint8_t *res_pages, int res_dtype, const void *v_new,
+                                    void *v_pages, void *stream) {
+  return group_append(false, k, k_dtype, B, Tn, HKV, pos, block_table, bt_stride, num_pages, k_pages, scale_pages,
+                      res_pages, res_dtype, v_new, v_pages, stream);
 }
 
 extern "C" int ffa_nf4_g64_append(const void *k, int k_dtype, int B, int Tn, int HKV, const int32_t *pos,
-                                  const int32_t *block_table, int bt_stride, uint8_t *k_pages, void *scale_pages,
-                                  uint8_t *res_pages, int res_dtype, const void *v_new, void *v_pages, void *stream) {
-  return group_append(true, k, k_dtype, B, Tn, HKV, pos, block_table, bt_stride, k_pages, scale_pages, res_pages,
-                      res_dtype, v_new, v_pages, stream);
+                                  const int32_t *block_table, int bt_stride, int num_pages, uint8_t *k_pages,
+                                  void *scale_pages, uint8_t *res_pages, int res_dtype, const void *v_new,
+                                  void *v_pages, void *stream) {
+  return group_append(true, k, k_dtype, B, Tn, HKV, pos, block_table, bt_stride, num_pages, k_pages, scale_pages,
+                      res_pages, res_dtype, v_new, v_pages, stream);
 }

@@ -268,9 +268,9 @@ template <int HDT>
 __global__ __launch_bounds__(512) void kproj_append_kernel(const void *h, const void *w, const void *bias,
                                                            const float *cos, const float *sin, int M, int Tn, int H,
                                                            int HKV, const int32_t *pos, const int32_t *bt, int bt_stride,
-                                                           uint8_t *kq_pages, uint16_t *s_pages, uint16_t *z_pages,
-                                                           uint8_t *r_pages, int res_e4m3, const void *v_new,
-                                                           void *v_pages) {
+                                                           int num_pages, uint8_t *kq_pages, uint16_t *s_pages,
+                                                           uint16_t *z_pages, uint8_t *r_pages, int res_e4m3,
+                                                           const void *v_new, void *v_pages) {
   constexpr int D = 128;
   __shared__ float red[kKpWaves][16][33];
   int ct, mt;
@@ -290,10 +290,11 @@ __global__ __launch_bounds__(512) void kproj_append_kernel(const void *h, const 
   const float partner = __shfl_xor(x, 1);
   // fp32 cos / sin promote the rotation to fp32
   const float k = rope_one(x, partner, (d & 1) != 0, cv, sv, FFA_DT_F32);
-  const int page = bt[(size_t)b * bt_stride + (P >> 6)];
+  const int page = append_page(bt, bt_stride, num_pages, b, P);
   const int slot = P & 63;
-  g32_quantize_lanes(k, m < M, page, slot, hkv, HKV, g, kq_pages, s_pages, z_pages, r_pages, res_e4m3);
-  if (v_new != nullptr && m < M)  // V^T pages: this workgroup's 32 channels of each token
+  const bool wr = m < M && page >= 0;  // uniform over the 32 lanes of a token's group
+  g32_quantize_lanes(k, wr, page, slot, hkv, HKV, g, kq_pages, s_pages, z_pages, r_pages, res_e4m3);
+  if (v_new != nullptr && wr)  // V^T pages: this workgroup's 32 channels of each token
     ((uint16_t *)v_pages)[((size_t)page * HKV + hkv) * (D * 64) + vt_off(d, slot)] = vv;
 }
 
@@ -303,9 +304,9 @@ __global__ __launch_bounds__(512) void kproj_append_kernel(const void *h, const 
 // lanes of a half wave, g32_quantize_lanes).  k [B, Tn, HKV, 128] (dtype kdt).
 __global__ __launch_bounds__(256) void q2_g32_append_kernel(const void *k, int kdt, int M, int Tn, int HKV,
                                                              const int32_t *pos, const int32_t *bt, int bt_stride,
-                                                             uint8_t *kq_pages, uint16_t *s_pages, uint16_t *z_pages,
-                                                             uint8_t *r_pages, int res_e4m3, const void *v_new,
-                                                             void *v_pages) {
+                                                             int num_pages, uint8_t *kq_pages, uint16_t *s_pages,
+                                                             uint16_t *z_pages, uint8_t *r_pages, int res_e4m3,
+                                                             const void *v_new, void *v_pages) {
   constexpr int D = 128;
   const size_t rowid = (size_t)blockIdx.x * 2 + (threadIdx.x >> 7);  // (token row, head)
   if (rowid >= (size_t)M * HKV) return;  // whole waves (a row is two waves)
@@ -314,11 +315,11 @@ __global__ __launch_bounds__(256) void q2_g32_append_kernel(const void *k, int k
   const int m = (int)(rowid / HKV);
   const int b = m / Tn, nn = m % Tn;
   const int P = pos[b] + nn;
-  const int page = bt[(size_t)b * bt_stride + (P >> 6)];
+  const int page = append_page(bt, bt_stride, num_pages, b, P);
   const int slot = P & 63;
   const float x = load_any(k, rowid * D + c, kdt);
-  g32_quantize_lanes(x, true, page, slot, hkv, HKV, g, kq_pages, s_pages, z_pages, r_pages, res_e4m3);
-  if (v_new != nullptr)
+  g32_quantize_lanes(x, page >= 0, page, slot, hkv, HKV, g, kq_pages, s_pages, z_pages, r_pages, res_e4m3);
+  if (v_new != nullptr && page >= 0)
     ((uint16_t *)v_pages)[((size_t)page * HKV + hkv) * (D * 64) + vt_off(c, slot)] = ((const uint16_t *)v_new)[rowid * D + c];
 }
 
@@ -403,10 +404,11 @@ extern "C" int ffa_kproj_rope_q2_channel(const void *h, const void *w_k, const v
 
 extern "C" int ffa_kproj_rope_q2_append(const void *h, const void *w_k, const void *bias, int h_dtype, const float *cos,
                                         const float *sin, int B, int Tn, int H, int HKV, const int32_t *pos,
-                                        const int32_t *block_table, int bt_stride, uint8_t *k_q_pages,
-                                        void *scale_pages, void *zero_pages, uint8_t *res_pages, int res_dtype,
-                                        const void *v_new, void *v_pages, int v_dtype, void *stream) {
+                                        const int32_t *block_table, int bt_stride, int num_pages,
+                                        uint8_t *k_q_pages, void *scale_pages, void *zero_pages, uint8_t *res_pages,
+                                        int res_dtype, const void *v_new, void *v_pages, int v_dtype, void *stream) {
   if (B <= 0 || Tn <= 0 || H <= 0 || HKV <= 0) return ffa_set_error_internal(FFA_E_INVALID, "bad dims");
+  if (bt_stride <= 0 || num_pages <= 0) return ffa_set_error_internal(FFA_E_INVALID, "empty block table or pool");
   if (!(h_dtype == FFA_DT_F16 || h_dtype == FFA_DT_BF16))
     return ffa_set_error_internal(FFA_E_UNSUPPORTED, "h must be fp16 or bf16");
   if (H % 32) return ffa_set_error_internal(FFA_E_UNSUPPORTED, "H must be a multiple of 32");
@@ -419,11 +421,13 @@ extern "C" int ffa_kproj_rope_q2_append(const void *h, const void *w_k, const vo
   const dim3 grid((unsigned)(HKV * 4 * ((M + 15) / 16)));
   if (h_dtype == FFA_DT_BF16)
     hipLaunchKernelGGL(ffa::kproj_append_kernel<FFA_DT_BF16>, grid, dim3(512), 0, st, h, w_k, bias, cos, sin, M, Tn, H,
-                       HKV, pos, block_table, bt_stride, k_q_pages, (uint16_t *)scale_pages, (uint16_t *)zero_pages,
+                       HKV, pos, block_table, bt_stride, num_pages, k_q_pages, (uint16_t *)scale_pages,
+                       (uint16_t *)zero_pages,
                        res_pages, res_dtype == FFA_DT_FP8_E4M3 ? 1 : 0, v_new, v_pages);
   else
     hipLaunchKernelGGL(ffa::kproj_append_kernel<FFA_DT_F16>, grid, dim3(512), 0, st, h, w_k, bias, cos, sin, M, Tn, H,
-                       HKV, pos, block_table, bt_stride, k_q_pages, (uint16_t *)scale_pages, (uint16_t *)zero_pages,
+                       HKV, pos, block_table, bt_stride, num_pages, k_q_pages, (uint16_t *)scale_pages,
+                       (uint16_t *)zero_pages,
                        res_pages, res_dtype == FFA_DT_FP8_E4M3 ? 1 : 0, v_new, v_pages);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return ffa_set_error_internal(FFA_E_LAUNCH, hipGetErrorString(e));
@@ -431,16 +435,17 @@ extern "C" int ffa_kproj_rope_q2_append(const void *h, const void *w_k, const vo
 }
 
 extern "C" int ffa_q2_quantize_g32_append(const void *k, int k_dtype, int B, int Tn, int HKV, const int32_t *pos,
-                                          const int32_t *block_table, int bt_stride, uint8_t *k_q_pages,
-                                          void *scale_pages, void *zero_pages, uint8_t *res_pages, int res_dtype,
-                                          const void *v_new, void *v_pages, void *stream) {
+                                          const int32_t *block_table, int bt_stride, int num_pages,
+                                          uint8_t *k_q_pages, void *scale_pages, void *zero_pages, uint8_t *res_pages,
+                                          int res_dtype, const void *v_new, void *v_pages, void *stream) {
   if (B <= 0 || Tn <= 0 || HKV <= 0) return ffa_set_error_internal(FFA_E_INVALID, "bad dims");
+  if (bt_stride <= 0 || num_pages <= 0) return ffa_set_error_internal(FFA_E_INVALID, "empty block table or pool");
   if (!(k_dtype >= FFA_DT_F16 && k_dtype <= FFA_DT_F32)) return ffa_set_error_internal(FFA_E_INVALID, "k dtype");
   if (!(res_dtype == FFA_DT_FP8_E4M3 || res_dtype == FFA_DT_FP8_E5M2))
     return ffa_set_error_internal(FFA_E_INVALID, "residual dtype must be fp8");
   const size_t rows = (size_t)B * Tn * HKV;
   hipLaunchKernelGGL(ffa::q2_g32_append_kernel, dim3((unsigned)((rows + 1) / 2)), dim3(256), 0,
-                     (hipStream_t)stream, k, k_dtype, B * Tn, Tn, HKV, pos, block_table, bt_stride, k_q_pages,
+                     (hipStream_t)stream, k, k_dtype, B * Tn, Tn, HKV, pos, block_table, bt_stride, num_pages, k_q_pages,
                      (uint16_t *)scale_pages, (uint16_t *)zero_pages, res_pages, res_dtype == FFA_DT_FP8_E4M3 ? 1 : 0,
                      v_new, v_pages);
   const hipError_t e = hipGetLastError();

@@ -158,6 +158,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     const bool need = lane < kPPW ? nv[lane & 1] > 0 : (lane == kPPW && do_probe && pa < Tb);
     const int idx = lane < kPPW ? c0 + lane : (pa >> 6);
     pg_lane = bload4(make_rsrc(p.bt + (size_t)b * p.bt_stride, p.bt_stride * 4), need ? idx * 4 : p.bt_stride * 4);
+    pg_lane = pg_lane < (uint32_t)p.num_pages ? pg_lane : 0u;  // ids outside the pools read page 0
   }
   const uint32_t es_q = p.q_dtype == 2 ? 4u : 2u;
   const int hwin = wv >> 1;
@@ -955,6 +956,10 @@ static int decode_params(const ffa_q2fp8_decode_args *a, ffa::DecodeParams &p) {
     return set_err(FFA_E_INVALID, "residual dtype");
   if (a->res_dtype != FFA_DT_NONE && !a->k_residual) return set_err(FFA_E_INVALID, "residual pointer is null");
   if (a->layout == FFA_LAYOUT_PAGED && !a->block_table) return set_err(FFA_E_INVALID, "paged layout needs a block table");
+  if (a->layout == FFA_LAYOUT_PAGED && a->num_pages <= 0)
+    return set_err(FFA_E_INVALID, "paged layout needs num_pages > 0 (pages in each pool)");
+  if (a->layout == FFA_LAYOUT_PAGED && (long)a->bt_stride * ffa::kPage < a->T)
+    return set_err(FFA_E_INVALID, "block table has fewer than ceil(T/64) columns");
   if (a->layout == FFA_LAYOUT_CONTIG && a->scale_mode != FFA_SCALE_CHANNEL)
     return set_err(FFA_E_UNSUPPORTED, "contiguous layout supports per-channel scales only");
   if (a->scale_mode == FFA_SCALE_G32 && a->scale_dtype != FFA_DT_F16)
@@ -983,6 +988,7 @@ static int decode_params(const ffa_q2fp8_decode_args *a, ffa::DecodeParams &p) {
   p.s_dtype = a->scale_dtype;
   p.out_dtype = a->out_dtype;
   p.bt_stride = a->bt_stride;
+  p.num_pages = a->layout == FFA_LAYOUT_PAGED ? a->num_pages : 0;
   p.B = a->B;
   p.T = a->T;
   p.HQ = a->HQ;

@@ -94,6 +94,7 @@ class DecodeArgs(ctypes.Structure):
         ("nparts", ctypes.c_int),
         ("mask", ctypes.c_void_p),
         ("ntbs", ctypes.c_int),
+        ("num_pages", ctypes.c_int),
     ]
 
 
@@ -132,6 +133,7 @@ class KfmtArgs(ctypes.Structure):
         ("layout", ctypes.c_int),
         ("block_table", ctypes.c_void_p),
         ("bt_stride", ctypes.c_int),
+        ("num_pages", ctypes.c_int),
     ]
 
 
@@ -170,10 +172,10 @@ def lib() -> ctypes.CDLL:
         L.ffa_kproj_rope_q2_channel.argtypes = [vp, vp, vp, ci, vp, vp, ci, ci, ci, ci, ci, ci, vp, vp, vp, vp, vp,
                                                 ci, vp, vp]
         L.ffa_kproj_rope_q2_channel.restype = ci
-        L.ffa_kproj_rope_q2_append.argtypes = [vp, vp, vp, ci, vp, vp, ci, ci, ci, ci, vp, vp, ci, vp, vp, vp, vp,
-                                               ci, vp, vp, ci, vp]
+        L.ffa_kproj_rope_q2_append.argtypes = [vp, vp, vp, ci, vp, vp, ci, ci, ci, ci, vp, vp, ci, ci, vp, vp, vp,
+                                               vp, ci, vp, vp, ci, vp]
         L.ffa_kproj_rope_q2_append.restype = ci
-        L.ffa_q2_quantize_g32_append.argtypes = [vp, ci, ci, ci, ci, vp, vp, ci, vp, vp, vp, vp, ci, vp, vp, vp]
+        L.ffa_q2_quantize_g32_append.argtypes = [vp, ci, ci, ci, ci, vp, vp, ci, ci, vp, vp, vp, vp, ci, vp, vp, vp]
         L.ffa_q2_quantize_g32_append.restype = ci
         L.ffa_kproj_rope.argtypes = [vp, vp, vp, ci, vp, vp, ci, ci, ci, ci, ci, ci, vp, vp]
         L.ffa_kproj_rope.restype = ci
@@ -188,7 +190,7 @@ def lib() -> ctypes.CDLL:
         L.ffa_nf4_quantize.argtypes = [vp, ci, ci, ci, ci, ci, vp, vp, vp, ci, vp, vp]
         L.ffa_nf4_quantize.restype = ci
         for name in ("ffa_nvfp4_g16_append", "ffa_nf4_g64_append"):
-            getattr(L, name).argtypes = [vp, ci, ci, ci, ci, vp, vp, ci, vp, vp, vp, ci, vp, vp, vp]
+            getattr(L, name).argtypes = [vp, ci, ci, ci, ci, vp, vp, ci, ci, vp, vp, vp, ci, vp, vp, vp]
             getattr(L, name).restype = ci
         _lib = L
         return _lib

@@ -132,6 +132,9 @@ def run_decode(
     a.layout = layout
     a.block_table = block_table.data_ptr() if block_table is not None else None
     a.bt_stride = block_table.shape[1] if block_table is not None else 0
+    if layout == N.LAYOUT_PAGED:  # pages every pool holds: the kernels read ids beyond them as page 0
+        pools = [k_q, v] + ([k_scale, k_zero] if scale_mode == N.SCALE_G32 else []) + ([k_residual] if use_res else [])
+        a.num_pages = min(int(t.shape[0]) for t in pools)
     a.seq_lens = seq_lens.data_ptr() if seq_lens is not None else None
     a.B, a.T, a.HQ, a.HKV = B, int(T), HQ, int(HKV)
     a.scale = float(scale)

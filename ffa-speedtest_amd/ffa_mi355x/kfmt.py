@@ -79,6 +79,9 @@ def run_kfmt_decode(
     a.layout = layout
     a.block_table = block_table.data_ptr() if block_table is not None else None
     a.bt_stride = block_table.shape[1] if block_table is not None else 0
+    if layout == N.LAYOUT_PAGED:  # pages every pool holds: the kernel reads ids beyond them as page 0
+        pools = [k, v] + ([k_scale] if k_scale is not None else []) + ([k_residual] if use_res else [])
+        a.num_pages = min(int(t.shape[0]) for t in pools)
     rc = N.lib().ffa_kfmt_decode(ctypes.byref(a), ctypes.c_void_p(N.stream_of(q.device)))
     N.check(rc, "ffa_kfmt_decode")
     return workspace

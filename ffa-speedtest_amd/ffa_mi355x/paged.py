@@ -115,7 +115,7 @@ class PagedQ2Cache:
         check_append_fits(pos, Tn, block_table, self.P)
         rc = N.lib().ffa_q2_quantize_g32_append(
             k.data_ptr(), N.dtype_code(k.dtype), B, Tn, HKV, pos.data_ptr(), block_table.data_ptr(),
-            block_table.shape[1], self.k_q.data_ptr(), self.k_scale.data_ptr(), self.k_zero.data_ptr(),
+            block_table.shape[1], self.P, self.k_q.data_ptr(), self.k_scale.data_ptr(), self.k_zero.data_ptr(),
             self.k_res.data_ptr(), N.dtype_code(self.res_dtype), N.ptr(v), self.v.data_ptr(),
             N.stream_of(k.device))
         N.check(rc, "ffa_q2_quantize_g32_append")

@@ -116,7 +116,7 @@ class PagedKfmtCache:
         check_append_fits(pos, Tn, block_table, self.P)
         fn = N.lib().ffa_nvfp4_g16_append if self.fmt == "nvfp4" else N.lib().ffa_nf4_g64_append
         rc = fn(k.data_ptr(), N.dtype_code(k.dtype), B, Tn, HKV, pos.data_ptr(), block_table.data_ptr(),
-                block_table.shape[1], self.k.data_ptr(), self.k_scale.data_ptr(), self.k_res.data_ptr(),
+                block_table.shape[1], self.P, self.k.data_ptr(), self.k_scale.data_ptr(), self.k_res.data_ptr(),
                 N.dtype_code(self.res_dtype), N.ptr(v), self.v.data_ptr(), N.stream_of(k.device))
         N.check(rc, f"ffa_{self.fmt}_append")
 

@@ -113,7 +113,7 @@ def kproj_rope_q2_append(cache: PagedQ2Cache, h, w_k, cos_rows, sin_rows, pos, b
     h = h.contiguous()
     rc = N.lib().ffa_kproj_rope_q2_append(
         h.data_ptr(), w_k.data_ptr(), N.ptr(bias), N.dtype_code(h.dtype), cos_rows.data_ptr(), sin_rows.data_ptr(),
-        B, Tn, H, HKV, pos.data_ptr(), block_table.data_ptr(), block_table.shape[1], cache.k_q.data_ptr(),
+        B, Tn, H, HKV, pos.data_ptr(), block_table.data_ptr(), block_table.shape[1], cache.P, cache.k_q.data_ptr(),
         cache.k_scale.data_ptr(), cache.k_zero.data_ptr(), cache.k_res.data_ptr(), N.dtype_code(cache.res_dtype),
         N.ptr(v_new), cache.v.data_ptr(), N.dtype_code(cache.v_dtype), N.stream_of(h.device))
     N.check(rc, "ffa_kproj_rope_q2_append")

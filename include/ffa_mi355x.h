@@ -117,7 +117,7 @@ typedef struct ffa_q2fp8_decode_args {
   const void *v;
   int v_dtype; /* F16 or BF16 */
   int layout;
-  const int32_t *block_table; /* [B, bt_stride] (paged only) */
+  const int32_t *block_table; /* [B, bt_stride] (paged only), bt_stride >= ceil(T/64) */
   int bt_stride;
   const int32_t *seq_lens; /* [B] or NULL (all sequences have length T); clamped to [0, T] */
   int B, T, HQ, HKV;
@@ -132,6 +132,7 @@ typedef struct ffa_q2fp8_decode_args {
   int nparts;
   int8_t *mask;
   int ntbs;
+  int num_pages; /* paged: pages P of every pool (> 0); block-table entries outside [0, P) read page 0 */
 } ffa_q2fp8_decode_args;
 
 /* Number of partial slots per query row the scratch buffers must hold for max length T. */
@@ -173,13 +174,16 @@ int ffa_kproj_rope_q2_channel(const void *h, const void *w_k, const void *bias, 
  * Fused K projection + RoPE + g32 quantize + append into the paged cache.
  *   h [B, Tn, H]; token n of sequence b goes to position pos[b] + n.
  *   cos/sin [B, Tn, D] f32 (per-token rows).  v_new [B, Tn, HKV, 128] (v_dtype)
- *   or NULL.  Writes codes/scale/zero/residual/V^T into the paged pools.
+ *   or NULL.  Writes codes/scale/zero/residual/V^T into the paged pools of num_pages
+ *   pages.  Every append entry point writes nothing for a token whose position lies
+ *   outside its block-table row (bt_stride columns) or whose page id is outside
+ *   [0, num_pages); callers check positions on the host beforehand.
  */
 int ffa_kproj_rope_q2_append(const void *h, const void *w_k, const void *bias, int h_dtype, const float *cos,
                              const float *sin, int B, int Tn, int H, int HKV, const int32_t *pos,
-                             const int32_t *block_table, int bt_stride, uint8_t *k_q_pages, void *scale_pages,
-                             void *zero_pages, uint8_t *res_pages, int res_dtype, const void *v_new,
-                             void *v_pages, int v_dtype, void *stream);
+                             const int32_t *block_table, int bt_stride, int num_pages, uint8_t *k_q_pages,
+                             void *scale_pages, void *zero_pages, uint8_t *res_pages, int res_dtype,
+                             const void *v_new, void *v_pages, int v_dtype, void *stream);
 
 /*
  * g32 quantize + append of given K rows into the paged cache (no projection):
@@ -188,9 +192,9 @@ int ffa_kproj_rope_q2_append(const void *h, const void *w_k, const void *bias, i
  *   v_new [B, Tn, HKV, 128] (2-byte dtype of the V pool) or NULL.
  */
 int ffa_q2_quantize_g32_append(const void *k, int k_dtype, int B, int Tn, int HKV, const int32_t *pos,
-                               const int32_t *block_table, int bt_stride, uint8_t *k_q_pages, void *scale_pages,
-                               void *zero_pages, uint8_t *res_pages, int res_dtype, const void *v_new, void *v_pages,
-                               void *stream);
+                               const int32_t *block_table, int bt_stride, int num_pages, uint8_t *k_q_pages,
+                               void *scale_pages, void *zero_pages, uint8_t *res_pages, int res_dtype,
+                               const void *v_new, void *v_pages, void *stream);
 
 /*
  * K projection + RoPE without quantization (the first half of every producer):
@@ -233,10 +237,11 @@ int ffa_nf4_quantize_nsplit(int T);
  * Pools as described at ffa_kfmt_decode.
  */
 int ffa_nvfp4_g16_append(const void *k, int k_dtype, int B, int Tn, int HKV, const int32_t *pos,
-                         const int32_t *block_table, int bt_stride, uint8_t *k_pages, uint8_t *scale_pages,
-                         uint8_t *res_pages, int res_dtype, const void *v_new, void *v_pages, void *stream);
+                         const int32_t *block_table, int bt_stride, int num_pages, uint8_t *k_pages,
+                         uint8_t *scale_pages, uint8_t *res_pages, int res_dtype, const void *v_new, void *v_pages,
+                         void *stream);
 int ffa_nf4_g64_append(const void *k, int k_dtype, int B, int Tn, int HKV, const int32_t *pos,
-                       const int32_t *block_table, int bt_stride, uint8_t *k_pages, void *scale_pages,
+                       const int32_t *block_table, int bt_stride, int num_pages, uint8_t *k_pages, void *scale_pages,
                        uint8_t *res_pages, int res_dtype, const void *v_new, void *v_pages, void *stream);
 int ffa_nf4_quantize(const void *k, int k_dtype, int B, int T, int HKV, int D, uint8_t *k_packed, void *scale,
                      uint8_t *residual, int res_dtype, float *absmax, void *stream);
@@ -299,8 +304,9 @@ typedef struct ffa_kfmt_decode_args {
   int8_t *mask;
   int ntbs;
   int layout;                 /* FFA_LAYOUT_CONTIG or FFA_LAYOUT_PAGED */
-  const int32_t *block_table; /* [B, bt_stride] (paged only) */
+  const int32_t *block_table; /* [B, bt_stride] (paged only), bt_stride >= ceil(T/64) */
   int bt_stride;
+  int num_pages; /* paged: pages P of every pool (> 0); block-table entries outside [0, P) read page 0 */
 } ffa_kfmt_decode_args;
 
 int ffa_kfmt_decode(const ffa_kfmt_decode_args *args, void *stream);

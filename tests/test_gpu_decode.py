@@ -201,3 +201,57 @@ def test_cudagraph_runner_paged(gpu):
         assert torch.equal(got, ref)
     o_ref, _ = oracle_paged(c, BS=64, SBS=64, delta=5.0)
     assert_out_close(f32(got), o_ref, "paged runner")
+
+
+def _pool_views(cache, P):
+    """Replace the cache's pools by pages [1, P + 1) of allocations two pages larger, so that page
+    ids -1 and P name real memory (allocation pages 0 and P + 1) outside the pools the library sees."""
+    allocs = {}
+    for name in ("k_q", "k_scale", "k_zero", "k_res", "v"):
+        t = getattr(cache, name)
+        big = torch.empty((P + 2,) + tuple(t.shape[1:]), dtype=t.dtype, device=t.device)
+        big.view(torch.uint8).fill_(0x3C)  # finite in every dtype of the pools
+        big[1:P + 1].copy_(t)
+        allocs[name] = big
+        setattr(cache, name, big[1:P + 1])
+    return allocs
+
+
+def test_page_ids_outside_the_pool(gpu):
+    """Block-table entries outside [0, P): the decoder reads them as page 0 and the g32 append
+    writes nothing for their tokens (no access outside the pools)."""
+    from ffa_mi355x import _native as N
+
+    case = paged_case(B=1, T=1024, HQ=32, HKV=8, seed=9, n_heavy=8)
+    cache = to_gpu_paged(case, gpu)
+    P = case["P"]
+    allocs = _pool_views(cache, P)
+    q = case["q"].to(gpu)
+    bt = case["block_table"].to(gpu)
+    bt_zero, bt_out = bt.clone(), bt.clone()
+    bt_zero[0, 3] = 0
+    bt_zero[0, 9] = 0
+    bt_out[0, 3] = -1
+    bt_out[0, 9] = P
+    w0 = cache.decode(q, bt_zero, T=1024, BS=64, delta=5.0)
+    o0, m0 = w0.o.clone(), w0.mask_buf.clone()
+    w1 = cache.decode(q, bt_out, T=1024, BS=64, delta=5.0)
+    torch.cuda.synchronize()
+    assert torch.equal(o0, w1.o) and torch.equal(m0, w1.mask_buf)
+
+    # append 128 tokens at positions 0..127 through pages bt_app = [P, 2]: page P is outside the pool
+    before = {k: v.clone() for k, v in allocs.items()}
+    k_new = torch.randn(1, 128, 8, 128, device=gpu, dtype=torch.bfloat16)
+    bt_app = torch.tensor([[P, 2]], dtype=torch.int32, device=gpu)
+    pos = torch.zeros(1, dtype=torch.int32, device=gpu)
+    rc = N.lib().ffa_q2_quantize_g32_append(
+        k_new.data_ptr(), N.DT_BF16, 1, 128, 8, pos.data_ptr(), bt_app.data_ptr(), 2, P, cache.k_q.data_ptr(),
+        cache.k_scale.data_ptr(), cache.k_zero.data_ptr(), cache.k_res.data_ptr(), N.dtype_code(cache.res_dtype),
+        None, cache.v.data_ptr(), N.stream_of(k_new.device))
+    N.check(rc, "ffa_q2_quantize_g32_append")
+    torch.cuda.synchronize()
+    for name, big in allocs.items():
+        b0 = before[name]
+        changed = [i for i in range(P + 2) if not torch.equal(big[i].view(torch.uint8), b0[i].view(torch.uint8))]
+        # only pool page 2 (allocation page 3) is written; the V pool is not (no v_new)
+        assert changed == ([] if name == "v" else [3]), (name, changed)

@@ -30,6 +30,24 @@ def test_library_exports_every_declared_symbol():
     assert set(N.EXPORTS) == declared
 
 
+def test_ctypes_argtypes_match_header_parameter_lists():
+    """Each function's ctypes argtypes have the header's parameter count, and the pointer /
+    integer / size_t kinds in the same order."""
+    from ffa_mi355x import _native as N
+
+    L = N.lib()
+    text = re.sub(r"/\*.*?\*/", "", (ROOT / "include" / "ffa_mi355x.h").read_text(), flags=re.S)
+    decls = re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(ffa_\w+)\s*\(([^)]*)\)\s*;", text, flags=re.M)
+    assert len(decls) == len(N.EXPORTS)
+    for name, params in decls:
+        params = [p.strip() for p in params.replace("\n", " ").split(",") if p.strip() not in ("", "void")]
+        want = ["p" if "*" in p else ("z" if p.startswith("size_t") else "i") for p in params]
+        kinds = {ctypes.c_void_p: "p", ctypes.c_int: "i", ctypes.c_size_t: "z", ctypes.c_float: "i"}
+        got = [("p" if hasattr(t, "contents") or t is ctypes.c_void_p else kinds[t])
+               for t in (getattr(L, name).argtypes or [])]
+        assert got == want, name
+
+
 @pytest.mark.parametrize("cname,pyname", [("ffa_q2fp8_decode_args", "DecodeArgs"),
                                            ("ffa_kfmt_decode_args", "KfmtArgs")])
 def test_ctypes_argument_structs_match_header(tmp_path, cname, pyname):
@@ -94,6 +112,19 @@ def test_invalid_arguments_are_rejected_without_launch():
     a.SBS = 64
     a.q_dtype, a.out_dtype, a.v_dtype, a.res_dtype = 0, 0, 9, 3
     assert L.ffa_q2fp8_decode(ctypes.byref(a), None) == -1
+    # paged: the pool size is required and the block table must cover T (checked before any launch)
+    a.v_dtype, a.res_dtype, a.layout = N.DT_BF16, N.DT_NONE, N.LAYOUT_PAGED
+    a.block_table, a.bt_stride, a.num_pages = 0x1000, 2, 0
+    assert L.ffa_q2fp8_decode(ctypes.byref(a), None) == -1 and b"num_pages" in L.ffa_last_error()
+    a.num_pages, a.bt_stride = 4, 1
+    assert L.ffa_q2fp8_decode(ctypes.byref(a), None) == -1 and b"block table" in L.ffa_last_error()
+    k = N.KfmtArgs()
+    k.B, k.T, k.HQ, k.HKV, k.BS, k.SBS = 1, 128, 32, 8, 64, 64
+    k.v_dtype, k.res_dtype, k.layout, k.block_table, k.bt_stride = N.DT_BF16, N.DT_NONE, N.LAYOUT_PAGED, 0x1000, 2
+    k.nparts, k.ntbs = 1, 2
+    assert L.ffa_kfmt_decode(ctypes.byref(k), None) == -1 and b"num_pages" in L.ffa_last_error()
+    k.num_pages, k.bt_stride = 4, 1
+    assert L.ffa_kfmt_decode(ctypes.byref(k), None) == -1 and b"block table" in L.ffa_last_error()
 
 
 def test_drop_in_signatures_match_reference():
