@@ -32,7 +32,8 @@ def _plant_heavy(q, k, lens, n_heavy, cos, g):
             for gi in range(G):
                 hq = h * G + gi
                 qh = q[b, hq] / q[b, hq].norm()
-                pos = [int(first[gi])] + [int(x) for x in rest[gi * (n_heavy - 1):(gi + 1) * (n_heavy - 1)]]
+                # sequences shorter than the group (or empty) get fewer heavy tokens
+                pos = [int(x) for x in first[gi:gi + 1]] + [int(x) for x in rest[gi * (n_heavy - 1):(gi + 1) * (n_heavy - 1)]]
                 for t in pos:
                     u = torch.randn(D, generator=g)
                     u = u - (u @ qh) * qh

@@ -258,6 +258,12 @@ def decode(
 
     for b in range(B):
         Tb = lens[b]
+        if Tb == 0:
+            # an empty sequence (ragged batches only): no blocks, both probe windows empty so the
+            # threshold is -inf, and the merge of no partials gives 0 (attn_kernel...q2fp8.py:167-171)
+            ntbs.append(0)
+            thr[b] = -np.inf
+            continue
         NTB, NSB_, idx, valid = _subblock_tokens(Tb, BS, SBS)
         NTBS = idx.shape[0]
         ntbs.append(NTBS)

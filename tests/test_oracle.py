@@ -251,3 +251,20 @@ def test_ragged_lengths_are_independent_sequences():
                      c["k_res"][1:, :130], res_fmt="e4m3fn", BS=64, scale_mode="g32", out_dtype="bf16", delta=3.0)
     assert np.array_equal(o[1:], o1)
     assert d["mask"][1, :, 3:].sum() == 0  # blocks past the sequence end do not exist
+
+
+def test_empty_and_one_token_sequences():
+    """An empty sequence gives zero output, no kept blocks and a -inf threshold; a one-token
+    sequence attends to its only token (softmax weight 1: the output is that token's V in bf16),
+    and the other sequences are unchanged by their presence."""
+    c = paged_case(B=3, T=300, HQ=8, HKV=2, seed=4, n_heavy=2, seq_lens=[300, 0, 1])
+    q, v = f32(c["q"]), f32(c["v"])
+    o, d = O.decode(q, c["k_q"], c["k_scale"], c["k_zero"], v, c["k_res"], res_fmt="e4m3fn", BS=64, scale_mode="g32",
+                    seq_lens=c["lens"], out_dtype="bf16", delta=3.0)
+    assert (o[1] == 0).all() and d["mask"][1].sum() == 0 and np.isneginf(d["threshold"][1]).all()
+    v1 = NM.round_bf16(v[2, 0])  # [HKV, 128]
+    assert np.array_equal(o[2], np.repeat(v1, 4, axis=0))
+    assert d["mask"][2, :, 0].all() and d["mask"][2, :, 1:].sum() == 0
+    o0, _ = O.decode(q[:1], c["k_q"][:1], c["k_scale"][:1], c["k_zero"][:1], v[:1], c["k_res"][:1],
+                     res_fmt="e4m3fn", BS=64, scale_mode="g32", out_dtype="bf16", delta=3.0)
+    assert np.array_equal(o[:1], o0)
