@@ -79,6 +79,16 @@ __device__ __forceinline__ int append_page(const int32_t *bt, int bt_stride, int
   const int page = bt[(size_t)b * bt_stride + (P >> 6)];
   return (unsigned)page < (unsigned)num_pages ? page : -1;
 }
+// A decode workgroup whose 512 tokens all lie past its sequence's end (ragged batches) writes
+// its survivor-mask bytes (all 0) and nothing else: the merge reads no partial slot past the
+// sequence end, and the threshold is written by the sequence's first workgroup.
+__device__ __forceinline__ void write_empty_mask(int8_t *mask_row, int cg, int SBS, int ntbs) {
+  const int nblk = kChunksPerWG * kPage / SBS;
+  for (int t = threadIdx.x; t < nblk; t += blockDim.x) {
+    const int jb = cg * nblk + t;
+    if (jb < ntbs) mask_row[jb] = 0;
+  }
+}
 enum { kChannel = 0, kG32 = 1 };
 enum { kResNone = 0, kResE4M3 = 1, kResE5M2 = 2 };
 enum { kVF16 = 0, kVBF16 = 1 };

@@ -109,6 +109,10 @@ void kfmt_decode_kernel(const DecodeParams p) {
 
   // ------------------------------------------------ phase 1: loads (issued on every path)
   const int Tb = p.seq_lens ? min(max(p.seq_lens[b], 0), p.T) : p.T;  // lengths beyond T are clamped to T
+  if (cg > 0 && cw * kPage >= Tb) {  // every token past the sequence end: mask bytes only
+    write_empty_mask(p.mask + ((size_t)b * p.HKV + hkv) * p.ntbs, cg, SBS, p.ntbs);
+    return;
+  }
   const int NTB = (Tb + p.BS - 1) / p.BS;
   const int NTBS_b = NTB * (p.BS / p.SBS);
   const int NTBk = (p.T + p.BS - 1) / p.BS;  // blocks of the block-scale tensor

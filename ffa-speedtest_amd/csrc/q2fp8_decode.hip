@@ -141,6 +141,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   // The q window is channels [32kc + 16h, +16) of the lane's row, h = wave / 2: it holds
   // every element of the operand this wave builds.
   const int Tb = p.seq_lens ? min(max(p.seq_lens[b], 0), p.T) : p.T;  // lengths beyond T are clamped to T
+  if (cg > 0 && cw * kPage >= Tb) {  // every token past the sequence end: mask bytes only
+    write_empty_mask(p.mask + ((size_t)b * p.HKV + hkv) * p.ntbs, cg, SBS, p.ntbs);
+    return;
+  }
   const int NTB = (Tb + p.BS - 1) / p.BS;
   const int NTBS_b = NTB * (p.BS / p.SBS);
   const bool do_probe = (p.th_in == nullptr) && wv < 2;
