@@ -299,7 +299,16 @@ void kfmt_decode_kernel(const DecodeParams p) {
       }
     } else {
       const uint32_t w = mp == 0 ? a.x : mp == 1 ? a.y : mp == 2 ? a.z : a.w;
-      if constexpr (FMT == kFP4) {
+      if constexpr (FMT == kFP4 && SCL == kSclG16) {
+        // e2m1 pairs of each byte (low nibble first) to fp16 (exact), times the e4m3 group scale
+        // in fp16: both have at most 4 significant bits and the product lies in [2^-10, 2688],
+        // so it is exact in fp16 and equals the reference's product rounded to fp16
+        const f16x2 s2 = {(_Float16)sc, (_Float16)sc};
+        r[0] = f16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 0) * s2);
+        r[1] = f16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 1) * s2);
+        r[2] = f16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 2) * s2);
+        r[3] = f16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 3) * s2);
+      } else if constexpr (FMT == kFP4) {
         // e2m1 pairs of each byte (low nibble first), exact in f32, times the scale, RNE to fp16
         const f32x2 v0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 0);
         const f32x2 v1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 1);
