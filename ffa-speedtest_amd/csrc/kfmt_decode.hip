@@ -34,6 +34,15 @@ namespace ffa {
 enum { kF8E4M3 = 0, kF8E5M2 = 1, kFP4 = 2, kNF4 = 3 };
 enum { kSclNone = 0, kSclToken = 1, kSclBlock = 2, kSclChannel = 3, kSclG16 = 4, kSclG64 = 5 };
 
+// fp16(a * sa) in the low half and fp16(b * sb) in the high half, each product in fp32 and then
+// rounded to fp16: v_fma_mixlo / v_fma_mixhi with a zero addend write one half and keep the other,
+// which saves the shift and OR of packing two separately rounded halves
+__device__ __forceinline__ uint32_t mul_pack_f16(float a, float sa, float b, float sb) {
+  uint32_t r;
+  asm("v_fma_mixlo_f16 %0, %1, %2, 0\n\tv_fma_mixhi_f16 %0, %3, %4, 0" : "=&v"(r) : "v"(a), "v"(sa), "v"(b), "v"(sb));
+  return r;
+}
+
 // QLoRA NF4 levels (the published 16 normal-float values), as fp32
 __constant__ float kNF4Levels[16] = {
     -1.0f, -0.6961928009986877f, -0.5229921340942383f, -0.39491748809814453f, -0.28444138169288635f,
@@ -319,12 +328,17 @@ void kfmt_decode_kernel(const DecodeParams p) {
         r[2] = pack_f16(v2[0] * sc, v2[1] * sc);
         r[3] = pack_f16(v3[0] * sc, v3[1] * sc);
       }
+      if constexpr (FMT == kNF4) {
+        // byte offsets of the codebook entries (nibble * 4), four per word: low and high nibbles
+        uint32_t lo4 = (w << 2) & 0x3c3c3c3cu, hi4 = (w >> 2) & 0x3c3c3c3cu;
+        asm("" : "+v"(lo4), "+v"(hi4));  // keep the byte-wise form: one extract per offset
+        const char *cb = (const char *)s_cb;
 #pragma unroll
-      for (int h = 0; h < 4; ++h) {
-        if constexpr (FMT == kNF4) {
-          const uint32_t byte = (w >> (8 * h)) & 0xffu;
+        for (int h = 0; h < 4; ++h) {
+          const float l0 = *(const float *)(cb + ((lo4 >> (8 * h)) & 0xffu));
+          const float l1 = *(const float *)(cb + ((hi4 >> (8 * h)) & 0xffu));
           const float s0 = kGrp ? sc : sch[8 * mp + 2 * h], s1 = kGrp ? sc : sch[8 * mp + 2 * h + 1];
-          r[h] = pack_f16(s_cb[byte & 15u] * s0, s_cb[byte >> 4] * s1);
+          r[h] = mul_pack_f16(l0, s0, l1, s1);
         }
       }
     }
