@@ -88,10 +88,10 @@ void kfmt_decode_kernel(const DecodeParams p) {
   constexpr int kLane = kRow / 4;      // bytes of one lane's 32 channels
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int u = blockIdx.x / p.nwg;
-  const int cg = blockIdx.x - u * p.nwg;  // workgroup index along the sequence = partial slot
-  const int b = u / p.HKV;
-  const int hkv = u - b * p.HKV;
+  // grid (span, KV head, sequence), the span fastest (consecutive workgroups on different XCDs)
+  const int cg = blockIdx.x;  // workgroup index along the sequence = partial slot
+  const int hkv = blockIdx.y;
+  const int b = blockIdx.z;
   const int G = p.G;
   const int cw = cg * kChunksPerWG;
   const int c0 = cw + wv * kPPW;
@@ -734,7 +734,7 @@ static hipError_t kfmt_launch(const ffa::DecodeParams &p, dim3 grid, hipStream_t
     hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, true>), grid, dim3(256), 0, st, p);
   } else {
     const int cus = ffa::device_cus();
-    if (cus > 0 && grid.x > (unsigned)cus)
+    if (cus > 0 && grid.x * grid.y * grid.z > (unsigned)cus)
       hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, true>), grid, dim3(256), 0, st, p);
     else
       hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, false>), grid, dim3(256), 0, st, p);
@@ -785,6 +785,8 @@ extern "C" int ffa_kfmt_decode(const ffa_kfmt_decode_args *a, void *stream) {
   if (a->ntbs < ntbs) return ffa_set_error_internal(FFA_E_INVALID, "mask holds too few blocks");
   const bool paged = a->layout == FFA_LAYOUT_PAGED;
   if (!paged && a->layout != FFA_LAYOUT_CONTIG) return ffa_set_error_internal(FFA_E_INVALID, "layout");
+  if (a->B > 65535 || a->HKV > 65535)
+    return ffa_set_error_internal(FFA_E_UNSUPPORTED, "B and HKV are grid dimensions (at most 65535)");
   if (paged && !a->block_table) return ffa_set_error_internal(FFA_E_INVALID, "paged layout needs a block table");
   if (paged && a->num_pages <= 0)
     return ffa_set_error_internal(FFA_E_INVALID, "paged layout needs num_pages > 0 (pages in each pool)");
@@ -828,7 +830,7 @@ extern "C" int ffa_kfmt_decode(const ffa_kfmt_decode_args *a, void *stream) {
   p.nwg = need;
 
   hipStream_t st = (hipStream_t)stream;
-  dim3 grid(need * a->B * a->HKV);
+  dim3 grid(need, a->HKV, a->B);
   hipError_t e = hipErrorInvalidValue;
   const int fmt = a->k_format, sk = a->scale_kind;
   constexpr int C = ffa::kContig, PG = ffa::kPaged;

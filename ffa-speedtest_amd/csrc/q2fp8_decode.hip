@@ -89,13 +89,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   constexpr bool kG = SMODE == kG32;
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // 1-D grid, workgroup index along the sequence fastest: consecutive workgroups land on
-  // different XCDs (dispatch is round-robin over the 8 XCDs), so the residual/V traffic of a
-  // (sequence, KV head) unit with many kept chunks is spread over every XCD's memory path.
-  const int u = blockIdx.x / p.nwg;
-  const int cg = blockIdx.x - u * p.nwg;  // workgroup index along the sequence = partial slot
-  const int b = u / p.HKV;
-  const int hkv = u - b * p.HKV;
+  // grid (span, KV head, sequence), the span along the sequence fastest: consecutive workgroups
+  // land on different XCDs (dispatch is round-robin over the 8 XCDs), so the residual/V traffic
+  // of a (sequence, KV head) with many kept chunks is spread over every XCD's memory path.
+  const int cg = blockIdx.x;  // workgroup index along the sequence = partial slot
+  const int hkv = blockIdx.y;
+  const int b = blockIdx.z;
   const int G = p.G;
   const int cw = cg * kChunksPerWG;  // first chunk of the workgroup
   const int c0 = cw + wv * kPPW;     // first chunk scored by this wave
@@ -918,7 +917,7 @@ static hipError_t launch_decode(const ffa::DecodeParams &p, dim3 grid, hipStream
   // paged g32 with more workgroups than two per CU: the three-per-CU build of the kernel
   if constexpr (L == ffa::kPaged && S == ffa::kG32) {
     const int cus = ffa::device_cus();
-    if (cus > 0 && grid.x > 2u * (unsigned)cus) {
+    if (cus > 0 && grid.x * grid.y * grid.z > 2u * (unsigned)cus) {
       hipLaunchKernelGGL((ffa::q2fp8_decode_kernel<L, S, R, V, 3>), grid, dim3(256), 0, st, p);
       return hipGetLastError();
     }
@@ -959,6 +958,7 @@ static int decode_params(const ffa_q2fp8_decode_args *a, ffa::DecodeParams &p) {
   if (!(a->res_dtype == FFA_DT_FP8_E4M3 || a->res_dtype == FFA_DT_FP8_E5M2 || a->res_dtype == FFA_DT_NONE))
     return set_err(FFA_E_INVALID, "residual dtype");
   if (a->res_dtype != FFA_DT_NONE && !a->k_residual) return set_err(FFA_E_INVALID, "residual pointer is null");
+  if (a->B > 65535 || a->HKV > 65535) return set_err(FFA_E_UNSUPPORTED, "B and HKV are grid dimensions (at most 65535)");
   if (a->layout == FFA_LAYOUT_PAGED && !a->block_table) return set_err(FFA_E_INVALID, "paged layout needs a block table");
   if (a->layout == FFA_LAYOUT_PAGED && a->num_pages <= 0)
     return set_err(FFA_E_INVALID, "paged layout needs num_pages > 0 (pages in each pool)");
@@ -1009,7 +1009,7 @@ static int decode_params(const ffa_q2fp8_decode_args *a, ffa::DecodeParams &p) {
 }
 
 static int launch_stage1(const ffa_q2fp8_decode_args *a, const ffa::DecodeParams &p, hipStream_t st) {
-  dim3 grid(p.nwg * a->B * a->HKV);
+  dim3 grid(p.nwg, a->HKV, a->B);
   hipError_t e;
   if (a->layout == FFA_LAYOUT_PAGED) {
     if (a->scale_mode == FFA_SCALE_G32)
