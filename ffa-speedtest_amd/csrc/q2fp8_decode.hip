@@ -79,9 +79,10 @@ __device__ __forceinline__ f16x8 dequant8_channel(uint32_t h, const uint32_t *sp
 // then sit at 16k + 4tau + u, one 8-byte load per lane and tile.
 __host__ __device__ constexpr int scale_pos(int t) { return 16 * (t >> 4) + 4 * (t & 3) + ((t >> 2) & 3); }
 
-// OCC = 3 asks the compiler for three waves per SIMD (at most 168 registers), so that three
-// workgroups share a CU: used when the grid has more workgroups than two per CU can hold
-// (large batches), where it trades a few spilled registers for a third workgroup in flight.
+// OCC = 4 asks the compiler for four waves per SIMD (at most 128 registers), so that four
+// workgroups share a CU (29 KB of LDS each): used when the grid has more workgroups than two per
+// CU can hold (large batches), where it trades a few spilled registers for two more workgroups
+// in flight.
 template <int LAYOUT, int SMODE, int RES, int VT, int OCC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void q2fp8_decode_kernel(
     const DecodeParams p) {
@@ -116,7 +117,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   __shared__ int s_kept[kChunksPerWG];             // chunk kept (some prune block survives)
   __shared__ int s_pgid[kChunksPerWG];             // pool page of the chunk
   __shared__ uint32_t s_bal[kChunksPerWG][2];      // survivor ballot of the chunk
-  __shared__ float4 s_R[kG ? kChunksPerWG : 1][4][64];        // g32: coarse scores of kept chunks
+  // g32: coarse scores of kept chunks, [q4][4 kc + row]: after the group sums the four lanes of a
+  // query row (one per group) hold its scores, and only group 0's lanes reach the partials
+  __shared__ float4 s_R[kG ? kChunksPerWG : 1][4][16];
   __shared__ uint64_t s_x[kG ? 1 : kChunksPerWG][kG ? 1 : 4][kG ? 1 : 64];  // channel: codes of kept chunks
   __shared__ float s_pm[kChunksPerWG][4], s_pl[kChunksPerWG][4];
   __shared__ __attribute__((aligned(16))) float s_po[kChunksPerWG][4][128];
@@ -461,7 +464,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
       if constexpr (kG) {
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4)
-          s_R[slot][q4][lane] = make_float4(R[j][4 * q4], R[j][4 * q4 + 1], R[j][4 * q4 + 2], R[j][4 * q4 + 3]);
+          if (jg == 0) s_R[slot][q4][4 * kc + ir] = make_float4(R[j][4 * q4], R[j][4 * q4 + 1], R[j][4 * q4 + 2], R[j][4 * q4 + 3]);
       } else {
 #pragma unroll
         for (int tau = 0; tau < 4; ++tau) s_x[slot][tau][lane] = x[j][tau];
@@ -513,12 +516,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
         }
       }
     }
+    // paged V^T: VH column blocks (of 8) are loaded with the residual; the large-batch build loads
+    // the second half after the first half's products, which keeps 32 fewer registers live
+    constexpr int VH = (LAYOUT == kPaged && OCC > 1) ? 4 : 8;
+    brsrc vs_p;
     if constexpr (LAYOUT == kPaged) {
-      const brsrc vs = make_rsrc((const uint16_t *)p.v + ((size_t)pgs_ * p.HKV + hkv) * (kD * kPage), kD * kPage * 2);
+      vs_p = make_rsrc((const uint16_t *)p.v + ((size_t)pgs_ * p.HKV + hkv) * (kD * kPage), kD * kPage * 2);
 #pragma unroll
-      for (int nu = 0; nu < 8; ++nu)
+      for (int nu = 0; nu < VH; ++nu)
 #pragma unroll
-        for (int kap = 0; kap < 2; ++kap) vv[nu][kap] = bload16(vs, ((nu * 2 + kap) * 64 + lane) * 16);  // block (nu, kap)
+        for (int kap = 0; kap < 2; ++kap) vv[nu][kap] = bload16(vs_p, ((nu * 2 + kap) * 64 + lane) * 16);  // block (nu, kap)
     } else {
       const brsrc vs = make_rsrc((const uint16_t *)p.v + (((size_t)b * p.T + t0) * p.HKV + hkv) * kD,
                                  ((nvs - 1) * p.HKV + 1) * kD * 2);
@@ -534,7 +541,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     if constexpr (kG) {
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
-        const float4 r4 = s_R[slot][q4][lane];
+        const float4 r4 = s_R[slot][q4][4 * kc + ir];
         Rj[4 * q4] = r4.x;
         Rj[4 * q4 + 1] = r4.y;
         Rj[4 * q4 + 2] = r4.z;
@@ -625,6 +632,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     if constexpr (LAYOUT == kPaged) {
 #pragma unroll
       for (int nu = 0; nu < 8; ++nu) {
+        if (nu == VH) {  // the second half of V^T, into the registers the first half has freed
+#pragma unroll
+          for (int n2 = VH; n2 < 8; ++n2)
+#pragma unroll
+            for (int kap = 0; kap < 2; ++kap) vv[n2][kap] = bload16(vs_p, ((n2 * 2 + kap) * 64 + lane) * 16);
+        }
 #pragma unroll
         for (int kap = 0; kap < 2; ++kap) {
           uint4 v4 = vv[nu][kap];
@@ -914,11 +927,11 @@ int device_cus() {
 
 template <int L, int S, int R, int V>
 static hipError_t launch_decode(const ffa::DecodeParams &p, dim3 grid, hipStream_t st) {
-  // paged g32 with more workgroups than two per CU: the three-per-CU build of the kernel
+  // paged g32 with more workgroups than two per CU: the four-per-CU build of the kernel
   if constexpr (L == ffa::kPaged && S == ffa::kG32) {
     const int cus = ffa::device_cus();
     if (cus > 0 && grid.x * grid.y * grid.z > 2u * (unsigned)cus) {
-      hipLaunchKernelGGL((ffa::q2fp8_decode_kernel<L, S, R, V, 3>), grid, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((ffa::q2fp8_decode_kernel<L, S, R, V, 4>), grid, dim3(256), 0, st, p);
       return hipGetLastError();
     }
   }
