@@ -492,7 +492,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     const bool keep16 = SBS == 16   ? ((bl >> (16 * kc)) & 0xffffull) != 0
                         : SBS == 32 ? ((bl >> (32 * (kc >> 1))) & 0xffffffffull) != 0
                                     : bl != 0;
-    // residual + V loads (the chunk is kept: whole resource)
+    // residual + V loads (the chunk is kept: whole resource).  In the large-batch build they are
+    // issued at raised wave priority, so that the arbiter favours them over the scoring of the
+    // other workgroups on the CU (config 5's decode 658 -> 599 us; at config 2, where every
+    // workgroup reaches its exact pass at about the same time, it cost 0.2 us)
+    if constexpr (OCC > 1) __builtin_amdgcn_s_setprio(2);
     uint4 rr[4][2];
     uint4 vv[8][2];
     if constexpr (RES != kResNone) {
@@ -536,6 +540,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
         vv[r >> 1][r & 1] = bload16(vs, tk * p.HKV * kD * 2 + 16 * vc);
       }
     }
+    if constexpr (OCC > 1) __builtin_amdgcn_s_setprio(0);  // back to normal once the chunk's loads are out
     // refined scores
     float Rj[16];
     if constexpr (kG) {
