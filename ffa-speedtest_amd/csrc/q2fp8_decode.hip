@@ -788,23 +788,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
 
 // --------------------------------------------------------------------------
 // Log-sum-exp merge of the workgroup partials (attn_kernel...q2fp8.py:142-171).
-// One wave per (sequence, query head, 32-column slab): lane k owns partials k,
+// One wave per (sequence, query head, 16-column slab): lane k owns partials k,
 // k + 64, ...; m, l and (small batches) the first 64 partials' columns are loaded in one
 // batch of unconditional buffer loads (validity = resource size), the maxima and sums go
 // through register exchanges, the column sums over lanes through LDS.
 // --------------------------------------------------------------------------
 template <bool LAZY>
 __device__ __forceinline__ void merge_partials(const DecodeParams &p) {
-  const int row = blockIdx.x >> 2;  // b * HQ + hq
-  const int slab = blockIdx.x & 3;
+  const int row = blockIdx.x >> 3;  // b * HQ + hq
+  const int slab = blockIdx.x & 7;  // 16-column slab
   const int b = row / p.HQ;
   const int lane = threadIdx.x;
   const int Tb = p.seq_lens ? min(max(p.seq_lens[b], 0), p.T) : p.T;  // lengths beyond T are clamped to T
   const int nparts = min((Tb + kChunksPerWG * kPage - 1) / (kChunksPerWG * kPage), p.nparts);
   const brsrc rm = make_rsrc(p.m_buf + (size_t)row * p.nparts, nparts * 4);
   const brsrc rl = make_rsrc(p.l_buf + (size_t)row * p.nparts, nparts * 4);
-  const brsrc ro = make_rsrc(p.o_buf + (size_t)row * p.nparts * 128 + 32 * slab, nparts > 0 ? ((nparts - 1) * 128 + 32) * 4 : 0);
-  __shared__ float s_o[64][33];
+  const brsrc ro = make_rsrc(p.o_buf + (size_t)row * p.nparts * 128 + 16 * slab, nparts > 0 ? ((nparts - 1) * 128 + 16) * 4 : 0);
+  __shared__ float s_o[64][17];
 
   // first partial of the lane (slots past nparts read as l = 0, o = 0).  Eager (small
   // batches): its columns are loaded with m and l in one round trip, kept or not.  LAZY (many
@@ -812,16 +812,16 @@ __device__ __forceinline__ void merge_partials(const DecodeParams &p) {
   // sequences hold pruned spans and reading them all would dominate the traffic.
   const float m0 = __uint_as_float(bload4(rm, lane * 4));
   const float l0 = __uint_as_float(bload4(rl, lane * 4));
-  uint4 o0[8];
+  uint4 o0[4];
   if constexpr (!LAZY) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o0[e] = bload16(ro, (lane * 128 + 4 * e) * 4);
+    for (int e = 0; e < 4; ++e) o0[e] = bload16(ro, (lane * 128 + 4 * e) * 4);
   } else {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o0[e] = make_uint4(0, 0, 0, 0);
+    for (int e = 0; e < 4; ++e) o0[e] = make_uint4(0, 0, 0, 0);
     if (l0 > 0.f) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o0[e] = bload16(ro, (lane * 128 + 4 * e) * 4);
+      for (int e = 0; e < 4; ++e) o0[e] = bload16(ro, (lane * 128 + 4 * e) * 4);
     }
   }
   float M = l0 > 0.f ? m0 : -INFINITY;
@@ -831,7 +831,7 @@ __device__ __forceinline__ void merge_partials(const DecodeParams &p) {
   }
   M = wave_max(M);
 
-  float acc[32];
+  float acc[16];
   float A;
   {
     // o is used only where l > 0: a slot whose span kept nothing holds no defined values
@@ -839,7 +839,7 @@ __device__ __forceinline__ void merge_partials(const DecodeParams &p) {
     const float wgt = keep ? exp2f(m0 - M) : 0.f;
     A = keep ? l0 * wgt : 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
+    for (int e = 0; e < 4; ++e) {
       acc[4 * e + 0] = keep ? __uint_as_float(o0[e].x) * wgt : 0.f;
       acc[4 * e + 1] = keep ? __uint_as_float(o0[e].y) * wgt : 0.f;
       acc[4 * e + 2] = keep ? __uint_as_float(o0[e].z) * wgt : 0.f;
@@ -852,7 +852,7 @@ __device__ __forceinline__ void merge_partials(const DecodeParams &p) {
       const float wgt = exp2f(__uint_as_float(bload4(rm, k * 4)) - M);
       A = __builtin_fmaf(l, wgt, A);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
+      for (int e = 0; e < 4; ++e) {
         const uint4 v = bload16(ro, (k * 128 + 4 * e) * 4);
         acc[4 * e + 0] = __builtin_fmaf(__uint_as_float(v.x), wgt, acc[4 * e + 0]);
         acc[4 * e + 1] = __builtin_fmaf(__uint_as_float(v.y), wgt, acc[4 * e + 1]);
@@ -862,20 +862,21 @@ __device__ __forceinline__ void merge_partials(const DecodeParams &p) {
     }
   }
   A = wave_sum(A);
-  // column sums over the 64 lanes through LDS: lane c < 32 sums column c of lanes 0..31,
-  // lane 32 + c of lanes 32..63
+  // column sums over the 64 lanes through LDS: lane 16 q + c sums column c of lanes 16 q .. 16 q + 15,
+  // then the four quarters are added by register exchanges
 #pragma unroll
-  for (int e = 0; e < 32; ++e) s_o[lane][e] = acc[e];
+  for (int e = 0; e < 16; ++e) s_o[lane][e] = acc[e];
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  const int c = lane & 31, h = lane >> 5;
+  const int c = lane & 15, h = lane >> 4;
   float sum = 0.f;
 #pragma unroll 8
-  for (int k = 32 * h; k < 32 * h + 32; ++k) sum += s_o[k][c];
-  sum = swap32_sum(sum);
-  if (lane < 32)
-    store_any(p.out, (size_t)row * 128 + 32 * slab + c, p.out_dtype, A == 0.f ? 0.f : sum / A);
+  for (int k = 16 * h; k < 16 * h + 16; ++k) sum += s_o[k][c];
+  sum += __shfl_xor(sum, 16);
+  sum += __shfl_xor(sum, 32);
+  if (lane < 16)
+    store_any(p.out, (size_t)row * 128 + 16 * slab + c, p.out_dtype, A == 0.f ? 0.f : sum / A);
 }
 
 __global__ __launch_bounds__(64) void q2fp8_merge_kernel(const DecodeParams p) { merge_partials<false>(p); }
@@ -883,7 +884,7 @@ __global__ __launch_bounds__(64) void q2fp8_merge_sparse_kernel(const DecodePara
 
 // more than 256 query rows (8 sequences of 32 heads): the lazy merge
 hipError_t launch_merge(const DecodeParams &p, hipStream_t st) {
-  const dim3 grid((unsigned)(p.B * p.HQ * 4));
+  const dim3 grid((unsigned)(p.B * p.HQ * 8));
   if (p.B * p.HQ > 256)
     hipLaunchKernelGGL(q2fp8_merge_sparse_kernel, grid, dim3(64), 0, st, p);
   else
