@@ -37,7 +37,95 @@ struct DecodeParams {
   float delta;
   int nparts, ntbs;
   int nwg;  // decode workgroups per (sequence, KV head)
+  // GQA groups of more than 4 query rows and prune blocks longer than a workgroup's 512 tokens
+  // run as two passes of the same kernel over "units" of at most 4 query rows of one KV head
+  // (grid y = HKV * nq):
+  //   pass 0  one pass: each workgroup decides its blocks from its own scores (G <= 4, SBS <= 512)
+  //   pass 1  scores only: the coarse maximum of every prune block (SBS <= 512) or 512-token span
+  //           (SBS > 512) per query row goes to pmax [B, HQ, npieces], the thresholds to th_out
+  //   pass 2  every block is decided from all G rows' maxima and thresholds (the group prune of
+  //           the single pass), then the exact pass and partials as in pass 0
+  int nq;        // units (quads of query rows) per KV head, ceil(G / 4)
+  int pass;      // 0, 1 or 2
+  float *pmax;   // pass 1 / 2 scratch, [B, HQ, npieces] f32
+  int npieces;   // NTBS (SBS <= 512) or nparts (SBS > 512)
 };
+
+// The (KV head, query rows) unit of a decode workgroup: grid y = hkv * nq + quad, rows
+// 4 quad .. 4 quad + Gu - 1 of the GQA group (query heads row0 ..).
+struct DecodeUnit {
+  int hkv, quad, Gu, row0;
+};
+__device__ __forceinline__ DecodeUnit decode_unit(const DecodeParams &p) {
+  DecodeUnit u;
+  u.hkv = p.nq == 1 ? (int)blockIdx.y : (int)blockIdx.y / p.nq;
+  u.quad = (int)blockIdx.y - u.hkv * p.nq;
+  u.Gu = min(4, p.G - 4 * u.quad);
+  u.row0 = u.hkv * p.G + 4 * u.quad;
+  return u;
+}
+
+// Pass 2: whether each prune block of the workgroup's span survives, from the coarse maxima pass 1
+// wrote for every query row of the group: kept iff some row r has !(max over the block's pieces of
+// pmax[r] < th[r]) -- the single pass's "prune iff every row is below its threshold".  s_keep[blk]
+// (blk < 512 / SBS, or 0 when SBS > 512) must be zero beforehand and is read after a barrier.
+// Spans past the sequence end (SBS > 512) are left out, as pass 1 wrote nothing for them.
+__device__ __forceinline__ void decide_blocks(const DecodeParams &p, int b, int hkv, int cw, int Tb, int *s_keep) {
+  const int G = p.G, SBS = p.SBS;
+  const int span_tok = 8 * 64;  // tokens of one workgroup span
+  const int nblk = SBS <= span_tok ? span_tok / SBS : 1;
+  const int per = SBS <= span_tok ? 1 : SBS / span_tok;                    // pieces per block
+  const int piece0 = SBS <= span_tok ? cw * 64 / SBS : (cw * 64 / SBS) * per;  // first piece of block 0
+  const float *thr = p.th_in != nullptr ? p.th_in : p.th_out;
+  for (int idx = threadIdx.x; idx < nblk * G; idx += blockDim.x) {
+    const int blk = idx / G, r = idx - blk * G;
+    const size_t row = (size_t)b * p.HQ + hkv * G + r;
+    float mx = -INFINITY;
+    for (int s = 0; s < per; ++s) {
+      const int piece = piece0 + blk * per + s;
+      if (piece >= p.npieces || (per > 1 && piece * span_tok >= Tb)) break;
+      const float v = p.pmax[row * p.npieces + piece];
+      mx = s == 0 ? v : fmaxf(mx, v);
+    }
+    if (!(mx < thr[row])) atomicOr(&s_keep[blk], 1);
+  }
+}
+
+// Survivor ballot of one 64-token chunk (first chunk of the workgroup cw, this chunk c): in pass 2
+// each lane votes its 16 tokens' block decision from s_keep, otherwise its row's block maximum
+// against the row's threshold (strict <; rows outside the unit do not vote).
+__device__ __forceinline__ uint64_t chunk_ballot(const DecodeParams &p, bool row_ok, float mb, float th,
+                                                 const int *s_keep, int cw, int c, int kc) {
+  if (p.pass == 2) {
+    const int rel = (c - cw) * 64 + 16 * kc;  // lane's first token relative to the span
+    const int blk = p.SBS <= 512 ? rel / p.SBS : 0;
+    return __ballot(row_ok && s_keep[blk] != 0);
+  }
+  return __ballot(row_ok && !(mb < th));
+}
+
+// Pass 1: the coarse maximum of the prune block holding the lane's tokens (SBS <= 512), or of
+// the whole span (SBS > 512), for the lane's query row; one lane per block and row writes.
+// mb[j] is the chunk's block maximum after the cross-lane / cross-wave reductions.
+__device__ __forceinline__ void write_piece_max(const DecodeParams &p, size_t row, int c0, int cg, int wv, int kc,
+                                                const float *mb) {
+  const int SBS = p.SBS;
+  float *dst = p.pmax + row * p.npieces;
+  if (SBS <= 64) {
+    const bool first = SBS == 16 || (SBS == 32 ? (kc & 1) == 0 : kc == 0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int jb = ((c0 + j) * 64 + 16 * kc) / SBS;
+      if (first && jb < p.npieces) dst[jb] = mb[j];
+    }
+  } else if (SBS <= 512) {
+    const int wpb = max(SBS / 128, 1);  // waves per block
+    const int jb = c0 * 64 / SBS;
+    if (kc == 0 && wv % wpb == 0 && jb < p.npieces) dst[jb] = mb[0];
+  } else if (kc == 0 && wv == 0 && cg < p.npieces) {
+    dst[cg] = mb[0];
+  }
+}
 
 enum { kContig = 0, kPaged = 1 };
 
@@ -83,6 +171,11 @@ __device__ __forceinline__ int append_page(const int32_t *bt, int bt_stride, int
 // its survivor-mask bytes (all 0) and nothing else: the merge reads no partial slot past the
 // sequence end, and the threshold is written by the sequence's first workgroup.
 __device__ __forceinline__ void write_empty_mask(int8_t *mask_row, int cg, int SBS, int ntbs) {
+  if (SBS > kChunksPerWG * kPage) {  // a block of several spans: its first span writes its byte
+    const int jb = cg * kChunksPerWG * kPage / SBS;
+    if (threadIdx.x == 0 && (cg * kChunksPerWG * kPage) % SBS == 0 && jb < ntbs) mask_row[jb] = 0;
+    return;
+  }
   const int nblk = kChunksPerWG * kPage / SBS;
   for (int t = threadIdx.x; t < nblk; t += blockDim.x) {
     const int jb = cg * nblk + t;

@@ -28,6 +28,8 @@
 #include <type_traits>
 
 extern "C" int ffa_set_error_internal(int code, const char *msg);
+extern "C" int ffa_decode_shape_check(int B, int T, int HQ, int HKV, int BS, int SBS, float *piece_max, int npieces,
+                                      const float *th_in, const float *th_out, ffa::DecodeParams *p);
 
 namespace ffa {
 
@@ -90,9 +92,9 @@ void kfmt_decode_kernel(const DecodeParams p) {
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // grid (span, KV head, sequence), the span fastest (consecutive workgroups on different XCDs)
   const int cg = blockIdx.x;  // workgroup index along the sequence = partial slot
-  const int hkv = blockIdx.y;
+  const DecodeUnit un = decode_unit(p);  // KV head and the (at most 4) query rows of this workgroup
+  const int hkv = un.hkv;
   const int b = blockIdx.z;
-  const int G = p.G;
   const int cw = cg * kChunksPerWG;
   const int c0 = cw + wv * kPPW;
   const int SBS = p.SBS;
@@ -102,12 +104,13 @@ void kfmt_decode_kernel(const DecodeParams p) {
   const int n = mrow;
   const int jg = n >> 2;
   const int ir = n & 3;
-  const bool row_ok = ir < G;
-  const int hq = hkv * G + (row_ok ? ir : 0);
+  const bool row_ok = ir < un.Gu;
+  const int hq = un.row0 + (row_ok ? ir : 0);
 
   __shared__ uint4 s_qa[4][64];
   __shared__ float s_probe[2][4];
   __shared__ float s_wmax[kWaves][4];
+  __shared__ int s_keep[kChunksPerWG * kPage / 16];  // pass 2: block decisions of the span
   __shared__ uint32_t s_bal[kChunksPerWG][2];
   __shared__ float s_pm[kChunksPerWG][4], s_pl[kChunksPerWG][4];
   __shared__ float s_po[kChunksPerWG][4][128];
@@ -119,9 +122,10 @@ void kfmt_decode_kernel(const DecodeParams p) {
   // ------------------------------------------------ phase 1: loads (issued on every path)
   const int Tb = p.seq_lens ? min(max(p.seq_lens[b], 0), p.T) : p.T;  // lengths beyond T are clamped to T
   if (cg > 0 && cw * kPage >= Tb) {  // every token past the sequence end: mask bytes only
-    write_empty_mask(p.mask + ((size_t)b * p.HKV + hkv) * p.ntbs, cg, SBS, p.ntbs);
+    if (p.pass != 1 && un.quad == 0) write_empty_mask(p.mask + ((size_t)b * p.HKV + hkv) * p.ntbs, cg, SBS, p.ntbs);
     return;
   }
+  if (threadIdx.x < kChunksPerWG * kPage / 16) s_keep[threadIdx.x] = 0;
   const int NTB = (Tb + p.BS - 1) / p.BS;
   const int NTBS_b = NTB * (p.BS / p.SBS);
   const int NTBk = (p.T + p.BS - 1) / p.BS;  // blocks of the block-scale tensor
@@ -419,16 +423,25 @@ void kfmt_decode_kernel(const DecodeParams p) {
   if (p.th_in != nullptr) th = row_ok ? th_pre : INFINITY;
   else th = row_ok ? fmaxf(s_probe[0][ir], s_probe[1][ir]) - p.delta : INFINITY;
   if (SBS > 128) {
-    const int wpb = SBS / (kPage * kPPW);
+    const int wpb = min(SBS / (kPage * kPPW), kWaves);  // waves per block (a block of several spans: all)
     const int w0 = (wv / wpb) * wpb;
     float m2 = -INFINITY;
     for (int w = w0; w < w0 + wpb; ++w) m2 = fmaxf(m2, s_wmax[w][ir]);
     mb[0] = mb[1] = m2;
   }
+  if (p.pass == 1) {  // two-pass decode, first pass: block maxima and thresholds only
+    if (row_ok && jg == 0) write_piece_max(p, (size_t)b * p.HQ + hq, c0, cg, wv, kc, mb);
+    if (p.th_out != nullptr && cg == 0 && threadIdx.x < un.Gu) p.th_out[(size_t)b * p.HQ + un.row0 + threadIdx.x] = th;
+    return;
+  }
+  if (p.pass == 2) {  // second pass: decide from every row's maxima
+    decide_blocks(p, b, hkv, cw, Tb, s_keep);
+    lds_barrier();
+  }
   // prune iff every row of the group is below its threshold (strict <); rows >= G do not vote
 #pragma unroll
   for (int j = 0; j < kPPW; ++j) {
-    bal[j] = __ballot(row_ok && !(mb[j] < th));
+    bal[j] = chunk_ballot(p, row_ok, mb[j], th, s_keep, cw, c0 + j, kc);
     const int slot = wv * kPPW + j;
     if (lane == 0) {
       s_bal[slot][0] = (uint32_t)bal[j];
@@ -667,7 +680,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
 
   // ------------------------------------------------ phase 4: mask, threshold, workgroup partial
   __syncthreads();
-  {
+  if (un.quad == 0) {
     int8_t *mrow_ptr = p.mask + ((size_t)b * p.HKV + hkv) * p.ntbs;
     const int t = threadIdx.x;
     if (SBS <= kPage) {
@@ -687,11 +700,12 @@ void kfmt_decode_kernel(const DecodeParams p) {
       if (jb < p.ntbs) mrow_ptr[jb] = (jb < NTBS_b && kk) ? 1 : 0;
     }
   }
-  if (p.th_out != nullptr && cg == 0 && threadIdx.x < G) p.th_out[(size_t)b * p.HQ + hkv * G + threadIdx.x] = th;
+  if (p.pass == 0 && p.th_out != nullptr && cg == 0 && threadIdx.x < un.Gu)
+    p.th_out[(size_t)b * p.HQ + un.row0 + threadIdx.x] = th;  // (pass 2: written by pass 1)
   {
     const int i = wv;
     const int c2 = 2 * lane;
-    if (i < G) {
+    if (i < un.Gu) {
       // slots whose ballot is empty hold no partial: skipped by scalar branches
       uint32_t km = 0;
 #pragma unroll
@@ -713,7 +727,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
           oy = __builtin_fmaf(s_po[ps][i][c2 + 1], wgt, oy);
         }
       }
-      const size_t row = (size_t)b * p.HQ + hkv * G + i;
+      const size_t row = (size_t)b * p.HQ + un.row0 + i;
       if (lane == 0) {
         p.m_buf[row * p.nparts + cg] = A > 0.f ? M : -INFINITY;
         p.l_buf[row * p.nparts + cg] = A;
@@ -758,16 +772,37 @@ static hipError_t kfmt_dispatch_rv(const ffa::DecodeParams &p, int res, int vdt,
   return hipErrorInvalidValue;
 }
 
+// one launch of the decoder instance of a K format and scale granularity (hipErrorInvalidValue
+// for a combination without an instance)
+static hipError_t kfmt_launch_format(const ffa::DecodeParams &p, int fmt, int sk, int res, int vdt, dim3 grid,
+                                     hipStream_t st) {
+  constexpr int C = ffa::kContig, PG = ffa::kPaged;
+  if (fmt == FFA_KFMT_FP8_E4M3 && sk == FFA_KSCALE_NONE)
+    return kfmt_dispatch_rv<C, ffa::kF8E4M3, ffa::kSclNone>(p, res, vdt, grid, st);
+  if (fmt == FFA_KFMT_FP8_E4M3 && sk == FFA_KSCALE_TOKEN)
+    return kfmt_dispatch_rv<C, ffa::kF8E4M3, ffa::kSclToken>(p, res, vdt, grid, st);
+  if (fmt == FFA_KFMT_FP8_E5M2 && sk == FFA_KSCALE_NONE)
+    return kfmt_dispatch_rv<C, ffa::kF8E5M2, ffa::kSclNone>(p, res, vdt, grid, st);
+  if (fmt == FFA_KFMT_FP8_E5M2 && sk == FFA_KSCALE_TOKEN)
+    return kfmt_dispatch_rv<C, ffa::kF8E5M2, ffa::kSclToken>(p, res, vdt, grid, st);
+  if (fmt == FFA_KFMT_NVFP4 && sk == FFA_KSCALE_BLOCK)
+    return kfmt_dispatch_rv<C, ffa::kFP4, ffa::kSclBlock>(p, res, vdt, grid, st);
+  if (fmt == FFA_KFMT_NF4 && sk == FFA_KSCALE_CHANNEL)
+    return kfmt_dispatch_rv<C, ffa::kNF4, ffa::kSclChannel>(p, res, vdt, grid, st);
+  if (fmt == FFA_KFMT_NVFP4 && sk == FFA_KSCALE_G16)
+    return kfmt_dispatch_rv<PG, ffa::kFP4, ffa::kSclG16>(p, res, vdt, grid, st);
+  if (fmt == FFA_KFMT_NF4 && sk == FFA_KSCALE_G64)
+    return kfmt_dispatch_rv<PG, ffa::kNF4, ffa::kSclG64>(p, res, vdt, grid, st);
+  return hipErrorInvalidValue;
+}
+
 extern "C" int ffa_kfmt_decode(const ffa_kfmt_decode_args *a, void *stream) {
   if (!a) return ffa_set_error_internal(FFA_E_INVALID, "null args");
-  if (a->B <= 0 || a->T <= 0 || a->HQ <= 0 || a->HKV <= 0) return ffa_set_error_internal(FFA_E_INVALID, "bad dims");
-  if (a->HQ % a->HKV) return ffa_set_error_internal(FFA_E_INVALID, "HQ must be a multiple of HKV");
+  ffa::DecodeParams p = {};
+  const int rc0 = ffa_decode_shape_check(a->B, a->T, a->HQ, a->HKV, a->BS, a->SBS, a->piece_max, a->npieces,
+                                         a->threshold_in, a->threshold_out, &p);
+  if (rc0 != FFA_OK) return rc0;
   const int G = a->HQ / a->HKV;
-  if (G > 4) return ffa_set_error_internal(FFA_E_UNSUPPORTED, "GQA group size > 4 is not implemented");
-  if (a->SBS <= 0 || a->BS <= 0 || a->BS % a->SBS)
-    return ffa_set_error_internal(FFA_E_UNSUPPORTED, "BS must be a multiple of SBS");
-  if (!(a->SBS == 16 || a->SBS == 32 || a->SBS == 64 || a->SBS == 128 || a->SBS == 256))
-    return ffa_set_error_internal(FFA_E_UNSUPPORTED, "SBS must be one of 16, 32, 64, 128, 256");
   if (!(a->q_dtype >= FFA_DT_F16 && a->q_dtype <= FFA_DT_F32)) return ffa_set_error_internal(FFA_E_INVALID, "q dtype");
   if (!(a->out_dtype >= FFA_DT_F16 && a->out_dtype <= FFA_DT_F32))
     return ffa_set_error_internal(FFA_E_INVALID, "out dtype");
@@ -785,8 +820,6 @@ extern "C" int ffa_kfmt_decode(const ffa_kfmt_decode_args *a, void *stream) {
   if (a->ntbs < ntbs) return ffa_set_error_internal(FFA_E_INVALID, "mask holds too few blocks");
   const bool paged = a->layout == FFA_LAYOUT_PAGED;
   if (!paged && a->layout != FFA_LAYOUT_CONTIG) return ffa_set_error_internal(FFA_E_INVALID, "layout");
-  if (a->B > 65535 || a->HKV > 65535)
-    return ffa_set_error_internal(FFA_E_UNSUPPORTED, "B and HKV are grid dimensions (at most 65535)");
   if (paged && !a->block_table) return ffa_set_error_internal(FFA_E_INVALID, "paged layout needs a block table");
   if (paged && a->num_pages <= 0)
     return ffa_set_error_internal(FFA_E_INVALID, "paged layout needs num_pages > 0 (pages in each pool)");
@@ -796,7 +829,6 @@ extern "C" int ffa_kfmt_decode(const ffa_kfmt_decode_args *a, void *stream) {
     return ffa_set_error_internal(FFA_E_UNSUPPORTED,
                                   "the paged layout takes the per-token group scales (G16 / G64) and only it");
 
-  ffa::DecodeParams p = {};
   p.q = a->q;
   p.kq = a->k;
   p.ks = a->k_scale;
@@ -830,30 +862,18 @@ extern "C" int ffa_kfmt_decode(const ffa_kfmt_decode_args *a, void *stream) {
   p.nwg = need;
 
   hipStream_t st = (hipStream_t)stream;
-  dim3 grid(need, a->HKV, a->B);
-  hipError_t e = hipErrorInvalidValue;
-  const int fmt = a->k_format, sk = a->scale_kind;
-  constexpr int C = ffa::kContig, PG = ffa::kPaged;
-  if (fmt == FFA_KFMT_FP8_E4M3 && sk == FFA_KSCALE_NONE)
-    e = kfmt_dispatch_rv<C, ffa::kF8E4M3, ffa::kSclNone>(p, a->res_dtype, a->v_dtype, grid, st);
-  else if (fmt == FFA_KFMT_FP8_E4M3 && sk == FFA_KSCALE_TOKEN)
-    e = kfmt_dispatch_rv<C, ffa::kF8E4M3, ffa::kSclToken>(p, a->res_dtype, a->v_dtype, grid, st);
-  else if (fmt == FFA_KFMT_FP8_E5M2 && sk == FFA_KSCALE_NONE)
-    e = kfmt_dispatch_rv<C, ffa::kF8E5M2, ffa::kSclNone>(p, a->res_dtype, a->v_dtype, grid, st);
-  else if (fmt == FFA_KFMT_FP8_E5M2 && sk == FFA_KSCALE_TOKEN)
-    e = kfmt_dispatch_rv<C, ffa::kF8E5M2, ffa::kSclToken>(p, a->res_dtype, a->v_dtype, grid, st);
-  else if (fmt == FFA_KFMT_NVFP4 && sk == FFA_KSCALE_BLOCK)
-    e = kfmt_dispatch_rv<C, ffa::kFP4, ffa::kSclBlock>(p, a->res_dtype, a->v_dtype, grid, st);
-  else if (fmt == FFA_KFMT_NF4 && sk == FFA_KSCALE_CHANNEL)
-    e = kfmt_dispatch_rv<C, ffa::kNF4, ffa::kSclChannel>(p, a->res_dtype, a->v_dtype, grid, st);
-  else if (fmt == FFA_KFMT_NVFP4 && sk == FFA_KSCALE_G16)
-    e = kfmt_dispatch_rv<PG, ffa::kFP4, ffa::kSclG16>(p, a->res_dtype, a->v_dtype, grid, st);
-  else if (fmt == FFA_KFMT_NF4 && sk == FFA_KSCALE_G64)
-    e = kfmt_dispatch_rv<PG, ffa::kNF4, ffa::kSclG64>(p, a->res_dtype, a->v_dtype, grid, st);
-  else
-    return ffa_set_error_internal(FFA_E_UNSUPPORTED, "unsupported K format / scale granularity combination");
-  if (e != hipSuccess) return ffa_set_error_internal(FFA_E_LAUNCH, hipGetErrorString(e));
-  e = ffa::launch_merge(p, st);
+  const dim3 grid(need, a->HKV * p.nq, a->B);
+  // one pass (pass 0), or (G > 4, SBS > 512) the maxima pass 1 and then the deciding pass 2
+  const bool two = p.pmax != nullptr;
+  for (int pass = two ? 1 : 0; pass <= (two ? 2 : 0); ++pass) {
+    ffa::DecodeParams pp = p;
+    pp.pass = pass;
+    const hipError_t e = kfmt_launch_format(pp, a->k_format, a->scale_kind, a->res_dtype, a->v_dtype, grid, st);
+    if (e == hipErrorInvalidValue)
+      return ffa_set_error_internal(FFA_E_UNSUPPORTED, "unsupported K format / scale granularity combination");
+    if (e != hipSuccess) return ffa_set_error_internal(FFA_E_LAUNCH, hipGetErrorString(e));
+  }
+  const hipError_t e = ffa::launch_merge(p, st);
   if (e != hipSuccess) return ffa_set_error_internal(FFA_E_LAUNCH, hipGetErrorString(e));
   return FFA_OK;
 }

@@ -61,9 +61,12 @@ __global__ __launch_bounds__(256) void fp8fp8_quant_kernel(const void *k, int kd
 
 // ---------------------------------------------------------------------------
 // per-token-scaled fp8 (no reference counterpart): for each row of D values (one token and
-// KV head) s = fp16(max(amax |k|, 1e-6) / fmax) (fmax = 448 for e4m3, 57344 for e5m2),
-// base = fp8(k / s), residual = fp8(k - value(base) * s); the product is exact (at most
-// 4 x 11 significant bits).  One wave per row, lane e holds elements e, e + 64, ...
+// KV head) s = max(fp16(max(amax |k|, 1e-6) / fmax), 2^-14) (fmax = 448 for e4m3, 57344 for
+// e5m2), base = fp8(k / s), residual = fp8(k - value(base) * s); the product is exact (at most
+// 4 x 11 significant bits).  The floor (the smallest normal fp16) keeps s non-zero for all-zero
+// and tiny rows and |k / s| within fmax (1 + 2^-11), which rounds to fmax: a subnormal s could
+// sit half a quantum below amax / fmax and push k / s past fmax (NaN in e4m3).
+// One wave per row, lane e holds elements e, e + 64, ...
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void fp8_scaled_quant_kernel(const void *k, int kdt, size_t rows, int D,
                                                                uint8_t *base, uint16_t *scale, uint8_t *res,
@@ -75,7 +78,7 @@ __global__ __launch_bounds__(256) void fp8_scaled_quant_kernel(const void *k, in
   float amax = 0.f;
   for (int d = lane; d < D; d += 64) amax = fmaxf(amax, fabsf(load_any(k, r0 + d, kdt)));
   amax = wave_max(amax);
-  const float s = (float)(_Float16)__fdiv_rn(fmaxf(amax, 1e-6f), e4m3 ? 448.f : 57344.f);
+  const float s = fmaxf((float)(_Float16)__fdiv_rn(fmaxf(amax, 1e-6f), e4m3 ? 448.f : 57344.f), 0x1p-14f);
   for (int d = lane; d < D; d += 64) {
     const float x = load_any(k, r0 + d, kdt);
     const uint32_t bb = f32_to_fp8(__fdiv_rn(x, s), e4m3);

@@ -94,9 +94,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   // land on different XCDs (dispatch is round-robin over the 8 XCDs), so the residual/V traffic
   // of a (sequence, KV head) with many kept chunks is spread over every XCD's memory path.
   const int cg = blockIdx.x;  // workgroup index along the sequence = partial slot
-  const int hkv = blockIdx.y;
+  const DecodeUnit un = decode_unit(p);  // KV head and the (at most 4) query rows of this workgroup
+  const int hkv = un.hkv;
   const int b = blockIdx.z;
-  const int G = p.G;
   const int cw = cg * kChunksPerWG;  // first chunk of the workgroup
   const int c0 = cw + wv * kPPW;     // first chunk scored by this wave
   const int SBS = p.SBS;
@@ -106,14 +106,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   const int n = mrow;          // output column = (j, i)
   const int jg = n >> 2;
   const int ir = n & 3;
-  const bool row_ok = ir < G;
-  const int hq = hkv * G + (row_ok ? ir : 0);
+  const bool row_ok = ir < un.Gu;
+  const int hq = un.row0 + (row_ok ? ir : 0);
 
   __shared__ uint4 s_qr[4][64];                    // B operands of the 4 residual MFMAs (g32)
   __shared__ uint4 s_sp[kG ? 1 : 4][kG ? 1 : 64];   // channel scales: fp16 (scale, scale) pairs of 8 channels
   __shared__ uint4 s_zp2[kG ? 1 : 4][kG ? 1 : 64];  // channel scales: fp16 (zero, zero) pairs
   __shared__ float s_probe[2][4];
   __shared__ float s_wmax[kWaves][4];
+  __shared__ int s_keep[kChunksPerWG * kPage / 16];  // pass 2: block decisions of the span
   __shared__ int s_kept[kChunksPerWG];             // chunk kept (some prune block survives)
   __shared__ int s_pgid[kChunksPerWG];             // pool page of the chunk
   __shared__ uint32_t s_bal[kChunksPerWG][2];      // survivor ballot of the chunk
@@ -144,9 +145,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   // every element of the operand this wave builds.
   const int Tb = p.seq_lens ? min(max(p.seq_lens[b], 0), p.T) : p.T;  // lengths beyond T are clamped to T
   if (cg > 0 && cw * kPage >= Tb) {  // every token past the sequence end: mask bytes only
-    write_empty_mask(p.mask + ((size_t)b * p.HKV + hkv) * p.ntbs, cg, SBS, p.ntbs);
+    if (p.pass != 1 && un.quad == 0) write_empty_mask(p.mask + ((size_t)b * p.HKV + hkv) * p.ntbs, cg, SBS, p.ntbs);
     return;
   }
+  if (threadIdx.x < kChunksPerWG * kPage / 16) s_keep[threadIdx.x] = 0;
   const int NTB = (Tb + p.BS - 1) / p.BS;
   const int NTBS_b = NTB * (p.BS / p.SBS);
   const bool do_probe = (p.th_in == nullptr) && wv < 2;
@@ -439,15 +441,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     th = row_ok ? fmaxf(s_probe[0][ir], s_probe[1][ir]) - p.delta : INFINITY;
   }
   if (SBS > 128) {
-    const int wpb = SBS / (kPage * kPPW);
+    const int wpb = min(SBS / (kPage * kPPW), kWaves);  // waves per block (a block of several spans: all)
     const int w0 = (wv / wpb) * wpb;
     float m2 = -INFINITY;
     for (int w = w0; w < w0 + wpb; ++w) m2 = fmaxf(m2, s_wmax[w][ir]);
     mb[0] = mb[1] = m2;
   }
+  if (p.pass == 1) {  // two-pass decode, first pass: block maxima and thresholds only
+    if (row_ok && jg == 0) write_piece_max(p, (size_t)b * p.HQ + hq, c0, cg, wv, kc, mb);
+    if (p.th_out != nullptr && cg == 0 && threadIdx.x < un.Gu) p.th_out[(size_t)b * p.HQ + un.row0 + threadIdx.x] = th;
+    return;
+  }
+  if (p.pass == 2) {  // second pass: decide from every row's maxima
+    decide_blocks(p, b, hkv, cw, Tb, s_keep);
+    lds_barrier();
+  }
   // prune iff every row of the group is below its threshold (strict <); rows >= G do not vote
 #pragma unroll
-  for (int j = 0; j < kPPW; ++j) bal[j] = __ballot(row_ok && !(mb[j] < th));
+  for (int j = 0; j < kPPW; ++j) bal[j] = chunk_ballot(p, row_ok, mb[j], th, s_keep, cw, c0 + j, kc);
 
   // publish the kept chunks: coarse scores (g32) or codes (channel scales), page, ballot
 #pragma unroll
@@ -733,7 +744,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   // Global stores come last: on gfx9 stores share the vector memory counter with loads, and a
   // pending store would make every later load wait a full write round trip.
   __syncthreads();
-  {
+  if (un.quad == 0) {
     // survivor mask, one byte per prune block (attn_kernel...q2fp8.py:99-104)
     int8_t *mrow_ptr = p.mask + ((size_t)b * p.HKV + hkv) * p.ntbs;
     const int t = threadIdx.x;
@@ -754,11 +765,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
       if (jb < p.ntbs) mrow_ptr[jb] = (jb < NTBS_b && kk) ? 1 : 0;
     }
   }
-  if (p.th_out != nullptr && cg == 0 && threadIdx.x < G) p.th_out[(size_t)b * p.HQ + hkv * G + threadIdx.x] = th;
+  if (p.pass == 0 && p.th_out != nullptr && cg == 0 && threadIdx.x < un.Gu)
+    p.th_out[(size_t)b * p.HQ + un.row0 + threadIdx.x] = th;  // (pass 2: written by pass 1)
   {
     const int i = wv;         // query row handled by this wave
     const int c2 = 2 * lane;  // columns c2, c2 + 1
-    if (i < G) {
+    if (i < un.Gu) {
       // only kept chunks hold partials (km, uniform): the others are skipped by scalar branches
       float M = -INFINITY;
 #pragma unroll
@@ -776,7 +788,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
           oy = __builtin_fmaf(s_po[ps][i][c2 + 1], wgt, oy);
         }
       }
-      const size_t row = (size_t)b * p.HQ + hkv * G + i;
+      const size_t row = (size_t)b * p.HQ + un.row0 + i;
       if (lane == 0) {
         p.m_buf[row * p.nparts + cg] = A > 0.f ? M : -INFINITY;
         p.l_buf[row * p.nparts + cg] = A;
@@ -917,6 +929,45 @@ extern "C" int ffa_q2fp8_decode_nparts(int T, int BS, int SBS) {
   return (int)((tokens + ffa::kChunksPerWG * ffa::kPage - 1) / (ffa::kChunksPerWG * ffa::kPage));
 }
 
+extern "C" int ffa_q2fp8_decode_pieces(int HQ, int HKV, int T, int BS, int SBS) {
+  if (HQ <= 0 || HKV <= 0 || HQ % HKV || T <= 0 || BS <= 0 || SBS <= 0 || BS % SBS) return 0;
+  const int G = HQ / HKV;
+  const int span = ffa::kChunksPerWG * ffa::kPage;
+  if (G <= 4 && SBS <= span) return 0;  // one pass
+  if (SBS > span) return ffa_q2fp8_decode_nparts(T, BS, SBS);
+  return (int)(((long)T + BS - 1) / BS * (BS / SBS));
+}
+
+// Shared validation of the decode shape (both the q2 and the other-format decoders): group size,
+// block sizes, two-pass scratch and grid limits; fills the two-pass fields of p.
+extern "C" __attribute__((visibility("hidden"))) int ffa_decode_shape_check(int B, int T, int HQ, int HKV, int BS,
+                                                                           int SBS, float *piece_max, int npieces,
+                                                                           const float *th_in, const float *th_out,
+                                                                           ffa::DecodeParams *p) {
+  if (B <= 0 || T <= 0 || HQ <= 0 || HKV <= 0) return set_err(FFA_E_INVALID, "bad dims");
+  if (HQ % HKV) return set_err(FFA_E_INVALID, "HQ must be a multiple of HKV");
+  const int G = HQ / HKV;
+  if (G > 16) return set_err(FFA_E_UNSUPPORTED, "GQA group size > 16 is not implemented (the reference's row tile is 16)");
+  if (SBS < 16 || (SBS & (SBS - 1)) != 0) return set_err(FFA_E_UNSUPPORTED, "SBS must be a power of two >= 16");
+  if (BS <= 0 || BS % SBS) return set_err(FFA_E_UNSUPPORTED, "BS must be a multiple of SBS");
+  const int nq = (G + 3) / 4;
+  if (B > 65535 || (long)HKV * nq > 65535)
+    return set_err(FFA_E_UNSUPPORTED, "B and HKV * ceil(G / 4) are grid dimensions (at most 65535)");
+  const int need = ffa_q2fp8_decode_pieces(HQ, HKV, T, BS, SBS);
+  if (need > 0) {
+    if (!piece_max || npieces < need)
+      return set_err(FFA_E_INVALID, "a decode with G > 4 or SBS > 512 runs in two passes and needs piece_max "
+                                    "scratch [B, HQ, npieces >= ffa_q2fp8_decode_pieces()]");
+    if (!th_in && !th_out)
+      return set_err(FFA_E_INVALID, "a two-pass decode (G > 4 or SBS > 512) needs threshold_out (or threshold_in)");
+  }
+  p->nq = nq;
+  p->pass = 0;
+  p->pmax = need > 0 ? piece_max : nullptr;
+  p->npieces = need > 0 ? npieces : 0;
+  return FFA_OK;
+}
+
 namespace ffa {
 int device_cus() {
   static int cache[64] = {0};
@@ -964,20 +1015,17 @@ static hipError_t dispatch_rv(const ffa::DecodeParams &p, int res, int vdt, dim3
 // Validates the arguments and fills the kernel parameters; returns FFA_OK or an error code.
 static int decode_params(const ffa_q2fp8_decode_args *a, ffa::DecodeParams &p) {
   if (!a) return set_err(FFA_E_INVALID, "null args");
-  if (a->B <= 0 || a->T <= 0 || a->HQ <= 0 || a->HKV <= 0) return set_err(FFA_E_INVALID, "bad dims");
-  if (a->HQ % a->HKV) return set_err(FFA_E_INVALID, "HQ must be a multiple of HKV");
+  p = ffa::DecodeParams{};
+  const int rc0 = ffa_decode_shape_check(a->B, a->T, a->HQ, a->HKV, a->BS, a->SBS, a->piece_max, a->npieces,
+                                         a->threshold_in, a->threshold_out, &p);
+  if (rc0 != FFA_OK) return rc0;
   const int G = a->HQ / a->HKV;
-  if (G > 4) return set_err(FFA_E_UNSUPPORTED, "GQA group size > 4 is not implemented");
-  if (a->SBS <= 0 || a->BS <= 0 || a->BS % a->SBS) return set_err(FFA_E_UNSUPPORTED, "BS must be a multiple of SBS");
-  if (!(a->SBS == 16 || a->SBS == 32 || a->SBS == 64 || a->SBS == 128 || a->SBS == 256))
-    return set_err(FFA_E_UNSUPPORTED, "SBS must be one of 16, 32, 64, 128, 256");
   if (!(a->q_dtype >= FFA_DT_F16 && a->q_dtype <= FFA_DT_F32)) return set_err(FFA_E_INVALID, "q dtype");
   if (!(a->out_dtype >= FFA_DT_F16 && a->out_dtype <= FFA_DT_F32)) return set_err(FFA_E_INVALID, "out dtype");
   if (!(a->v_dtype == FFA_DT_F16 || a->v_dtype == FFA_DT_BF16)) return set_err(FFA_E_INVALID, "v dtype");
   if (!(a->res_dtype == FFA_DT_FP8_E4M3 || a->res_dtype == FFA_DT_FP8_E5M2 || a->res_dtype == FFA_DT_NONE))
     return set_err(FFA_E_INVALID, "residual dtype");
   if (a->res_dtype != FFA_DT_NONE && !a->k_residual) return set_err(FFA_E_INVALID, "residual pointer is null");
-  if (a->B > 65535 || a->HKV > 65535) return set_err(FFA_E_UNSUPPORTED, "B and HKV are grid dimensions (at most 65535)");
   if (a->layout == FFA_LAYOUT_PAGED && !a->block_table) return set_err(FFA_E_INVALID, "paged layout needs a block table");
   if (a->layout == FFA_LAYOUT_PAGED && a->num_pages <= 0)
     return set_err(FFA_E_INVALID, "paged layout needs num_pages > 0 (pages in each pool)");
@@ -1027,18 +1075,24 @@ static int decode_params(const ffa_q2fp8_decode_args *a, ffa::DecodeParams &p) {
   return FFA_OK;
 }
 
-static int launch_stage1(const ffa_q2fp8_decode_args *a, const ffa::DecodeParams &p, hipStream_t st) {
-  dim3 grid(p.nwg, a->HKV, a->B);
-  hipError_t e;
-  if (a->layout == FFA_LAYOUT_PAGED) {
-    if (a->scale_mode == FFA_SCALE_G32)
-      e = dispatch_rv<ffa::kPaged, ffa::kG32>(p, a->res_dtype, a->v_dtype, grid, st);
-    else
-      e = dispatch_rv<ffa::kPaged, ffa::kChannel>(p, a->res_dtype, a->v_dtype, grid, st);
-  } else {
-    e = dispatch_rv<ffa::kContig, ffa::kChannel>(p, a->res_dtype, a->v_dtype, grid, st);
+static int launch_stage1(const ffa_q2fp8_decode_args *a, const ffa::DecodeParams &p0, hipStream_t st) {
+  dim3 grid(p0.nwg, a->HKV * p0.nq, a->B);
+  // one pass (pass 0), or (G > 4, SBS > 512) the maxima pass 1 and then the deciding pass 2
+  const bool two = p0.pmax != nullptr;
+  for (int pass = two ? 1 : 0; pass <= (two ? 2 : 0); ++pass) {
+    ffa::DecodeParams p = p0;
+    p.pass = pass;
+    hipError_t e;
+    if (a->layout == FFA_LAYOUT_PAGED) {
+      if (a->scale_mode == FFA_SCALE_G32)
+        e = dispatch_rv<ffa::kPaged, ffa::kG32>(p, a->res_dtype, a->v_dtype, grid, st);
+      else
+        e = dispatch_rv<ffa::kPaged, ffa::kChannel>(p, a->res_dtype, a->v_dtype, grid, st);
+    } else {
+      e = dispatch_rv<ffa::kContig, ffa::kChannel>(p, a->res_dtype, a->v_dtype, grid, st);
+    }
+    if (e != hipSuccess) return set_err(FFA_E_LAUNCH, hipGetErrorString(e));
   }
-  if (e != hipSuccess) return set_err(FFA_E_LAUNCH, hipGetErrorString(e));
   return FFA_OK;
 }
 
@@ -1068,3 +1122,4 @@ extern "C" int ffa_q2fp8_decode(const ffa_q2fp8_decode_args *a, void *stream) {
   rc = launch_stage1(a, p, (hipStream_t)stream);
   return rc != FFA_OK ? rc : launch_stage2(a, p, (hipStream_t)stream);
 }
+

@@ -6,7 +6,7 @@ Same names and signatures:
   encode_k_nf4_fp8_residual                        (:72-96)   -> HIP quantizer, bit-exact
   kproj_rope_nf4_reference                         (:415-437) -> torch GEMM + RoPE, HIP quantizer
   kproj_rope_nf4_triton / kproj_rope_nf4_fused     (:440-580) -> HIP GEMM + RoPE kernel, HIP quantizer
-  run_smoke_test, parse_args, main                 (:583-677)
+  run_smoke_test, parse_args, main  (entry names of :583-677; the check is ffa_mi355x.producer_check)
 The fused producer quantizes the rotated K with the torch path's rules (the reference's
 two Triton kernels round their own way); its scale has the dtype of h, as in the reference.
 """
@@ -20,6 +20,7 @@ import torch.nn.functional as F
 
 sys.path.insert(0, str(Path(__file__).resolve().parents[1]))  # ffa-speedtest_amd/
 from ffa_mi355x import kfmt_quant as _KQ  # noqa: E402
+from ffa_mi355x import producer_check as _check  # noqa: E402
 from ffa_mi355x.quant import _normalize_k_weight  # noqa: E402,F401
 from ffa_mi355x.rope import apply_rope, build_rope_cache, rotate_half  # noqa: E402,F401
 
@@ -141,48 +142,19 @@ def kproj_rope_nf4_fused(
                                  bias=bias, fp8_dtype=fp8_dtype)
 
 
-def run_smoke_test(device, dtype, fp8_dtype, B, T, H, HKV, K) -> None:
-    """Same check and tolerances as the reference smoke test (:583-638)."""
-    torch.manual_seed(0)
-    h = torch.randn(B, T, H, device=device, dtype=dtype)
-    w_k = torch.randn(HKV * K, H, device=device, dtype=dtype)
-    cos, sin = build_rope_cache(T, K, device=device, dtype=dtype)
-    k_nf4_ref, scale_ref, k_res_ref = kproj_rope_nf4_reference(h=h, w_k=w_k, cos=cos, sin=sin, num_kv_heads=HKV,
-                                                               head_dim=K, fp8_dtype=fp8_dtype)
-    k_nf4_fused, scale_fused, k_res_fused = kproj_rope_nf4_triton(h=h, w_k=w_k, cos=cos, sin=sin, num_kv_heads=HKV,
-                                                                  head_dim=K, fp8_dtype=fp8_dtype)
-    packed_mismatch = (k_nf4_ref != k_nf4_fused).float().mean().item()
-    scale_max = (scale_ref.float() - scale_fused.float()).abs().max().item()
-    res_mean = (k_res_ref.float() - k_res_fused.float()).abs().mean().item()
-    if packed_mismatch > 0.01 or scale_max > 0.05 or res_mean > 0.05:
-        raise AssertionError(
-            "fused output mismatch: "
-            f"packed_mismatch={packed_mismatch:.6f}, scale_max={scale_max:.6f}, res_mean={res_mean:.6f}")
-    print(f"[OK] fused output matches reference within tolerances (packed_mismatch={packed_mismatch:.6f}, "
-          f"scale_max={scale_max:.6f}, res_mean={res_mean:.6f})")
-    print(f"device={device}, dtype={dtype}, fp8_dtype={fp8_dtype}, B={B}, T={T}, H={H}, HKV={HKV}, K={K}")
+def run_smoke_test(device, dtype, fp8_dtype, B, T, H, HKV, K, seed=0) -> None:
+    """Torch producer against the fused HIP producer on one seeded case (ffa_mi355x.producer_check)."""
+    _check.run("nf4fp8 producer", kproj_rope_nf4_reference, kproj_rope_nf4_triton, ("codes", "scale", "residual"),
+               device, dtype, fp8_dtype, B, T, H, HKV, K, seed=seed)
 
 
-def parse_args() -> argparse.Namespace:
-    p = argparse.ArgumentParser(description="Fuse K projection + RoPE + nf4/fp8 split and test.")
-    p.add_argument("--device", type=str, default="cuda" if torch.cuda.is_available() else "cpu")
-    p.add_argument("--dtype", type=str, default="fp16", choices=["fp16", "bf16", "fp32"])
-    p.add_argument("--B", type=int, default=2)
-    p.add_argument("--T", type=int, default=32)
-    p.add_argument("--H", type=int, default=256)
-    p.add_argument("--HKV", type=int, default=4)
-    p.add_argument("--K", type=int, default=64)
-    return p.parse_args()
+def parse_args(argv=None) -> argparse.Namespace:
+    return _check.parse("nf4fp8 producer", argv)
 
 
-def main() -> None:
-    args = parse_args()
-    dtype = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[args.dtype]
-    device = torch.device(args.device)
-    if device.type == "cpu":
-        raise RuntimeError("This test requires a GPU device.")
-    run_smoke_test(device=device, dtype=dtype, fp8_dtype=_resolve_fp8_dtype(device), B=args.B, T=args.T, H=args.H,
-                   HKV=args.HKV, K=args.K)
+def main(argv=None) -> None:
+    ns = parse_args(argv)
+    _check.main_for("nf4fp8 producer", lambda *a: run_smoke_test(*a, seed=ns.seed), ns)
 
 
 if __name__ == "__main__":

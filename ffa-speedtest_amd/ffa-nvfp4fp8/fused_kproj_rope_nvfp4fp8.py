@@ -5,7 +5,7 @@ Same names and signatures:
   encode_k_nvfp4_fp8_residual                      (:62-114)  -> HIP quantizer, bit-exact
   kproj_rope_quantize_reference                    (:117-140) -> torch GEMM + RoPE, HIP quantizer
   kproj_rope_quantize_triton / _fused              (:143-190) -> HIP GEMM + RoPE kernel, HIP quantizer
-  run_smoke_test, parse_args, main                 (:193-290)
+  run_smoke_test, parse_args, main  (entry names of :193-290; the check is ffa_mi355x.producer_check)
 The reference's "triton" producer is a placeholder that calls its torch path; here it is
 a real fused kernel, so the two producers agree to the GEMM's last bit, not bitwise.
 """
@@ -19,6 +19,7 @@ import torch.nn.functional as F
 
 sys.path.insert(0, str(Path(__file__).resolve().parents[1]))  # ffa-speedtest_amd/
 from ffa_mi355x import kfmt_quant as _KQ  # noqa: E402
+from ffa_mi355x import producer_check as _check  # noqa: E402
 from ffa_mi355x.quant import _normalize_k_weight  # noqa: E402,F401
 from ffa_mi355x.rope import apply_rope, build_rope_cache, rotate_half  # noqa: E402,F401
 
@@ -99,52 +100,20 @@ def kproj_rope_quantize_fused(
                                       head_dim=head_dim, page_size=page_size, bias=bias, fp8_dtype=fp8_dtype)
 
 
-def run_smoke_test(device, dtype, fp8_dtype, B, T, H, HKV, K, page_size) -> None:
-    """Torch-GEMM producer vs the fused HIP producer.  The quantizer is bit-exact on the same K;
-    the two GEMMs may differ in the last bit, so a few codes may flip (the nf4 reference's
-    smoke tolerances, ffa-nf4fp8/fused_kproj_rope_nf4fp8.py:620-628)."""
-    torch.manual_seed(0)
-    h = torch.randn(B, T, H, device=device, dtype=dtype)
-    w_k = torch.randn(HKV * K, H, device=device, dtype=dtype)
-    cos, sin = build_rope_cache(T, K, device=device, dtype=dtype)
-    k_fp4_ref, k_scale_ref, k_res_ref = kproj_rope_quantize_reference(
-        h=h, w_k=w_k, cos=cos, sin=sin, num_kv_heads=HKV, head_dim=K, page_size=page_size, fp8_dtype=fp8_dtype)
-    k_fp4_fused, k_scale_fused, k_res_fused = kproj_rope_quantize_triton(
-        h=h, w_k=w_k, cos=cos, sin=sin, num_kv_heads=HKV, head_dim=K, page_size=page_size, fp8_dtype=fp8_dtype)
-    packed_mismatch = (k_fp4_ref != k_fp4_fused).float().mean().item()
-    scale_max = (k_scale_ref.float() - k_scale_fused.float()).abs().max().item()
-    res_mean = (k_res_ref.float() - k_res_fused.float()).abs().mean().item()
-    if packed_mismatch > 0.01 or scale_max > 0.05 or res_mean > 0.05:
-        raise AssertionError(
-            "fused output mismatch: "
-            f"packed_mismatch={packed_mismatch:.6f}, scale_max={scale_max:.6f}, res_mean={res_mean:.6f}")
-    print(f"[OK] nvfp4 base/scale/residual outputs match reference (packed_mismatch={packed_mismatch:.6f}, "
-          f"scale_max={scale_max:.6f}, res_mean={res_mean:.6f})")
-    print(f"device={device}, dtype={dtype}, fp8_dtype={fp8_dtype}, B={B}, T={T}, H={H}, HKV={HKV}, K={K}, "
-          f"page_size={page_size}")
+def run_smoke_test(device, dtype, fp8_dtype, B, T, H, HKV, K, page_size, seed=0) -> None:
+    """Torch producer against the fused HIP producer on one seeded case (ffa_mi355x.producer_check)."""
+    _check.run("nvfp4fp8 producer", kproj_rope_quantize_reference, kproj_rope_quantize_triton,
+               ("codes", "scale", "residual"), device, dtype, fp8_dtype, B, T, H, HKV, K, seed=seed,
+               page_size=page_size)
 
 
-def parse_args() -> argparse.Namespace:
-    p = argparse.ArgumentParser(description="Fuse K projection + RoPE + nvfp4/fp8 split and test.")
-    p.add_argument("--device", type=str, default="cuda" if torch.cuda.is_available() else "cpu")
-    p.add_argument("--dtype", type=str, default="fp16", choices=["fp16", "bf16", "fp32"])
-    p.add_argument("--B", type=int, default=2)
-    p.add_argument("--T", type=int, default=32)
-    p.add_argument("--H", type=int, default=256)
-    p.add_argument("--HKV", type=int, default=4)
-    p.add_argument("--K", type=int, default=64)
-    p.add_argument("--page-size", type=int, default=128)
-    return p.parse_args()
+def parse_args(argv=None) -> argparse.Namespace:
+    return _check.parse("nvfp4fp8 producer", argv, page_size=True)
 
 
-def main() -> None:
-    args = parse_args()
-    dtype = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[args.dtype]
-    device = torch.device(args.device)
-    if device.type == "cpu":
-        raise RuntimeError("This test requires a CUDA device for fp8 storage.")
-    run_smoke_test(device=device, dtype=dtype, fp8_dtype=_resolve_fp8_dtype(device), B=args.B, T=args.T, H=args.H,
-                   HKV=args.HKV, K=args.K, page_size=args.page_size)
+def main(argv=None) -> None:
+    ns = parse_args(argv)
+    _check.main_for("nvfp4fp8 producer", lambda *a, **kw: run_smoke_test(*a, seed=ns.seed, **kw), ns)
 
 
 if __name__ == "__main__":

@@ -12,8 +12,10 @@ Extensions, all through **kwargs (reference :206):
   block_table=[B, npages] int32  -> paged cache (ffa_mi355x.paged layout): k_q,
                                     k_scale, k_zero, k_residual and v are the page
                                     pools; k_scale/k_zero [P,HKV,4,64] fp16 (g32).
-  seq_lens=[B] int32             -> ragged lengths (paged cache only).
-  T=int                          -> max length for paged calls without seq_lens.
+  seq_lens=[B] int32             -> ragged lengths.
+  T=int                          -> longest length a paged call may see; default the block
+                                    table's capacity, block_table.shape[1] * 64 (lengths past
+                                    T are clamped to T).
 """
 import math
 import sys
@@ -50,7 +52,7 @@ def allocate_q2fp8_decode_workspace(q, k_q, v, BS: int = 128, SBS=None, **kwargs
     if kwargs.get("block_table") is not None:
         HKV = k_q.shape[1]
         V = v.shape[2]
-        T = kwargs.get("T") or int(kwargs["block_table"].shape[1]) * 64
+        T = _paged_T(kwargs["block_table"], kwargs.get("T"))
         if Tq != 1:
             raise ValueError("K/V layouts must be [B, T, HKV, D]")
     else:
@@ -59,6 +61,33 @@ def allocate_q2fp8_decode_workspace(q, k_q, v, BS: int = 128, SBS=None, **kwargs
         if B != Bk or B != Bv or Tq != 1 or T != Tv or HKV != HKVv:
             raise ValueError("K/V layouts must be [B, T, HKV, D]")
     return Q2FP8DecodeWorkspace(B, HQ, HKV, V, T, BS, SBS, q.device, q.dtype)
+
+
+def _paged_T(block_table: torch.Tensor, T=None) -> int:
+    """Longest length of a paged call: the caller's T, else the block table's capacity (no host sync,
+    and the same value for a workspace allocated ahead and for the calls that use it)."""
+    return int(T) if T is not None else int(block_table.shape[1]) * 64
+
+
+def _check_paged_pools(q, k_q, k_scale, k_zero, v, k_residual, g32: bool) -> None:
+    """Shapes and dtypes of the page pools (ffa_mi355x.paged): k_q [P, HKV, 4, 64, 8] u8, g32
+    k_scale / k_zero [P, HKV, 4, 64] fp16 (or per-channel [B, HKV, 128]), k_residual
+    [P, HKV, 64, 128] fp8, v [P, HKV, 128, 64] (V^T pages)."""
+    assert q.is_contiguous() and k_q.is_contiguous() and v.is_contiguous(), "paged pools and q must be contiguous"
+    if k_q.ndim != 5 or tuple(k_q.shape[2:]) != (4, 64, 8) or k_q.dtype != torch.uint8:
+        raise ValueError(f"paged k_q must be [P, HKV, 4, 64, 8] uint8, got {tuple(k_q.shape)} {k_q.dtype}")
+    P, HKV = k_q.shape[:2]
+    if v.ndim != 4 or v.shape[1] != HKV or tuple(v.shape[2:]) != (128, 64):
+        raise ValueError(f"paged v must be [P, HKV, 128, 64] (V^T pages), got {tuple(v.shape)}")
+    if g32:
+        for name, t in (("k_scale", k_scale), ("k_zero", k_zero)):
+            if t.ndim != 4 or t.shape[1] != HKV or tuple(t.shape[2:]) != (4, 64) or t.dtype != torch.float16:
+                raise ValueError(f"paged g32 {name} must be [P, HKV, 4, 64] float16, got {tuple(t.shape)} {t.dtype}")
+            assert t.is_contiguous(), f"{name} must be contiguous"
+    if k_residual is not None:
+        if k_residual.ndim != 4 or k_residual.shape[1] != HKV or tuple(k_residual.shape[2:]) != (64, 128):
+            raise ValueError(f"paged k_residual must be [P, HKV, 64, 128], got {tuple(k_residual.shape)}")
+        assert k_residual.is_contiguous(), "k_residual must be contiguous"
 
 
 def _normalize_scale_zero(k_scale: torch.Tensor, k_zero: torch.Tensor, expect_shape):
@@ -139,15 +168,16 @@ def attn_forward_decode_quantized(
             seq_lens = seq_lens.to(device=q.device, dtype=torch.int32).contiguous()
         layout, smode = _N.LAYOUT_CONTIG, _N.SCALE_CHANNEL
     else:
+        smode = _N.SCALE_G32 if k_scale.ndim == 4 else _N.SCALE_CHANNEL
+        _check_paged_pools(q, k_q, k_scale, k_zero, v, k_residual if use_res else None, smode == _N.SCALE_G32)
         HKV = k_q.shape[1]
+        if smode == _N.SCALE_CHANNEL:
+            k_scale, k_zero = _normalize_scale_zero(k_scale, k_zero, (B, HKV, K))
         block_table = block_table.to(device=q.device, dtype=torch.int32).contiguous()
         if seq_lens is not None:
             seq_lens = seq_lens.to(device=q.device, dtype=torch.int32).contiguous()
-        T = kwargs.get("T")
-        if T is None:
-            T = int(seq_lens.max().item()) if seq_lens is not None else block_table.shape[1] * 64
+        T = _paged_T(block_table, kwargs.get("T"))
         layout = _N.LAYOUT_PAGED
-        smode = _N.SCALE_G32 if k_scale.ndim == 4 else _N.SCALE_CHANNEL
     if precomputed_threshold is not None:
         assert precomputed_threshold.is_cuda and precomputed_threshold.shape == (B, HQ)
 

@@ -83,10 +83,11 @@ class CUDAGraphDecodeRunnerQ2FP8:
         for name in ("block_table", "seq_lens"):
             if kwargs.get(name) is not None:
                 self._kw[name] = _static_copy(kwargs[name].to(device=dev, dtype=torch.int32), dev)
+        # The captured grid and scratch are sized for T: the caller's, else the block table's
+        # capacity, so replays may grow seq_lens up to the table's end (a decode loop appends a
+        # token per step); lengths past T would be clamped to T.
         if kwargs.get("T") is not None:
             self._kw["T"] = int(kwargs["T"])
-        elif "seq_lens" in self._kw:
-            self._kw["T"] = int(self._kw["seq_lens"].max().item())  # fixed for the captured shape
         elif "block_table" in self._kw:
             self._kw["T"] = int(self._kw["block_table"].shape[1]) * 64
 

@@ -22,6 +22,7 @@ KSCALE_NONE, KSCALE_TOKEN, KSCALE_BLOCK, KSCALE_CHANNEL, KSCALE_G16, KSCALE_G64 
 
 EXPORTS = (
     "ffa_q2fp8_decode_nparts",
+    "ffa_q2fp8_decode_pieces",
     "ffa_q2fp8_decode",
     "ffa_q2fp8_decode_stage1",
     "ffa_q2fp8_decode_stage2",
@@ -95,6 +96,8 @@ class DecodeArgs(ctypes.Structure):
         ("mask", ctypes.c_void_p),
         ("ntbs", ctypes.c_int),
         ("num_pages", ctypes.c_int),
+        ("piece_max", ctypes.c_void_p),
+        ("npieces", ctypes.c_int),
     ]
 
 
@@ -134,6 +137,8 @@ class KfmtArgs(ctypes.Structure):
         ("block_table", ctypes.c_void_p),
         ("bt_stride", ctypes.c_int),
         ("num_pages", ctypes.c_int),
+        ("piece_max", ctypes.c_void_p),
+        ("npieces", ctypes.c_int),
     ]
 
 
@@ -159,6 +164,8 @@ def lib() -> ctypes.CDLL:
         L.ffa_last_error.restype = ctypes.c_char_p
         L.ffa_version.restype = ctypes.c_char_p
         L.ffa_q2fp8_decode_nparts.argtypes = [ci, ci, ci]
+        L.ffa_q2fp8_decode_pieces.argtypes = [ci, ci, ci, ci, ci]
+        L.ffa_q2fp8_decode_pieces.restype = ci
         L.ffa_q2fp8_decode_nparts.restype = ci
         for name in ("ffa_q2fp8_decode", "ffa_q2fp8_decode_stage1", "ffa_q2fp8_decode_stage2"):
             getattr(L, name).argtypes = [ctypes.POINTER(DecodeArgs), vp]

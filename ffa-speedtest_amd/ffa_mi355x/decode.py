@@ -31,13 +31,20 @@ def decode_ntbs(T: int, BS: int, SBS: int) -> int:
     return _cdiv(T, BS) * _cdiv(BS, SBS)
 
 
+def decode_pieces(HQ: int, HKV: int, T: int, BS: int, SBS: int) -> int:
+    """Per-row slots of the two-pass scratch (GQA groups above 4 rows or SBS > 512), else 0."""
+    return int(N.lib().ffa_q2fp8_decode_pieces(int(HQ), int(HKV), int(T), int(BS), int(SBS)))
+
+
 class DecodeWorkspace:
     """Caller-owned scratch of one decode shape (graph-capture friendly).
 
     Mirrors Q2FP8DecodeWorkspace (ffa-q2fp8-h100/attn_kernel/attn_kernel_v1210_fused_bsz_q2fp8.py:232-257):
     o, m_buf, l_buf, o_buf, mask_buf, threshold_buf.  Partials are kept per
     512-token span (m_buf/l_buf [B, HQ, nparts], o_buf [B, HQ, nparts, 128]),
-    mask_buf holds one byte per prune block [B, HKV, NTBS].
+    mask_buf holds one byte per prune block [B, HKV, NTBS].  GQA groups of more
+    than 4 query rows and prune blocks longer than 512 tokens decode in two
+    passes and add piece_max [B, HQ, npieces] (the first pass's block maxima).
     """
 
     def __init__(self, B, HQ, HKV, T, BS, SBS, device, dtype):
@@ -54,6 +61,9 @@ class DecodeWorkspace:
         self.o_buf = torch.empty((B, HQ, self.nparts, HEAD_DIM), device=device, dtype=torch.float32)
         self.mask_buf = torch.empty((B, HKV, self.NTBS), device=device, dtype=torch.int8)
         self.threshold_buf = torch.empty((B, HQ), device=device, dtype=torch.float32)
+        self.npieces = decode_pieces(HQ, HKV, T, BS, SBS)
+        self.piece_max = (torch.empty((B, HQ, self.npieces), device=device, dtype=torch.float32)
+                          if self.npieces else None)
 
     def matches(self, B, HQ, HKV, T, BS, SBS, device, dtype) -> bool:
         return (
@@ -62,6 +72,7 @@ class DecodeWorkspace:
             and self.HKV == int(HKV)
             and self.nparts >= decode_nparts(T, BS, SBS)
             and self.NTBS == decode_ntbs(T, BS, SBS)
+            and self.npieces >= decode_pieces(HQ, HKV, T, BS, SBS)
             and self.device == torch.device(device)
             and self.dtype == dtype
         )
@@ -75,7 +86,23 @@ def _res_code(k_residual, use_res: bool) -> int:
     raise ValueError(f"k_residual must be float8_e4m3fn or float8_e5m2, got {k_residual.dtype}")
 
 
-def run_decode(
+def run_decode(*, workspace: DecodeWorkspace | None = None, stage: str = "both", **kw) -> DecodeWorkspace:
+    """Launch one decode step; returns the workspace holding o / mask / thresholds.
+
+    stage: "both" (stage 1 + stage 2), or "stage1" / "stage2" alone, the two launches of
+    attn_forward_decode_quantized (attn_kernel...q2fp8.py:283-304).  Keyword arguments as
+    decode_args.
+    """
+    if stage not in _STAGE_FN:
+        raise ValueError(f"stage must be one of {sorted(_STAGE_FN)}")
+    a, workspace = decode_args(workspace=workspace, **kw)
+    fn = _STAGE_FN[stage]
+    rc = getattr(N.lib(), fn)(ctypes.byref(a), ctypes.c_void_p(N.stream_of(kw["q"].device)))
+    N.check(rc, fn)
+    return workspace
+
+
+def decode_args(
     *,
     q: torch.Tensor,  # [B, HQ, 128]
     k_q: torch.Tensor,
@@ -96,15 +123,9 @@ def run_decode(
     block_table=None,
     seq_lens=None,
     workspace: DecodeWorkspace | None = None,
-    stage: str = "both",
-) -> DecodeWorkspace:
-    """Launch one decode step; returns the workspace holding o / mask / thresholds.
-
-    stage: "both" (stage 1 + stage 2), or "stage1" / "stage2" alone, the two launches of
-    attn_forward_decode_quantized (attn_kernel...q2fp8.py:283-304).
-    """
-    if stage not in _STAGE_FN:
-        raise ValueError(f"stage must be one of {sorted(_STAGE_FN)}")
+):
+    """Validate one decode step and fill its C argument struct; returns (args, workspace).  The
+    struct holds raw pointers of the tensors passed in: keep them alive until the call."""
     B, HQ, D = q.shape
     if D != HEAD_DIM:
         raise NotImplementedError(f"head_dim {D} is not supported (this build implements {HEAD_DIM})")
@@ -150,10 +171,10 @@ def run_decode(
     a.nparts = workspace.nparts
     a.mask = workspace.mask_buf.data_ptr()
     a.ntbs = workspace.NTBS
-    fn = _STAGE_FN[stage]
-    rc = getattr(N.lib(), fn)(ctypes.byref(a), ctypes.c_void_p(N.stream_of(q.device)))
-    N.check(rc, fn)
-    return workspace
+    a.piece_max = workspace.piece_max.data_ptr() if workspace.piece_max is not None else None
+    a.npieces = workspace.npieces
+    a._keep = th_in  # the converted threshold must outlive the call
+    return a, workspace
 
 
 def skip_ratio_of(mask: torch.Tensor, seq_lens=None, BS=None, SBS=None) -> float:

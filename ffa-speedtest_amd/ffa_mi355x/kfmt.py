@@ -76,6 +76,8 @@ def run_kfmt_decode(
     a.m_buf, a.l_buf, a.o_buf = workspace.m_buf.data_ptr(), workspace.l_buf.data_ptr(), workspace.o_buf.data_ptr()
     a.nparts = workspace.nparts
     a.mask, a.ntbs = workspace.mask_buf.data_ptr(), workspace.NTBS
+    a.piece_max = workspace.piece_max.data_ptr() if workspace.piece_max is not None else None
+    a.npieces = workspace.npieces
     a.layout = layout
     a.block_table = block_table.data_ptr() if block_table is not None else None
     a.bt_stride = block_table.shape[1] if block_table is not None else 0

@@ -95,14 +95,21 @@ enum {
 
 /*
  * Arguments of one pruned decode step.  Shapes use B sequences, HQ query
- * heads, HKV KV heads (G = HQ/HKV <= 4), head dim D = DV = 128.
+ * heads, HKV KV heads (G = HQ/HKV <= 16, the reference's 16-row tile,
+ * attn_kernel_v1210_fused_bsz_q2fp8.py:19, 40-41), head dim D = DV = 128,
+ * SBS a power of two >= 16 and BS a multiple of SBS.
  *
  * Scratch (caller-owned, see ffa_q2fp8_decode_nparts): one partial per query
  * row and 512-token span,
  *   m_buf, l_buf [B, HQ, nparts] f32; o_buf [B, HQ, nparts, 128] f32;
  *   mask [B, HKV, ntbs] i8 (1 = block kept, written for every block).
  * Two launches on `stream`: score + prune + exact pass, then the log-sum-exp
- * merge.  Calls that share scratch must be ordered on one stream.
+ * merge.  A group of more than 4 query rows or a prune block longer than 512
+ * tokens (SBS > 512) needs every row's block maxima before any block is
+ * decided: stage 1 is then two launches (maxima, then decide + exact pass) and
+ * needs piece_max [B, HQ, npieces] f32 with npieces >= ffa_q2fp8_decode_pieces()
+ * and threshold_out (or threshold_in).  Calls that share scratch must be
+ * ordered on one stream.
  */
 typedef struct ffa_q2fp8_decode_args {
   const void *q; /* [B, HQ, 128], dtype q_dtype */
@@ -133,13 +140,20 @@ typedef struct ffa_q2fp8_decode_args {
   int8_t *mask;
   int ntbs;
   int num_pages; /* paged: pages P of every pool (> 0); block-table entries outside [0, P) read page 0 */
+  float *piece_max; /* two-pass decodes only (else NULL): [B, HQ, npieces] f32 */
+  int npieces;
 } ffa_q2fp8_decode_args;
 
 /* Number of partial slots per query row the scratch buffers must hold for max length T. */
 int ffa_q2fp8_decode_nparts(int T, int BS, int SBS);
+/* Pieces per query row of the two-pass scratch piece_max (prune blocks when SBS <= 512, else
+ * 512-token spans), or 0 when the decode runs in one pass (G <= 4 and SBS <= 512).  Same rule
+ * for ffa_kfmt_decode. */
+int ffa_q2fp8_decode_pieces(int HQ, int HKV, int T, int BS, int SBS);
 
 /* Both stages back to back on `stream`. */
 int ffa_q2fp8_decode(const ffa_q2fp8_decode_args *args, void *stream);
+
 /* Stage 1: coarse scores, threshold, prune (mask, threshold_out) and the exact pass over
  * kept blocks, writing the partials m_buf/l_buf/o_buf. */
 int ffa_q2fp8_decode_stage1(const ffa_q2fp8_decode_args *args, void *stream);
@@ -307,6 +321,8 @@ typedef struct ffa_kfmt_decode_args {
   const int32_t *block_table; /* [B, bt_stride] (paged only), bt_stride >= ceil(T/64) */
   int bt_stride;
   int num_pages; /* paged: pages P of every pool (> 0); block-table entries outside [0, P) read page 0 */
+  float *piece_max; /* two-pass decodes only (G > 4 or SBS > 512), as in ffa_q2fp8_decode_args */
+  int npieces;
 } ffa_kfmt_decode_args;
 
 int ffa_kfmt_decode(const ffa_kfmt_decode_args *args, void *stream);

@@ -77,11 +77,19 @@ def khat_fp8(base: np.ndarray, fmt: str) -> np.ndarray:
 
 
 def quantize_fp8_scaled(k: np.ndarray, fmt: str = "e4m3fn"):
-    """Per-token-scaled fp8: s = fp16(max(amax_d |k|, 1e-6) / 448) per (b, t, h); base = fp8(k / s);
-    residual = fp8(k - base * s).  Returns (base u8 [B,T,HKV,D], scale f32 [B,T,HKV], residual u8)."""
+    """Per-token-scaled fp8: s = max(fp16(max(amax_d |k|, 1e-6) / fmax), 2^-14) per (b, t, h)
+    (fmax = 448 for e4m3fn, 57344 for e5m2); base = fp8(k / s); residual = fp8(k - base * s).
+    Returns (base u8 [B,T,HKV,D], scale f32 [B,T,HKV], residual u8).
+
+    The floor 2^-14 (the smallest normal fp16) keeps s non-zero for all-zero and tiny rows, and
+    keeps k / s within fmax: a subnormal fp16 s can be up to half its quantum (2^-25) below
+    amax / fmax, which for amax = 3.5e-5 would give k / s = 587 > 448, a NaN in e4m3fn.  With a
+    normal s the rounding is at most 2^-11 relative, so |k / s| <= fmax * (1 + 2^-11), which both
+    formats round to fmax."""
     k = np.asarray(k, F32)
     fmax = 448.0 if fmt == "e4m3fn" else 57344.0
     s = round_f16((np.maximum(np.abs(k).max(axis=-1), F32(1e-6)) / F32(fmax)).astype(F32))
+    s = np.maximum(s, F32(2.0**-14)).astype(F32)
     base = fp8_encode((k / s[..., None]).astype(F32), fmt)
     deq = (fp8_decode(base, fmt) * s[..., None]).astype(F32)  # exact: 4 x 11 significant bits
     res = fp8_encode((k - deq).astype(F32), fmt)

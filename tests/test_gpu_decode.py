@@ -203,6 +203,51 @@ def test_cudagraph_runner_paged(gpu):
     assert_out_close(f32(got), o_ref, "paged runner")
 
 
+def test_cudagraph_runner_paged_growing_lengths(gpu):
+    """Capture with short lengths, then replay as a decode loop does, with seq_lens growing past
+    the capture-time maximum: every replay equals an eager call and the oracle at those lengths
+    (the captured grid covers the block table's capacity)."""
+    import attn_kernel.attn_kernel_v1210_fused_bsz_q2fp8 as K
+    from attn_kernel.attn_kernel_v1210_fused_bsz_q2fp8_cudagraph import CUDAGraphDecodeRunnerQ2FP8
+
+    c = paged_case(B=2, T=1500, HQ=32, HKV=8, seed=23, n_heavy=16)  # both sequences hold 1500 tokens
+    cache = to_gpu_paged(c, gpu)
+    q = c["q"].to(gpu).unsqueeze(1).contiguous()
+    bt = c["block_table"].to(gpu)
+    args = (q, cache.k_q, cache.k_scale, cache.k_zero, cache.v)
+    lens0 = torch.tensor([700, 300], dtype=torch.int32, device=gpu)
+    runner = CUDAGraphDecodeRunnerQ2FP8(*args, k_residual=cache.k_res, BS=64, delta=5.0, block_table=bt,
+                                        seq_lens=lens0)
+    for lens in ([700, 300], [701, 301], [1100, 900], [1500, 1500]):
+        lt = torch.tensor(lens, dtype=torch.int32, device=gpu)
+        got = runner(*args, k_residual=cache.k_res, seq_lens=lt).clone()
+        torch.cuda.synchronize()
+        ref = K.attn_forward_decode_quantized(*args, k_residual=cache.k_res, BS=64, delta=5.0, block_table=bt,
+                                              seq_lens=lt)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), f"replay != eager at lengths {lens}"
+        o_ref, _ = O.decode(f32(c["q"]), c["k_q"], c["k_scale"], c["k_zero"], f32(c["v"]), c["k_res"],
+                            res_fmt=c["res"], scale_mode="g32", seq_lens=lens, out_dtype="bf16", BS=64, SBS=64,
+                            delta=5.0)
+        assert_out_close(f32(got), o_ref, f"growing lengths {lens}")
+
+
+def test_workspace_allocated_ahead_matches_paged_call(gpu):
+    """allocate_q2fp8_decode_workspace and the call agree on T for a paged cache (both default to the
+    block table's capacity), so the H100-style allocate-then-call pattern works with seq_lens."""
+    import attn_kernel.attn_kernel_v1210_fused_bsz_q2fp8 as K
+
+    c = paged_case(B=2, T=1000, HQ=32, HKV=8, seed=24, n_heavy=16, seq_lens=[1000, 450])
+    cache = to_gpu_paged(c, gpu)
+    q = c["q"].to(gpu).unsqueeze(1).contiguous()
+    kw = dict(block_table=c["block_table"].to(gpu), seq_lens=torch.tensor(c["lens"], dtype=torch.int32, device=gpu))
+    ws = K.allocate_q2fp8_decode_workspace(q, cache.k_q, cache.v, BS=64, **kw)
+    o = K.attn_forward_decode_quantized(q, cache.k_q, cache.k_scale, cache.k_zero, cache.v, k_residual=cache.k_res,
+                                        BS=64, delta=5.0, workspace=ws, **kw)
+    o_ref, _ = oracle_paged(c, BS=64, SBS=64, delta=5.0)
+    assert_out_close(f32(o), o_ref, "workspace allocated ahead")
+
+
 def _pool_views(cache, P):
     """Replace the cache's pools by pages [1, P + 1) of allocations two pages larger, so that page
     ids -1 and P name real memory (allocation pages 0 and P + 1) outside the pools the library sees."""

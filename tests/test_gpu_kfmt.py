@@ -84,6 +84,34 @@ def test_fp8_scaled_decoder_baseline_config1(gpu):
     _check(o, ws, o_ref, diag, "fp8 scaled (config 1)")
 
 
+def test_fp8_scaled_decoder_zero_and_tiny_rows(gpu):
+    """A config-1 cache holding an all-zero K row and a row of amplitude 3.5e-5 (whose fp16
+    scale would be subnormal without the floor): the HIP quantizer's bytes decode to finite
+    outputs that match the oracle on the same bytes."""
+    from ffa_mi355x import kfmt_quant as KQ
+
+    T = 1024
+    q, k, v = _inputs(1, T, "bf16", 4, 16)
+    k[0, 17, 3] = 0.0
+    row = torch.randn(128)
+    k[0, 300, 5] = (row * (3.5e-5 / row.abs().max())).to(torch.bfloat16)
+    k[0, 301, 0] = 0.0
+    base, s, res = KQ.quantize_fp8_scaled(k.to(gpu), torch.float8_e4m3fn)
+    torch.cuda.synchronize()
+    bo, so, ro = OF.quantize_fp8_scaled(f32(k), "e4m3fn")
+    assert np.array_equal(base.view(torch.uint8).cpu().numpy(), bo)
+    assert np.array_equal(f32(s), so) and np.array_equal(res.view(torch.uint8).cpu().numpy(), ro)
+    kh = OF.khat_fp8_scaled(bo, so, "e4m3fn")
+    o_ref, diag = O.decode(f32(q), bo, None, None, f32(v), ro, res_fmt="e4m3fn", BS=64, SBS=64, delta=5.0,
+                           khat=kh, out_dtype="bf16")
+    assert np.isfinite(o_ref).all()
+    ws = F8K.__dict__["DecodeWorkspace"](1, 32, 8, T, 64, 64, gpu, torch.bfloat16)
+    o = F8K.attn_forward_decode_fp8fp8(q.to(gpu).unsqueeze(1).contiguous(), base, v.to(gpu), k_residual=res,
+                                       BS=64, delta=5.0, k_scale=s, workspace=ws)
+    assert torch.isfinite(o.float()).all()
+    _check(o, ws, o_ref, diag, "fp8 scaled with zero / tiny rows")
+
+
 @pytest.mark.parametrize("tau,T,BS,SBS,delta", [
     ("bf16", 2048, 64, 64, 5.0),
     ("fp16", 1100, 128, 64, 4.0),  # NTB = 9 != HKV: see test_nvfp4_scale_normalisation_quirk

@@ -55,19 +55,21 @@ def test_fp8_scaled_quantizer_bit_exact(gpu, tau, fmt, D):
     from ffa_mi355x import kfmt_quant as KQ
 
     k = _k((2, 300, 8, D), tau, 3)
-    k[0, 5, 2] = 0.0  # amax 0: s = fp16(1e-6 / fmax)
+    k[0, 5, 2] = 0.0  # amax 0: the scale floor 2^-14
     k[1, 7, 1] = (torch.randn(D) * 1e-7).to(TORCH_DT[tau])
+    row = torch.randn(D)
+    k[1, 9, 3] = (row * (3.5e-5 / row.abs().max())).to(TORCH_DT[tau])  # fp16(amax / 448) is subnormal
     base, sc, res = KQ.quantize_fp8_scaled(k.to(gpu), FP8_DT[fmt])
     torch.cuda.synchronize()
     ob, osc, orr = OF.quantize_fp8_scaled(f32(k), fmt)
     assert base.shape == k.shape and sc.shape == k.shape[:-1] and sc.dtype == torch.float16
     assert np.array_equal(_u8(base), ob)
     assert np.array_equal(f32(sc), osc)
-    # rows whose scale underflows fp16 to 0 give NaN bases and residuals (NaN sign not specified)
-    nan = (lambda b: (b & 0x7F) == 0x7F) if fmt == "e4m3fn" else (lambda b: ((b & 0x7C) == 0x7C) & ((b & 3) != 0))
-    g = _u8(res)
-    assert np.array_equal(g[~nan(orr)], orr[~nan(orr)]) and nan(g[nan(orr)]).all()
-    assert (osc[0, 5, 2] == 0.0) and nan(orr[0, 5, 2]).all()
+    assert np.array_equal(_u8(res), orr)
+    # no NaN / inf byte anywhere (e4m3fn: 0x7F / 0xFF; e5m2: exponent all ones)
+    bad = (lambda b: (b & 0x7F) == 0x7F) if fmt == "e4m3fn" else (lambda b: (b & 0x7C) == 0x7C)
+    assert not bad(_u8(base)).any() and not bad(_u8(res)).any()
+    assert f32(sc).min() >= 2.0 ** -14
 
 
 @pytest.mark.parametrize("tau", ["bf16", "fp16", "fp32"])

@@ -107,7 +107,7 @@ def test_kproj_rope_channel(gpu, h_dtype, cs_dtype):
 
 
 def test_reference_smoke_test(gpu):
-    """The reference's own smoke check (fused_kproj_rope_q2fp8.py:569-625) passes for the drop-in."""
+    """The drop-in's producer self-check (run_smoke_test): torch and fused HIP producers agree."""
     import fused_kproj_rope_q2fp8 as FK
 
     FK.run_smoke_test(gpu, torch.float16, torch.float8_e5m2, B=2, T=32, H=256, HKV=4, K=64)

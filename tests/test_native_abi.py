@@ -95,6 +95,13 @@ def test_host_only_helpers():
     assert L.ffa_q2fp8_decode_nparts(100, 128, 128) == 1
     assert L.ffa_q2fp8_decode_nparts(1000, 64, 64) == 2
     assert L.ffa_q2_quantize_nsplit(32768) == 64
+    # two-pass scratch: none for G <= 4 and SBS <= 512; prune blocks (SBS <= 512) or 512-token spans
+    assert L.ffa_q2fp8_decode_pieces(32, 8, 32768, 64, 64) == 0
+    assert L.ffa_q2fp8_decode_pieces(32, 8, 32768, 512, 512) == 0
+    assert L.ffa_q2fp8_decode_pieces(64, 8, 32768, 64, 64) == 512  # G = 8
+    assert L.ffa_q2fp8_decode_pieces(48, 8, 1000, 128, 32) == 8 * 4  # G = 6, ceil(1000/128) * 4
+    assert L.ffa_q2fp8_decode_pieces(32, 8, 5000, 4096, 4096) == 16  # SBS = 4096: ceil(5000/4096)*4096/512
+    assert L.ffa_q2fp8_decode_pieces(32, 8, 5000, 2048, 1024) == 12
 
 
 def test_invalid_arguments_are_rejected_without_launch():
@@ -102,11 +109,15 @@ def test_invalid_arguments_are_rejected_without_launch():
 
     L = N.lib()
     a = N.DecodeArgs()
-    a.B, a.T, a.HQ, a.HKV = 1, 128, 40, 8  # G = 5 -> unsupported
+    a.B, a.T, a.HQ, a.HKV = 1, 128, 136, 8  # G = 17 -> beyond the reference's 16-row tile
     a.BS, a.SBS = 64, 64
     rc = L.ffa_q2fp8_decode(ctypes.byref(a), None)
     assert rc == -2 and b"group" in L.ffa_last_error()
-    a.HQ = 32
+    a.HQ = 40  # G = 5: two passes, which need the piece_max scratch
+    assert L.ffa_q2fp8_decode(ctypes.byref(a), None) == -1 and b"piece_max" in L.ffa_last_error()
+    a.HQ, a.BS, a.SBS = 32, 1024, 1024  # SBS > 512: two passes as well
+    assert L.ffa_q2fp8_decode(ctypes.byref(a), None) == -1 and b"piece_max" in L.ffa_last_error()
+    a.BS = 64
     a.SBS = 48
     assert L.ffa_q2fp8_decode(ctypes.byref(a), None) == -2
     a.SBS = 64

@@ -63,6 +63,37 @@ def test_fp8_scaled_quantizer_invariants():
     assert np.array_equal(kh, NM.round_f16(deq))
 
 
+@pytest.mark.parametrize("fmt", ["e4m3fn", "e5m2"])
+def test_fp8_scaled_zero_and_tiny_rows_stay_finite(fmt):
+    """All-zero rows and rows whose amax / fmax is an fp16 subnormal: the scale is floored at
+    the smallest normal fp16, so no byte is NaN / inf and k / s never passes fmax."""
+    fmax = 448.0 if fmt == "e4m3fn" else 57344.0
+    rng = np.random.default_rng(5)
+    k = rng.standard_normal((1, 6, 1, 128)).astype(np.float32)
+    k[0, 0] = 0.0
+    k[0, 1] *= 3.5e-5 / np.abs(k[0, 1]).max()  # amax 3.5e-5: fp16(amax / 448) is one subnormal quantum
+    k[0, 2] *= 1e-7
+    k[0, 3] *= 1e-3
+    base, s, res = OF.quantize_fp8_scaled(k, fmt)
+    assert (s >= 2.0 ** -14).all() and np.array_equal(s, NM.round_f16(s))
+    b, r = NM.fp8_decode(base, fmt), NM.fp8_decode(res, fmt)
+    assert np.isfinite(b).all() and np.isfinite(r).all()
+    assert np.abs(b).max() <= fmax
+    assert (b[0, 0] == 0).all() and (r[0, 0] == 0).all()
+    # the 3.5e-5 row: k / s is the plain quotient by 2^-14 (well inside the range), and base +
+    # residual recovers k to the residual's precision
+    assert np.array_equal(b[0, 1], NM.fp8_decode(NM.fp8_encode(k[0, 1] / np.float32(2.0 ** -14), fmt), fmt))
+    rec = b * s[..., None] + r
+    err = np.abs(rec - k)
+    # the residual is RNE-rounded fp8: relative 2^-4 (e4m3) / 2^-3 (e5m2) of |k - base * s| for a
+    # normal result, at most half the smallest subnormal (2^-10 / 2^-17) otherwise
+    rel, sub = (2.0 ** -4, 2.0 ** -10) if fmt == "e4m3fn" else (2.0 ** -3, 2.0 ** -17)
+    assert (err <= np.maximum(np.abs(k - b * s[..., None]) * rel, sub) + 1e-12).all()
+    # a normal row keeps the old scale (fp16(amax / fmax) is normal for amax >= 448 * 2^-14 / 1)
+    big = np.abs(k[0, 4:]).max(axis=-1)
+    assert np.array_equal(s[0, 4:], NM.round_f16((big / np.float32(fmax)).astype(np.float32)).clip(2.0 ** -14))
+
+
 # ----------------------------------------------------------------------------- nvfp4
 def test_e2m1_decode_closed_form():
     codes = np.arange(16)
