@@ -41,6 +41,7 @@
 
 #include <stdio.h>
 
+#include <mutex>
 #include <type_traits>
 
 namespace ffa {
@@ -1123,3 +1124,89 @@ extern "C" int ffa_q2fp8_decode(const ffa_q2fp8_decode_args *a, void *stream) {
   return rc != FFA_OK ? rc : launch_stage2(a, p, (hipStream_t)stream);
 }
 
+// ============================================================================
+// Decode without allocations: the scratch lives in a static device array
+// ============================================================================
+// For callers that cannot allocate device memory (code under HIP graph capture, tight serving
+// loops, harnesses that forbid hipMalloc).  The per-call scratch of ffa_q2fp8_decode -- partials,
+// two-pass block maxima, and the survivor mask / thresholds when the caller passes none -- is
+// carved out of `scratch`, one copy per GPU for the life of the process.  Its device address is
+// taken once per device with hipGetSymbolAddress and only that address reaches the kernels (the
+// array's name in host code is a host-side stand-in).  Nothing in it has to start at zero: every
+// slot a kernel reads is written earlier in the same call.  Calls that overlap on one GPU (two
+// streams, two host threads) share the array and race.
+namespace {
+constexpr size_t kStaticScratchBytes = FFA_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t *g_scratch_ptr[kMaxDevices] = {};
+
+int static_scratch_of_current_device(uint8_t **out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return set_err(FFA_E_LAUNCH, "no current HIP device for the static scratch");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) return set_err(FFA_E_LAUNCH, "hipGetSymbolAddress(scratch) failed");
+    g_scratch_ptr[dev] = static_cast<uint8_t *>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return FFA_OK;
+}
+}  // namespace
+
+extern "C" int ffa_q2fp8_decode_noalloc(const ffa_q2fp8_decode_args *a, void *stream) {
+  if (!a) return set_err(FFA_E_INVALID, "null args");
+  if (a->B <= 0 || a->T <= 0 || a->HQ <= 0 || a->HKV <= 0 || a->BS <= 0 || a->SBS <= 0)
+    return set_err(FFA_E_INVALID, "bad dims");
+  const size_t B = (size_t)a->B, HQ = (size_t)a->HQ, HKV = (size_t)a->HKV;
+  const size_t nparts = (size_t)ffa_q2fp8_decode_nparts(a->T, a->BS, a->SBS);
+  const size_t ntbs = (size_t)((a->T + a->BS - 1) / a->BS) * (size_t)(a->BS / a->SBS);
+  const size_t npieces = (size_t)ffa_q2fp8_decode_pieces(a->HQ, a->HKV, a->T, a->BS, a->SBS);
+  // the size in floating point first, so that no product of the dimensions can wrap
+  const double rows = (double)B * (double)HQ;
+  const double need = rows * (double)nparts * 130.0 * 4.0 + (double)B * (double)HKV * (double)ntbs + rows * 4.0 +
+                      rows * (double)npieces * 4.0;
+  if (need > (double)kStaticScratchBytes) {
+    char msg[200];
+    snprintf(msg, sizeof(msg), "ffa_q2fp8_decode_noalloc: this shape needs %.0f bytes of scratch, the static array holds %zu",
+             need, kStaticScratchBytes);
+    return set_err(FFA_E_UNSUPPORTED, msg);
+  }
+  size_t used = 0;
+  auto take = [&](size_t bytes) {  // 256-byte aligned regions
+    const size_t at = used;
+    used += (bytes + 255) & ~size_t(255);
+    return at;
+  };
+  const size_t m_at = take(B * HQ * nparts * 4), l_at = take(B * HQ * nparts * 4);
+  const size_t o_at = take(B * HQ * nparts * 128 * 4);
+  const size_t mask_at = a->mask ? 0 : take(B * HKV * ntbs);
+  const size_t th_at = a->threshold_out ? 0 : take(B * HQ * 4);
+  const size_t pm_at = npieces ? take(B * HQ * npieces * 4) : 0;
+  if (used > kStaticScratchBytes) {
+    char msg[200];
+    snprintf(msg, sizeof(msg), "ffa_q2fp8_decode_noalloc: this shape needs %zu bytes of scratch, the static array holds %zu",
+             used, kStaticScratchBytes);
+    return set_err(FFA_E_UNSUPPORTED, msg);
+  }
+  uint8_t *base = nullptr;
+  const int rc = static_scratch_of_current_device(&base);
+  if (rc != FFA_OK) return rc;
+  ffa_q2fp8_decode_args s = *a;
+  s.m_buf = reinterpret_cast<float *>(base + m_at);
+  s.l_buf = reinterpret_cast<float *>(base + l_at);
+  s.o_buf = reinterpret_cast<float *>(base + o_at);
+  s.nparts = (int)nparts;
+  if (!a->mask) {
+    s.mask = reinterpret_cast<int8_t *>(base + mask_at);
+    s.ntbs = (int)ntbs;
+  }
+  if (!a->threshold_out) s.threshold_out = reinterpret_cast<float *>(base + th_at);
+  s.piece_max = npieces ? reinterpret_cast<float *>(base + pm_at) : nullptr;
+  s.npieces = (int)npieces;
+  return ffa_q2fp8_decode(&s, stream);
+}

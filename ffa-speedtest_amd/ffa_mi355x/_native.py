@@ -26,6 +26,7 @@ EXPORTS = (
     "ffa_q2fp8_decode",
     "ffa_q2fp8_decode_stage1",
     "ffa_q2fp8_decode_stage2",
+    "ffa_q2fp8_decode_noalloc",
     "ffa_kfmt_decode",
     "ffa_q2_quantize_nsplit",
     "ffa_q2_quantize_channel",
@@ -167,7 +168,8 @@ def lib() -> ctypes.CDLL:
         L.ffa_q2fp8_decode_pieces.argtypes = [ci, ci, ci, ci, ci]
         L.ffa_q2fp8_decode_pieces.restype = ci
         L.ffa_q2fp8_decode_nparts.restype = ci
-        for name in ("ffa_q2fp8_decode", "ffa_q2fp8_decode_stage1", "ffa_q2fp8_decode_stage2"):
+        for name in ("ffa_q2fp8_decode", "ffa_q2fp8_decode_stage1", "ffa_q2fp8_decode_stage2",
+                     "ffa_q2fp8_decode_noalloc"):
             getattr(L, name).argtypes = [ctypes.POINTER(DecodeArgs), vp]
             getattr(L, name).restype = ci
         L.ffa_kfmt_decode.argtypes = [ctypes.POINTER(KfmtArgs), vp]

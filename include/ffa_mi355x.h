@@ -154,6 +154,20 @@ int ffa_q2fp8_decode_pieces(int HQ, int HKV, int T, int BS, int SBS);
 /* Both stages back to back on `stream`. */
 int ffa_q2fp8_decode(const ffa_q2fp8_decode_args *args, void *stream);
 
+/*
+ * ffa_q2fp8_decode without any caller scratch and without allocating: no counterpart in the
+ * reference; for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  The caller passes inputs and `out` as for
+ * ffa_q2fp8_decode; m_buf, l_buf, o_buf, nparts, piece_max and npieces are ignored; mask (with
+ * ntbs) and threshold_out are written when given, else kept in the scratch.  The scratch is a
+ * static device array of FFA_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; a shape
+ * whose scratch (partials 520 B per query row and 512-token span, plus mask, thresholds and the
+ * two-pass maxima) exceeds it returns FFA_E_UNSUPPORTED before any launch.  Calls that overlap on
+ * one GPU share the array and race: order them on one stream.
+ */
+#define FFA_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+int ffa_q2fp8_decode_noalloc(const ffa_q2fp8_decode_args *args, void *stream);
+
 /* Stage 1: coarse scores, threshold, prune (mask, threshold_out) and the exact pass over
  * kept blocks, writing the partials m_buf/l_buf/o_buf. */
 int ffa_q2fp8_decode_stage1(const ffa_q2fp8_decode_args *args, void *stream);
