@@ -65,28 +65,75 @@ def measured_traffic():
     return {"bytes": int(m.group(1)), "source": f"profiles/{f.name}"} if m else None
 
 
-def cpu_baseline(q, k, v, BS, SBS, delta, seconds):
-    """The numpy oracle on this host (1 thread) on the same workload: microseconds per layer-step."""
+MIN_TIMED_STEPS = 200  # at least this many timed layer-steps, whatever --steps asks for
+MIN_WARMUP_STEPS = 50
+
+
+def host_cores() -> int:
+    """Host cores this process may run on (16 at most: the GPU box's CPU share for one GPU)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def host_cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def oracle_decode_parallel(qf, pk, s, z, vf, r, HKV, threads, **kw):
+    """The numpy oracle split by KV head over `threads` host threads (the (sequence, KV head) units are
+    independent); numpy's per-element work releases the GIL, BLAS is held at one thread per task.
+    Returns (o, mask [B, HKV, NTBS], margin [B, HKV, NTBS])."""
     import numpy as np
+    from concurrent.futures import ThreadPoolExecutor
     from threadpoolctl import threadpool_limits
 
+    from oracle import q2fp8 as O
+
+    G = qf.shape[1] // HKV
+    khat = kw.pop("khat", None)
+
+    def one(h):
+        sl = slice(h, h + 1)
+        cut = lambda a: None if a is None else a[:, :, sl]  # noqa: E731
+        return O.decode(qf[:, h * G:(h + 1) * G], pk[:, :, sl], cut(s), cut(z), vf[:, :, sl], r[:, :, sl],
+                        khat=cut(khat), **kw)
+
+    with threadpool_limits(1), ThreadPoolExecutor(max_workers=threads) as ex:
+        parts = list(ex.map(one, range(HKV)))
+    o = np.concatenate([p_[0] for p_ in parts], axis=1)
+    mask = np.concatenate([p_[1]["mask"] for p_ in parts], axis=1)
+    margin = np.concatenate([p_[1]["margin"] for p_ in parts], axis=1)
+    return o, mask, margin
+
+
+def cpu_baseline(q, k, v, BS, SBS, delta, seconds):
+    """The numpy oracle on this host's cores (split by KV head) on the same workload: microseconds per
+    layer-step, the thread count, and the oracle's mask and margins of the last run."""
     from oracle import q2fp8 as O
 
     kf = k.float().numpy()
     pk, s, z, r = O.quantize_g32(kf, "e4m3fn")  # cache building, not timed
     qf, vf = q.float().numpy(), v.float().numpy()
+    threads = host_cores()
     times = []
-    with threadpool_limits(1):
-        t_end = time.perf_counter() + seconds
-        while True:
-            t0 = time.perf_counter()
-            O.decode(qf, pk, s, z, vf, r, res_fmt="e4m3fn", BS=BS, SBS=SBS, delta=delta, scale_mode="g32",
-                     out_dtype="bf16")
-            times.append(time.perf_counter() - t0)
-            if time.perf_counter() > t_end and len(times) >= 3:
-                break
-    del np
-    return statistics.median(times) * 1e6, len(times)
+    t_end = time.perf_counter() + seconds
+    while True:
+        t0 = time.perf_counter()
+        _, mask, margin = oracle_decode_parallel(qf, pk, s, z, vf, r, k.shape[2], threads, res_fmt="e4m3fn", BS=BS,
+                                                 SBS=SBS, delta=delta, scale_mode="g32", out_dtype="bf16")
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() > t_end and len(times) >= 5:
+            break
+    return statistics.median(times) * 1e6, len(times), threads, mask, margin
 
 
 WORKLOADS = {
@@ -108,6 +155,16 @@ _EVERY = {"config3": 64 + 8, "config4": 64 + 4, "config5": 32 + 16}
 _KEPT = 128 + 256
 
 
+def _warm(R, per_graph=1):
+    """Untimed steps before the timed replays: R eager steps plus the warm-up replays of _graph_time."""
+    return R + max(1, math.ceil(MIN_WARMUP_STEPS / (R * per_graph))) * R * per_graph
+
+
+def _reps(steps, R):
+    """Graph replays of R steps that time at least MIN_TIMED_STEPS steps (and at least `steps`)."""
+    return max(1, math.ceil(max(steps, MIN_TIMED_STEPS) / R))
+
+
 def _graph_time(step, R, reps, stream, per_graph=1):
     """Microseconds per call of step(r): a HIP graph of `per_graph` rounds of step(0..R-1), replayed `reps`
     times, hipEvents around the replays (per_graph > 1 amortises the replay launch for short calls)."""
@@ -122,7 +179,8 @@ def _graph_time(step, R, reps, stream, per_graph=1):
             for r in range(R):
                 step(r)
     torch.cuda.synchronize()
-    g.replay()
+    for _ in range(max(1, math.ceil(MIN_WARMUP_STEPS / (R * per_graph)))):  # untimed warm-up replays
+        g.replay()
     torch.cuda.synchronize()
     cur = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -166,7 +224,7 @@ def bench_config2_reference_layout(args):
     o0, mask = ws.o.clone(), ws.mask_buf.clone()
     stream = torch.cuda.Stream()
     setup_s = time.perf_counter() - t_setup
-    us, steps = _graph_time(step, R, max(1, math.ceil(args.steps / R)), stream)
+    us, steps = _graph_time(step, R, _reps(args.steps, R), stream)
     assert torch.equal(o0, ws.o), "graph replays must match the eager step"
     kept_th = kept_token_heads(mask, T, SBS)
     keep_frac = float(mask.float().mean().item())
@@ -175,7 +233,7 @@ def bench_config2_reference_layout(args):
     gbs = nbytes / (us * 1e-6) / 1e9
     line = {
         "metric": "config2 (reference layout) decode-attn us/step + HBM TB/s on the algorithmic bytes",
-        "value": round(us, 3), "unit": "us/step", "n_gpus": 1, "steps": steps, "warmup": R,
+        "value": round(us, 3), "unit": "us/step", "n_gpus": 1, "steps": steps, "warmup": _warm(R),
         "ms_per_step": round(us / 1e3, 6), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "q2 per-channel + e5m2 residual K, bf16 V; f16/bf16 MFMA, f32 accumulate",
         "data": "synthetic (seeded N(0,1) bf16 with planted heavy tokens)",
@@ -226,7 +284,7 @@ def bench_config1(args):
     o0, mask = ws.o.clone(), ws.mask_buf.clone()
     stream = torch.cuda.Stream()
     setup_s = time.perf_counter() - t_setup
-    us, steps = _graph_time(step, R, max(1, math.ceil(args.steps / R)), stream)
+    us, steps = _graph_time(step, R, _reps(args.steps, R), stream)
     assert torch.equal(o0, ws.o), "graph replays must match the eager step"
     kept_th = kept_token_heads(mask, T, SBS)
     keep_frac = float(mask.float().mean().item())
@@ -241,23 +299,24 @@ def bench_config1(args):
         kf, qf, vf = k.float().numpy(), q.float().numpy(), v.float().numpy()
         ob, osc, ores = OF.quantize_fp8_scaled(kf, "e4m3fn")  # cache building, not timed
         kh = OF.khat_fp8_scaled(ob, osc, "e4m3fn")
+        threads = host_cores()
         times = []
-        with threadpool_limits(1):
-            t_end = time.perf_counter() + args.cpu_seconds
-            while True:
-                t0 = time.perf_counter()
-                O.decode(qf, ob, None, None, vf, ores, res_fmt="e4m3fn", BS=BS, SBS=SBS, delta=args.delta, khat=kh,
-                         out_dtype="bf16")
-                times.append(time.perf_counter() - t0)
-                if time.perf_counter() > t_end and len(times) >= 3:
-                    break
-        cpu = {"value": round(statistics.median(times) * 1e6, 1), "unit": "us/step", "cores": 1, "kind": "port",
-               "sample": f"full workload (B=1, T={T}, 32/8/128, per-token fp8 + e4m3 residual), numpy oracle, 1 thread, "
-                         f"median of {len(times)} runs; cache quantization not timed"}
+        t_end = time.perf_counter() + args.cpu_seconds
+        while True:
+            t0 = time.perf_counter()
+            oracle_decode_parallel(qf, ob, None, None, vf, ores, HKV, threads, res_fmt="e4m3fn", BS=BS, SBS=SBS,
+                                   delta=args.delta, khat=kh, out_dtype="bf16")
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() > t_end and len(times) >= 5:
+                break
+        cpu = {"value": round(statistics.median(times) * 1e6, 1), "unit": "us/step", "cores": threads,
+               "kind": "port", "cpu": host_cpu_model(), "torch": torch.__version__,
+               "sample": f"full workload (B=1, T={T}, 32/8/128, per-token fp8 + e4m3 residual), numpy oracle split "
+                         f"by KV head over {threads} threads, median of {len(times)} runs; cache quantization not timed"}
         del np
     line = {
         "metric": "config1 decode-attn us/step + HBM TB/s on the algorithmic bytes",
-        "value": round(us, 3), "unit": "us/step", "n_gpus": 1, "steps": steps, "warmup": R,
+        "value": round(us, 3), "unit": "us/step", "n_gpus": 1, "steps": steps, "warmup": _warm(R),
         "ms_per_step": round(us / 1e3, 6), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "e4m3 K x fp16 token scale + e4m3 residual, bf16 V; f16/bf16 MFMA, f32 accumulate",
         "data": "synthetic (seeded N(0,1) bf16, 4 K channels x10)",
@@ -357,7 +416,7 @@ def bench_workload(args):
     o0, mask = ws.o.clone(), ws.mask_buf.clone()
     stream = torch.cuda.Stream()
     setup_s = time.perf_counter() - t_setup
-    reps = max(1, math.ceil(args.steps / R))
+    reps = _reps(args.steps, R)
     us, steps = _graph_time(step, R, reps, stream)
     assert torch.equal(o0, ws.o), "graph replays must match the eager step"
     if wl == "config5":
@@ -376,7 +435,7 @@ def bench_workload(args):
     gbs = nbytes / (decode_us * 1e-6) / 1e9
     line = {
         "metric": f"{wl} decode-attn us/step + HBM TB/s on the algorithmic bytes",
-        "value": round(us, 3), "unit": "us/step", "n_gpus": 1, "steps": steps, "warmup": R,
+        "value": round(us, 3), "unit": "us/step", "n_gpus": 1, "steps": steps, "warmup": _warm(R),
         "ms_per_step": round(us / 1e3, 6), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": {"config3": "e2m1 K x e4m3 g16 scale + e4m3 residual, bf16 V",
                   "config4": "nf4 K x fp16 g64 absmax + e4m3 residual, bf16 V",
@@ -489,8 +548,8 @@ def main():
     torch.cuda.synchronize()
     setup_s = time.perf_counter() - t_setup
 
-    n_warm = max(1, math.ceil(args.warmup / R))
-    n_rep = max(1, math.ceil(args.steps / R))
+    n_warm = max(1, math.ceil(max(args.warmup, MIN_WARMUP_STEPS) / R))
+    n_rep = max(1, math.ceil(max(args.steps, MIN_TIMED_STEPS) / R))
     for _ in range(n_warm):
         graph.replay()
     torch.cuda.synchronize()
@@ -538,11 +597,22 @@ def main():
     traffic = measured_traffic()
 
     cpu = None
+    mask_check = None
     if not args.no_cpu_baseline:
-        cpu_us, n = cpu_baseline(q, k, v, args.BS, args.SBS, args.delta, args.cpu_seconds)
-        cpu = {"value": round(cpu_us, 1), "unit": "us/layer", "cores": 1, "kind": "port",
-               "sample": f"full workload (B=1, T={T}, 32/8/128, g32 q2 + e4m3 residual), numpy oracle, "
-                         f"1 thread, median of {n} runs; cache quantization not timed"}
+        import numpy as np
+        import torch as _t
+
+        cpu_us, n, threads, o_mask, o_margin = cpu_baseline(q, k, v, args.BS, args.SBS, args.delta, args.cpu_seconds)
+        cpu = {"value": round(cpu_us, 1), "unit": "us/layer", "cores": threads, "kind": "port",
+               "cpu": host_cpu_model(), "torch": _t.__version__,
+               "sample": f"full workload (B=1, T={T}, 32/8/128, g32 q2 + e4m3 residual), numpy oracle split by KV "
+                         f"head over {threads} threads, median of {n} runs; cache quantization not timed"}
+        g_mask = mask.cpu().numpy()[..., : o_mask.shape[-1]]
+        near = np.abs(o_margin) <= 1e-3
+        differ = g_mask != o_mask
+        mask_check = {"blocks": int(o_mask.size), "near_threshold_blocks": int(near.sum()),
+                      "mismatch_far": int((differ & ~near).sum()), "mismatch_near": int((differ & near).sum()),
+                      "rule": "survivor mask against the CPU oracle on the same inputs; near = |margin| <= 1e-3"}
 
     line = {
         "metric": "q2fp8 decode-attn us/layer + HBM TB/s (% of peak) at 32K ctx, bs=1",
@@ -579,6 +649,7 @@ def main():
             "traffic_source": traffic["source"] if traffic else None,
         },
         "cpu_baseline": cpu,
+        "mask_vs_oracle": mask_check,
         "setup_s": round(setup_s, 1),
     }
     print(json.dumps(line), flush=True)
