@@ -63,6 +63,29 @@ __global__ __launch_bounds__(256) void q2_scale_kernel(const float *minmax, int 
 }
 
 // one thread per (token, packed byte) of a [B, T, HKV, D] tensor
+// One packed byte (channels 4 byte .. 4 byte + 3) of one K row under per-channel scale / zero
+// (tau values at sz_off + d): codes and residuals with the reference's per-element ops.  The
+// full quantizer runs it with K's own scale / zero, the per-channel append with the cache's.
+__device__ __forceinline__ void quant_channel_byte(const void *k, int kdt, size_t k_row, int D, int byte,
+                                                   const void *scale, const void *zero, size_t sz_off,
+                                                   uint8_t *kq_byte, uint8_t *res_row, int res_e4m3) {
+  uint32_t packed = 0;
+  for (int e = 0; e < 4; ++e) {
+    const int d = 4 * byte + e;
+    if (d >= D) break;
+    const float kv = load_any(k, k_row * D + d, kdt);
+    const float sc = load_any(scale, sz_off + d, kdt);
+    const float zr = load_any(zero, sz_off + d, kdt);
+    const float xs = round_to(kv - zr, kdt);               // (k - zero) in tau
+    const float xd = round_to(__fdiv_rn(xs, sc), kdt);     // / scale in tau
+    const float cq = fminf(fmaxf(__builtin_rintf(xd), 0.f), 3.f);  // round (RNE), clamp(0,3)
+    const float deq = (cq * sc) + zr;                      // two fp32 roundings
+    res_row[d] = (uint8_t)f32_to_fp8(kv - deq, res_e4m3);
+    packed |= ((uint32_t)cq) << (2 * e);
+  }
+  *kq_byte = (uint8_t)packed;
+}
+
 __global__ __launch_bounds__(256) void q2_quant_channel_kernel(const void *k, int kdt, int B, int T, int HKV,
                                                                 int D, const void *scale, const void *zero,
                                                                 uint8_t *kq, uint8_t *res, int res_e4m3) {
@@ -74,22 +97,32 @@ __global__ __launch_bounds__(256) void q2_quant_channel_kernel(const void *k, in
   const size_t row = id / DP;  // (b, t, hkv)
   const int hkv = (int)(row % HKV);
   const int b = (int)(row / ((size_t)HKV * T));
-  const int C = HKV * D;
-  uint32_t packed = 0;
-  for (int e = 0; e < 4; ++e) {
-    const int d = 4 * byte + e;
-    if (d >= D) break;
-    const float kv = load_any(k, row * D + d, kdt);
-    const float sc = load_any(scale, (size_t)b * C + hkv * D + d, kdt);
-    const float zr = load_any(zero, (size_t)b * C + hkv * D + d, kdt);
-    const float xs = round_to(kv - zr, kdt);               // (k - zero) in tau
-    const float xd = round_to(__fdiv_rn(xs, sc), kdt);     // / scale in tau
-    const float cq = fminf(fmaxf(__builtin_rintf(xd), 0.f), 3.f);  // round (RNE), clamp(0,3)
-    const float deq = (cq * sc) + zr;                      // two fp32 roundings
-    res[row * D + d] = (uint8_t)f32_to_fp8(kv - deq, res_e4m3);
-    packed |= ((uint32_t)cq) << (2 * e);
-  }
-  kq[row * DP + byte] = (uint8_t)packed;
+  quant_channel_byte(k, kdt, row, D, byte, scale, zero, ((size_t)b * HKV + hkv) * D, kq + row * DP + byte,
+                     res + row * D, res_e4m3);
+}
+
+// Reference-layout append: token n of sequence b (k_new [B, Tn, HKV, D]) is quantized with the
+// cache's per-channel scale / zero [B, HKV, D] and written at position pos[b] + n of
+// k_q [B, T_cap, HKV, ceil(D/4)] and residual [B, T_cap, HKV, D]; positions outside
+// [0, T_cap) are not written.
+__global__ __launch_bounds__(256) void q2_append_channel_kernel(const void *k_new, int kdt, int B, int Tn, int HKV,
+                                                                 int D, const int32_t *pos, int T_cap,
+                                                                 const void *scale, const void *zero, uint8_t *kq,
+                                                                 uint8_t *res, int res_e4m3) {
+  const int DP = (D + 3) / 4;
+  const size_t total = (size_t)B * Tn * HKV * DP;
+  const size_t id = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (id >= total) return;
+  const int byte = (int)(id % DP);
+  const size_t row = id / DP;  // (b, n, hkv) of k_new
+  const int hkv = (int)(row % HKV);
+  const int n = (int)((row / HKV) % Tn);
+  const int b = (int)(row / ((size_t)HKV * Tn));
+  const int t = pos[b] + n;
+  if (t < 0 || t >= T_cap) return;
+  const size_t dst = ((size_t)b * T_cap + t) * HKV + hkv;
+  quant_channel_byte(k_new, kdt, row, D, byte, scale, zero, ((size_t)b * HKV + hkv) * D, kq + dst * DP + byte,
+                     res + dst * D, res_e4m3);
 }
 
 // K projection GEMM tile: 16 tokens x 32 output channels per 512-thread workgroup.  The 32-wide k
@@ -351,6 +384,22 @@ static int launch_quant_channel(const void *k, int kdt, int B, int T, int HKV, i
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return ffa_set_error_internal(FFA_E_LAUNCH, hipGetErrorString(e));
   return FFA_OK;
+}
+
+extern "C" int ffa_q2_append_channel(const void *k_new, int k_dtype, int B, int Tn, int HKV, int D, const int32_t *pos,
+                                     int T_cap, const void *scale, const void *zero, uint8_t *k_q, uint8_t *residual,
+                                     int res_dtype, void *stream) {
+  if (B <= 0 || Tn <= 0 || HKV <= 0 || D <= 0 || T_cap <= 0) return ffa_set_error_internal(FFA_E_INVALID, "bad dims");
+  if (!(k_dtype >= FFA_DT_F16 && k_dtype <= FFA_DT_F32)) return ffa_set_error_internal(FFA_E_INVALID, "k dtype");
+  if (!(res_dtype == FFA_DT_FP8_E4M3 || res_dtype == FFA_DT_FP8_E5M2))
+    return ffa_set_error_internal(FFA_E_INVALID, "residual dtype");
+  if (!k_new || !pos || !scale || !zero || !k_q || !residual) return ffa_set_error_internal(FFA_E_INVALID, "null pointer");
+  const size_t total = (size_t)B * Tn * HKV * ((D + 3) / 4);
+  hipLaunchKernelGGL(ffa::q2_append_channel_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, k_new, k_dtype, B, Tn, HKV, D, pos, T_cap, scale, zero, k_q, residual,
+                     res_dtype == FFA_DT_FP8_E4M3 ? 1 : 0);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? FFA_OK : ffa_set_error_internal(FFA_E_LAUNCH, hipGetErrorString(e));
 }
 
 extern "C" int ffa_q2_quantize_channel(const void *k, int k_dtype, int B, int T, int HKV, int D, uint8_t *k_q,

@@ -30,6 +30,7 @@ EXPORTS = (
     "ffa_kfmt_decode",
     "ffa_q2_quantize_nsplit",
     "ffa_q2_quantize_channel",
+    "ffa_q2_append_channel",
     "ffa_kproj_rope_q2_channel",
     "ffa_kproj_rope_q2_append",
     "ffa_q2_quantize_g32_append",
@@ -177,6 +178,8 @@ def lib() -> ctypes.CDLL:
         L.ffa_q2_quantize_nsplit.argtypes = [ci]
         L.ffa_q2_quantize_nsplit.restype = ci
         L.ffa_q2_quantize_channel.argtypes = [vp, ci, ci, ci, ci, ci, vp, vp, vp, vp, ci, vp, vp]
+        L.ffa_q2_append_channel.argtypes = [vp, ci, ci, ci, ci, ci, vp, ci, vp, vp, vp, vp, ci, vp]
+        L.ffa_q2_append_channel.restype = ci
         L.ffa_q2_quantize_channel.restype = ci
         L.ffa_kproj_rope_q2_channel.argtypes = [vp, vp, vp, ci, vp, vp, ci, ci, ci, ci, ci, ci, vp, vp, vp, vp, vp,
                                                 ci, vp, vp]

@@ -43,6 +43,48 @@ def quantize_per_channel(k: torch.Tensor, fp8_dtype=torch.float8_e5m2):
     return k_q, scale, zero, res
 
 
+def append_per_channel(k_q: torch.Tensor, k_scale: torch.Tensor, k_zero: torch.Tensor, k_residual: torch.Tensor,
+                       k_new: torch.Tensor, pos, v: torch.Tensor | None = None, v_new: torch.Tensor | None = None):
+    """Append new tokens to a reference-layout cache (k_q [B, T_cap, HKV, ceil(D/4)], residual
+    [B, T_cap, HKV, D], per-channel scale / zero [B, HKV, D] as quantize_per_channel made them), in place.
+
+    No reference counterpart (incremental quantization is a TODO there, ffa-q2fp8/OPTIMIZATION_NOTES.md:
+    23-26).  Policy: the scale / zero stay as they are and the new tokens k_new [B, Tn, HKV, D] are
+    quantized with them by the reference's per-element ops, so a value outside [zero, zero + 3 scale]
+    takes code 0 or 3 and the fp8 residual carries the difference (e5m2 reaches 57344, e4m3 448).
+    Token n of sequence b goes to position pos[b] + n (pos: int or [B] int tensor); v_new [B, Tn, HKV, DV]
+    is copied into v at the same positions.  Positions must fit the cache (checked on the host).
+    """
+    for t, name in ((k_q, "k_q"), (k_scale, "k_scale"), (k_zero, "k_zero"), (k_residual, "k_residual"),
+                    (k_new, "k_new")):
+        if not t.is_cuda or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous CUDA tensor")
+    B, T_cap, HKV, DP = k_q.shape
+    Bn, Tn, HKVn, D = k_new.shape
+    if Bn != B or HKVn != HKV or DP != (D + 3) // 4 or tuple(k_residual.shape) != (B, T_cap, HKV, D):
+        raise ValueError("k_new [B, Tn, HKV, D] must match the cache [B, T_cap, HKV, ceil(D/4)] / [B, T_cap, HKV, D]")
+    if tuple(k_scale.shape) != (B, HKV, D) or tuple(k_zero.shape) != (B, HKV, D):
+        raise ValueError("k_scale / k_zero must be [B, HKV, D]")
+    if k_scale.dtype != k_new.dtype or k_zero.dtype != k_new.dtype:
+        raise ValueError("k_scale / k_zero must have k_new's dtype (the quantizer's arithmetic type)")
+    dev = k_q.device
+    pos_t = torch.full((B,), int(pos), dtype=torch.int32) if isinstance(pos, int) else pos.to(torch.int32).cpu()
+    if pos_t.shape != (B,) or int(pos_t.min()) < 0 or int(pos_t.max()) + Tn > T_cap:
+        raise ValueError(f"positions pos + {Tn} tokens must lie in [0, {T_cap}]")
+    pos_d = pos_t.to(dev)
+    rc = N.lib().ffa_q2_append_channel(k_new.data_ptr(), N.dtype_code(k_new.dtype), B, Tn, HKV, D, pos_d.data_ptr(),
+                                       T_cap, k_scale.data_ptr(), k_zero.data_ptr(), k_q.data_ptr(),
+                                       k_residual.data_ptr(), N.dtype_code(k_residual.dtype), N.stream_of(dev))
+    N.check(rc, "ffa_q2_append_channel")
+    if v_new is not None:
+        if v is None or v.shape[0] != B or v.shape[2:] != v_new.shape[2:] or v_new.shape[1] != Tn:
+            raise ValueError("v_new [B, Tn, HKV, DV] needs v [B, T_cap, HKV, DV]")
+        for b in range(B):
+            p0 = int(pos_t[b])
+            v[b, p0:p0 + Tn].copy_(v_new[b])
+    return k_q, k_residual
+
+
 def kproj_rope_q2_channel(h, w_k, cos, sin, num_kv_heads, head_dim, bias=None, fp8_dtype=torch.float8_e5m2,
                           return_k=False):
     """K = RoPE(h W_k^T + b) then the per-channel q2 quantizer, on the GPU (one GEMM pass).

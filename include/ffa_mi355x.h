@@ -21,6 +21,9 @@
  *                              ffa-q2fp8/fused_kproj_rope_q2fp8.py:40-68)
  *   ffa_kproj_rope_q2_channel ffa-q2fp8/fused_kproj_rope_q2fp8.py:492-542
  *                             (the two Triton launches of kproj_rope_quantize_triton)
+ *   ffa_q2_append_channel     no reference counterpart (the reference's incremental-quantization
+ *                             TODO, ffa-q2fp8/OPTIMIZATION_NOTES.md:23-26): append to the
+ *                             reference-layout cache with its existing per-channel scale / zero
  *   ffa_q2_quantize_g32_append no reference counterpart: g32 quantize + paged append of
  *                             given K rows (the paged g32 cache layout)
  *   ffa_kproj_rope_q2_append  no reference counterpart: decode-time append of
@@ -184,6 +187,19 @@ int ffa_q2_quantize_nsplit(int T);
 int ffa_q2_quantize_channel(const void *k, int k_dtype, int B, int T, int HKV, int D, uint8_t *k_q,
                             void *scale, void *zero, uint8_t *residual, int res_dtype, float *minmax,
                             void *stream);
+
+/*
+ * Append to the reference-layout cache (no reference counterpart: incremental quantization is
+ * a TODO there, ffa-q2fp8/OPTIMIZATION_NOTES.md:23-26).  New tokens k_new [B, Tn, HKV, D]
+ * (k_dtype) are quantized with the cache's existing per-channel scale / zero [B, HKV, D]
+ * (k_dtype, as ffa_q2_quantize_channel wrote them) by the same per-element ops, so values
+ * outside [zero, zero + 3 scale] take code 0 or 3 and the fp8 residual carries the rest; token n
+ * of sequence b goes to position pos[b] + n of k_q [B, T_cap, HKV, ceil(D/4)] and residual
+ * [B, T_cap, HKV, D]; positions outside [0, T_cap) are not written.  V is a plain copy (not here).
+ */
+int ffa_q2_append_channel(const void *k_new, int k_dtype, int B, int Tn, int HKV, int D, const int32_t *pos, int T_cap,
+                          const void *scale, const void *zero, uint8_t *k_q, uint8_t *residual, int res_dtype,
+                          void *stream);
 
 /*
  * Fused K projection + RoPE + per-channel q2 quantize (reference producer).

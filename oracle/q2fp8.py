@@ -84,12 +84,46 @@ def quantize_per_channel(k: np.ndarray, tau: str, fp8: str = "e5m2"):
     clamped = round_to(np.maximum(diff, F32(1e-6)), tau)  # .clamp_min(1e-6)
     scale = round_to(clamped / F32(3.0), tau)  # / 3.0 in tau
     zero = k_min  # :83
+    packed, res = quantize_with_channel_scale(k, scale, zero, tau, fp8)
+    return packed, scale.astype(F32), zero.astype(F32), res
+
+
+def quantize_with_channel_scale(k: np.ndarray, scale: np.ndarray, zero: np.ndarray, tau: str, fp8: str = "e5m2"):
+    """Codes and residual of K [B, T, HKV, D] under given per-channel scale / zero [B, HKV, D] (tau
+    values), with the reference quantizer's per-element ops (run_attn_bench_q2.py:84-88):
+    c = clamp(rne(tau(tau(k - zero) / scale)), 0, 3); res = fp8(f32(k) - (f32(c * scale) + zero)).
+    quantize_per_channel runs it with the scale / zero of K itself; the per-channel append runs it
+    on new tokens with the cache's existing scale / zero, so a value outside [zero, zero + 3 scale]
+    takes code 0 or 3 and the residual carries the rest (no reference counterpart: incremental
+    quantization is a TODO there, ffa-q2fp8/OPTIMIZATION_NOTES.md:23-26).  Returns
+    (packed u8 [B, T, HKV, ceil(D/4)], residual fp8 bytes [B, T, HKV, D])."""
+    k = np.asarray(k, dtype=F32)
+    scale = np.asarray(scale, F32)
+    zero = np.asarray(zero, F32)
     xs = round_to(k - zero[:, None], tau)  # (k - zero) in tau
     xd = round_to(xs / scale[:, None], tau)  # / scale in tau
     codes = np.clip(np.rint(xd), 0, 3).astype(np.uint8)  # torch.round = RNE; clamp(0,3)
     deq = (codes.astype(F32) * scale[:, None]).astype(F32) + zero[:, None]  # :85-87, no FMA
     res = fp8_encode((k - deq).astype(F32), fp8)  # :88
-    return pack_2bit(codes), scale.astype(F32), zero.astype(F32), res
+    return pack_2bit(codes), res
+
+
+def append_per_channel(k_q: np.ndarray, k_res: np.ndarray, k_new: np.ndarray, scale: np.ndarray, zero: np.ndarray,
+                       pos, tau: str, fp8: str = "e5m2"):
+    """Reference-layout cache append: tokens k_new [B, Tn, HKV, D] go to positions pos[b] .. pos[b] + Tn - 1
+    of k_q [B, T_cap, HKV, ceil(D/4)] / k_res [B, T_cap, HKV, D] (copies are returned), quantized by
+    quantize_with_channel_scale with the cache's scale / zero; positions past T_cap are dropped."""
+    k_q = np.array(k_q, copy=True)
+    k_res = np.array(k_res, copy=True)
+    pk, rr = quantize_with_channel_scale(k_new, scale, zero, tau, fp8)
+    T_cap = k_q.shape[1]
+    for b in range(k_new.shape[0]):
+        for n in range(k_new.shape[1]):
+            t = int(pos[b]) + n
+            if 0 <= t < T_cap:
+                k_q[b, t] = pk[b, n]
+                k_res[b, t] = rr[b, n]
+    return k_q, k_res
 
 
 def quantize_g32(k: np.ndarray, fp8: str = "e4m3fn", group: int = 32):

@@ -9,8 +9,10 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import FP8_DT, TORCH_DT, f32
+from helpers import FP8_DT, TORCH_DT, assert_out_close, f32
 from oracle import producer as OP
+from ffa_mi355x import quant as Q
+from ffa_mi355x import synth
 from ffa_mi355x.paged import scale_pos
 from oracle import q2fp8 as O
 
@@ -221,3 +223,62 @@ def test_kproj_append_config5_small(gpu):
         assert np.array_equal(s_pool[page, :, :, slot], s2[b, 0]), "scales"
         assert np.array_equal(z_pool[page, :, :, slot], z2[b, 0]), "zeros"
         assert np.array_equal(r_pool[page, :, slot], r2[b, 0]), "residual"
+
+
+@pytest.mark.parametrize("tau", ["bf16", "fp16", "fp32"])
+@pytest.mark.parametrize("fmt", ["e5m2", "e4m3fn"])
+def test_append_per_channel_bit_exact(gpu, tau, fmt):
+    """Reference-layout append: new tokens (many outside the cache's per-channel range) quantized with
+    the cache's scale / zero are byte-identical to the oracle's; an overwrite of earlier positions too."""
+    g = torch.Generator().manual_seed(61)
+    B, T0, Tcap, HKV, D = 2, 300, 400, 4, 128
+    k0 = (torch.randn(B, T0, HKV, D, generator=g) * 2).to(TORCH_DT[tau])
+    kq0, s, z, r0 = Q.quantize_per_channel(k0.to(gpu), FP8_DT[fmt])
+    kq = torch.zeros((B, Tcap, HKV, D // 4), dtype=torch.uint8, device=gpu)
+    kr = torch.zeros((B, Tcap, HKV, D), dtype=FP8_DT[fmt], device=gpu)
+    kq[:, :T0].copy_(kq0)
+    kr[:, :T0].copy_(r0)
+    k_new = (torch.randn(B, 17, HKV, D, generator=g) * 4).to(TORCH_DT[tau])
+    pos = torch.tensor([300, 250], dtype=torch.int32)
+    Q.append_per_channel(kq, s, z, kr, k_new.to(gpu), pos)
+    torch.cuda.synchronize()
+    cache_q = np.concatenate([kq0.cpu().numpy(), np.zeros((B, Tcap - T0, HKV, D // 4), np.uint8)], axis=1)
+    cache_r = np.concatenate([r0.view(torch.uint8).cpu().numpy(), np.zeros((B, Tcap - T0, HKV, D), np.uint8)], axis=1)
+    oq, orr = O.append_per_channel(cache_q, cache_r, f32(k_new), f32(s), f32(z), pos.tolist(), tau, fmt)
+    assert np.array_equal(kq.cpu().numpy(), oq)
+    assert np.array_equal(kr.view(torch.uint8).cpu().numpy(), orr)
+    c = O.unpack_2bit(oq[:, 300:317], D)
+    assert (c == 0).any() and (c == 3).any()
+
+
+def test_append_per_channel_then_decode(gpu):
+    """A reference-layout cache filled by the quantizer over its first tokens and by appends for the
+    rest decodes (through the drop-in) to the oracle's result on the oracle's appended cache."""
+    import attn_kernel.attn_kernel_v1210_fused_bsz_q2fp8 as K
+
+    B, T0, T, HQ, HKV = 2, 1500, 2048, 32, 8
+    q, k, v = synth.attention_inputs(B=B, T=T, HQ=HQ, HKV=HKV, seed=62, n_heavy=16, dtype=torch.float16)
+    kd = k.to(gpu)
+    kq0, s, z, r0 = Q.quantize_per_channel(kd[:, :T0].contiguous(), torch.float8_e5m2)
+    kq = torch.zeros((B, T, HKV, 32), dtype=torch.uint8, device=gpu)
+    kr = torch.zeros((B, T, HKV, 128), dtype=torch.float8_e5m2, device=gpu)
+    vd = torch.zeros((B, T, HKV, 128), dtype=torch.float16, device=gpu)
+    kq[:, :T0].copy_(kq0)
+    kr[:, :T0].copy_(r0)
+    vd[:, :T0].copy_(v[:, :T0].to(gpu))
+    for a in range(T0, T, 200):  # appends of 200 tokens (the last one shorter)
+        e = min(a + 200, T)
+        Q.append_per_channel(kq, s, z, kr, kd[:, a:e].contiguous(), a, v=vd, v_new=v[:, a:e].to(gpu))
+    qd = q.to(gpu).unsqueeze(1).contiguous()
+    o = K.attn_forward_decode_quantized(qd, kq, s, z, vd, k_residual=kr, BS=64, delta=5.0)
+    torch.cuda.synchronize()
+    # the oracle's cache: its quantizer over the first T0 tokens, its append for the rest
+    pk0, os_, oz, or0 = O.quantize_per_channel(f32(k[:, :T0]), "fp16", "e5m2")
+    okq = np.concatenate([pk0, np.zeros((B, T - T0, HKV, 32), np.uint8)], axis=1)
+    okr = np.concatenate([or0, np.zeros((B, T - T0, HKV, 128), np.uint8)], axis=1)
+    okq, okr = O.append_per_channel(okq, okr, f32(k[:, T0:]), os_, oz, [T0, T0], "fp16", "e5m2")
+    assert np.array_equal(kq.cpu().numpy(), okq) and np.array_equal(kr.view(torch.uint8).cpu().numpy(), okr)
+    o_ref, diag = O.decode(f32(q), okq, os_, oz, f32(v), okr, res_fmt="e5m2", BS=64, SBS=64, delta=5.0,
+                           out_dtype="fp16")
+    mx, mean = assert_out_close(f32(o), o_ref, "appended reference-layout cache")
+    print(f"[out] append + decode max_abs={mx:.3e} mean_abs={mean:.3e} skip={diag['skip_ratio']:.3f}")

@@ -111,6 +111,56 @@ def test_quantizer_known_answers():
     assert (pk[..., 1] >> 4 == 0).all()
 
 
+@pytest.mark.parametrize("tau", ["bf16", "fp16", "fp32"])
+@pytest.mark.parametrize("fmt", ["e5m2", "e4m3fn"])
+def test_channel_append_matches_torch_ops_with_the_cache_scale(tau, fmt):
+    """New tokens quantized with an existing cache's scale / zero: the reference's op sequence
+    (run_attn_bench_q2.py:84-88) run by torch with those scale / zero, including values outside
+    [zero, zero + 3 scale] (codes clamp to 0 / 3, the residual carries the rest)."""
+    g = torch.Generator().manual_seed(12)
+    k0 = (torch.randn(2, 200, 3, 130, generator=g) * 2).to(TORCH_DT[tau])
+    _, s, z, _ = O.quantize_per_channel(f32(k0), tau, fmt)
+    k_new = (torch.randn(2, 9, 3, 130, generator=g) * 4).to(TORCH_DT[tau])  # many outside the cache's range
+    pk, rr = O.quantize_with_channel_scale(f32(k_new), s, z, tau, fmt)
+    ts, tz = torch.from_numpy(s).to(TORCH_DT[tau]), torch.from_numpy(z).to(TORCH_DT[tau])
+    c = torch.round((k_new - tz[:, None]) / ts[:, None]).clamp(0, 3).to(torch.uint8)
+    deq = c.to(torch.float32) * ts[:, None].to(torch.float32) + tz[:, None].to(torch.float32)
+    tr = (k_new.to(torch.float32) - deq).to(FP8_DT[fmt])
+    cu = O.unpack_2bit(pk, 130)
+    assert (cu == c.numpy()).all()
+    assert (rr == tr.view(torch.uint8).numpy()).all()
+    assert (cu == 0).any() and (cu == 3).any()
+
+
+def test_channel_append_reproduces_the_quantizer_and_drops_positions_past_the_end():
+    rng = np.random.default_rng(13)
+    k = NM.round_bf16(rng.standard_normal((2, 100, 2, 128)).astype(np.float32))
+    pk, s, z, r = O.quantize_per_channel(k, "bf16", "e5m2")
+    # re-appending tokens 60..99 of each sequence over a cache that holds only tokens 0..59
+    kq0 = pk.copy()
+    kr0 = r.copy()
+    kq0[:, 60:] = 0
+    kr0[:, 60:] = 0
+    kq1, kr1 = O.append_per_channel(kq0, kr0, k[:, 60:], s, z, [60, 60], "bf16", "e5m2")
+    assert np.array_equal(kq1, pk) and np.array_equal(kr1, r)
+    # positions beyond the cache are dropped, earlier positions overwritten
+    kq2, kr2 = O.append_per_channel(pk, r, k[:, :5], s, z, [97, -2], "bf16", "e5m2")
+    assert np.array_equal(kq2[0, 97:], pk[0, :3]) and np.array_equal(kq2[0, :97], pk[0, :97])
+    assert np.array_equal(kq2[1, :3], pk[1, 2:5]) and np.array_equal(kq2[1, 3:], pk[1, 3:])
+
+
+def test_channel_append_known_answers():
+    # one channel with zero 0 and scale 1 (cache values 0 .. 3): a new token's -2 takes code 0 and
+    # residual -2, 7 takes code 3 and residual 4, 1.5 takes code 2 (half to even) and residual -0.5;
+    # 7.5 also takes code 3, its residual 4.5 rounds to 4 in e5m2 (half to even)
+    s = np.ones((1, 1, 1), np.float32)
+    z = np.zeros((1, 1, 1), np.float32)
+    k_new = np.array([-2.0, 7.0, 1.5, 7.5], np.float32).reshape(1, 4, 1, 1)
+    pk, rr = O.quantize_with_channel_scale(k_new, s, z, "fp32", "e5m2")
+    assert list(O.unpack_2bit(pk, 1)[0, :, 0, 0]) == [0, 3, 2, 3]
+    assert list(NM.fp8_decode(rr[0, :, 0, 0], "e5m2")) == [-2.0, 4.0, -0.5, 4.0]
+
+
 def test_g32_quantizer_invariants():
     rng = np.random.default_rng(5)
     k = NM.round_bf16(rng.standard_normal((2, 70, 4, 128)).astype(np.float32) * 2)
