@@ -1,0 +1,202 @@
+"""Hugging Face integration of the q2fp8 pruned decode: a paged KV cache and a decode attention hook.
+
+The reference integrates its fp8fp8 kernel into a copied Llama (ffa-fp8fp8/e2e/fp8fp8_cache.py:183-224,
+ffa-fp8fp8/e2e/modeling_llama.py:293-321): a `Cache` subclass stores the quantized K, and the attention
+forward calls the FFA decode when a step has one query token.  Its cache rebuilds a dequantized copy of
+all keys on every update (fp8fp8_cache.py:60-69) and grows by `torch.cat`.
+
+Here, for q2fp8, on the MI355X library:
+
+* `Q2FP8Cache` / `Q2FP8PagedLayer`: every layer keeps a `PagedQ2Cache` (64-token pages, g32 2-bit codes +
+  fp8 residual K, V^T pages) sized once for `max_batch_size` x `max_cache_len`, with a seeded page table.
+  `update()` g32-quantizes and appends the new (already rotated) K and V in one kernel
+  (`ffa_q2_quantize_g32_append`) and never dequantizes the cache.
+* `ffa_q2fp8_attention`: registered with transformers' attention registry as "ffa_q2fp8", so an
+  unmodified `LlamaForCausalLM` (or any model whose attention goes through `ALL_ATTENTION_FUNCTIONS`)
+  uses it once `enable_ffa_q2fp8(model, ...)` is called.  A step with one query token per sequence runs
+  the pruned decode over the paged cache (`attn_settings`: BS, SBS, delta, use_fp8_residual as in the
+  reference's `config.attn_settings`, e2e/bench_llama_fp8fp8.py:179-189); a prefill into an empty cache
+  runs exact causal attention on the prompt's own K / V (in fp32), as the reference runs FlashAttention
+  for prefill (modeling_llama.py:322-337).
+
+The HF models apply RoPE (their half-split `rotate_half`) before `Cache.update`, so the cache receives
+rotated K and appends it with the quantize-append entry point; the fused K-projection + RoPE producer
+follows the reference producer's interleaved-pair RoPE instead and serves the benchmark path.
+
+Limits: all sequences of a batch have the same length (no padding), one prefill per cache (prefill
+after decode steps would need the dequantized past), no beam search reordering.
+"""
+from __future__ import annotations
+
+import math
+import sys
+import threading
+from pathlib import Path
+from typing import Any, Callable, Optional
+
+import torch
+from transformers import AttentionInterface
+from transformers.cache_utils import Cache, CacheLayerMixin
+
+sys.path.insert(0, str(Path(__file__).resolve().parents[2]))  # ffa-speedtest_amd/
+from ffa_mi355x.decode import DecodeWorkspace  # noqa: E402
+from ffa_mi355x.paged import PAGE, PagedQ2Cache  # noqa: E402
+
+__all__ = ["Q2FP8Cache", "Q2FP8PagedLayer", "ffa_q2fp8_attention", "enable_ffa_q2fp8"]
+
+ATTN_NAME = "ffa_q2fp8"
+DEFAULT_SETTINGS = dict(use_ffa_decode=True, BS=64, SBS=64, delta=5.0, use_fp8_residual=True)
+_current = threading.local()  # the layer whose update() ran last on this thread
+
+
+class Q2FP8PagedLayer(CacheLayerMixin):
+    """One layer's paged q2fp8 cache (pools allocated on the first update)."""
+
+    is_sliding = False
+
+    def __init__(self, max_batch_size: int, max_cache_len: int, res_dtype=torch.float8_e4m3fn, page_seed: int = 0):
+        super().__init__()
+        self.max_batch_size = int(max_batch_size)
+        self.max_cache_len = int(max_cache_len)
+        self.res_dtype = res_dtype
+        self.page_seed = page_seed
+        self.pool: Optional[PagedQ2Cache] = None
+        self.block_table: Optional[torch.Tensor] = None
+        self.seq_lens: Optional[torch.Tensor] = None
+        self.seq_len = 0
+        self._workspace: Optional[DecodeWorkspace] = None
+
+    @property
+    def capacity(self) -> int:
+        return self.block_table.shape[1] * PAGE
+
+    def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        B, HKV, _, D = key_states.shape
+        if D != 128:
+            raise NotImplementedError(f"head_dim {D}: the q2fp8 decode implements 128")
+        if B > self.max_batch_size:
+            raise ValueError(f"batch {B} exceeds max_batch_size {self.max_batch_size}")
+        self.dtype, self.device = key_states.dtype, key_states.device
+        npg = -(-self.max_cache_len // PAGE)
+        v_dtype = value_states.dtype if value_states.dtype in (torch.float16, torch.bfloat16) else torch.bfloat16
+        self.pool = PagedQ2Cache(B * npg, HKV, self.device, res_dtype=self.res_dtype, v_dtype=v_dtype)
+        # a seeded permutation of the pool: sequences' pages are scattered as in a serving cache
+        perm = torch.randperm(B * npg, generator=torch.Generator().manual_seed(self.page_seed))
+        self.block_table = perm.view(B, npg).to(torch.int32).to(self.device)
+        self.seq_lens = torch.zeros(B, dtype=torch.int32, device=self.device)
+        self.seq_len = 0
+        self.is_initialized = True
+
+    def update(self, key_states: torch.Tensor, value_states: torch.Tensor, *args, **kwargs):
+        """Append K / V [B, HKV, Tn, 128] (rotated) at the current length; returns them unchanged."""
+        if not self.is_initialized:
+            self.lazy_initialization(key_states, value_states)
+        B, HKV, Tn, D = key_states.shape
+        if B != self.block_table.shape[0] or HKV != self.pool.HKV:
+            raise ValueError("key_states do not match the cache's batch / KV heads")
+        if self.seq_len + Tn > self.capacity:
+            raise ValueError(f"cache holds {self.capacity} tokens, {self.seq_len + Tn} requested")
+        pos = torch.full((B,), self.seq_len, dtype=torch.int32, device=self.device)
+        self.pool.append(key_states.transpose(1, 2).contiguous(), value_states.transpose(1, 2).contiguous(), pos,
+                         self.block_table)
+        self.seq_len += Tn
+        self.seq_lens.fill_(self.seq_len)
+        self.last_query_len = Tn
+        return key_states, value_states
+
+    def workspace(self, HQ: int, BS: int, SBS: int, dtype) -> DecodeWorkspace:
+        B = self.block_table.shape[0]
+        ws = self._workspace
+        if ws is None or not ws.matches(B, HQ, self.pool.HKV, self.capacity, BS, SBS, self.device, dtype):
+            ws = self._workspace = DecodeWorkspace(B, HQ, self.pool.HKV, self.capacity, BS, SBS, self.device, dtype)
+        return ws
+
+    def get_mask_sizes(self, query_length: int) -> tuple[int, int]:
+        return self.seq_len + query_length, 0
+
+    def get_seq_length(self) -> int:
+        return self.seq_len
+
+    def get_max_length(self) -> int:
+        return self.max_cache_len
+
+    def reset(self) -> None:
+        self.seq_len = 0
+        if self.seq_lens is not None:
+            self.seq_lens.zero_()
+
+    def reorder_cache(self, beam_idx: torch.LongTensor) -> None:
+        raise NotImplementedError("beam search reordering is not supported by the paged q2fp8 cache")
+
+    def offload(self):
+        raise NotImplementedError("offloading is not supported by the paged q2fp8 cache")
+
+    def prefetch(self):
+        pass
+
+
+class Q2FP8Cache(Cache):
+    """Paged q2fp8 KV cache for a whole model (one Q2FP8PagedLayer per decoder layer)."""
+
+    def __init__(self, num_layers: int, max_batch_size: int, max_cache_len: int, res_dtype=torch.float8_e4m3fn,
+                 page_seed: int = 0):
+        layers = [Q2FP8PagedLayer(max_batch_size, max_cache_len, res_dtype, page_seed + i) for i in range(num_layers)]
+        super().__init__(layers=layers)
+
+    def update(self, key_states: torch.Tensor, value_states: torch.Tensor, layer_idx: int, *args, **kwargs):
+        out = self.layers[layer_idx].update(key_states, value_states)
+        _current.layer = self.layers[layer_idx]  # read by ffa_q2fp8_attention for the same layer
+        return out
+
+
+def _prefill_attention(query, key, value, scaling):
+    """Exact causal attention of a prompt on its own K / V (fp32, contiguous operands)."""
+    B, HQ, L, D = query.shape
+    G = HQ // key.shape[1]
+    k = key.float().repeat_interleave(G, dim=1).contiguous()
+    v = value.float().repeat_interleave(G, dim=1).contiguous()
+    s = torch.matmul(query.float().contiguous(), k.transpose(2, 3).contiguous()) * scaling
+    s = s.masked_fill(torch.ones(L, L, dtype=torch.bool, device=s.device).triu(1), float("-inf"))
+    p = torch.softmax(s, dim=-1)
+    return torch.matmul(p, v).to(query.dtype).transpose(1, 2).contiguous()  # [B, L, HQ, D]
+
+
+def ffa_q2fp8_attention(module, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, attention_mask,
+                        scaling: Optional[float] = None, dropout: float = 0.0, **kwargs):
+    """Attention of one layer (the transformers attention-function signature); query [B, HQ, L, D] rotated.
+
+    L == 1: the pruned q2fp8 decode over the layer's paged cache (modeling_llama.py:293-321's branch);
+    otherwise exact causal attention of the prompt on the K / V it just appended."""
+    settings = dict(DEFAULT_SETTINGS)
+    settings.update(getattr(module.config, "attn_settings", None) or {})
+    layer = getattr(_current, "layer", None)
+    if not isinstance(layer, Q2FP8PagedLayer):
+        raise RuntimeError("ffa_q2fp8 attention needs a Q2FP8Cache passed as past_key_values")
+    B, HQ, L, D = query.shape
+    scale = scaling if scaling is not None else 1.0 / math.sqrt(D)
+    if L == 1 and settings["use_ffa_decode"]:
+        ws = layer.workspace(HQ, settings["BS"], settings["SBS"], query.dtype)
+        layer.pool.decode(query[:, :, 0, :].contiguous(), layer.block_table, layer.seq_lens, T=layer.capacity,
+                          scale=scale, BS=settings["BS"], SBS=settings["SBS"], delta=settings["delta"],
+                          use_fp8_residual=settings["use_fp8_residual"], workspace=ws)
+        out = ws.o.unsqueeze(1)  # [B, 1, HQ, D]
+        hook: Optional[Callable] = settings.get("on_decode")
+        if hook is not None:
+            hook(module.layer_idx, query[:, :, 0, :], out[:, 0], layer)
+        return out, None
+    if layer.seq_len != L:
+        raise NotImplementedError("a prefill after earlier tokens (chunked prefill) is not supported: the paged "
+                                  "q2fp8 cache keeps no full-precision keys")
+    return _prefill_attention(query, key, value, scale), None
+
+
+def enable_ffa_q2fp8(model, **attn_settings: Any) -> None:
+    """Route the model's attention through ffa_q2fp8_attention (registered once) with these settings
+    (BS, SBS, delta, use_fp8_residual, use_ffa_decode; optional on_decode(layer_idx, q, o, cache_layer))."""
+    AttentionInterface.register(ATTN_NAME, ffa_q2fp8_attention)
+    cfg = model.config
+    cfg.attn_settings = {**DEFAULT_SETTINGS, **attn_settings}
+    if hasattr(model, "set_attn_implementation"):
+        model.set_attn_implementation(ATTN_NAME)
+    else:
+        cfg._attn_implementation = ATTN_NAME
