@@ -3,7 +3,8 @@
 
 Workload: one decode-attention step ("layer-step") of batch 1 over a 32K
 context, 32 query / 8 KV heads, head dim 128.  K is 2-bit (groups of 32 along
-D, fp16 scale/zero per token) plus an fp8 e4m3 residual, V is bf16, paged in
+D, fp16 scale/zero per token) plus an fp8 e4m3 residual, V is bf16 (held as
+fp16, the type the decode's P.V uses, as the reference casts v to fp16), paged in
 64-token pages through a seeded random page table; 16 heavy tokens per query
 head are planted (cosine 0.8 with q).  Inputs are synthetic (seeded), already
 resident in HBM when timing starts.
@@ -37,7 +38,7 @@ PAGE = 64
 
 
 def algorithmic_bytes(T_list, HKV, HQ, kept_tokens_heads, D=128):
-    """Bytes one layer-step must touch: every token's codes + g32 scale/zero, the fp8 residual and bf16 V of
+    """Bytes one layer-step must touch: every token's codes + g32 scale/zero, the fp8 residual and 16-bit V of
     kept tokens, q, o and the page table."""
     every = sum(T_list) * HKV * (D // 4 + (D // 32) * 4)
     kept = kept_tokens_heads * (D + 2 * D)
@@ -235,7 +236,7 @@ def bench_config2_reference_layout(args):
         "metric": "config2 (reference layout) decode-attn us/step + HBM TB/s on the algorithmic bytes",
         "value": round(us, 3), "unit": "us/step", "n_gpus": 1, "steps": steps, "warmup": _warm(R),
         "ms_per_step": round(us / 1e3, 6), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-        "dtype": "q2 per-channel + e5m2 residual K, bf16 V; f16/bf16 MFMA, f32 accumulate",
+        "dtype": "q2 per-channel + e5m2 residual K, bf16 V; f16 MFMA (P.V on fp16 p and fp16 v), f32 accumulate",
         "data": "synthetic (seeded N(0,1) bf16 with planted heavy tokens)",
         "config": {"workload": WORKLOADS["config2ref"], "B": B, "T": T, "HQ": HQ, "HKV": HKV, "D": D, "BS": BS,
                    "SBS": SBS, "delta": args.delta, "keep_fraction": round(keep_frac, 4), "algorithmic_bytes": nbytes,
@@ -318,7 +319,7 @@ def bench_config1(args):
         "metric": "config1 decode-attn us/step + HBM TB/s on the algorithmic bytes",
         "value": round(us, 3), "unit": "us/step", "n_gpus": 1, "steps": steps, "warmup": _warm(R),
         "ms_per_step": round(us / 1e3, 6), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-        "dtype": "e4m3 K x fp16 token scale + e4m3 residual, bf16 V; f16/bf16 MFMA, f32 accumulate",
+        "dtype": "e4m3 K x fp16 token scale + e4m3 residual, bf16 V; f16 MFMA (P.V on fp16 p and fp16 v), f32 accumulate",
         "data": "synthetic (seeded N(0,1) bf16, 4 K channels x10)",
         "config": {"workload": WORKLOADS["config1"], "B": B, "T": T, "HQ": HQ, "HKV": HKV, "D": D, "BS": BS,
                    "SBS": SBS, "delta": args.delta, "keep_fraction": round(keep_frac, 4), "algorithmic_bytes": nbytes,
@@ -440,7 +441,7 @@ def bench_workload(args):
         "dtype": {"config3": "e2m1 K x e4m3 g16 scale + e4m3 residual, bf16 V",
                   "config4": "nf4 K x fp16 g64 absmax + e4m3 residual, bf16 V",
                   "config5": "bf16 K-proj (f32 accumulate); q2 g32 + e4m3 residual K, bf16 V"}[wl]
-                 + "; f16/bf16 MFMA, f32 accumulate",
+                 + "; f16 MFMA (P.V on fp16 p and fp16 v), f32 accumulate",
         "data": "synthetic (N(0,1) bf16 drawn on the device per sequence, 16 heavy tokens per query head)",
         "config": {"workload": WORKLOADS[wl], "B": B, "T_max": T, "tokens": sum(final), "HQ": HQ, "HKV": HKV,
                    "D": D, "BS": BS, "SBS": SBS, "delta": delta, "keep_fraction": round(keep_frac, 4),
@@ -625,7 +626,7 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q2+fp8(e4m3) K, bf16 V; f16/bf16 MFMA, f32 accumulate",
+        "dtype": "q2+fp8(e4m3) K, bf16 V held as fp16 V^T pages; f16 MFMA (P.V on fp16 p and fp16 v), f32 accumulate",
         "data": "synthetic (seeded N(0,1) bf16 with planted heavy tokens)",
         "hbm_tbps": round(achieved_gbs / 1e3, 4),
         "hbm_pct_peak": round(100.0 * achieved_gbs / HBM_PEAK_GBS, 2),

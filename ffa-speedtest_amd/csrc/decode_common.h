@@ -209,18 +209,12 @@ __device__ __forceinline__ f16x8 fp8x8_to_f16x8(uint32_t lo, uint32_t hi) {
   return __builtin_bit_cast(f16x8, r);
 }
 
+// P.V runs on fp16 operands whatever V's storage type, as the reference's decode kernels cast
+// both p and v to fp16 before the product (attn_kernel_v1210_fused_bsz_q2fp8.py:130-131 and the
+// same lines of the fp8fp8 / nvfp4fp8 / nf4fp8 kernels): fp16 P keeps 11 significant bits, and
+// bf16 V is rounded to fp16 (round to nearest even) in registers.
 template <int VT>
 struct VTraits;
-template <>
-struct VTraits<kVBF16> {
-  typedef bf16x8 vec;
-  __device__ static __forceinline__ f32x4 mfma(vec a, vec b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
-  __device__ static __forceinline__ uint32_t pack2(float x, float y) {
-    return f32_to_bf16_bits(x) | (f32_to_bf16_bits(y) << 16);
-  }
-};
 template <>
 struct VTraits<kVF16> {
   typedef f16x8 vec;
@@ -229,6 +223,20 @@ struct VTraits<kVF16> {
   }
   __device__ static __forceinline__ uint32_t pack2(float x, float y) {
     return f32_to_f16_bits(x) | (f32_to_f16_bits(y) << 16);
+  }
+  // 8 stored V elements (4 words) -> the B operand
+  __device__ static __forceinline__ vec operand(u32x4 w) { return __builtin_bit_cast(vec, w); }
+};
+template <>
+struct VTraits<kVBF16> : VTraits<kVF16> {
+  __device__ static __forceinline__ vec operand(u32x4 w) {
+    u32x4 r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = __uint_as_float(w[e] << 16), hi = __uint_as_float(w[e] & 0xffff0000u);
+      r[e] = f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16);
+    }
+    return __builtin_bit_cast(vec, r);
   }
 };
 

@@ -605,7 +605,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
             v4 = make_uint4(w4[0], w4[1], w4[2], w4[3]);
           }
           const u32x4 w = {v4.x, v4.y, v4.z, v4.w};
-          oacc[nu] = VTr::mfma(pa2[kap], __builtin_bit_cast(typename VTr::vec, w), oacc[nu]);
+          oacc[nu] = VTr::mfma(pa2[kap], VTr::operand(w), oacc[nu]);
         }
       }
     } else {
@@ -648,7 +648,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
             const uint32_t hi = *(const uint16_t *)(st + (tk + 2 * e + 1) * kPitch + 2 * vcol);
             w[e] = lo | (hi << 16);
           }
-          oacc[nu] = VTr::mfma(pa2[kap], __builtin_bit_cast(typename VTr::vec, w), oacc[nu]);
+          oacc[nu] = VTr::mfma(pa2[kap], VTr::operand(w), oacc[nu]);
         }
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

@@ -670,7 +670,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
             v4 = make_uint4(w4[0], w4[1], w4[2], w4[3]);
           }
           const u32x4 w = {v4.x, v4.y, v4.z, v4.w};
-          oacc[nu] = VTr::mfma(pa2[kap], __builtin_bit_cast(typename VTr::vec, w), oacc[nu]);
+          oacc[nu] = VTr::mfma(pa2[kap], VTr::operand(w), oacc[nu]);
         }
       }
     } else {
@@ -710,7 +710,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
               const uint32_t hi = *(const uint16_t *)(st + (tk + 2 * e + 1) * kVRowHalf + 2 * vcol);
               w[e] = lo | (hi << 16);
             }
-            oacc[nu] = VTr::mfma(pa2[kap], __builtin_bit_cast(typename VTr::vec, w), oacc[nu]);
+            oacc[nu] = VTr::mfma(pa2[kap], VTr::operand(w), oacc[nu]);
           }
         }
         // the other half (and the next kept chunk) reuses the staging buffer

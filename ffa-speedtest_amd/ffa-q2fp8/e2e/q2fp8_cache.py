@@ -78,8 +78,8 @@ class Q2FP8PagedLayer(CacheLayerMixin):
             raise ValueError(f"batch {B} exceeds max_batch_size {self.max_batch_size}")
         self.dtype, self.device = key_states.dtype, key_states.device
         npg = -(-self.max_cache_len // PAGE)
-        v_dtype = value_states.dtype if value_states.dtype in (torch.float16, torch.bfloat16) else torch.bfloat16
-        self.pool = PagedQ2Cache(B * npg, HKV, self.device, res_dtype=self.res_dtype, v_dtype=v_dtype)
+        # V pages hold fp16(V): the decode's P.V operand, converted once per token at append
+        self.pool = PagedQ2Cache(B * npg, HKV, self.device, res_dtype=self.res_dtype, v_dtype=torch.float16)
         # a seeded permutation of the pool: sequences' pages are scattered as in a serving cache
         perm = torch.randperm(B * npg, generator=torch.Generator().manual_seed(self.page_seed))
         self.block_table = perm.view(B, npg).to(torch.int32).to(self.device)

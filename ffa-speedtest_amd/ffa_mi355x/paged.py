@@ -9,7 +9,9 @@ kernels (all per (page, KV head) blocks contiguous):
     k_scale  [P, HKV, 4, 64]     f16   g32 scale per token and group (slot order below)
     k_zero   [P, HKV, 4, 64]     f16   g32 zero point (slot order below)
     k_res    [P, HKV, 64, 128]   fp8   residual (e4m3fn by default)
-    v        [P, HKV, 128, 64]   bf16  V^T pages (token-minor)
+    v        [P, HKV, 128, 64]   fp16  V^T pages (token-minor); fp16 by default, since the decode
+                                       computes P.V on fp16(V) as the reference does (bf16 pages
+                                       are accepted and rounded to fp16 in registers)
 
 block_table[b, i] is the pool page of tokens [64 i, 64 i + 64) of sequence b;
 seq_lens[b] is its length.  Token t of a page keeps its scale/zero in slot
@@ -85,7 +87,7 @@ def check_append_fits(pos: torch.Tensor, Tn: int, block_table: torch.Tensor, num
 
 
 class PagedQ2Cache:
-    def __init__(self, num_pages, HKV, device, res_dtype=torch.float8_e4m3fn, v_dtype=torch.bfloat16):
+    def __init__(self, num_pages, HKV, device, res_dtype=torch.float8_e4m3fn, v_dtype=torch.float16):
         self.P, self.HKV = int(num_pages), int(HKV)
         self.device = torch.device(device)
         self.res_dtype, self.v_dtype = res_dtype, v_dtype

@@ -10,7 +10,7 @@ one page pool shared by all sequences, with scales along head_dim instead:
     k_scale  [P, HKV, 64, 8]    e4m3  nvfp4: scale of each 16-channel block
              [P, HKV, 64, 2]    f16   nf4:   absmax scale of each 64-channel block
     k_res    [P, HKV, 64, 128]  fp8   residual (e4m3fn by default)
-    v        [P, HKV, 128, 64]  bf16  V^T pages (token-minor)
+    v        [P, HKV, 128, 64]  fp16  V^T pages (token-minor; fp16 by default, the P.V operand type)
 
 block_table[b, i] is the pool page of tokens [64 i, 64 i + 64) of sequence b.
 Quantization rules: ffa_nvfp4_g16_append / ffa_nf4_g64_append in include/ffa_mi355x.h.
@@ -82,7 +82,7 @@ def decode_pools(fmt, q, k, k_scale, v, k_res, block_table, seq_lens=None, *, T=
 class PagedKfmtCache:
     """Page pools of one format ("nvfp4" or "nf4"), with append (quantize + write) and decode."""
 
-    def __init__(self, fmt, num_pages, HKV, device, res_dtype=torch.float8_e4m3fn, v_dtype=torch.bfloat16):
+    def __init__(self, fmt, num_pages, HKV, device, res_dtype=torch.float8_e4m3fn, v_dtype=torch.float16):
         if fmt not in FORMATS:
             raise ValueError(f"fmt must be one of {FORMATS}")
         self.fmt = fmt

@@ -245,6 +245,7 @@ def decode(
     force_mask=None,
     khat=None,
     khat_probe1=None,
+    pv_dtype: str = "fp16",
 ):
     """Appendix-A decode semantics over the contiguous layout.
 
@@ -258,6 +259,9 @@ def decode(
     fp8 bytes.  seq_lens (optional) gives each sequence its own length.
     force_mask [B,HKV,NTBS] (optional) replaces the prune decision, so that an
     implementation's arithmetic can be checked under its own block mask.
+    pv_dtype: the type p and v are rounded to for P.V, "fp16" as the reference casts
+    both (attn_kernel...q2fp8.py:130-131); "bf16" exists only for tests that show a
+    bf16 P operand is caught.
 
     Returns (o [B,HQ,DV] float32 holding out_dtype values, diag dict with
     'mask' [B,HKV,NTBS] int8, 'threshold' [B,HQ], 'block_max' [B,HQ,NTBS]
@@ -348,9 +352,9 @@ def decode(
                 p = np.where(valid[kept][:, :, None], np.exp2((Sk - m[:, None, :]).astype(np.float64)), 0.0)
             p = p.astype(F32)
             lsum = p.astype(np.float64).sum(axis=1).astype(F32)  # [K, G] (:124)
-            v16 = round_f16(v[b, :Tb, h][idx[kept]])  # [K, SBS, DV]
+            v16 = round_to(np.asarray(v[b, :Tb, h][idx[kept]], F32), pv_dtype)  # [K, SBS, DV]
             v16 = np.where(valid[kept][:, :, None], v16, 0.0)
-            ob = np.einsum("kug,kuv->kgv", round_f16(p).astype(np.float64), v16.astype(np.float64))  # (:131)
+            ob = np.einsum("kug,kuv->kgv", round_to(p, pv_dtype).astype(np.float64), v16.astype(np.float64))  # (:131)
             m_out[b, h * G:(h + 1) * G][:, kept] = m.T
             l_out[b, h * G:(h + 1) * G][:, kept] = lsum.T
             # stage 2 merge (:156-169), evaluated exactly

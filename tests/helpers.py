@@ -96,7 +96,7 @@ def to_gpu_paged(case, dev):
     cache.k_scale.copy_(torch.from_numpy(p["k_scale"].view(np.int16)).view(torch.float16))
     cache.k_zero.copy_(torch.from_numpy(p["k_zero"].view(np.int16)).view(torch.float16))
     cache.k_res.copy_(torch.from_numpy(p["k_res"]).view(FP8_DT[case["res"]]))
-    cache.v.copy_(torch.from_numpy(p["v"].view(np.int16)).view(torch.bfloat16))
+    cache.v.copy_(torch.from_numpy(p["v"].view(np.int16)).view(torch.bfloat16))  # stored as the pool dtype
     return cache
 
 

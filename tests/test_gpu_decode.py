@@ -300,3 +300,46 @@ def test_page_ids_outside_the_pool(gpu):
         changed = [i for i in range(P + 2) if not torch.equal(big[i].view(torch.uint8), b0[i].view(torch.uint8))]
         # only pool page 2 (allocation page 3) is written; the V pool is not (no v_new)
         assert changed == ([] if name == "v" else [3]), (name, changed)
+
+
+# P.V operand pin: with fp32 output and prune blocks of one 64-token chunk (the kernel's softmax
+# reference maximum is then the block maximum of the reference), the kernel's output agrees with
+# the oracle's fp16 p / fp16 v to within PV_PIN_TOL, while the same oracle with bf16 p / bf16 v (the
+# planted mistake) lies further away than that on the same inputs.
+PV_PIN_TOL = 2e-4
+
+
+@pytest.mark.parametrize("layout", ["paged", "contig"])
+def test_pv_operands_are_fp16(gpu, layout):
+    from ffa_mi355x import _native as N
+    from ffa_mi355x.decode import run_decode
+
+    T, BS, SBS, delta = 4096, 64, 64, 5.0
+    if layout == "paged":
+        case = paged_case(B=1, T=T, HQ=32, HKV=8, seed=11, n_heavy=16)
+        cache = to_gpu_paged(case, gpu)
+        bt = case["block_table"].to(gpu)
+        ws = cache.decode(case["q"].float().to(gpu), bt, None, T=T, BS=BS, SBS=SBS, delta=delta)
+        kw = dict(res_fmt=case["res"], scale_mode="g32")
+    else:
+        case = contig_case(B=1, T=T, HQ=32, HKV=8, tau="bf16", res="e5m2", seed=11, n_heavy=16)
+        g = to_gpu_contig(case, gpu)
+        ws = run_decode(q=g["q"][:, 0].float().contiguous(), k_q=g["k_q"], k_scale=g["k_scale"],
+                        k_zero=g["k_zero"], v=g["v"], k_residual=g["k_residual"], layout=N.LAYOUT_CONTIG,
+                        scale_mode=N.SCALE_CHANNEL, T=T, HKV=8, scale=1.0 / math.sqrt(128), BS=BS, SBS=SBS,
+                        delta=delta, use_res=True)
+        kw = dict(res_fmt=case["res"], scale_mode="per_channel")
+    torch.cuda.synchronize()
+    assert ws.o.dtype == torch.float32
+    mask = ws.mask_buf.cpu().numpy()
+    args = (f32(case["q"]), case["k_q"], case["k_scale"], case["k_zero"], f32(case["v"]), case["k_res"])
+    o16, _ = O.decode(*args, BS=BS, SBS=SBS, delta=delta, out_dtype="fp32", force_mask=mask, **kw)
+    ob, _ = O.decode(*args, BS=BS, SBS=SBS, delta=delta, out_dtype="fp32", force_mask=mask, pv_dtype="bf16", **kw)
+    og = f32(ws.o)
+    d16 = np.abs(og - o16).max()
+    dbf = np.abs(og - ob).max()
+    gap = np.abs(o16 - ob).max()
+    print(f"[pv] {layout}: |gpu - oracle fp16 P| = {d16:.3e}, |gpu - oracle bf16 P| = {dbf:.3e}, "
+          f"|oracle fp16 - bf16| = {gap:.3e}")
+    assert gap > PV_PIN_TOL  # the tolerance tells the two operand precisions apart
+    assert d16 <= PV_PIN_TOL

@@ -47,7 +47,7 @@ def q2_sequence(cache, bt_row, L):
     r = tok(to_logical(cache.k_res[pg].view(torch.uint8).cpu().numpy(), RES_ORDER))
     v = to_logical(cache.v[pg].view(torch.int16).cpu().numpy(), VT_ORDER)  # [n, HKV, 128, 64]
     v = torch.from_numpy(np.ascontiguousarray(v.transpose(0, 3, 1, 2).reshape(n * 64, H, 128)[:L]))
-    return kq, s, z, r, f32(v.view(torch.bfloat16))
+    return kq, s, z, r, f32(v.view(cache.v.dtype))
 
 
 def kfmt_sequence(cache, bt_row, L):
@@ -64,7 +64,7 @@ def kfmt_sequence(cache, bt_row, L):
     r = tok(to_logical(cache.k_res[pg].view(torch.uint8).cpu().numpy(), RES_ORDER))
     v = to_logical(cache.v[pg].view(torch.int16).cpu().numpy(), VT_ORDER)
     v = torch.from_numpy(np.ascontiguousarray(v.transpose(0, 3, 1, 2).reshape(n * 64, H, 128)[:L]))
-    return k, sc, r, f32(v.view(torch.bfloat16))
+    return k, sc, r, f32(v.view(cache.v.dtype))
 
 
 def _fill(cache, q, lens, bt, seed):
@@ -111,7 +111,7 @@ def test_config2_full_size_vs_oracle(gpu):
     kq, sg, zg, rg, vg = q2_sequence(cache, bt[0], T)
     assert np.array_equal(kq, pk[0]) and np.array_equal(rg, r[0]), "codes / residual"
     assert np.array_equal(sg, s[0]) and np.array_equal(zg, z[0]), "scales / zeros"
-    assert np.array_equal(vg, f32(v)[0]), "V"
+    assert np.array_equal(vg, f32(v.to(cache.v.dtype))[0]), "V (rounded to the pool dtype)"
     o_ref, diag = O.decode(f32(q), pk, s, z, f32(v), r, res_fmt="e4m3fn", BS=64, SBS=64, delta=5.0,
                            scale_mode="g32", out_dtype="bf16")
     far, near, n_near = compare_masks(ws.mask_buf.cpu().numpy(), diag)

@@ -71,7 +71,7 @@ def test_paged_append_bit_exact(gpu, fmt):
     spool = cache.k_scale.view(torch.uint8).cpu().numpy() if fmt == "nvfp4" else f32(cache.k_scale)
     rpool = to_logical(cache.k_res.view(torch.uint8).cpu().numpy(), RES_ORDER)
     vpool = to_logical(cache.v.view(torch.int16).cpu().numpy(), VT_ORDER)
-    vb = v.view(torch.int16).numpy()
+    vb = v.to(cache.v.dtype).view(torch.int16).numpy()
     for b in range(B):
         assert np.array_equal(_gather(kpool, bt, lens, b), pk[b]), "codes"
         assert np.array_equal(_gather(spool, bt, lens, b), sc[b]), "scales"

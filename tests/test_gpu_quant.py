@@ -69,7 +69,7 @@ def test_g32_append_bit_exact(gpu):
     z_pool = to_logical(cache.k_zero.float().cpu().numpy(), GSCALE_ORDER)[..., spos]
     r_pool = to_logical(cache.k_res.view(torch.uint8).cpu().numpy(), RES_ORDER)
     v_pool = to_logical(cache.v.view(torch.int16).cpu().numpy(), VT_ORDER)
-    vb = v.view(torch.int16).numpy()
+    vb = v.to(cache.v.dtype).view(torch.int16).numpy()
     for b in range(B):
         for t in range(0, T, 64):
             page, n = int(bt[b, t // 64]), min(64, T - t)
@@ -153,7 +153,7 @@ def test_kproj_append_multi_token_bit_exact(gpu, B, Tn, H, use_bias):
     z_pool = to_logical(cache.k_zero.float().cpu().numpy(), GSCALE_ORDER)[..., sp]
     r_pool = to_logical(cache.k_res.view(torch.uint8).cpu().numpy(), RES_ORDER)
     v_pool = to_logical(cache.v.view(torch.int16).cpu().numpy(), VT_ORDER)
-    vb = v_new.view(torch.int16).numpy()
+    vb = v_new.to(cache.v.dtype).view(torch.int16).numpy()
     for b in range(B):
         for n in range(Tn):
             t = int(pos[b]) + n
@@ -193,7 +193,7 @@ def test_kproj_append_config5_small(gpu):
     kq_pool = to_logical(cache.k_q.cpu().numpy(), CODES_ORDER, 8)
     s_pool = to_logical(cache.k_scale.float().cpu().numpy(), GSCALE_ORDER)[..., [scale_pos(t) for t in range(64)]]
     r_pool = to_logical(cache.k_res.view(torch.uint8).cpu().numpy(), RES_ORDER)
-    v_pool = torch.from_numpy(to_logical(cache.v.view(torch.int16).cpu().numpy(), VT_ORDER)).view(torch.bfloat16)
+    v_pool = torch.from_numpy(to_logical(cache.v.view(torch.int16).cpu().numpy(), VT_ORDER)).view(cache.v.dtype)
     mism = 0
     for b in range(B):
         page, slot = int(bt[b, int(pos[b]) // 64]), int(pos[b]) % 64
