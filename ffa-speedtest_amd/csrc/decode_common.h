@@ -49,6 +49,12 @@ struct DecodeParams {
   int pass;      // 0, 1 or 2
   float *pmax;   // pass 1 / 2 scratch, [B, HQ, npieces] f32
   int npieces;   // NTBS (SBS <= 512) or nparts (SBS > 512)
+  // mean-V fallback (q2fp8 decode only; null = pruned blocks are dropped): stage 1 also writes,
+  // per query row and partial slot, the maximum am and the sum al = sum 2^(s - am) of the coarse
+  // scores s of the slot's pruned tokens; the merge gives that mass the value v_mean.
+  const void *v_mean;  // [B, HKV, 128], dtype vm_dtype
+  int vm_dtype;
+  float *am_buf, *al_buf;  // [B, HQ, nparts] f32
 };
 
 // The (KV head, query rows) unit of a decode workgroup: grid y = hkv * nq + quad, rows

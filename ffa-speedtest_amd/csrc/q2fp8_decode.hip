@@ -124,6 +124,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   __shared__ float4 s_R[kG ? kChunksPerWG : 1][4][16];
   __shared__ uint64_t s_x[kG ? 1 : kChunksPerWG][kG ? 1 : 4][kG ? 1 : 64];  // channel: codes of kept chunks
   __shared__ float s_pm[kChunksPerWG][4], s_pl[kChunksPerWG][4];
+  __shared__ float s_am[kWaves][4], s_al[kWaves][4];  // mean-V: pruned-token mass per wave and row
   __shared__ __attribute__((aligned(16))) float s_po[kChunksPerWG][4][128];
   // B operands of the 4 score MFMAs, per lane: read once after the operand barrier, long
   // before the exact pass writes s_po (two barriers later), so they share its storage
@@ -460,6 +461,48 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   // prune iff every row of the group is below its threshold (strict <); rows >= G do not vote
 #pragma unroll
   for (int j = 0; j < kPPW; ++j) bal[j] = chunk_ballot(p, row_ok, mb[j], th, s_keep, cw, c0 + j, kc);
+  // whether the prune block holding the lane's 16 tokens survives, from a chunk's ballot
+  auto lane_kept = [&](uint64_t bl) {
+    return SBS == 16   ? ((bl >> (16 * kc)) & 0xffffull) != 0
+           : SBS == 32 ? ((bl >> (32 * (kc >> 1))) & 0xffffffffull) != 0
+                       : bl != 0;
+  };
+
+  // mean-V fallback (attn_kernel_v1210_meanv_bsz_q2fp8.py:109-119): the softmax mass of the
+  // wave's pruned tokens on their coarse scores, max am and sum 2^(s - am) per query row (every
+  // lane of a row holds its scores; the reductions run over the row's four token quarters)
+  if (p.v_mean != nullptr) {
+    bool pr[kPPW];
+    float am = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kPPW; ++j) {
+      const int tl = (c0 + j) * kPage + 16 * kc;  // the lane's first token
+      pr[j] = row_ok && (c0 + j) * kPage < Tb && !lane_kept(bal[j]);
+      if (pr[j]) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+          if (tl + k < Tb) am = fmaxf(am, (R[j][k] * cs1) * kLog2e);
+      }
+    }
+    am = xor_max(am, 16);
+    am = xor_max(am, 32);
+    float al = 0.f;
+#pragma unroll
+    for (int j = 0; j < kPPW; ++j) {
+      const int tl = (c0 + j) * kPage + 16 * kc;
+      if (pr[j]) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+          if (tl + k < Tb) al += exp2f((R[j][k] * cs1) * kLog2e - am);
+      }
+    }
+    al = xor_sum(al, 16);
+    al = xor_sum(al, 32);
+    if (lane < 4) {  // lane == ir
+      s_am[wv][lane] = am;
+      s_al[wv][lane] = al;
+    }
+  }
 
   // publish the kept chunks: coarse scores (g32) or codes (channel scales), page, ballot
 #pragma unroll
@@ -500,10 +543,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     const int t0 = (cw + slot) * kPage;
     const int nvs = min(Tb - t0, kPage);
     const int pgs_ = __builtin_amdgcn_readfirstlane(s_pgid[slot]);
-    const uint64_t bl = ((uint64_t)s_bal[slot][1] << 32) | s_bal[slot][0];
-    const bool keep16 = SBS == 16   ? ((bl >> (16 * kc)) & 0xffffull) != 0
-                        : SBS == 32 ? ((bl >> (32 * (kc >> 1))) & 0xffffffffull) != 0
-                                    : bl != 0;
+    const bool keep16 = lane_kept(((uint64_t)s_bal[slot][1] << 32) | s_bal[slot][0]);
     // residual + V loads (the chunk is kept: whole resource).  In the large-batch build they are
     // issued at raised wave priority, so that the arbiter favours them over the scoring of the
     // other workgroups on the CU (config 5's decode 658 -> 599 us; at config 2, where every
@@ -793,6 +833,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
       if (lane == 0) {
         p.m_buf[row * p.nparts + cg] = A > 0.f ? M : -INFINITY;
         p.l_buf[row * p.nparts + cg] = A;
+        if (p.v_mean != nullptr) {  // the four waves' pruned-token masses of the row
+          float AM = -INFINITY, AL = 0.f;
+#pragma unroll
+          for (int w = 0; w < kWaves; ++w)
+            if (s_al[w][i] > 0.f) AM = fmaxf(AM, s_am[w][i]);
+#pragma unroll
+          for (int w = 0; w < kWaves; ++w)
+            if (s_al[w][i] > 0.f) AL = __builtin_fmaf(s_al[w][i], exp2f(s_am[w][i] - AM), AL);
+          p.am_buf[row * p.nparts + cg] = AL > 0.f ? AM : -INFINITY;
+          p.al_buf[row * p.nparts + cg] = AL;
+        }
       }
       if (A > 0.f) *(float2 *)(p.o_buf + (row * p.nparts + cg) * 128 + c2) = make_float2(ox, oy);
     }
@@ -875,6 +926,23 @@ __device__ __forceinline__ void merge_partials(const DecodeParams &p) {
     }
   }
   A = wave_sum(A);
+  // mean-V fallback: the pruned tokens' mass of every slot (attn_kernel_v1210_meanv_bsz_q2fp8.py:
+  // 172-191, the approximate blocks' running max and sum)
+  float AM = -INFINITY, AL = 0.f;
+  if (p.v_mean != nullptr) {
+    const brsrc ram = make_rsrc(p.am_buf + (size_t)row * p.nparts, nparts * 4);
+    const brsrc ral = make_rsrc(p.al_buf + (size_t)row * p.nparts, nparts * 4);
+    for (int k = lane; k < nparts; k += 64) {
+      const float l = __uint_as_float(bload4(ral, k * 4));
+      if (l > 0.f) AM = fmaxf(AM, __uint_as_float(bload4(ram, k * 4)));
+    }
+    AM = wave_max(AM);
+    for (int k = lane; k < nparts; k += 64) {
+      const float l = __uint_as_float(bload4(ral, k * 4));
+      if (l > 0.f) AL = __builtin_fmaf(l, exp2f(__uint_as_float(bload4(ram, k * 4)) - AM), AL);
+    }
+    AL = wave_sum(AL);
+  }
   // column sums over the 64 lanes through LDS: lane 16 q + c sums column c of lanes 16 q .. 16 q + 15,
   // then the four quarters are added by register exchanges
 #pragma unroll
@@ -888,8 +956,23 @@ __device__ __forceinline__ void merge_partials(const DecodeParams &p) {
   for (int k = 16 * h; k < 16 * h + 16; ++k) sum += s_o[k][c];
   sum += __shfl_xor(sum, 16);
   sum += __shfl_xor(sum, 32);
-  if (lane < 16)
-    store_any(p.out, (size_t)row * 128 + 16 * slab + c, p.out_dtype, A == 0.f ? 0.f : sum / A);
+  if (lane < 16) {
+    float val;
+    if (p.v_mean == nullptr) {
+      val = A == 0.f ? 0.f : sum / A;
+    } else {
+      // kept blocks' o and mass, plus the pruned mass times v_mean, each rescaled to the common
+      // maximum (attn_kernel_v1210_meanv_bsz_q2fp8.py:192-202)
+      const float Mx = fmaxf(A > 0.f ? M : -INFINITY, AL > 0.f ? AM : -INFINITY);
+      const float re = A > 0.f ? exp2f(M - Mx) : 0.f;
+      const float ra = AL > 0.f ? exp2f(AM - Mx) : 0.f;
+      const int hkv = (row - b * p.HQ) / p.G;
+      const float vm = load_any(p.v_mean, ((size_t)b * p.HKV + hkv) * 128 + 16 * slab + c, p.vm_dtype);
+      const float den = A * re + AL * ra;
+      val = den > 0.f ? (sum * re + vm * (AL * ra)) / den : 0.f;
+    }
+    store_any(p.out, (size_t)row * 128 + 16 * slab + c, p.out_dtype, val);
+  }
 }
 
 __global__ __launch_bounds__(64) void q2fp8_merge_kernel(const DecodeParams p) { merge_partials<false>(p); }
@@ -1040,6 +1123,11 @@ static int decode_params(const ffa_q2fp8_decode_args *a, ffa::DecodeParams &p) {
   if (a->nparts < need) return set_err(FFA_E_INVALID, "scratch holds too few partial slots");
   const int ntbs = ((a->T + a->BS - 1) / a->BS) * (a->BS / a->SBS);
   if (a->ntbs < ntbs) return set_err(FFA_E_INVALID, "mask holds too few blocks");
+  if (a->v_mean != nullptr) {
+    if (!(a->v_mean_dtype >= FFA_DT_F16 && a->v_mean_dtype <= FFA_DT_F32)) return set_err(FFA_E_INVALID, "v_mean dtype");
+    if (!a->approx_m || !a->approx_l)
+      return set_err(FFA_E_INVALID, "the mean-V fallback needs approx_m / approx_l scratch [B, HQ, nparts]");
+  }
 
   p.q = a->q;
   p.kq = a->k_q;
@@ -1073,6 +1161,10 @@ static int decode_params(const ffa_q2fp8_decode_args *a, ffa::DecodeParams &p) {
   p.nparts = a->nparts;
   p.ntbs = a->ntbs;
   p.nwg = need;
+  p.v_mean = a->v_mean;
+  p.vm_dtype = a->v_mean_dtype;
+  p.am_buf = a->v_mean ? a->approx_m : nullptr;
+  p.al_buf = a->v_mean ? a->approx_l : nullptr;
   return FFA_OK;
 }
 
@@ -1168,8 +1260,8 @@ extern "C" int ffa_q2fp8_decode_noalloc(const ffa_q2fp8_decode_args *a, void *st
   const size_t npieces = (size_t)ffa_q2fp8_decode_pieces(a->HQ, a->HKV, a->T, a->BS, a->SBS);
   // the size in floating point first, so that no product of the dimensions can wrap
   const double rows = (double)B * (double)HQ;
-  const double need = rows * (double)nparts * 130.0 * 4.0 + (double)B * (double)HKV * (double)ntbs + rows * 4.0 +
-                      rows * (double)npieces * 4.0;
+  const double need = rows * (double)nparts * (a->v_mean ? 132.0 : 130.0) * 4.0 +
+                      (double)B * (double)HKV * (double)ntbs + rows * 4.0 + rows * (double)npieces * 4.0;
   if (need > (double)kStaticScratchBytes) {
     char msg[200];
     snprintf(msg, sizeof(msg), "ffa_q2fp8_decode_noalloc: this shape needs %.0f bytes of scratch, the static array holds %zu",
@@ -1187,6 +1279,8 @@ extern "C" int ffa_q2fp8_decode_noalloc(const ffa_q2fp8_decode_args *a, void *st
   const size_t mask_at = a->mask ? 0 : take(B * HKV * ntbs);
   const size_t th_at = a->threshold_out ? 0 : take(B * HQ * 4);
   const size_t pm_at = npieces ? take(B * HQ * npieces * 4) : 0;
+  const size_t am_at = a->v_mean ? take(B * HQ * nparts * 4) : 0;
+  const size_t al_at = a->v_mean ? take(B * HQ * nparts * 4) : 0;
   if (used > kStaticScratchBytes) {
     char msg[200];
     snprintf(msg, sizeof(msg), "ffa_q2fp8_decode_noalloc: this shape needs %zu bytes of scratch, the static array holds %zu",
@@ -1208,5 +1302,7 @@ extern "C" int ffa_q2fp8_decode_noalloc(const ffa_q2fp8_decode_args *a, void *st
   if (!a->threshold_out) s.threshold_out = reinterpret_cast<float *>(base + th_at);
   s.piece_max = npieces ? reinterpret_cast<float *>(base + pm_at) : nullptr;
   s.npieces = (int)npieces;
+  s.approx_m = a->v_mean ? reinterpret_cast<float *>(base + am_at) : nullptr;
+  s.approx_l = a->v_mean ? reinterpret_cast<float *>(base + al_at) : nullptr;
   return ffa_q2fp8_decode(&s, stream);
 }

@@ -103,24 +103,12 @@ def _normalize_scale_zero(k_scale: torch.Tensor, k_zero: torch.Tensor, expect_sh
     return k_scale.contiguous(), k_zero.contiguous()
 
 
-def attn_forward_decode_quantized(
-    q: torch.Tensor,           # [B, 1, HQ, K]
-    k_q: torch.Tensor,         # [B, T, HKV, ceil(K / (8 / k_bits))], packed quantized ints
-    k_scale: torch.Tensor,     # [B, HKV, K] (token dimension removed)
-    k_zero: torch.Tensor,      # same shape as k_scale
-    v: torch.Tensor,           # [B, T, HKV, V]
-    k_residual: torch.Tensor | None = None,  # [B, T, HKV, K], fp8 residual
-    k_bits: int = 2,
-    scale: float = None,
-    BS: int = 128,
-    SBS: int | None = None,
-    delta: float = 5.0,
-    return_skip_ratio: bool = False,
-    precomputed_threshold: torch.Tensor | None = None,
-    use_fp8_residual: bool = True,
-    workspace: Q2FP8DecodeWorkspace | None = None,
-    **kwargs,
-):
+def _decode(q, k_q, k_scale, k_zero, v, k_residual, k_bits, scale, BS, SBS, delta, precomputed_threshold,
+            use_fp8_residual, workspace, v_mean_of=None, **kwargs):
+    """Argument checks of reference :211-281 and one decode; returns (workspace, seq_lens, HKV, T, BS, SBS).
+
+    v_mean_of(v, layout, block_table, seq_lens, T) (optional, after the checks) gives the mean-V
+    fallback's v_mean [B, HKV, 128]."""
     assert q.is_cuda and k_q.is_cuda and v.is_cuda
     if k_residual is not None and not k_residual.is_cuda:
         raise ValueError("k_residual must be a CUDA tensor when provided")
@@ -183,11 +171,35 @@ def attn_forward_decode_quantized(
 
     if workspace is not None and not isinstance(workspace, DecodeWorkspace):
         raise TypeError("workspace must be a Q2FP8DecodeWorkspace")
+    v_mean = v_mean_of(v, layout, block_table, seq_lens, T) if v_mean_of is not None else None
     ws = run_decode(
         q=q[:, 0], k_q=k_q, k_scale=k_scale, k_zero=k_zero, v=v, k_residual=k_residual, layout=layout,
         scale_mode=smode, T=T, HKV=HKV, scale=scale, BS=BS, SBS=SBS, delta=delta, use_res=use_res,
         precomputed_threshold=precomputed_threshold, block_table=block_table, seq_lens=seq_lens,
-        workspace=workspace)
+        workspace=workspace, v_mean=v_mean)
+    return ws, seq_lens, HKV, T, BS, SBS
+
+
+def attn_forward_decode_quantized(
+    q: torch.Tensor,           # [B, 1, HQ, K]
+    k_q: torch.Tensor,         # [B, T, HKV, ceil(K / (8 / k_bits))], packed quantized ints
+    k_scale: torch.Tensor,     # [B, HKV, K] (token dimension removed)
+    k_zero: torch.Tensor,      # same shape as k_scale
+    v: torch.Tensor,           # [B, T, HKV, V]
+    k_residual: torch.Tensor | None = None,  # [B, T, HKV, K], fp8 residual
+    k_bits: int = 2,
+    scale: float = None,
+    BS: int = 128,
+    SBS: int | None = None,
+    delta: float = 5.0,
+    return_skip_ratio: bool = False,
+    precomputed_threshold: torch.Tensor | None = None,
+    use_fp8_residual: bool = True,
+    workspace: Q2FP8DecodeWorkspace | None = None,
+    **kwargs,
+):
+    ws, seq_lens, HKV, T, BS, SBS = _decode(q, k_q, k_scale, k_zero, v, k_residual, k_bits, scale, BS, SBS, delta,
+                                           precomputed_threshold, use_fp8_residual, workspace, **kwargs)
     o = ws.o
 
     if return_skip_ratio:

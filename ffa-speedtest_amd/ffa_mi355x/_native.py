@@ -27,6 +27,8 @@ EXPORTS = (
     "ffa_q2fp8_decode_stage1",
     "ffa_q2fp8_decode_stage2",
     "ffa_q2fp8_decode_noalloc",
+    "ffa_v_mean_nsplit",
+    "ffa_v_mean",
     "ffa_kfmt_decode",
     "ffa_q2_quantize_nsplit",
     "ffa_q2_quantize_channel",
@@ -100,6 +102,10 @@ class DecodeArgs(ctypes.Structure):
         ("num_pages", ctypes.c_int),
         ("piece_max", ctypes.c_void_p),
         ("npieces", ctypes.c_int),
+        ("v_mean", ctypes.c_void_p),
+        ("v_mean_dtype", ctypes.c_int),
+        ("approx_m", ctypes.c_void_p),
+        ("approx_l", ctypes.c_void_p),
     ]
 
 
@@ -173,6 +179,10 @@ def lib() -> ctypes.CDLL:
                      "ffa_q2fp8_decode_noalloc"):
             getattr(L, name).argtypes = [ctypes.POINTER(DecodeArgs), vp]
             getattr(L, name).restype = ci
+        L.ffa_v_mean_nsplit.argtypes = [ci]
+        L.ffa_v_mean_nsplit.restype = ci
+        L.ffa_v_mean.argtypes = [vp, ci, ci, vp, ci, ci, vp, ci, ci, ci, vp, ci, vp, ci, vp]
+        L.ffa_v_mean.restype = ci
         L.ffa_kfmt_decode.argtypes = [ctypes.POINTER(KfmtArgs), vp]
         L.ffa_kfmt_decode.restype = ci
         L.ffa_q2_quantize_nsplit.argtypes = [ci]

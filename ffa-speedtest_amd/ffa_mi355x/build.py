@@ -17,7 +17,7 @@ INCLUDE = ROOT.parent / "include"
 LIB_NAME = "libffa_mi355x.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 
-SOURCES = ["q2fp8_decode.hip", "kfmt_decode.hip", "q2_quant.hip", "kfmt_quant.hip"]
+SOURCES = ["q2fp8_decode.hip", "kfmt_decode.hip", "q2_quant.hip", "kfmt_quant.hip", "value_mean.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

@@ -45,6 +45,8 @@ class DecodeWorkspace:
     mask_buf holds one byte per prune block [B, HKV, NTBS].  GQA groups of more
     than 4 query rows and prune blocks longer than 512 tokens decode in two
     passes and add piece_max [B, HQ, npieces] (the first pass's block maxima).
+    approx_m / approx_l [B, HQ, nparts] hold the pruned tokens' softmax mass of the mean-V
+    fallback (used only when a decode is given v_mean).
     """
 
     def __init__(self, B, HQ, HKV, T, BS, SBS, device, dtype):
@@ -64,6 +66,8 @@ class DecodeWorkspace:
         self.npieces = decode_pieces(HQ, HKV, T, BS, SBS)
         self.piece_max = (torch.empty((B, HQ, self.npieces), device=device, dtype=torch.float32)
                           if self.npieces else None)
+        self.approx_m = torch.empty((B, HQ, self.nparts), device=device, dtype=torch.float32)
+        self.approx_l = torch.empty((B, HQ, self.nparts), device=device, dtype=torch.float32)
 
     def matches(self, B, HQ, HKV, T, BS, SBS, device, dtype) -> bool:
         return (
@@ -123,9 +127,14 @@ def decode_args(
     block_table=None,
     seq_lens=None,
     workspace: DecodeWorkspace | None = None,
+    v_mean: torch.Tensor | None = None,
 ):
     """Validate one decode step and fill its C argument struct; returns (args, workspace).  The
-    struct holds raw pointers of the tensors passed in: keep them alive until the call."""
+    struct holds raw pointers of the tensors passed in: keep them alive until the call.
+
+    v_mean [B, HKV, 128] (optional) turns on the mean-V fallback: pruned blocks keep their
+    coarse-score softmax mass with v_mean as value (ffa-q2fp8-meanv/attn_kernel/
+    attn_kernel_v1210_meanv_bsz_q2fp8.py:109-119, 156-202)."""
     B, HQ, D = q.shape
     if D != HEAD_DIM:
         raise NotImplementedError(f"head_dim {D} is not supported (this build implements {HEAD_DIM})")
@@ -173,6 +182,15 @@ def decode_args(
     a.ntbs = workspace.NTBS
     a.piece_max = workspace.piece_max.data_ptr() if workspace.piece_max is not None else None
     a.npieces = workspace.npieces
+    if v_mean is not None:
+        if tuple(v_mean.shape) != (B, int(HKV), HEAD_DIM) or v_mean.device != q.device:
+            raise ValueError(f"v_mean must be [B, HKV, {HEAD_DIM}] on the query's device, got {tuple(v_mean.shape)}")
+        if not v_mean.is_contiguous():
+            raise ValueError("v_mean must be contiguous")
+        a.v_mean = v_mean.data_ptr()
+        a.v_mean_dtype = N.dtype_code(v_mean.dtype)
+        a.approx_m = workspace.approx_m.data_ptr()
+        a.approx_l = workspace.approx_l.data_ptr()
     a._keep = th_in  # the converted threshold must outlive the call
     return a, workspace
 

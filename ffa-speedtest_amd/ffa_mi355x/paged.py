@@ -123,12 +123,20 @@ class PagedQ2Cache:
         N.check(rc, "ffa_q2_quantize_g32_append")
 
     # ------------------------------------------------------------------ decode
+    def value_mean(self, block_table, seq_lens=None, *, T=None, out_dtype=None):
+        """Mean over each sequence's tokens of its V pages, [B, HKV, 128] (the mean-V fallback's v_mean)."""
+        from .meanv import value_mean
+
+        return value_mean(self.v, block_table=block_table, seq_lens=seq_lens, T=T, out_dtype=out_dtype)
+
     def decode(self, q, block_table, seq_lens=None, *, T=None, scale=None, BS=64, SBS=None, delta=5.0,
                precomputed_threshold=None, use_fp8_residual=True, workspace: DecodeWorkspace | None = None,
-               stage="both"):
+               stage="both", v_mean=None):
         """Pruned decode of q [B, HQ, 128] (or [B, 1, HQ, 128]) over the paged cache.
 
         stage: "both", or "stage1" (scores, prune, exact partials) / "stage2" (merge) alone.
+        v_mean [B, HKV, 128] (optional): the mean-V fallback (pruned blocks keep their coarse-score
+        mass with v_mean as value), e.g. from value_mean().
         """
         if q.ndim == 4:
             if q.shape[1] != 1:
@@ -151,4 +159,4 @@ class PagedQ2Cache:
             q=q, k_q=self.k_q, k_scale=self.k_scale, k_zero=self.k_zero, v=self.v, k_residual=self.k_res,
             layout=N.LAYOUT_PAGED, scale_mode=N.SCALE_G32, T=T, HKV=self.HKV, scale=scale, BS=BS, SBS=SBS,
             delta=delta, use_res=use_fp8_residual, precomputed_threshold=precomputed_threshold,
-            block_table=block_table, seq_lens=seq_lens, workspace=workspace, stage=stage)
+            block_table=block_table, seq_lens=seq_lens, workspace=workspace, stage=stage, v_mean=v_mean)

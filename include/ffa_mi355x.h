@@ -145,6 +145,15 @@ typedef struct ffa_q2fp8_decode_args {
   int num_pages; /* paged: pages P of every pool (> 0); block-table entries outside [0, P) read page 0 */
   float *piece_max; /* two-pass decodes only (else NULL): [B, HQ, npieces] f32 */
   int npieces;
+  /* Mean-V fallback (ffa-q2fp8-meanv/attn_kernel/attn_kernel_v1210_meanv_bsz_q2fp8.py:109-119,
+   * 156-202): with v_mean non-NULL a pruned block that holds tokens keeps its softmax mass on the
+   * coarse (2-bit) scores, with v_mean as its value:
+   *   out = (sum_kept 2^s v + sum_pruned 2^s_coarse * v_mean) / (sum_kept 2^s + sum_pruned 2^s_coarse).
+   * NULL: pruned blocks are dropped (the q2fp8 decode).  approx_m / approx_l: scratch for the pruned
+   * mass per query row and partial slot. */
+  const void *v_mean; /* [B, HKV, 128], dtype v_mean_dtype (F16 / BF16 / F32), e.g. from ffa_v_mean */
+  int v_mean_dtype;
+  float *approx_m, *approx_l; /* with v_mean: [B, HQ, nparts] f32 each */
 } ffa_q2fp8_decode_args;
 
 /* Number of partial slots per query row the scratch buffers must hold for max length T. */
@@ -158,14 +167,29 @@ int ffa_q2fp8_decode_pieces(int HQ, int HKV, int T, int BS, int SBS);
 int ffa_q2fp8_decode(const ffa_q2fp8_decode_args *args, void *stream);
 
 /*
+ * Mean over each sequence's tokens of V, the mean-V fallback's v_mean (replaces
+ * `v.mean(dim=1, dtype=torch.float32).to(v.dtype)`, ffa-q2fp8-meanv/attn_kernel/
+ * attn_kernel_v1210_meanv_bsz_q2fp8.py:332): fp32 sums, one rounding to out_dtype.
+ *   layout CONTIG: v [B, T, HKV, 128]; PAGED: V^T pages [P, HKV, 128, 64] through block_table
+ *   (entries outside [0, num_pages) read page 0, as in the decode).  seq_lens [B] or NULL (length T).
+ *   out [B, HKV, 128] (0 for an empty sequence); partial: f32 scratch [B, HKV, nsplit, 128] with
+ *   nsplit >= ffa_v_mean_nsplit(T).
+ */
+int ffa_v_mean_nsplit(int T);
+int ffa_v_mean(const void *v, int v_dtype, int layout, const int32_t *block_table, int bt_stride, int num_pages,
+               const int32_t *seq_lens, int B, int T, int HKV, float *partial, int nsplit, void *out, int out_dtype,
+               void *stream);
+
+/*
  * ffa_q2fp8_decode without any caller scratch and without allocating: no counterpart in the
  * reference; for callers that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc).  The caller passes inputs and `out` as for
- * ffa_q2fp8_decode; m_buf, l_buf, o_buf, nparts, piece_max and npieces are ignored; mask (with
- * ntbs) and threshold_out are written when given, else kept in the scratch.  The scratch is a
- * static device array of FFA_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; a shape
- * whose scratch (partials 520 B per query row and 512-token span, plus mask, thresholds and the
- * two-pass maxima) exceeds it returns FFA_E_UNSUPPORTED before any launch.  Calls that overlap on
+ * ffa_q2fp8_decode; m_buf, l_buf, o_buf, nparts, piece_max, npieces, approx_m and approx_l are
+ * ignored; mask (with ntbs) and threshold_out are written when given, else kept in the scratch.
+ * The scratch is a static device array of FFA_NOALLOC_SCRATCH_BYTES per GPU, held until the
+ * process ends; a shape whose scratch (partials 520 B per query row and 512-token span, 8 B more
+ * with v_mean, plus mask, thresholds and the two-pass maxima) exceeds it returns FFA_E_UNSUPPORTED
+ * before any launch.  Calls that overlap on
  * one GPU share the array and race: order them on one stream.
  */
 #define FFA_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)

@@ -17,6 +17,9 @@ checkout):
                          per_channel mode rounds dequantized and refined K to fp16
                          as the reference's tl.dot inputs do (:93, :109-115); g32 mode
                          (no reference counterpart) keeps them exact.
+  decode(v_mean=...)     the mean-V variant, ffa-q2fp8-meanv/attn_kernel/
+                         attn_kernel_v1210_meanv_bsz_q2fp8.py stage1 :109-152, stage2 :156-202
+* value_mean             the same file :332 (v.mean(dim=1, dtype=float32).to(v.dtype))
 * threshold_external     ffa-fp8/attn_kernel/attn_kernel_v1208_fused_bsz_fp8.py:174-234
 * decode_bruteforce      same semantics as `decode`, written as scalar loops
                          for tiny shapes (an independent second statement).
@@ -246,6 +249,7 @@ def decode(
     khat=None,
     khat_probe1=None,
     pv_dtype: str = "fp16",
+    v_mean=None,
 ):
     """Appendix-A decode semantics over the contiguous layout.
 
@@ -262,6 +266,10 @@ def decode(
     pv_dtype: the type p and v are rounded to for P.V, "fp16" as the reference casts
     both (attn_kernel...q2fp8.py:130-131); "bf16" exists only for tests that show a
     bf16 P operand is caught.
+    v_mean [B,HKV,DV] (optional): the mean-V variant (..._meanv_bsz_q2fp8.py): a pruned
+    block holding tokens keeps m = max of its coarse scores and l = sum 2^(s - m) (:109-119);
+    stage 2 merges kept and approximated blocks apart and folds l with v_mean (:172-202).
+    diag then has 'approx' [B,HKV,NTBS] and 'approx_ratio' = approx.sum()/approx.size (:326-330).
 
     Returns (o [B,HQ,DV] float32 holding out_dtype values, diag dict with
     'mask' [B,HKV,NTBS] int8, 'threshold' [B,HQ], 'block_max' [B,HQ,NTBS]
@@ -290,6 +298,7 @@ def decode(
     margin = np.full((B, HKV, NTBS_max), -np.inf, F32)
     m_out = np.full((B, HQ, NTBS_max), -np.inf, F32)
     l_out = np.zeros((B, HQ, NTBS_max), F32)
+    approx = np.zeros((B, HKV, NTBS_max), np.int8)
     ntbs = []
     kept_total = 0
     blocks_total = 0
@@ -335,7 +344,25 @@ def decode(
             mask[b, h, :NTBS] = keep
             kept = np.nonzero(keep)[0]
             kept_total += len(kept)
+            # mean-V: pruned blocks holding tokens, their coarse max and mass (meanv :109-119)
+            Mp = np.full(G, -np.inf)
+            Ap = np.zeros(G)
+            if v_mean is not None:
+                apx = np.nonzero(~keep & valid.any(axis=1))[0]
+                approx[b, h, apx] = 1
+                if len(apx):
+                    Sa = np.where(valid[apx][:, :, None], Sq[idx[apx]], -np.inf).astype(np.float64)  # [A, SBS, G]
+                    ma = Sa.max(axis=1)  # [A, G]
+                    la = np.where(valid[apx][:, :, None], np.exp2(Sa - ma[:, None, :]), 0.0).astype(F32).astype(
+                        np.float64).sum(axis=1)  # [A, G]
+                    Mp = ma.max(axis=0)
+                    Ap = (la * np.exp2(ma - Mp[None, :])).sum(axis=0)
             if len(kept) == 0:
+                if v_mean is not None:
+                    vm = np.asarray(v_mean, np.float64)[b, h]  # [DV]
+                    with np.errstate(invalid="ignore", divide="ignore"):
+                        out = np.where(Ap[:, None] > 0, (vm[None, :] * Ap[:, None]) / Ap[:, None], 0.0)
+                    o[b, h * G:(h + 1) * G] = round_to(out.astype(F32), out_dtype)
                 continue
             if use_res:
                 r16 = fp8_decode(k_residual[b, :Tb, h], res_fmt)  # exact in fp16
@@ -364,6 +391,14 @@ def decode(
                 w = np.where(np.isfinite(mf), np.exp2(mf - M[None, :]), 0.0)  # [K, G]
             A = (lsum.astype(np.float64) * w).sum(axis=0)
             O = (ob * w[:, :, None]).sum(axis=0)  # [G, DV]
+            if v_mean is not None:  # meanv stage 2 fold (:192-202)
+                vm = np.asarray(v_mean, np.float64)[b, h]
+                Mx = np.maximum(np.where(A > 0, M, -np.inf), np.where(Ap > 0, Mp, -np.inf))
+                with np.errstate(invalid="ignore"):
+                    rb = np.where(A > 0, np.exp2(M - Mx), 0.0)
+                    rp = np.where(Ap > 0, np.exp2(Mp - Mx), 0.0)
+                O = O * rb[:, None] + vm[None, :] * (Ap * rp)[:, None]
+                A = A * rb + Ap * rp
             with np.errstate(invalid="ignore", divide="ignore"):
                 out = np.where(A[:, None] == 0.0, 0.0, O / A[:, None])
             o[b, h * G:(h + 1) * G] = round_to(out.astype(F32), out_dtype)
@@ -378,7 +413,24 @@ def decode(
         ntbs=ntbs,
         skip_ratio=1.0 - kept_total / max(blocks_total, 1),
     )
+    if v_mean is not None:
+        diag["approx"] = approx
+        diag["approx_ratio"] = float(approx.sum()) / max(blocks_total, 1)
     return o, diag
+
+
+def value_mean(v, seq_lens=None, out_dtype: str = "bf16"):
+    """Mean over tokens of v [B,T,HKV,DV] per (b, head), rounded once to out_dtype
+    (..._meanv_bsz_q2fp8.py:332; the sum is exact here, fp32 in the reference).  With seq_lens each
+    sequence averages its own tokens, and an empty one gives 0."""
+    v = np.asarray(v, np.float64)
+    B, T = v.shape[:2]
+    lens = [T] * B if seq_lens is None else [min(max(int(x), 0), T) for x in seq_lens]
+    out = np.zeros((B,) + v.shape[2:], np.float64)
+    for b, L in enumerate(lens):
+        if L > 0:
+            out[b] = v[b, :L].sum(axis=0) / L
+    return round_to(out.astype(F32), out_dtype)
 
 
 def threshold_external(q, k_fp16, scale, NTB, delta, HKV, HQ, T_BS_: int = T_BS):

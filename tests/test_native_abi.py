@@ -150,6 +150,27 @@ def test_drop_in_signatures_match_reference():
     assert sig.parameters["use_fp8_residual"].default is True
 
 
+def test_meanv_drop_in_loads_and_keeps_the_reference_signature():
+    """ffa-q2fp8-meanv's two modules load (the mean-V one loads the q2fp8 drop-in while it loads)
+    and keep the reference signature (..._meanv_bsz_q2fp8.py:222-238)."""
+    import torch
+
+    from ffa_mi355x.dropins import _ROOT, _load
+
+    base = _ROOT / "ffa-q2fp8-meanv" / "attn_kernel"
+    M = _load("ffa_mi355x_meanv_dropin", base / "attn_kernel_v1210_meanv_bsz_q2fp8.py")
+    F = _load("ffa_mi355x_meanv_fused_copy", base / "attn_kernel_v1210_fused_bsz_q2fp8.py")
+    ref = ["q", "k_q", "k_scale", "k_zero", "v", "k_residual", "k_bits", "scale", "BS", "SBS", "delta",
+           "return_skip_ratio", "precomputed_threshold", "use_fp8_residual"]
+    for mod in (M, F):
+        params = list(inspect.signature(mod.attn_forward_decode_quantized).parameters)
+        assert params[: len(ref)] == ref
+    assert inspect.signature(M.attn_forward_decode_quantized).parameters["BS"].default == 128
+    with pytest.raises(AssertionError):  # CPU tensors, as the reference's first check
+        M.attn_forward_decode_quantized(torch.zeros(1, 1, 4, 128), torch.zeros(1, 8, 1, 32, dtype=torch.uint8),
+                                        torch.zeros(1, 1, 128), torch.zeros(1, 1, 128), torch.zeros(1, 8, 1, 128))
+
+
 def test_drop_in_rejects_cpu_tensors():
     import torch
 

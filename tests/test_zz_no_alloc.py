@@ -84,3 +84,24 @@ def test_noalloc_refuses_shapes_beyond_the_static_array(gpu):
     a.T = 1 << 20
     rc = N.lib().ffa_q2fp8_decode_noalloc(ctypes.byref(a), ctypes.c_void_p(N.stream_of(gpu)))
     assert rc == -2 and b"static array" in N.lib().ffa_last_error()
+
+
+def test_noalloc_mean_v(gpu):
+    """The mean-V fallback through the no-allocation entry point: its pruned-mass scratch is carved
+    from the static array too (approx_m / approx_l cleared here); bit-identical to the decode."""
+    c = paged_case(B=2, T=3000, HQ=32, HKV=8, seed=54, n_heavy=8, seq_lens=[3000, 1700])
+    cache = to_gpu_paged(c, gpu)
+    kw, (q, bt, sl) = _args(c, cache, gpu, 64, 64, 3.0, c["lens"])
+    kw["v_mean"] = cache.value_mean(bt, sl, T=kw["T"])
+    ws = D.run_decode(**kw)
+    torch.cuda.synchronize()
+    a, _ = D.decode_args(**kw)
+    out = torch.full_like(ws.o, float("nan"))
+    a.out = out.data_ptr()
+    a.m_buf = a.l_buf = a.o_buf = a.approx_m = a.approx_l = None
+    a.nparts = 0
+    a.mask, a.threshold_out = None, None
+    rc = N.lib().ffa_q2fp8_decode_noalloc(ctypes.byref(a), ctypes.c_void_p(N.stream_of(gpu)))
+    N.check(rc, "ffa_q2fp8_decode_noalloc")
+    torch.cuda.synchronize()
+    assert torch.equal(out, ws.o)
