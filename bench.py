@@ -197,20 +197,59 @@ def _graph_time(step, R, reps, stream, per_graph=1):
 def bench_config2_reference_layout(args):
     """Config 2's inputs in the reference's contiguous per-channel layout, quantized by the HIP port of the
     reference quantizer and decoded through the stage-1 + merge launches; 24 rotated copies."""
+    from ffa_mi355x import synth
+
+    t_setup = time.perf_counter()
+    q, k, v = synth.attention_inputs(B=1, T=args.T, HQ=32, HKV=8, D=128, seed=0, n_heavy=16, cos=0.8)
+    _bench_contiguous(args, q, k, v, t_setup, WORKLOADS["config2ref"],
+                      "config2 (reference layout) decode-attn us/step + HBM TB/s on the algorithmic bytes",
+                      "synthetic (seeded N(0,1) bf16 with planted heavy tokens)")
+
+
+def bench_layer_data(args):
+    """Recorded layers (the reference's layer_data/layer_i/{q_rope,k_rope,v}.pt, read tensors-only by
+    ffa_mi355x.layer_data): layers --layer .. --layer + --bsz - 1 stacked along the batch, the decode of the
+    last recorded token (or --max-length) over the reference layout, as run_attn_bench_q2.py:146-170, 256-283
+    does with these files."""
+    import torch
+
+    from ffa_mi355x import layer_data as LD
+
+    if not args.layer_data:
+        print(json.dumps({"error": "--workload layerdata needs --layer-data DIR (a layer_data directory)"}))
+        sys.exit(2)
+    t_setup = time.perf_counter()
+    dt = {"bf16": torch.bfloat16, "fp16": torch.float16}[args.dtype]
+    qr, kr, vr = LD.load_layer_batch(args.layer_data, range(args.layer, args.layer + args.bsz), dt,
+                                     max_length=args.max_length)
+    q, k, v = LD.decode_step_inputs(qr, kr, vr)
+    B, HQ, D = q.shape
+    T, HKV = k.shape[1], k.shape[2]
+    desc = (f"recorded layers {args.layer}..{args.layer + args.bsz - 1} of {args.layer_data} as the batch "
+            f"(B={B}, T={T}, {HQ}/{HKV}/{D}), reference per-channel layout, BS={args.BS}, SBS={args.SBS}, "
+            f"delta={args.delta}")
+    _bench_contiguous(args, q, k, v, t_setup, desc,
+                      "recorded-layer q2fp8 decode-attn us/step + HBM TB/s on the algorithmic bytes",
+                      f"recorded ({args.dtype})")
+
+
+def _bench_contiguous(args, q, k, v, t_setup, workload, metric, data):
+    """q [B, HQ, D], k / v [B, T, HKV, D] (host or device): the reference quantizer (HIP port), then the
+    stage-1 + merge launches over R rotated copies of the cache in one HIP graph."""
     import torch
 
     from ffa_mi355x import _native as N
-    from ffa_mi355x import quant, synth
+    from ffa_mi355x import quant
     from ffa_mi355x.decode import DecodeWorkspace, run_decode
 
     dev = torch.device("cuda:0")
-    B, HQ, HKV, D, T, BS, SBS, R = 1, 32, 8, 128, args.T, args.BS, args.SBS, args.rotations
-    t_setup = time.perf_counter()
-    q, k, v = synth.attention_inputs(B=B, T=T, HQ=HQ, HKV=HKV, D=D, seed=0, n_heavy=16, cos=0.8)
+    B, HQ, D = q.shape
+    T, HKV = k.shape[1], k.shape[2]
+    BS, SBS, R = args.BS, args.SBS, args.rotations
     qd, vd = q.to(dev), v.to(dev)
     kq, ks, kz, kr = quant.quantize_per_channel(k.to(dev), torch.float8_e5m2)
     copies = [(kq.clone(), kr.clone(), vd.clone()) for _ in range(R)]
-    ws = DecodeWorkspace(B, HQ, HKV, T, BS, SBS, dev, torch.bfloat16)
+    ws = DecodeWorkspace(B, HQ, HKV, T, BS, SBS, dev, qd.dtype)
     scale = 1.0 / math.sqrt(D)
 
     def step(r):
@@ -233,12 +272,13 @@ def bench_config2_reference_layout(args):
     nbytes = T * HKV * (D // 4) + B * HKV * D * 2 * 2 + kept_th * _KEPT + B * HQ * D * 4
     gbs = nbytes / (us * 1e-6) / 1e9
     line = {
-        "metric": "config2 (reference layout) decode-attn us/step + HBM TB/s on the algorithmic bytes",
+        "metric": metric,
         "value": round(us, 3), "unit": "us/step", "n_gpus": 1, "steps": steps, "warmup": _warm(R),
         "ms_per_step": round(us / 1e3, 6), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-        "dtype": "q2 per-channel + e5m2 residual K, bf16 V; f16 MFMA (P.V on fp16 p and fp16 v), f32 accumulate",
-        "data": "synthetic (seeded N(0,1) bf16 with planted heavy tokens)",
-        "config": {"workload": WORKLOADS["config2ref"], "B": B, "T": T, "HQ": HQ, "HKV": HKV, "D": D, "BS": BS,
+        "dtype": f"q2 per-channel + e5m2 residual K, {str(vd.dtype).replace('torch.', '')} V; f16 MFMA (P.V on fp16 p "
+                 "and fp16 v), f32 accumulate",
+        "data": data,
+        "config": {"workload": workload, "B": B, "T": T, "HQ": HQ, "HKV": HKV, "D": D, "BS": BS,
                    "SBS": SBS, "delta": args.delta, "keep_fraction": round(keep_frac, 4), "algorithmic_bytes": nbytes,
                    "rotations": R, "timing": "HIP graph of R steps (decode + merge), hipEvents over the replays"},
         "decode_hbm_tbps": round(gbs / 1e3, 4),
@@ -471,8 +511,14 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run 5 device copies of 256 MiB (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
-    ap.add_argument("--workload", choices=("config2",) + tuple(WORKLOADS), default="config2",
-                    help="config2 (default) is the metric's line; config2ref, config1/3/4/5 time the other BASELINE decodes")
+    ap.add_argument("--workload", choices=("config2", "layerdata") + tuple(WORKLOADS), default="config2",
+                    help="config2 (default) is the metric's line; config2ref, config1/3/4/5 time the other BASELINE "
+                         "decodes; layerdata times recorded layers (--layer-data)")
+    ap.add_argument("--layer-data", default=None, help="layerdata: a layer_data directory (layer_0, layer_1, ...)")
+    ap.add_argument("--layer", type=int, default=0, help="layerdata: first layer")
+    ap.add_argument("--bsz", type=int, default=1, help="layerdata: consecutive layers stacked as the batch")
+    ap.add_argument("--max-length", type=int, default=None, help="layerdata: cut the recorded tokens to this many")
+    ap.add_argument("--dtype", choices=("bf16", "fp16"), default="bf16", help="layerdata: q / k / v dtype")
     args = ap.parse_args()
     if args.copy_probe:
         import torch
@@ -496,6 +542,9 @@ def main():
         return
     if args.workload == "config2ref":
         bench_config2_reference_layout(args)
+        return
+    if args.workload == "layerdata":
+        bench_layer_data(args)
         return
     if args.workload != "config2":
         bench_workload(args)
