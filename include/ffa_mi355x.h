@@ -16,6 +16,9 @@
  *                             attn_forward_stage1_fused_threshold_qbits :10-139)
  *   ffa_q2fp8_decode_stage2   the stage-2 launch alone (:299-304, kernel
  *                             attn_forward_stage2_masked :142-171)
+ *   ffa_q2fp8_decode with     ffa-q2fp8-meanv/attn_kernel/attn_kernel_v1210_meanv_bsz_q2fp8.py
+ *     v_mean set              (the mean-V variant: stage 1 :10-153, stage 2 :156-202)
+ *   ffa_v_mean                the same file :332 (v.mean(dim=1, dtype=float32).to(v.dtype))
  *   ffa_q2_quantize_channel   ffa-q2fp8/run_attn_bench_q2.py:78-105
  *                             (quantize_k_2bit_fp8_residual; same as
  *                              ffa-q2fp8/fused_kproj_rope_q2fp8.py:40-68)
