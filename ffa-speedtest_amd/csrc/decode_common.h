@@ -188,6 +188,12 @@ __device__ __forceinline__ void write_empty_mask(int8_t *mask_row, int cg, int S
     if (jb < ntbs) mask_row[jb] = 0;
   }
 }
+// 2^x on the hardware exponential (v_exp_f32, about 1 ulp).  The arguments are differences of
+// log2-scaled scores, x <= 0; a result below 2^-126, which exp2f would return as a denormal after
+// a range fix-up (five more instructions), is 0 here: far below the fp16 P operand's 2^-24 and the
+// fp32 sums' resolution.
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
 enum { kChannel = 0, kG32 = 1 };
 enum { kResNone = 0, kResE4M3 = 1, kResE5M2 = 2 };
 enum { kVF16 = 0, kVBF16 = 1 };

@@ -569,7 +569,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
     float lsum = 0.f;
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
-      const float e = (P[k] == -INFINITY) ? 0.f : exp2f(P[k] - mrow_max);
+      const float e = (P[k] == -INFINITY) ? 0.f : exp2_hw(P[k] - mrow_max);
       P[k] = e;
       lsum += e;
     }
@@ -721,7 +721,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
         if (!((km >> ps) & 1u)) continue;
         const float l = s_pl[ps][i];
         if (l > 0.f) {
-          const float wgt = exp2f(s_pm[ps][i] - M);
+          const float wgt = exp2_hw(s_pm[ps][i] - M);
           A = __builtin_fmaf(l, wgt, A);
           ox = __builtin_fmaf(s_po[ps][i][c2], wgt, ox);
           oy = __builtin_fmaf(s_po[ps][i][c2 + 1], wgt, oy);

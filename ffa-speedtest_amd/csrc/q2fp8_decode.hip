@@ -493,7 +493,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
       if (pr[j]) {
 #pragma unroll
         for (int k = 0; k < 16; ++k)
-          if (tl + k < Tb) al += exp2f((R[j][k] * cs1) * kLog2e - am);
+          if (tl + k < Tb) al += exp2_hw((R[j][k] * cs1) * kLog2e - am);
       }
     }
     al = xor_sum(al, 16);
@@ -667,7 +667,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     float lsum = 0.f;
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
-      const float e = (P[k] == -INFINITY) ? 0.f : exp2f(P[k] - mrow_max);
+      const float e = (P[k] == -INFINITY) ? 0.f : exp2_hw(P[k] - mrow_max);
       P[k] = e;
       lsum += e;
     }
@@ -823,7 +823,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
         if (!((km >> ps) & 1u)) continue;
         const float l = s_pl[ps][i];
         if (l > 0.f) {
-          const float wgt = exp2f(s_pm[ps][i] - M);
+          const float wgt = exp2_hw(s_pm[ps][i] - M);
           A = __builtin_fmaf(l, wgt, A);
           ox = __builtin_fmaf(s_po[ps][i][c2], wgt, ox);
           oy = __builtin_fmaf(s_po[ps][i][c2 + 1], wgt, oy);
@@ -840,7 +840,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
             if (s_al[w][i] > 0.f) AM = fmaxf(AM, s_am[w][i]);
 #pragma unroll
           for (int w = 0; w < kWaves; ++w)
-            if (s_al[w][i] > 0.f) AL = __builtin_fmaf(s_al[w][i], exp2f(s_am[w][i] - AM), AL);
+            if (s_al[w][i] > 0.f) AL = __builtin_fmaf(s_al[w][i], exp2_hw(s_am[w][i] - AM), AL);
           p.am_buf[row * p.nparts + cg] = AL > 0.f ? AM : -INFINITY;
           p.al_buf[row * p.nparts + cg] = AL;
         }
@@ -900,7 +900,7 @@ __device__ __forceinline__ void merge_partials(const DecodeParams &p) {
   {
     // o is used only where l > 0: a slot whose span kept nothing holds no defined values
     const bool keep = l0 > 0.f;
-    const float wgt = keep ? exp2f(m0 - M) : 0.f;
+    const float wgt = keep ? exp2_hw(m0 - M) : 0.f;
     A = keep ? l0 * wgt : 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -913,7 +913,7 @@ __device__ __forceinline__ void merge_partials(const DecodeParams &p) {
   for (int k = lane + 64; k < nparts; k += 64) {
     const float l = __uint_as_float(bload4(rl, k * 4));
     if (l > 0.f) {
-      const float wgt = exp2f(__uint_as_float(bload4(rm, k * 4)) - M);
+      const float wgt = exp2_hw(__uint_as_float(bload4(rm, k * 4)) - M);
       A = __builtin_fmaf(l, wgt, A);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -939,7 +939,7 @@ __device__ __forceinline__ void merge_partials(const DecodeParams &p) {
     AM = wave_max(AM);
     for (int k = lane; k < nparts; k += 64) {
       const float l = __uint_as_float(bload4(ral, k * 4));
-      if (l > 0.f) AL = __builtin_fmaf(l, exp2f(__uint_as_float(bload4(ram, k * 4)) - AM), AL);
+      if (l > 0.f) AL = __builtin_fmaf(l, exp2_hw(__uint_as_float(bload4(ram, k * 4)) - AM), AL);
     }
     AL = wave_sum(AL);
   }
@@ -964,8 +964,8 @@ __device__ __forceinline__ void merge_partials(const DecodeParams &p) {
       // kept blocks' o and mass, plus the pruned mass times v_mean, each rescaled to the common
       // maximum (attn_kernel_v1210_meanv_bsz_q2fp8.py:192-202)
       const float Mx = fmaxf(A > 0.f ? M : -INFINITY, AL > 0.f ? AM : -INFINITY);
-      const float re = A > 0.f ? exp2f(M - Mx) : 0.f;
-      const float ra = AL > 0.f ? exp2f(AM - Mx) : 0.f;
+      const float re = A > 0.f ? exp2_hw(M - Mx) : 0.f;
+      const float ra = AL > 0.f ? exp2_hw(AM - Mx) : 0.f;
       const int hkv = (row - b * p.HQ) / p.G;
       const float vm = load_any(p.v_mean, ((size_t)b * p.HKV + hkv) * 128 + 16 * slab + c, p.vm_dtype);
       const float den = A * re + AL * ra;
