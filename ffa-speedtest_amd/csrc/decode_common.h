@@ -11,6 +11,8 @@ constexpr int kPage = 64;
 constexpr int kWaves = 4;
 constexpr int kPPW = 2;                      // 64-token chunks (pages) per wave
 constexpr int kChunksPerWG = kWaves * kPPW;  // 512 tokens per workgroup
+constexpr int kMinSpan = 2;                  // smallest span (chunks per workgroup) of a small grid
+constexpr int kSmallSpanTokens = 8192;       // sequences up to this many tokens get slots for it
 constexpr int kVRow = 260;      // LDS row pitch (bytes) of a staged V tile: 256 + 4 keeps banks apart
 constexpr int kVRowHalf = 132;  // the same for half a tile (64 columns)
 
@@ -55,7 +57,14 @@ struct DecodeParams {
   const void *v_mean;  // [B, HKV, 128], dtype vm_dtype
   int vm_dtype;
   float *am_buf, *al_buf;  // [B, HQ, nparts] f32
+  // 64-token chunks per workgroup (one partial slot each): kChunksPerWG, or 4 / 2 when a small grid
+  // would leave CUs idle (the other-format decoder, one pass, SBS <= 64); each wave then owns one
+  // chunk, and waves past the span only help with the operands, the probe and the merge
+  int span;
 };
+
+// chunks per decode workgroup of a launch (0 in the struct means the default span)
+__device__ __forceinline__ int decode_span(const DecodeParams &p) { return p.span > 0 ? p.span : kChunksPerWG; }
 
 // The (KV head, query rows) unit of a decode workgroup: grid y = hkv * nq + quad, rows
 // 4 quad .. 4 quad + Gu - 1 of the GQA group (query heads row0 ..).
@@ -176,13 +185,13 @@ __device__ __forceinline__ int append_page(const int32_t *bt, int bt_stride, int
 // A decode workgroup whose 512 tokens all lie past its sequence's end (ragged batches) writes
 // its survivor-mask bytes (all 0) and nothing else: the merge reads no partial slot past the
 // sequence end, and the threshold is written by the sequence's first workgroup.
-__device__ __forceinline__ void write_empty_mask(int8_t *mask_row, int cg, int SBS, int ntbs) {
-  if (SBS > kChunksPerWG * kPage) {  // a block of several spans: its first span writes its byte
-    const int jb = cg * kChunksPerWG * kPage / SBS;
-    if (threadIdx.x == 0 && (cg * kChunksPerWG * kPage) % SBS == 0 && jb < ntbs) mask_row[jb] = 0;
+__device__ __forceinline__ void write_empty_mask(int8_t *mask_row, int cg, int SBS, int ntbs, int span = kChunksPerWG) {
+  if (SBS > span * kPage) {  // a block of several spans: its first span writes its byte
+    const int jb = cg * span * kPage / SBS;
+    if (threadIdx.x == 0 && (cg * span * kPage) % SBS == 0 && jb < ntbs) mask_row[jb] = 0;
     return;
   }
-  const int nblk = kChunksPerWG * kPage / SBS;
+  const int nblk = span * kPage / SBS;
   for (int t = threadIdx.x; t < nblk; t += blockDim.x) {
     const int jb = cg * nblk + t;
     if (jb < ntbs) mask_row[jb] = 0;

@@ -30,6 +30,7 @@
 extern "C" int ffa_set_error_internal(int code, const char *msg);
 extern "C" int ffa_decode_shape_check(int B, int T, int HQ, int HKV, int BS, int SBS, float *piece_max, int npieces,
                                       const float *th_in, const float *th_out, ffa::DecodeParams *p);
+extern "C" int ffa_decode_slots(int T, int BS, int span);
 
 namespace ffa {
 
@@ -95,9 +96,19 @@ void kfmt_decode_kernel(const DecodeParams p) {
   const DecodeUnit un = decode_unit(p);  // KV head and the (at most 4) query rows of this workgroup
   const int hkv = un.hkv;
   const int b = blockIdx.z;
-  const int cw = cg * kChunksPerWG;
-  const int c0 = cw + wv * kPPW;
+  // span: chunks of this workgroup (8, or 4 / 2 for small grids, where each wave owns one chunk
+  // and waves past the span own none); slot (w, j) = wave w's j-th chunk
+  const int span = decode_span(p);
+  const int ppw = span >= kChunksPerWG ? kPPW : 1;
+  const int cw = cg * span;
+  const int c0 = cw + wv * ppw;
   const int SBS = p.SBS;
+  bool own[kPPW];
+#pragma unroll
+  for (int j = 0; j < kPPW; ++j) own[j] = j < ppw && wv * ppw + j < span;
+  // first chunk of slot sl (and whether the slot holds a chunk of this workgroup)
+  auto slot_chunk = [&](int sl) { return cw + (sl >> 1) * ppw + (sl & 1); };
+  auto slot_owned = [&](int sl) { return (sl & 1) < ppw && (sl >> 1) * ppw + (sl & 1) < span; };
 
   const int mrow = lane & 15;
   const int kc = lane >> 4;
@@ -122,7 +133,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
   // ------------------------------------------------ phase 1: loads (issued on every path)
   const int Tb = p.seq_lens ? min(max(p.seq_lens[b], 0), p.T) : p.T;  // lengths beyond T are clamped to T
   if (cg > 0 && cw * kPage >= Tb) {  // every token past the sequence end: mask bytes only
-    if (p.pass != 1 && un.quad == 0) write_empty_mask(p.mask + ((size_t)b * p.HKV + hkv) * p.ntbs, cg, SBS, p.ntbs);
+    if (p.pass != 1 && un.quad == 0) write_empty_mask(p.mask + ((size_t)b * p.HKV + hkv) * p.ntbs, cg, SBS, p.ntbs, span);
     return;
   }
   if (threadIdx.x < kChunksPerWG * kPage / 16) s_keep[threadIdx.x] = 0;
@@ -131,9 +142,9 @@ void kfmt_decode_kernel(const DecodeParams p) {
   const int NTBk = (p.T + p.BS - 1) / p.BS;  // blocks of the block-scale tensor
   const bool do_probe = (p.th_in == nullptr) && wv < 2;
   const int pa = wv == 0 ? 0 : max(NTB - 1, 0) * 16;  // probe window (attn_kernel...q2fp8.py:58-73)
-  int nv[kPPW];
+  int nv[kPPW];  // valid tokens of the wave's chunks (0 for a chunk it does not own)
 #pragma unroll
-  for (int j = 0; j < kPPW; ++j) nv[j] = min(max(Tb - (c0 + j) * kPage, 0), kPage);
+  for (int j = 0; j < kPPW; ++j) nv[j] = own[j] ? min(max(Tb - (c0 + j) * kPage, 0), kPage) : 0;
 
   uint32_t pg_lane = 0;
   if constexpr (LAYOUT == kPaged) {
@@ -384,7 +395,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
   auto score_page = [&](auto J) {
     constexpr int j = decltype(J)::value;
     const int t0 = (c0 + j) * kPage;
-    if (t0 < Tb) {
+    if (nv[j] > 0) {
 #pragma unroll
       for (int tau = 0; tau < 4; ++tau) {
         float r4[4];
@@ -400,7 +411,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
     }  // a page past the sequence end leaves R[j] unset: lane_max gives -inf and it is never kept
   };
   auto lane_max = [&](int j) -> float {
-    if ((c0 + j) * kPage >= Tb) return -INFINITY;
+    if (nv[j] <= 0) return -INFINITY;
     float m = R[j][0];
 #pragma unroll
     for (int k = 1; k < 16; ++k) m = fmaxf(m, R[j][k]);
@@ -442,6 +453,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
 #pragma unroll
   for (int j = 0; j < kPPW; ++j) {
     bal[j] = chunk_ballot(p, row_ok, mb[j], th, s_keep, cw, c0 + j, kc);
+    if (nv[j] <= 0) bal[j] = 0;  // past the sequence end, or not this wave's chunk
     const int slot = wv * kPPW + j;
     if (lane == 0) {
       s_bal[slot][0] = (uint32_t)bal[j];
@@ -673,9 +685,9 @@ void kfmt_decode_kernel(const DecodeParams p) {
       s_pl[slot][lane] = 0.f;
     }
   };
-  if ((c0 + 0) * kPage < Tb && bal[0] != 0) exact_chunk(std::integral_constant<int, 0>());
+  if (nv[0] > 0 && bal[0] != 0) exact_chunk(std::integral_constant<int, 0>());
   else empty_chunk(wv * kPPW);
-  if ((c0 + 1) * kPage < Tb && bal[1] != 0) exact_chunk(std::integral_constant<int, 1>());
+  if (nv[1] > 0 && bal[1] != 0) exact_chunk(std::integral_constant<int, 1>());
   else empty_chunk(wv * kPPW + 1);
 
   // ------------------------------------------------ phase 4: mask, threshold, workgroup partial
@@ -685,10 +697,10 @@ void kfmt_decode_kernel(const DecodeParams p) {
     const int t = threadIdx.x;
     if (SBS <= kPage) {
       const int per = kPage / SBS;
-      if (t < kChunksPerWG * per) {
+      if (t < kChunksPerWG * per && slot_owned(t / per)) {
         const int slot = t / per, k = t - slot * per;
         const uint64_t bl = ((uint64_t)s_bal[slot][1] << 32) | s_bal[slot][0];
-        const int jb = (cw + slot) * per + k;
+        const int jb = slot_chunk(slot) * per + k;
         const bool kk = SBS == 16   ? ((bl >> (16 * k)) & 0xffffull) != 0
                         : SBS == 32 ? ((bl >> (32 * k)) & 0xffffffffull) != 0
                                     : bl != 0;
@@ -814,7 +826,7 @@ extern "C" int ffa_kfmt_decode(const ffa_kfmt_decode_args *a, void *stream) {
   if (scaled && !(a->scale_dtype >= FFA_DT_F16 && a->scale_dtype <= FFA_DT_F32))
     return ffa_set_error_internal(FFA_E_INVALID, "scale dtype");
   if (scaled && !a->k_scale) return ffa_set_error_internal(FFA_E_INVALID, "scale pointer is null");
-  const int need = ffa_q2fp8_decode_nparts(a->T, a->BS, a->SBS);
+  const int need = ffa_decode_slots(a->T, a->BS, ffa::kChunksPerWG);
   if (a->nparts < need) return ffa_set_error_internal(FFA_E_INVALID, "scratch holds too few partial slots");
   const int ntbs = ((a->T + a->BS - 1) / a->BS) * (a->BS / a->SBS);
   if (a->ntbs < ntbs) return ffa_set_error_internal(FFA_E_INVALID, "mask holds too few blocks");
@@ -860,9 +872,24 @@ extern "C" int ffa_kfmt_decode(const ffa_kfmt_decode_args *a, void *stream) {
   p.nparts = a->nparts;
   p.ntbs = a->ntbs;
   p.nwg = need;
+  p.span = ffa::kChunksPerWG;
+  // small grids (fewer workgroups than CUs): shorter spans, one chunk per wave, while the slots
+  // fit the caller's scratch.  One pass with prune blocks of at most one chunk only (the longer
+  // blocks' maxima span two chunks of a wave).
+  if (p.pmax == nullptr && a->SBS <= ffa::kPage) {
+    const int cus = ffa::device_cus();
+    const long units = (long)a->B * a->HKV * p.nq;
+    for (int span = ffa::kChunksPerWG / 2; span >= ffa::kMinSpan; span /= 2) {
+      if (cus <= 0 || units * p.nwg >= cus) break;
+      const int slots = ffa_decode_slots(a->T, a->BS, span);
+      if (slots > a->nparts) break;
+      p.span = span;
+      p.nwg = slots;
+    }
+  }
 
   hipStream_t st = (hipStream_t)stream;
-  const dim3 grid(need, a->HKV * p.nq, a->B);
+  const dim3 grid(p.nwg, a->HKV * p.nq, a->B);
   // one pass (pass 0), or (G > 4, SBS > 512) the maxima pass 1 and then the deciding pass 2
   const bool two = p.pmax != nullptr;
   for (int pass = two ? 1 : 0; pass <= (two ? 2 : 0); ++pass) {

@@ -864,7 +864,8 @@ __device__ __forceinline__ void merge_partials(const DecodeParams &p) {
   const int b = row / p.HQ;
   const int lane = threadIdx.x;
   const int Tb = p.seq_lens ? min(max(p.seq_lens[b], 0), p.T) : p.T;  // lengths beyond T are clamped to T
-  const int nparts = min((Tb + kChunksPerWG * kPage - 1) / (kChunksPerWG * kPage), p.nparts);
+  const int span_tok = decode_span(p) * kPage;
+  const int nparts = min((Tb + span_tok - 1) / span_tok, p.nparts);
   const brsrc rm = make_rsrc(p.m_buf + (size_t)row * p.nparts, nparts * 4);
   const brsrc rl = make_rsrc(p.l_buf + (size_t)row * p.nparts, nparts * 4);
   const brsrc ro = make_rsrc(p.o_buf + (size_t)row * p.nparts * 128 + 16 * slab, nparts > 0 ? ((nparts - 1) * 128 + 16) * 4 : 0);
@@ -1006,11 +1007,20 @@ extern "C" __attribute__((visibility("hidden"))) int ffa_set_error_internal(int 
 }
 extern "C" const char *ffa_version(void) { return "ffa_mi355x 0.1 (gfx950)"; }
 
+// Partial slots per query row of a launch whose workgroups cover `span` chunks: the sub-blocks
+// cover ceil(T/BS)*BS tokens.
+extern "C" __attribute__((visibility("hidden"))) int ffa_decode_slots(int T, int BS, int span) {
+  if (T <= 0 || BS <= 0 || span <= 0) return 0;
+  const long tokens = (long)((T + BS - 1) / BS) * BS;
+  const long span_tok = (long)span * ffa::kPage;
+  return (int)((tokens + span_tok - 1) / span_tok);
+}
+
 extern "C" int ffa_q2fp8_decode_nparts(int T, int BS, int SBS) {
   if (T <= 0 || BS <= 0 || SBS <= 0) return 0;
-  const long ntb = (T + BS - 1) / BS;
-  const long tokens = ntb * BS;  // the sub-blocks cover ceil(T/BS)*BS tokens
-  return (int)((tokens + ffa::kChunksPerWG * ffa::kPage - 1) / (ffa::kChunksPerWG * ffa::kPage));
+  // short sequences may decode with two-chunk workgroups (small grids): room for their slots
+  const long tokens = (long)((T + BS - 1) / BS) * BS;
+  return ffa_decode_slots(T, BS, tokens <= ffa::kSmallSpanTokens ? ffa::kMinSpan : ffa::kChunksPerWG);
 }
 
 extern "C" int ffa_q2fp8_decode_pieces(int HQ, int HKV, int T, int BS, int SBS) {
@@ -1018,7 +1028,7 @@ extern "C" int ffa_q2fp8_decode_pieces(int HQ, int HKV, int T, int BS, int SBS) 
   const int G = HQ / HKV;
   const int span = ffa::kChunksPerWG * ffa::kPage;
   if (G <= 4 && SBS <= span) return 0;  // one pass
-  if (SBS > span) return ffa_q2fp8_decode_nparts(T, BS, SBS);
+  if (SBS > span) return ffa_decode_slots(T, BS, ffa::kChunksPerWG);  // one piece per 512-token span
   return (int)(((long)T + BS - 1) / BS * (BS / SBS));
 }
 
@@ -1119,7 +1129,7 @@ static int decode_params(const ffa_q2fp8_decode_args *a, ffa::DecodeParams &p) {
     return set_err(FFA_E_UNSUPPORTED, "contiguous layout supports per-channel scales only");
   if (a->scale_mode == FFA_SCALE_G32 && a->scale_dtype != FFA_DT_F16)
     return set_err(FFA_E_INVALID, "g32 scales must be fp16");
-  const int need = ffa_q2fp8_decode_nparts(a->T, a->BS, a->SBS);
+  const int need = ffa_decode_slots(a->T, a->BS, ffa::kChunksPerWG);
   if (a->nparts < need) return set_err(FFA_E_INVALID, "scratch holds too few partial slots");
   const int ntbs = ((a->T + a->BS - 1) / a->BS) * (a->BS / a->SBS);
   if (a->ntbs < ntbs) return set_err(FFA_E_INVALID, "mask holds too few blocks");
@@ -1161,6 +1171,7 @@ static int decode_params(const ffa_q2fp8_decode_args *a, ffa::DecodeParams &p) {
   p.nparts = a->nparts;
   p.ntbs = a->ntbs;
   p.nwg = need;
+  p.span = ffa::kChunksPerWG;
   p.v_mean = a->v_mean;
   p.vm_dtype = a->v_mean_dtype;
   p.am_buf = a->v_mean ? a->approx_m : nullptr;
