@@ -98,9 +98,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   const DecodeUnit un = decode_unit(p);  // KV head and the (at most 4) query rows of this workgroup
   const int hkv = un.hkv;
   const int b = blockIdx.z;
-  const int cw = cg * kChunksPerWG;  // first chunk of the workgroup
-  const int c0 = cw + wv * kPPW;     // first chunk scored by this wave
+  // span: chunks of this workgroup (8, or 4 / 2 for small grids, where each wave owns one chunk and
+  // waves past the span own none); slot (w, j) = wave w's j-th chunk
+  const int span = decode_span(p);
+  const int ppw = span >= kChunksPerWG ? kPPW : 1;
+  const int cw = cg * span;      // first chunk of the workgroup
+  const int c0 = cw + wv * ppw;  // first chunk scored by this wave
   const int SBS = p.SBS;
+  bool own[kPPW];
+#pragma unroll
+  for (int j = 0; j < kPPW; ++j) own[j] = j < ppw && wv * ppw + j < span;
+  auto slot_chunk = [&](int sl) { return cw + (sl >> 1) * ppw + (sl & 1); };  // chunk of slot sl
+  auto slot_owned = [&](int sl) { return (sl & 1) < ppw && (sl >> 1) * ppw + (sl & 1) < span; };
 
   const int mrow = lane & 15;  // MFMA row (A) / column (B) index
   const int kc = lane >> 4;    // k-chunk of the operands == channel group of the A lane
@@ -147,7 +156,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   // every element of the operand this wave builds.
   const int Tb = p.seq_lens ? min(max(p.seq_lens[b], 0), p.T) : p.T;  // lengths beyond T are clamped to T
   if (cg > 0 && cw * kPage >= Tb) {  // every token past the sequence end: mask bytes only
-    if (p.pass != 1 && un.quad == 0) write_empty_mask(p.mask + ((size_t)b * p.HKV + hkv) * p.ntbs, cg, SBS, p.ntbs);
+    if (p.pass != 1 && un.quad == 0) write_empty_mask(p.mask + ((size_t)b * p.HKV + hkv) * p.ntbs, cg, SBS, p.ntbs, span);
     return;
   }
   if (threadIdx.x < kChunksPerWG * kPage / 16) s_keep[threadIdx.x] = 0;
@@ -155,9 +164,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   const int NTBS_b = NTB * (p.BS / p.SBS);
   const bool do_probe = (p.th_in == nullptr) && wv < 2;
   const int pa = wv == 0 ? 0 : max(NTB - 1, 0) * 16;  // probe window (attn_kernel...q2fp8.py:58-73)
-  int nv[kPPW];                                       // valid tokens of the wave's chunks
+  int nv[kPPW];  // valid tokens of the wave's chunks (0 for a chunk it does not own)
 #pragma unroll
-  for (int j = 0; j < kPPW; ++j) nv[j] = min(max(Tb - (c0 + j) * kPage, 0), kPage);
+  for (int j = 0; j < kPPW; ++j) nv[j] = own[j] ? min(max(Tb - (c0 + j) * kPage, 0), kPage) : 0;
 
   int pg[kPPW] = {0, 0};
   int ppg = 0;
@@ -390,7 +399,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   auto score_page = [&](auto J) {
     constexpr int j = decltype(J)::value;
     const int t0 = (c0 + j) * kPage;
-    if (t0 < Tb) {
+    if (nv[j] > 0) {
       const uint32_t sw[8] = {gs[j][0].x, gs[j][0].y, gs[j][0].z, gs[j][0].w,
                               gs[j][1].x, gs[j][1].y, gs[j][1].z, gs[j][1].w};
       const uint32_t zw[8] = {gz[j][0].x, gz[j][0].y, gz[j][0].z, gz[j][0].w,
@@ -413,7 +422,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   // when the block spans several 16-token sub-blocks
   auto lane_max = [&](auto J) -> float {
     constexpr int j = decltype(J)::value;
-    if ((c0 + j) * kPage >= Tb) return -INFINITY;
+    if (nv[j] <= 0) return -INFINITY;
     float m = R[j][0];
 #pragma unroll
     for (int k = 1; k < 16; ++k) m = fmaxf(m, R[j][k]);
@@ -460,7 +469,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   }
   // prune iff every row of the group is below its threshold (strict <); rows >= G do not vote
 #pragma unroll
-  for (int j = 0; j < kPPW; ++j) bal[j] = chunk_ballot(p, row_ok, mb[j], th, s_keep, cw, c0 + j, kc);
+  for (int j = 0; j < kPPW; ++j) bal[j] = nv[j] > 0 ? chunk_ballot(p, row_ok, mb[j], th, s_keep, cw, c0 + j, kc) : 0;
   // whether the prune block holding the lane's 16 tokens survives, from a chunk's ballot
   auto lane_kept = [&](uint64_t bl) {
     return SBS == 16   ? ((bl >> (16 * kc)) & 0xffffull) != 0
@@ -477,7 +486,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
 #pragma unroll
     for (int j = 0; j < kPPW; ++j) {
       const int tl = (c0 + j) * kPage + 16 * kc;  // the lane's first token
-      pr[j] = row_ok && (c0 + j) * kPage < Tb && !lane_kept(bal[j]);
+      pr[j] = row_ok && nv[j] > 0 && !lane_kept(bal[j]);
       if (pr[j]) {
 #pragma unroll
         for (int k = 0; k < 16; ++k)
@@ -508,7 +517,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
 #pragma unroll
   for (int j = 0; j < kPPW; ++j) {
     const int slot = wv * kPPW + j;
-    const bool kept = (c0 + j) * kPage < Tb && bal[j] != 0;
+    const bool kept = nv[j] > 0 && bal[j] != 0;
     if (lane == 0) {
       s_kept[slot] = kept ? 1 : 0;
       s_pgid[slot] = pg[j];
@@ -540,7 +549,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   km = __builtin_amdgcn_readfirstlane(km);
 
   auto exact_chunk = [&](int slot) {
-    const int t0 = (cw + slot) * kPage;
+    const int t0 = slot_chunk(slot) * kPage;
     const int nvs = min(Tb - t0, kPage);
     const int pgs_ = __builtin_amdgcn_readfirstlane(s_pgid[slot]);
     const bool keep16 = lane_kept(((uint64_t)s_bal[slot][1] << 32) | s_bal[slot][0]);
@@ -791,10 +800,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     const int t = threadIdx.x;
     if (SBS <= kPage) {
       const int per = kPage / SBS;
-      if (t < kChunksPerWG * per) {
+      if (t < kChunksPerWG * per && slot_owned(t / per)) {
         const int slot = t / per, k = t - slot * per;
         const uint64_t bl = ((uint64_t)s_bal[slot][1] << 32) | s_bal[slot][0];
-        const int jb = (cw + slot) * per + k;
+        const int jb = slot_chunk(slot) * per + k;
         const bool kk = SBS == 16   ? ((bl >> (16 * k)) & 0xffffull) != 0
                         : SBS == 32 ? ((bl >> (32 * k)) & 0xffffffffull) != 0
                                     : bl != 0;
@@ -1172,6 +1181,19 @@ static int decode_params(const ffa_q2fp8_decode_args *a, ffa::DecodeParams &p) {
   p.ntbs = a->ntbs;
   p.nwg = need;
   p.span = ffa::kChunksPerWG;
+  // small grids (fewer workgroups than CUs): shorter spans, one chunk per wave, while the slots fit
+  // the caller's scratch.  One pass with prune blocks of at most one chunk only.
+  if (p.pmax == nullptr && a->SBS <= ffa::kPage) {
+    const int cus = ffa::device_cus();
+    const long units = (long)a->B * a->HKV * p.nq;
+    for (int span = ffa::kChunksPerWG / 2; span >= ffa::kMinSpan; span /= 2) {
+      if (cus <= 0 || units * p.nwg >= cus) break;
+      const int slots = ffa_decode_slots(a->T, a->BS, span);
+      if (slots > a->nparts) break;
+      p.span = span;
+      p.nwg = slots;
+    }
+  }
   p.v_mean = a->v_mean;
   p.vm_dtype = a->v_mean_dtype;
   p.am_buf = a->v_mean ? a->approx_m : nullptr;
