@@ -97,8 +97,9 @@ void kfmt_decode_kernel(const DecodeParams p) {
   const int hkv = un.hkv;
   const int b = blockIdx.z;
   // span: chunks of this workgroup (8, or 4 / 2 for small grids, where each wave owns one chunk
-  // and waves past the span own none); slot (w, j) = wave w's j-th chunk
-  const int span = decode_span(p);
+  // and waves past the span own none); slot (w, j) = wave w's j-th chunk.  The paged build serves
+  // large batches and keeps the whole span as a constant (the runtime form costs it registers)
+  const int span = LAYOUT == kPaged ? kChunksPerWG : decode_span(p);
   const int ppw = span >= kChunksPerWG ? kPPW : 1;
   const int cw = cg * span;
   const int c0 = cw + wv * ppw;
@@ -873,10 +874,10 @@ extern "C" int ffa_kfmt_decode(const ffa_kfmt_decode_args *a, void *stream) {
   p.ntbs = a->ntbs;
   p.nwg = need;
   p.span = ffa::kChunksPerWG;
-  // small grids (fewer workgroups than CUs): shorter spans, one chunk per wave, while the slots
-  // fit the caller's scratch.  One pass with prune blocks of at most one chunk only (the longer
-  // blocks' maxima span two chunks of a wave).
-  if (p.pmax == nullptr && a->SBS <= ffa::kPage) {
+  // small grids (fewer workgroups than CUs) of the contiguous layouts: shorter spans, one chunk
+  // per wave, while the slots fit the caller's scratch.  One pass with prune blocks of at most one
+  // chunk only (the longer blocks' maxima span two chunks of a wave).
+  if (!paged && p.pmax == nullptr && a->SBS <= ffa::kPage) {
     const int cus = ffa::device_cus();
     const long units = (long)a->B * a->HKV * p.nq;
     for (int span = ffa::kChunksPerWG / 2; span >= ffa::kMinSpan; span /= 2) {
