@@ -37,13 +37,17 @@ namespace ffa {
 enum { kF8E4M3 = 0, kF8E5M2 = 1, kFP4 = 2, kNF4 = 3 };
 enum { kSclNone = 0, kSclToken = 1, kSclBlock = 2, kSclChannel = 3, kSclG16 = 4, kSclG64 = 5 };
 
-// fp16(a * sa) in the low half and fp16(b * sb) in the high half, each product in fp32 and then
-// rounded to fp16: v_fma_mixlo / v_fma_mixhi with a zero addend write one half and keep the other,
-// which saves the shift and OR of packing two separately rounded halves
+// fp16(a * sa) in the low half and fp16(b * sb) in the high half: the compiler turns each rounded
+// fma with a zero addend into v_fma_mixlo_f16 / v_fma_mixhi_f16, which write one half and keep the
+// other (no shift and OR to pack two separately rounded halves).  Written in C rather than inline
+// assembly so that the compiler sees the two VALU writes and pads them before the MFMA that reads
+// the register: an asm block is opaque to its hazard checks, and with one wait state between the
+// asm's write and the MFMA (two are required) the MFMA could read the register's previous value.
 __device__ __forceinline__ uint32_t mul_pack_f16(float a, float sa, float b, float sb) {
-  uint32_t r;
-  asm("v_fma_mixlo_f16 %0, %1, %2, 0\n\tv_fma_mixhi_f16 %0, %3, %4, 0" : "=&v"(r) : "v"(a), "v"(sa), "v"(b), "v"(sb));
-  return r;
+  const _Float16 lo = (_Float16)__builtin_fmaf(a, sa, 0.f);
+  const _Float16 hi = (_Float16)__builtin_fmaf(b, sb, 0.f);
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, h2{lo, hi});
 }
 
 // QLoRA NF4 levels (the published 16 normal-float values), as fp32

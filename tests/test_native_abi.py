@@ -340,3 +340,20 @@ def test_page_orders_match_the_kernels(tmp_path):
     got = [np.array(line.split(), dtype=np.int64) for line in lines]
     for g, order in zip(got, (PG.RES_ORDER, PG.VT_ORDER, PG.CODES_ORDER, PG.GSCALE_ORDER, PG.K4_ORDER)):
         assert np.array_equal(g, order.ravel())
+
+
+def test_kernel_sources_have_no_register_writing_inline_asm():
+    """Inline assembly is opaque to the compiler's hazard checks: a VALU write inside an asm block
+    gets the wait states the compiler would give an unknown instruction, not the two an MFMA read of
+    the same register needs, so the MFMA can read the register's previous value (a deterministic
+    wrong score that comes and goes with register allocation).  The kernels keep only asm that
+    writes no register: waits and barriers, and empty constraint-only statements."""
+    allowed = {"", "s_waitcnt lgkmcnt(0)\\n\\ts_barrier"}
+    found = []
+    for src in sorted((ROOT / "ffa-speedtest_amd" / "csrc").glob("*.[hc]*")):
+        text = re.sub(r"//[^\n]*", "", src.read_text())
+        for m in re.finditer(r"\basm\s*(?:volatile\s*)?\(\s*\"((?:[^\"\\]|\\.)*)\"", text):
+            found.append((src.name, m.group(1)))
+    assert found, "no asm statements found: the pattern no longer matches the sources"
+    bad = [(f, body) for f, body in found if body not in allowed]
+    assert not bad, f"inline asm that emits instructions other than waits and barriers: {bad}"
