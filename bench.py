@@ -478,9 +478,10 @@ def bench_workload(args):
         "metric": f"{wl} decode-attn us/step + HBM TB/s on the algorithmic bytes",
         "value": round(us, 3), "unit": "us/step", "n_gpus": 1, "steps": steps, "warmup": _warm(R),
         "ms_per_step": round(us / 1e3, 6), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-        "dtype": {"config3": "e2m1 K x e4m3 g16 scale + e4m3 residual, bf16 V",
-                  "config4": "nf4 K x fp16 g64 absmax + e4m3 residual, bf16 V",
-                  "config5": "bf16 K-proj (f32 accumulate); q2 g32 + e4m3 residual K, bf16 V"}[wl]
+        "dtype": {"config3": "e2m1 K x e4m3 g16 scale + e4m3 residual, bf16 V held as fp16 V^T pages",
+                  "config4": "nf4 K x fp16 g64 absmax + e4m3 residual, bf16 V held as fp16 V^T pages",
+                  "config5": "bf16 K-proj (f32 accumulate); q2 g32 + e4m3 residual K, bf16 V held as fp16 V^T "
+                             "pages"}[wl]
                  + "; f16 MFMA (P.V on fp16 p and fp16 v), f32 accumulate",
         "data": "synthetic (N(0,1) bf16 drawn on the device per sequence, 16 heavy tokens per query head)",
         "config": {"workload": WORKLOADS[wl], "B": B, "T_max": T, "tokens": sum(final), "HQ": HQ, "HKV": HKV,
