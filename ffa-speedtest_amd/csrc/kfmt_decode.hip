@@ -723,26 +723,29 @@ void kfmt_decode_kernel(const DecodeParams p) {
     const int i = wv;
     const int c2 = 2 * lane;
     if (i < un.Gu) {
-      // slots whose ballot is empty hold no partial: skipped by scalar branches
-      uint32_t km = 0;
+      // Every slot's m, l and o columns in one batch of LDS reads, then selects (reads issued slot by
+      // slot behind branches on l were dependent LDS round trips at the end of every workgroup).  A
+      // slot without a kept chunk has l = 0 (empty_chunk); its o was never written and is selected
+      // away, not weighted by 0.
+      float pm[kChunksPerWG], pl[kChunksPerWG];
+      float2 po[kChunksPerWG];
 #pragma unroll
-      for (int sl = 0; sl < kChunksPerWG; ++sl) km |= ((s_bal[sl][0] | s_bal[sl][1]) != 0u ? 1u : 0u) << sl;
-      km = __builtin_amdgcn_readfirstlane(km);
+      for (int ps = 0; ps < kChunksPerWG; ++ps) {
+        pm[ps] = s_pm[ps][i];
+        pl[ps] = s_pl[ps][i];
+        po[ps] = *reinterpret_cast<const float2 *>(&s_po[ps][i][c2]);
+      }
       float M = -INFINITY;
 #pragma unroll
-      for (int ps = 0; ps < kChunksPerWG; ++ps)
-        if (((km >> ps) & 1u) && s_pl[ps][i] > 0.f) M = fmaxf(M, s_pm[ps][i]);
+      for (int ps = 0; ps < kChunksPerWG; ++ps) M = pl[ps] > 0.f ? fmaxf(M, pm[ps]) : M;
       float A = 0.f, ox = 0.f, oy = 0.f;
 #pragma unroll
       for (int ps = 0; ps < kChunksPerWG; ++ps) {
-        if (!((km >> ps) & 1u)) continue;
-        const float l = s_pl[ps][i];
-        if (l > 0.f) {
-          const float wgt = exp2_hw(s_pm[ps][i] - M);
-          A = __builtin_fmaf(l, wgt, A);
-          ox = __builtin_fmaf(s_po[ps][i][c2], wgt, ox);
-          oy = __builtin_fmaf(s_po[ps][i][c2 + 1], wgt, oy);
-        }
+        const bool use = pl[ps] > 0.f;
+        const float wgt = exp2_hw(use ? pm[ps] - M : -INFINITY);
+        A = use ? __builtin_fmaf(pl[ps], wgt, A) : A;
+        ox = use ? __builtin_fmaf(po[ps].x, wgt, ox) : ox;
+        oy = use ? __builtin_fmaf(po[ps].y, wgt, oy) : oy;
       }
       const size_t row = (size_t)b * p.HQ + un.row0 + i;
       if (lane == 0) {

@@ -548,6 +548,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   for (int sl = 0; sl < kChunksPerWG; ++sl) km |= (s_kept[sl] != 0 ? 1u : 0u) << sl;
   km = __builtin_amdgcn_readfirstlane(km);
 
+  // Survivor mask, one byte per prune block (attn_kernel...q2fp8.py:99-104): final once the chunks
+  // are published, so each thread's byte and address are worked out here, off the workgroup's
+  // tail, and stored in phase 4 (stores come last).  mask_at < 0: this thread writes no byte.
+  int mask_at = -1;
+  int8_t mask_byte = 0;
+  if (un.quad == 0) {
+    const int t = threadIdx.x;
+    if (SBS <= kPage) {
+      const int lp = SBS == 16 ? 2 : (SBS == 32 ? 1 : 0);  // blocks per chunk = 1 << lp
+      const int slot = t >> lp, k = t & ((1 << lp) - 1);
+      if (t < (kChunksPerWG << lp) && slot_owned(slot)) {
+        const uint64_t bl = ((uint64_t)s_bal[slot][1] << 32) | s_bal[slot][0];
+        const int jb = (slot_chunk(slot) << lp) + k;
+        const bool kk = SBS == 16   ? ((bl >> (16 * k)) & 0xffffull) != 0
+                        : SBS == 32 ? ((bl >> (32 * k)) & 0xffffffffull) != 0
+                                    : bl != 0;
+        if (jb < p.ntbs) {
+          mask_at = jb;
+          mask_byte = (jb < NTBS_b && kk) ? 1 : 0;
+        }
+      }
+    } else if (t < kChunksPerWG && ((cw + t) * kPage) % SBS == 0) {
+      const int jb = (cw + t) * kPage / SBS;
+      const bool kk = (s_bal[t][0] | s_bal[t][1]) != 0;
+      if (jb < p.ntbs) {
+        mask_at = jb;
+        mask_byte = (jb < NTBS_b && kk) ? 1 : 0;
+      }
+    }
+  }
+
   auto exact_chunk = [&](int slot) {
     const int t0 = slot_chunk(slot) * kPage;
     const int nvs = min(Tb - t0, kPage);
@@ -794,62 +825,54 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   // Global stores come last: on gfx9 stores share the vector memory counter with loads, and a
   // pending store would make every later load wait a full write round trip.
   __syncthreads();
-  if (un.quad == 0) {
-    // survivor mask, one byte per prune block (attn_kernel...q2fp8.py:99-104)
-    int8_t *mrow_ptr = p.mask + ((size_t)b * p.HKV + hkv) * p.ntbs;
-    const int t = threadIdx.x;
-    if (SBS <= kPage) {
-      const int per = kPage / SBS;
-      if (t < kChunksPerWG * per && slot_owned(t / per)) {
-        const int slot = t / per, k = t - slot * per;
-        const uint64_t bl = ((uint64_t)s_bal[slot][1] << 32) | s_bal[slot][0];
-        const int jb = slot_chunk(slot) * per + k;
-        const bool kk = SBS == 16   ? ((bl >> (16 * k)) & 0xffffull) != 0
-                        : SBS == 32 ? ((bl >> (32 * k)) & 0xffffffffull) != 0
-                                    : bl != 0;
-        if (jb < p.ntbs) mrow_ptr[jb] = (jb < NTBS_b && kk) ? 1 : 0;
-      }
-    } else if (t < kChunksPerWG && ((cw + t) * kPage) % SBS == 0) {
-      const int jb = (cw + t) * kPage / SBS;
-      const bool kk = (s_bal[t][0] | s_bal[t][1]) != 0;
-      if (jb < p.ntbs) mrow_ptr[jb] = (jb < NTBS_b && kk) ? 1 : 0;
-    }
-  }
+  if (mask_at >= 0) p.mask[((size_t)b * p.HKV + hkv) * p.ntbs + mask_at] = mask_byte;
   if (p.pass == 0 && p.th_out != nullptr && cg == 0 && threadIdx.x < un.Gu)
     p.th_out[(size_t)b * p.HQ + un.row0 + threadIdx.x] = th;  // (pass 2: written by pass 1)
   {
     const int i = wv;         // query row handled by this wave
     const int c2 = 2 * lane;  // columns c2, c2 + 1
     if (i < un.Gu) {
-      // only kept chunks hold partials (km, uniform): the others are skipped by scalar branches
+      // Every slot's m, l and o columns in one batch of LDS reads, then selects: reads issued slot
+      // by slot behind branches on l were ~40 dependent LDS round trips (about 1 us) at the end of
+      // every workgroup with a kept chunk.  A slot without a kept chunk has l = 0 (written when the
+      // chunks were published); its o was never written and is selected away, not weighted by 0.
+      float pm[kChunksPerWG], pl[kChunksPerWG];
+      float2 po[kChunksPerWG];
+#pragma unroll
+      for (int ps = 0; ps < kChunksPerWG; ++ps) {
+        pm[ps] = s_pm[ps][i];
+        pl[ps] = s_pl[ps][i];
+        po[ps] = *reinterpret_cast<const float2 *>(&s_po[ps][i][c2]);
+      }
       float M = -INFINITY;
 #pragma unroll
-      for (int ps = 0; ps < kChunksPerWG; ++ps)
-        if (((km >> ps) & 1u) && s_pl[ps][i] > 0.f) M = fmaxf(M, s_pm[ps][i]);
+      for (int ps = 0; ps < kChunksPerWG; ++ps) M = pl[ps] > 0.f ? fmaxf(M, pm[ps]) : M;
       float A = 0.f, ox = 0.f, oy = 0.f;
 #pragma unroll
       for (int ps = 0; ps < kChunksPerWG; ++ps) {
-        if (!((km >> ps) & 1u)) continue;
-        const float l = s_pl[ps][i];
-        if (l > 0.f) {
-          const float wgt = exp2_hw(s_pm[ps][i] - M);
-          A = __builtin_fmaf(l, wgt, A);
-          ox = __builtin_fmaf(s_po[ps][i][c2], wgt, ox);
-          oy = __builtin_fmaf(s_po[ps][i][c2 + 1], wgt, oy);
-        }
+        const bool use = pl[ps] > 0.f;
+        const float wgt = exp2_hw(use ? pm[ps] - M : -INFINITY);
+        A = use ? __builtin_fmaf(pl[ps], wgt, A) : A;
+        ox = use ? __builtin_fmaf(po[ps].x, wgt, ox) : ox;
+        oy = use ? __builtin_fmaf(po[ps].y, wgt, oy) : oy;
       }
       const size_t row = (size_t)b * p.HQ + un.row0 + i;
       if (lane == 0) {
         p.m_buf[row * p.nparts + cg] = A > 0.f ? M : -INFINITY;
         p.l_buf[row * p.nparts + cg] = A;
         if (p.v_mean != nullptr) {  // the four waves' pruned-token masses of the row
+          float am[kWaves], al[kWaves];  // one batch of LDS reads, as above
+#pragma unroll
+          for (int w = 0; w < kWaves; ++w) {
+            am[w] = s_am[w][i];
+            al[w] = s_al[w][i];
+          }
           float AM = -INFINITY, AL = 0.f;
 #pragma unroll
-          for (int w = 0; w < kWaves; ++w)
-            if (s_al[w][i] > 0.f) AM = fmaxf(AM, s_am[w][i]);
+          for (int w = 0; w < kWaves; ++w) AM = al[w] > 0.f ? fmaxf(AM, am[w]) : AM;
 #pragma unroll
           for (int w = 0; w < kWaves; ++w)
-            if (s_al[w][i] > 0.f) AL = __builtin_fmaf(s_al[w][i], exp2_hw(s_am[w][i] - AM), AL);
+            AL = al[w] > 0.f ? __builtin_fmaf(al[w], exp2_hw(am[w] - AM), AL) : AL;
           p.am_buf[row * p.nparts + cg] = AL > 0.f ? AM : -INFINITY;
           p.al_buf[row * p.nparts + cg] = AL;
         }
