@@ -205,5 +205,21 @@ __device__ __forceinline__ uint64_t bload8u(brsrc r, uint32_t off) {
   const uint2 v = bload8(r, off);
   return ((uint64_t)v.y << 32) | v.x;
 }
+// The same loads with the non-temporal hint (cache-policy bit 1, `nt` on gfx950), for data a launch
+// reads once: the cache pages a decode streams (codes, scales, residual, V).  Data that several
+// workgroups re-read (q, probe windows, page ids) keeps the default policy.
+constexpr int kNonTemporal = 2;
+__device__ __forceinline__ uint4 bload16_nt(brsrc r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kNonTemporal);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint2 bload8_nt(brsrc r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, kNonTemporal);
+  return make_uint2(v[0], v[1]);
+}
+__device__ __forceinline__ uint64_t bload8u_nt(brsrc r, uint32_t off) {
+  const uint2 v = bload8_nt(r, off);
+  return ((uint64_t)v.y << 32) | v.x;
+}
 
 }  // namespace ffa

@@ -230,7 +230,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
       const size_t blk = (size_t)pg[j] * p.HKV + hkv;
       const brsrc rc = make_rsrc(p.kq + blk * (4 * kPage * 8), nv[j] > 0 ? 4 * kPage * 8 : 0);
       // tokens 4 mrow + (0, 1) and 4 mrow + (2, 3) of group kc: two 1 KB blocks, lane-ordered
-      const uint4 q0 = bload16(rc, lane * 16), q1 = bload16(rc, (64 + lane) * 16);
+      const uint4 q0 = bload16_nt(rc, lane * 16), q1 = bload16_nt(rc, (64 + lane) * 16);
       x[j][0] = ((uint64_t)q0.y << 32) | q0.x;
       x[j][1] = ((uint64_t)q0.w << 32) | q0.z;
       x[j][2] = ((uint64_t)q1.y << 32) | q1.x;
@@ -240,16 +240,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
         const brsrc rz = make_rsrc((const uint16_t *)p.kz + blk * (4 * kPage), nv[j] > 0 ? 4 * kPage * 2 : 0);
         // slots 16 kc + (0..7) and 16 kc + (8..15) of group jg
         const uint32_t so0 = gscale_off(jg, 16 * kc) * 2, so1 = gscale_off(jg, 16 * kc + 8) * 2;
-        gs[j][0] = bload16(rs, so0);
-        gs[j][1] = bload16(rs, so1);
-        gz[j][0] = bload16(rz, so0);
-        gz[j][1] = bload16(rz, so1);
+        gs[j][0] = bload16_nt(rs, so0);
+        gs[j][1] = bload16_nt(rs, so1);
+        gz[j][0] = bload16_nt(rz, so0);
+        gz[j][1] = bload16_nt(rz, so1);
       }
     } else {
       const size_t base = (((size_t)b * p.T + t0) * p.HKV + hkv) * 32;
       const brsrc rc = make_rsrc(p.kq + base, nv[j] > 0 ? ((nv[j] - 1) * p.HKV + 1) * 32 : 0);
 #pragma unroll
-      for (int tau = 0; tau < 4; ++tau) x[j][tau] = bload8u(rc, (4 * mrow + tau) * p.HKV * 32 + 8 * kc);
+      for (int tau = 0; tau < 4; ++tau) x[j][tau] = bload8u_nt(rc, (4 * mrow + tau) * p.HKV * 32 + 8 * kc);
     }
   }
 
@@ -604,11 +604,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
 #pragma unroll
       for (int tau = 0; tau < 4; ++tau) {
         if constexpr (LAYOUT == kPaged) {  // token 4 mrow + tau, channels 32 kc + 16 h + (0..15): block (tau, h)
-          rr[tau][0] = bload16(rr_s, ((tau * 2 + 0) * 64 + lane) * 16);
-          rr[tau][1] = bload16(rr_s, ((tau * 2 + 1) * 64 + lane) * 16);
+          rr[tau][0] = bload16_nt(rr_s, ((tau * 2 + 0) * 64 + lane) * 16);
+          rr[tau][1] = bload16_nt(rr_s, ((tau * 2 + 1) * 64 + lane) * 16);
         } else {
-          rr[tau][0] = bload16(rr_s, ro[tau]);
-          rr[tau][1] = bload16(rr_s, ro[tau] + 16);
+          rr[tau][0] = bload16_nt(rr_s, ro[tau]);
+          rr[tau][1] = bload16_nt(rr_s, ro[tau] + 16);
         }
       }
     }
@@ -621,7 +621,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
 #pragma unroll
       for (int nu = 0; nu < VH; ++nu)
 #pragma unroll
-        for (int kap = 0; kap < 2; ++kap) vv[nu][kap] = bload16(vs_p, ((nu * 2 + kap) * 64 + lane) * 16);  // block (nu, kap)
+        for (int kap = 0; kap < 2; ++kap) vv[nu][kap] = bload16_nt(vs_p, ((nu * 2 + kap) * 64 + lane) * 16);  // block (nu, kap)
     } else {
       const brsrc vs = make_rsrc((const uint16_t *)p.v + (((size_t)b * p.T + t0) * p.HKV + hkv) * kD,
                                  ((nvs - 1) * p.HKV + 1) * kD * 2);
@@ -629,7 +629,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
       for (int r = 0; r < 16; ++r) {
         const int idx = r * 64 + lane;
         const int tk = idx >> 4, vc = idx & 15;
-        vv[r >> 1][r & 1] = bload16(vs, tk * p.HKV * kD * 2 + 16 * vc);
+        vv[r >> 1][r & 1] = bload16_nt(vs, tk * p.HKV * kD * 2 + 16 * vc);
       }
     }
     if constexpr (OCC > 1) __builtin_amdgcn_s_setprio(0);  // back to normal once the chunk's loads are out
@@ -733,7 +733,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
 #pragma unroll
           for (int n2 = VH; n2 < 8; ++n2)
 #pragma unroll
-            for (int kap = 0; kap < 2; ++kap) vv[n2][kap] = bload16(vs_p, ((n2 * 2 + kap) * 64 + lane) * 16);
+            for (int kap = 0; kap < 2; ++kap) vv[n2][kap] = bload16_nt(vs_p, ((n2 * 2 + kap) * 64 + lane) * 16);
         }
 #pragma unroll
         for (int kap = 0; kap < 2; ++kap) {
