@@ -205,9 +205,10 @@ __device__ __forceinline__ uint64_t bload8u(brsrc r, uint32_t off) {
   const uint2 v = bload8(r, off);
   return ((uint64_t)v.y << 32) | v.x;
 }
-// The same loads with the non-temporal hint (cache-policy bit 1, `nt` on gfx950), for data a launch
-// reads once: the cache pages a decode streams (codes, scales, residual, V).  Data that several
-// workgroups re-read (q, probe windows, page ids) keeps the default policy.
+// The same loads with the non-temporal hint (cache-policy bit 1, `nt` on gfx950), for data one
+// workgroup reads once: the paged (page, KV head) blocks of codes and scales, and the residual and
+// V rows.  Data that several workgroups read keeps the default policy: q, probe windows, page ids,
+// and the reference layout's code rows, whose cache lines hold several KV heads' codes.
 constexpr int kNonTemporal = 2;
 __device__ __forceinline__ uint4 bload16_nt(brsrc r, uint32_t off) {
   const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kNonTemporal);

@@ -256,7 +256,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
       const brsrc rs = page_rows((const uint8_t *)p.ks, pg[j], SCL == kSclG16 ? 8 : 4, nv[j] > 0);
 #pragma unroll
       for (int tau = 0; tau < 4; ++tau) {
-        xa[j][tau] = bload16(rc, (tau * 64 + lane) * 16);  // block tau: token 4 mrow + tau, bytes 16 kc + (0..15)
+        xa[j][tau] = bload16_nt(rc, (tau * 64 + lane) * 16);  // block tau: token 4 mrow + tau, bytes 16 kc + (0..15)
         xb[j][tau] = make_uint4(0, 0, 0, 0);
         xs[j][tau] = 1.f;
         xg[j][tau] = group_scales(rs, 4 * mrow + tau);
@@ -521,12 +521,12 @@ void kfmt_decode_kernel(const DecodeParams p) {
 #pragma unroll
       for (int tau = 0; tau < 4; ++tau) {
         if constexpr (LAYOUT == kPaged) {  // blocks (tau, h) of the page's residual
-          rr[tau][0] = bload16(rs, ((tau * 2 + 0) * 64 + lane) * 16);
-          rr[tau][1] = bload16(rs, ((tau * 2 + 1) * 64 + lane) * 16);
+          rr[tau][0] = bload16_nt(rs, ((tau * 2 + 0) * 64 + lane) * 16);
+          rr[tau][1] = bload16_nt(rs, ((tau * 2 + 1) * 64 + lane) * 16);
         } else {
           const uint32_t off = (4 * mrow + tau) * p.HKV * kD + 32 * kc;
-          rr[tau][0] = bload16(rs, off);
-          rr[tau][1] = bload16(rs, off + 16);
+          rr[tau][0] = bload16_nt(rs, off);
+          rr[tau][1] = bload16_nt(rs, off + 16);
         }
       }
     }
@@ -536,7 +536,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
 #pragma unroll
       for (int nu = 0; nu < 8; ++nu)
 #pragma unroll
-        for (int kap = 0; kap < 2; ++kap) vv[nu][kap] = bload16(vs, ((nu * 2 + kap) * 64 + lane) * 16);  // block (nu, kap)
+        for (int kap = 0; kap < 2; ++kap) vv[nu][kap] = bload16_nt(vs, ((nu * 2 + kap) * 64 + lane) * 16);  // block (nu, kap)
     } else {
       const brsrc vs = make_rsrc((const uint16_t *)p.v + (((size_t)b * p.T + t0) * p.HKV + hkv) * kD,
                                  ((nvs - 1) * p.HKV + 1) * kD * 2);
@@ -544,7 +544,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
       for (int r = 0; r < 16; ++r) {
         const int idx = r * 64 + lane;
         const int tk = idx >> 4, vc = idx & 15;
-        vv[r >> 1][r & 1] = bload16(vs, tk * p.HKV * kD * 2 + 16 * vc);
+        vv[r >> 1][r & 1] = bload16_nt(vs, tk * p.HKV * kD * 2 + 16 * vc);
       }
     }
     float Rj[16];

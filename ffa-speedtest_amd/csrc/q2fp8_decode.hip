@@ -249,7 +249,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
       const size_t base = (((size_t)b * p.T + t0) * p.HKV + hkv) * 32;
       const brsrc rc = make_rsrc(p.kq + base, nv[j] > 0 ? ((nv[j] - 1) * p.HKV + 1) * 32 : 0);
 #pragma unroll
-      for (int tau = 0; tau < 4; ++tau) x[j][tau] = bload8u_nt(rc, (4 * mrow + tau) * p.HKV * 32 + 8 * kc);
+      for (int tau = 0; tau < 4; ++tau) x[j][tau] = bload8u(rc, (4 * mrow + tau) * p.HKV * 32 + 8 * kc);
     }
   }
 
