@@ -834,27 +834,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     if (i < un.Gu) {
       // Every slot's m, l and o columns in one batch of LDS reads, then selects: reads issued slot
       // by slot behind branches on l were ~40 dependent LDS round trips (about 1 us) at the end of
-      // every workgroup with a kept chunk.  A slot without a kept chunk has l = 0 (written when the
-      // chunks were published); its o was never written and is selected away, not weighted by 0.
-      float pm[kChunksPerWG], pl[kChunksPerWG];
-      float2 po[kChunksPerWG];
+      // every workgroup with a kept chunk.  The arithmetic runs only for kept slots (km, uniform:
+      // scalar branches), and a workgroup without one skips the merge.  A kept slot's l may still
+      // be 0 (no active token of this row); its o is then selected away, not weighted by 0.
+      float M = -INFINITY, A = 0.f, ox = 0.f, oy = 0.f;
+      if (km != 0u) {
+        float pm[kChunksPerWG], pl[kChunksPerWG];
+        float2 po[kChunksPerWG];
 #pragma unroll
-      for (int ps = 0; ps < kChunksPerWG; ++ps) {
-        pm[ps] = s_pm[ps][i];
-        pl[ps] = s_pl[ps][i];
-        po[ps] = *reinterpret_cast<const float2 *>(&s_po[ps][i][c2]);
-      }
-      float M = -INFINITY;
+        for (int ps = 0; ps < kChunksPerWG; ++ps) {
+          pm[ps] = s_pm[ps][i];
+          pl[ps] = s_pl[ps][i];
+          po[ps] = *reinterpret_cast<const float2 *>(&s_po[ps][i][c2]);
+        }
 #pragma unroll
-      for (int ps = 0; ps < kChunksPerWG; ++ps) M = pl[ps] > 0.f ? fmaxf(M, pm[ps]) : M;
-      float A = 0.f, ox = 0.f, oy = 0.f;
+        for (int ps = 0; ps < kChunksPerWG; ++ps)
+          if ((km >> ps) & 1u) M = pl[ps] > 0.f ? fmaxf(M, pm[ps]) : M;
 #pragma unroll
-      for (int ps = 0; ps < kChunksPerWG; ++ps) {
-        const bool use = pl[ps] > 0.f;
-        const float wgt = exp2_hw(use ? pm[ps] - M : -INFINITY);
-        A = use ? __builtin_fmaf(pl[ps], wgt, A) : A;
-        ox = use ? __builtin_fmaf(po[ps].x, wgt, ox) : ox;
-        oy = use ? __builtin_fmaf(po[ps].y, wgt, oy) : oy;
+        for (int ps = 0; ps < kChunksPerWG; ++ps) {
+          if (!((km >> ps) & 1u)) continue;
+          const bool use = pl[ps] > 0.f;
+          const float wgt = exp2_hw(use ? pm[ps] - M : -INFINITY);
+          A = use ? __builtin_fmaf(pl[ps], wgt, A) : A;
+          ox = use ? __builtin_fmaf(po[ps].x, wgt, ox) : ox;
+          oy = use ? __builtin_fmaf(po[ps].y, wgt, oy) : oy;
+        }
       }
       const size_t row = (size_t)b * p.HQ + un.row0 + i;
       if (lane == 0) {
