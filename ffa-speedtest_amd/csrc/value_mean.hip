@@ -160,6 +160,8 @@ extern "C" int ffa_v_mean(const void *v, int v_dtype, int layout, const int32_t 
   } else {
     return ffa_set_error_internal(FFA_E_INVALID, "layout");
   }
+  const hipError_t e1 = hipGetLastError();  // the finalize pass would read partials never written
+  if (e1 != hipSuccess) return ffa_set_error_internal(FFA_E_LAUNCH, hipGetErrorString(e1));
   hipLaunchKernelGGL(ffa::vmean_finalize, dim3((unsigned)(B * HKV)), dim3(ffa::kD), 0, st, partial, used, seq_lens, T,
                      HKV, out, out_dtype);
   const hipError_t e = hipGetLastError();
