@@ -337,7 +337,10 @@ def decode(
             Sb = np.where(valid[:, :, None], Sq[idx], -np.inf)  # [NTBS, SBS, G]
             mb = Sb.max(axis=1)  # [NTBS, G] (:97)
             bmax[b, h * G:(h + 1) * G, :NTBS] = mb.T
-            margin[b, h, :NTBS] = (mb - th[None, :]).max(axis=1)
+            # diagnostic only: NaN where an empty block (-inf) meets an infinite threshold (delta = +inf
+            # makes th = -inf); the keep rule below does not use it
+            with np.errstate(invalid="ignore"):
+                margin[b, h, :NTBS] = (mb - th[None, :]).max(axis=1)
             keep = ~np.all(mb < th[None, :], axis=1)  # prune iff all rows below (:99-102)
             if force_mask is not None:
                 keep = np.asarray(force_mask)[b, h, :NTBS].astype(bool)
