@@ -266,9 +266,17 @@ struct VTraits<kVBF16> : VTraits<kVF16> {
 struct Raw16 {
   uint4 v[4];
 };
-__device__ __forceinline__ void raw16_load(Raw16 &r, brsrc rs, uint32_t off) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) r.v[i] = bload16(rs, off + 16 * i);
+// 16 elements of element size es (2 or 4 bytes) at byte offset off of a resource of `bytes`
+// bytes.  All four loads are issued whatever the dtype: for 16-bit dtypes the upper two read at
+// `bytes`, past the resource (zeros, no memory access), and are OR-ed into the lower two.  Every
+// load then has a use on every dtype path, so the compiler neither moves the f32-only loads into
+// that path, behind loads issued later, nor counts them among the outstanding loads of the other
+// paths: the waits for the window stay exact and do not wait for the cache loads behind it.
+__device__ __forceinline__ void raw16_load(Raw16 &r, brsrc rs, uint32_t off, uint32_t es, uint32_t bytes) {
+  r.v[0] = bload16(rs, off);
+  r.v[1] = bload16(rs, off + 16);
+  r.v[2] = bload16(rs, es == 4 ? off + 32 : bytes);
+  r.v[3] = bload16(rs, es == 4 ? off + 48 : bytes);
 }
 __device__ __forceinline__ void raw16_to_f32(const Raw16 &r, int dt, float *out) {
   if (dt == 2) {
@@ -282,7 +290,9 @@ __device__ __forceinline__ void raw16_to_f32(const Raw16 &r, int dt, float *out)
   } else if (dt == 1) {  // one uniform branch per dtype, not a select per element
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const uint32_t w[4] = {r.v[i].x, r.v[i].y, r.v[i].z, r.v[i].w};
+      // r.v[i + 2] is zero for 16-bit dtypes (see raw16_load)
+      const uint32_t w[4] = {r.v[i].x | r.v[i + 2].x, r.v[i].y | r.v[i + 2].y, r.v[i].z | r.v[i + 2].z,
+                             r.v[i].w | r.v[i + 2].w};
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         out[8 * i + 2 * k] = __uint_as_float(w[k] << 16);
@@ -292,7 +302,9 @@ __device__ __forceinline__ void raw16_to_f32(const Raw16 &r, int dt, float *out)
   } else {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const uint32_t w[4] = {r.v[i].x, r.v[i].y, r.v[i].z, r.v[i].w};
+      // r.v[i + 2] is zero for 16-bit dtypes (see raw16_load)
+      const uint32_t w[4] = {r.v[i].x | r.v[i + 2].x, r.v[i].y | r.v[i + 2].y, r.v[i].z | r.v[i + 2].z,
+                             r.v[i].w | r.v[i + 2].w};
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         out[8 * i + 2 * k] = f16_bits_to_f32(w[k] & 0xffffu);

@@ -68,12 +68,16 @@ __device__ __forceinline__ uint32_t pack_f16(float a, float b) {  // two RNE con
   return f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16);
 }
 
-// one scale value of a float tensor of dtype dt (0=f16, 1=bf16, 2=f32) at element index i
-__device__ __forceinline__ float load_scale(brsrc rs, uint32_t i, int dt) {
-  const uint32_t es = dt == 2 ? 4u : 2u;
-  const uint32_t off = i * es;
-  const uint32_t w = bload4(rs, off & ~3u);
-  const uint32_t bits = dt == 2 ? w : ((off & 2u) ? (w >> 16) : (w & 0xffffu));
+// Scale value i of a float tensor of dtype dt (0=f16, 1=bf16, 2=f32), in two steps: scale_word
+// loads the aligned 32-bit word holding it, scale_value converts it (odd = i & 1 picks the upper
+// half of a 16-bit pair).  The conversion branches on the dtype, and a wait inside such a branch
+// covers every load issued before it, so a group's words are converted only once all of the
+// group's loads are out.
+__device__ __forceinline__ uint32_t scale_word(brsrc rs, uint32_t i, int dt) {
+  return bload4(rs, dt == 2 ? i * 4u : (i * 2u) & ~3u);
+}
+__device__ __forceinline__ float scale_value(uint32_t w, uint32_t odd, int dt) {
+  const uint32_t bits = dt == 2 ? w : (odd ? (w >> 16) : (w & 0xffffu));
   return dt == 2 ? __uint_as_float(bits) : (dt == 1 ? bf16_bits_to_f32(bits) : f16_bits_to_f32(bits));
 }
 
@@ -164,13 +168,15 @@ void kfmt_decode_kernel(const DecodeParams p) {
   const int hwin = wv >> 1;
   Raw16 qraw;
   raw16_load(qraw, make_rsrc((const char *)p.q + (size_t)b * p.HQ * kD * es_q, p.HQ * kD * es_q),
-             (hq * kD + 32 * kc + 16 * hwin) * es_q);
+             (hq * kD + 32 * kc + 16 * hwin) * es_q, es_q, p.HQ * kD * es_q);
   const float th_pre = __uint_as_float(
       bload8(make_rsrc(p.th_in + (p.th_in ? (size_t)b * p.HQ : 0), p.th_in ? p.HQ * 4 : 0), hq * 4).x);
   int pg[kPPW] = {0, 0};
   int ppg = 0;
+  // the q loads go out before the wait for the page ids and before the code loads, whose waits
+  // would otherwise cover them
+  __builtin_amdgcn_sched_barrier(0);
   if constexpr (LAYOUT == kPaged) {
-    __builtin_amdgcn_sched_barrier(0);  // the q loads go out before the wait for the page ids
 #pragma unroll
     for (int j = 0; j < kPPW; ++j) pg[j] = __builtin_amdgcn_readlane(pg_lane, j);
     ppg = __builtin_amdgcn_readlane(pg_lane, kPPW);
@@ -217,15 +223,16 @@ void kfmt_decode_kernel(const DecodeParams p) {
   const brsrc rsc = make_rsrc(p.ks, SCL == kSclToken ? (uint32_t)(p.B * p.T * p.HKV) * (p.s_dtype == 2 ? 4u : 2u)
                                    : SCL == kSclBlock ? (uint32_t)(p.B * NTBk * p.HKV) * (p.s_dtype == 2 ? 4u : 2u)
                                                       : 0u);
-  // scale of token t for the token / block modes
-  auto tok_scale = [&](int t, int blk) -> float {
-    if constexpr (SCL == kSclToken) return load_scale(rsc, ((uint32_t)b * p.T + (uint32_t)min(t, p.T - 1)) * p.HKV + hkv, p.s_dtype);
-    else if constexpr (SCL == kSclBlock) return load_scale(rsc, ((uint32_t)b * NTBk + (uint32_t)blk) * p.HKV + hkv, p.s_dtype);
-    else return 1.f;
+  // element index of the scale of token t (token mode) or of block blk (block mode)
+  constexpr bool kTokScale = SCL == kSclToken || SCL == kSclBlock;
+  auto scale_index = [&](int t, int blk) -> uint32_t {
+    if constexpr (SCL == kSclToken) return ((uint32_t)b * p.T + (uint32_t)min(t, p.T - 1)) * p.HKV + hkv;
+    else return ((uint32_t)b * NTBk + (uint32_t)blk) * p.HKV + hkv;
   };
   // probe tile: MFMA row m <-> token pa + m
   uint4 pxa, pxb = make_uint4(0, 0, 0, 0);
   float psc = 1.f;
+  uint32_t psw = 0, psodd = 0;  // probe scale word, converted after the chunk loads
   f32x2 pgs = {1.f, 1.f};
   {
     const bool pv = do_probe && pa < Tb;
@@ -242,11 +249,16 @@ void kfmt_decode_kernel(const DecodeParams p) {
       pxa = bload16(rc, off);
       if constexpr (!k4) pxb = bload16(rc, off + 16);
       // nvfp4: window 0 uses block 0's scale, window 1 block NTB-1's (attn_kernel...nvfp4fp8.py:86-97)
-      psc = tok_scale(pa + mrow, wv == 0 ? 0 : max(NTB - 1, 0));
+      if constexpr (kTokScale) {
+        const uint32_t si = scale_index(pa + mrow, wv == 0 ? 0 : max(NTB - 1, 0));
+        psw = scale_word(rsc, si, p.s_dtype);
+        psodd = si & 1u;
+      }
     }
   }
   uint4 xa[kPPW][4], xb[kPPW][4];
   float xs[kPPW][4];
+  uint32_t xsw[kPPW][4], xsodd = 0;  // token / block scale words (bit 4j + tau of xsodd: odd index)
   f32x2 xg[kPPW][4];  // group scales (paged modes)
 #pragma unroll
   for (int j = 0; j < kPPW; ++j) {
@@ -271,7 +283,12 @@ void kfmt_decode_kernel(const DecodeParams p) {
         xb[j][tau] = make_uint4(0, 0, 0, 0);
         if constexpr (!k4) xb[j][tau] = bload16(rc, off + 16);
         const int t = t0 + 4 * mrow + tau;
-        xs[j][tau] = tok_scale(t, min(t, max(Tb - 1, 0)) / p.BS);
+        xs[j][tau] = 1.f;
+        if constexpr (kTokScale) {
+          const uint32_t si = scale_index(t, min(t, max(Tb - 1, 0)) / p.BS);
+          xsw[j][tau] = scale_word(rsc, si, p.s_dtype);
+          xsodd |= (si & 1u) << (4 * j + tau);
+        }
         xg[j][tau] = f32x2{1.f, 1.f};
       }
     }
@@ -380,6 +397,16 @@ void kfmt_decode_kernel(const DecodeParams p) {
   const float cs1 = p.scale;
 
   // ------------------------------------------------ phase 2b: probe, scores, prune
+  // token / block scales: converted here, after the operands, so that the dtype branches' waits
+  // (which cover every load issued before them) come after the q operands are built
+  if constexpr (LAYOUT != kPaged && kTokScale) {
+    __builtin_amdgcn_sched_barrier(0);
+    psc = scale_value(psw, psodd, p.s_dtype);
+#pragma unroll
+    for (int j = 0; j < kPPW; ++j)
+#pragma unroll
+      for (int tau = 0; tau < 4; ++tau) xs[j][tau] = scale_value(xsw[j][tau], (xsodd >> (4 * j + tau)) & 1u, p.s_dtype);
+  }
   float R[kPPW][16];
   uint64_t bal[kPPW] = {0, 0};
   float th = INFINITY;
@@ -483,6 +510,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
     uint4 ka[4], kb[4];
     float ksc[4];
     f32x2 kg[4];
+    uint32_t ksw[4], ksodd = 0;  // reloaded scale words, converted once the residual and V loads are out
     if constexpr (LAYOUT == kPaged) {
       const brsrc rc = page_rows(p.kq, pg[j], kRow, true);
       const brsrc rs = page_rows((const uint8_t *)p.ks, pg[j], SCL == kSclG16 ? 8 : 4, true);
@@ -510,7 +538,12 @@ void kfmt_decode_kernel(const DecodeParams p) {
         kb[tau] = make_uint4(0, 0, 0, 0);
         if constexpr (!k4) kb[tau] = bload16(rc, off + 16);
         const int t = t0 + 4 * mrow + tau;
-        ksc[tau] = tok_scale(t, min(t, max(Tb - 1, 0)) / p.BS);
+        ksc[tau] = 1.f;
+        if constexpr (kTokScale) {
+          const uint32_t si = scale_index(t, min(t, max(Tb - 1, 0)) / p.BS);
+          ksw[tau] = scale_word(rsc, si, p.s_dtype);
+          ksodd |= (si & 1u) << tau;
+        }
         kg[tau] = f32x2{1.f, 1.f};
       }
     }
@@ -546,6 +579,11 @@ void kfmt_decode_kernel(const DecodeParams p) {
         const int tk = idx >> 4, vc = idx & 15;
         vv[r >> 1][r & 1] = bload16_nt(vs, tk * p.HKV * kD * 2 + 16 * vc);
       }
+    }
+    if constexpr (LAYOUT != kPaged && RELOAD && kTokScale) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int tau = 0; tau < 4; ++tau) ksc[tau] = scale_value(ksw[tau], (ksodd >> tau) & 1u, p.s_dtype);
     }
     float Rj[16];
 #pragma unroll

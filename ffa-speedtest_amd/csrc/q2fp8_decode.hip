@@ -183,18 +183,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   const int hwin = wv >> 1;
   Raw16 qraw, sraw, zraw;
   raw16_load(qraw, make_rsrc((const char *)p.q + (size_t)b * p.HQ * kD * es_q, p.HQ * kD * es_q),
-             (hq * kD + 32 * kc + 16 * hwin) * es_q);
+             (hq * kD + 32 * kc + 16 * hwin) * es_q, es_q, p.HQ * kD * es_q);
   if constexpr (!kG) {
     const uint32_t es_s = p.s_dtype == 2 ? 4u : 2u;
     const size_t so = ((size_t)b * p.HKV + hkv) * kD * es_s;
-    raw16_load(sraw, make_rsrc((const char *)p.ks + so, kD * es_s), (32 * kc + 16 * hwin) * es_s);
-    raw16_load(zraw, make_rsrc((const char *)p.kz + so, kD * es_s), (32 * kc + 16 * hwin) * es_s);
+    raw16_load(sraw, make_rsrc((const char *)p.ks + so, kD * es_s), (32 * kc + 16 * hwin) * es_s, es_s, kD * es_s);
+    raw16_load(zraw, make_rsrc((const char *)p.kz + so, kD * es_s), (32 * kc + 16 * hwin) * es_s, es_s, kD * es_s);
   }
   // caller's threshold of the lane's query row (zeros when none is given)
   const float th_pre = __uint_as_float(
       bload8(make_rsrc(p.th_in + (p.th_in ? (size_t)b * p.HQ : 0), p.th_in ? p.HQ * 4 : 0), hq * 4).x);
+  // the q (and channel scale) loads go out before the wait for the page ids and before the code
+  // loads, whose waits would otherwise cover them
+  __builtin_amdgcn_sched_barrier(0);
   if constexpr (LAYOUT == kPaged) {
-    __builtin_amdgcn_sched_barrier(0);  // the q loads go out before the wait for the page ids
 #pragma unroll
     for (int j = 0; j < kPPW; ++j) pg[j] = __builtin_amdgcn_readlane(pg_lane, j);
     ppg = __builtin_amdgcn_readlane(pg_lane, kPPW);
