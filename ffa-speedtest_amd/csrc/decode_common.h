@@ -230,6 +230,27 @@ __device__ __forceinline__ f16x8 fp8x8_to_f16x8(uint32_t lo, uint32_t hi) {
   return __builtin_bit_cast(f16x8, r);
 }
 
+// The same 8 residual bytes in the element order of the reference-layout score operands: channel
+// pairs (0,2) (4,6) (1,3) (5,7)
+template <int RES>
+__device__ __forceinline__ f16x8 fp8x8_to_f16x8_perm(uint32_t lo, uint32_t hi) {
+  u32x4 r;
+  if constexpr (RES == kResE5M2) {
+    r[0] = __builtin_amdgcn_perm(lo, lo, 0x020c000cu);
+    r[1] = __builtin_amdgcn_perm(hi, hi, 0x020c000cu);
+    r[2] = __builtin_amdgcn_perm(lo, lo, 0x030c010cu);
+    r[3] = __builtin_amdgcn_perm(hi, hi, 0x030c010cu);
+  } else {
+    const uint32_t x = __builtin_amdgcn_perm(lo, lo, 0x03010200u);  // bytes 0, 2, 1, 3
+    const uint32_t y = __builtin_amdgcn_perm(hi, hi, 0x03010200u);
+    r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x, 1.0f, false));
+    r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(y, 1.0f, false));
+    r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x, 1.0f, true));
+    r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(y, 1.0f, true));
+  }
+  return __builtin_bit_cast(f16x8, r);
+}
+
 // P.V runs on fp16 operands whatever V's storage type, as the reference's decode kernels cast
 // both p and v to fp16 before the product (attn_kernel_v1210_fused_bsz_q2fp8.py:130-131 and the
 // same lines of the fp8fp8 / nvfp4fp8 / nf4fp8 kernels): fp16 P keeps 11 significant bits, and

@@ -197,28 +197,15 @@ void kfmt_decode_kernel(const DecodeParams p) {
       return f32x2{sc, sc};
     }
   };
-  // per-channel scales of the lane's 32 channels (nf4): eight 16-byte loads whatever the dtype
+  // per-channel scales of the lane's 32 channels (nf4): eight 16-byte loads whatever the dtype,
+  // converted in phase 2b (a conversion here would hold the code loads behind their round trip)
   float sch[32];
+  uint4 sraw[8];
   if constexpr (SCL == kSclChannel) {
     const uint32_t es = p.s_dtype == 2 ? 4u : 2u;
     const brsrc rs = make_rsrc((const char *)p.ks + ((size_t)b * p.HKV + hkv) * kD * es, kD * es);
-    uint4 raw[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) raw[i] = bload16(rs, 32 * kc * es + 16 * i);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t w[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        if (p.s_dtype == 2) {
-          sch[4 * i + k] = __uint_as_float(w[k]);
-        } else if (i < 4) {
-          const uint32_t lo = w[k] & 0xffffu, hi = w[k] >> 16;
-          sch[8 * i + 2 * k] = p.s_dtype == 1 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
-          sch[8 * i + 2 * k + 1] = p.s_dtype == 1 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
-        }
-      }
-    }
+    for (int i = 0; i < 8; ++i) sraw[i] = bload16(rs, 32 * kc * es + 16 * i);
   }
   const brsrc rsc = make_rsrc(p.ks, SCL == kSclToken ? (uint32_t)(p.B * p.T * p.HKV) * (p.s_dtype == 2 ? 4u : 2u)
                                    : SCL == kSclBlock ? (uint32_t)(p.B * NTBk * p.HKV) * (p.s_dtype == 2 ? 4u : 2u)
@@ -406,6 +393,22 @@ void kfmt_decode_kernel(const DecodeParams p) {
     for (int j = 0; j < kPPW; ++j)
 #pragma unroll
       for (int tau = 0; tau < 4; ++tau) xs[j][tau] = scale_value(xsw[j][tau], (xsodd >> (4 * j + tau)) & 1u, p.s_dtype);
+  }
+  if constexpr (SCL == kSclChannel) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t w[4] = {sraw[i].x, sraw[i].y, sraw[i].z, sraw[i].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (p.s_dtype == 2) {
+          sch[4 * i + k] = __uint_as_float(w[k]);
+        } else if (i < 4) {
+          const uint32_t lo = w[k] & 0xffffu, hi = w[k] >> 16;
+          sch[8 * i + 2 * k] = p.s_dtype == 1 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
+          sch[8 * i + 2 * k + 1] = p.s_dtype == 1 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
+        }
+      }
+    }
   }
   float R[kPPW][16];
   uint64_t bal[kPPW] = {0, 0};

@@ -59,21 +59,32 @@ __device__ __forceinline__ f16x8 codes_to_f16x8(uint32_t w, int s) {
   return __builtin_bit_cast(f16x8, r);
 }
 
-// Reference-layout dequantization of 8 channels: k_hat = fp16(c * s + z) with one rounding
-// (c*s is exact in fp32, so this equals the reference's fp16(fp32(fp32(c*s) + z))).
-// h holds 8 codes (code e at bits 2e); sp/zp hold the (s, z) fp16 pairs of channels (2q, 2q+1).
-__device__ __forceinline__ f16x8 dequant8_channel(uint32_t h, const uint32_t *sp, const uint32_t *zp) {
-  const uint32_t y = h | (h << 14);  // code 2q at bits 4q, code 2q+1 at bits 16+4q
-  const f16x2 m1024 = {(_Float16)-1024.f, (_Float16)-1024.f};
-  u32x4 r;
+// Reference-layout dequantization of 16 channels (one 32-bit code word, code i at bits 2i) into
+// the A operands of two score MFMAs: k_hat = fp16(c * s + z) with one rounding (c*s is exact in
+// fp32, so this equals the reference's fp16(fp32(fp32(c*s) + z))).  A code zero-extended to a
+// nibble is the e2m1 value c/2, so the hardware fp4 conversion with scale 2 yields c exactly, two
+// codes per instruction: masking with 0x33 leaves codes 4k and 4k+2 in the nibbles of byte k.
+// Element order inside each 8 channels: kChanPerm pairs (0,2) (4,6) (1,3) (5,7); the q operand,
+// the (s, z) pairs sp / zp (4 per operand) and the residual follow the same order.
+__device__ __forceinline__ void dequant16_channel(uint32_t w, const uint32_t *sp, const uint32_t *zp, f16x8 &k0,
+                                                  f16x8 &k1) {
+  const uint32_t e = w & 0x33333333u;         // byte k: codes 4k, 4k + 2
+  const uint32_t o = (w >> 2) & 0x33333333u;  // byte k: codes 4k + 1, 4k + 3
+  const f16x2 c[8] = {__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(e, 2.0f, 0), __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(e, 2.0f, 1),
+                      __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(o, 2.0f, 0), __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(o, 2.0f, 1),
+                      __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(e, 2.0f, 2), __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(e, 2.0f, 3),
+                      __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(o, 2.0f, 2), __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(o, 2.0f, 3)};
+  u32x4 r0, r1;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    const uint32_t pat = ((y >> (4 * q)) & 0x00030003u) | 0x64006400u;  // fp16 1024 + c
-    const f16x2 c = bits_f16x2(pat) + m1024;                          // exact codes
-    r[q] = f16x2_bits(__builtin_elementwise_fma(c, bits_f16x2(sp[q]), bits_f16x2(zp[q])));
+    r0[q] = f16x2_bits(__builtin_elementwise_fma(c[q], bits_f16x2(sp[q]), bits_f16x2(zp[q])));
+    r1[q] = f16x2_bits(__builtin_elementwise_fma(c[4 + q], bits_f16x2(sp[4 + q]), bits_f16x2(zp[4 + q])));
   }
-  return __builtin_bit_cast(f16x8, r);
+  k0 = __builtin_bit_cast(f16x8, r0);
+  k1 = __builtin_bit_cast(f16x8, r1);
 }
+// channel (within 8) of each element of a reference-layout score operand
+__host__ __device__ constexpr int kChanPerm(int e) { return (e & 1) * 2 + ((e >> 1) & 1) * 4 + (e >> 2); }
 
 // Position of token t (0..63) inside a page row of g32 scales / zeros.  Tile-major:
 // the scores of MFMA tile tau hold tokens 16k + 4u + tau (u = 0..3), whose scales
@@ -285,26 +296,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
       for (int e = 0; e < 8; ++e) zs += (float)(_Float16)qv[8 * s + e];
       s_zs[w][lane] = row_ok ? zs : 0.f;
     } else {
+      // element order kChanPerm, as dequant16_channel produces the codes
 #pragma unroll
       for (int qq = 0; qq < 4; ++qq) {
-        const float e0 = (row_ok && kc == jg) ? (float)(_Float16)qv[8 * s + 2 * qq] : 0.f;
-        const float e1 = (row_ok && kc == jg) ? (float)(_Float16)qv[8 * s + 2 * qq + 1] : 0.f;
+        const float e0 = (row_ok && kc == jg) ? (float)(_Float16)qv[8 * s + kChanPerm(2 * qq)] : 0.f;
+        const float e1 = (row_ok && kc == jg) ? (float)(_Float16)qv[8 * s + kChanPerm(2 * qq + 1)] : 0.f;
         a4[qq] = f32_to_f16_bits(e0) | (f32_to_f16_bits(e1) << 16);
       }
       float sv[16], zv[16];
       raw16_to_f32(sraw, p.s_dtype, sv);
       raw16_to_f32(zraw, p.s_dtype, zv);
-      uint4 sp, zp;
-      sp.x = f32_to_f16_bits(sv[8 * s + 0]) | (f32_to_f16_bits(sv[8 * s + 1]) << 16);
-      sp.y = f32_to_f16_bits(sv[8 * s + 2]) | (f32_to_f16_bits(sv[8 * s + 3]) << 16);
-      sp.z = f32_to_f16_bits(sv[8 * s + 4]) | (f32_to_f16_bits(sv[8 * s + 5]) << 16);
-      sp.w = f32_to_f16_bits(sv[8 * s + 6]) | (f32_to_f16_bits(sv[8 * s + 7]) << 16);
-      zp.x = f32_to_f16_bits(zv[8 * s + 0]) | (f32_to_f16_bits(zv[8 * s + 1]) << 16);
-      zp.y = f32_to_f16_bits(zv[8 * s + 2]) | (f32_to_f16_bits(zv[8 * s + 3]) << 16);
-      zp.z = f32_to_f16_bits(zv[8 * s + 4]) | (f32_to_f16_bits(zv[8 * s + 5]) << 16);
-      zp.w = f32_to_f16_bits(zv[8 * s + 6]) | (f32_to_f16_bits(zv[8 * s + 7]) << 16);
-      s_sp[w][lane] = sp;
-      s_zp2[w][lane] = zp;
+      uint32_t spw[4], zpw[4];
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        spw[qq] = f32_to_f16_bits(sv[8 * s + kChanPerm(2 * qq)]) | (f32_to_f16_bits(sv[8 * s + kChanPerm(2 * qq + 1)]) << 16);
+        zpw[qq] = f32_to_f16_bits(zv[8 * s + kChanPerm(2 * qq)]) | (f32_to_f16_bits(zv[8 * s + kChanPerm(2 * qq + 1)]) << 16);
+      }
+      s_sp[w][lane] = make_uint4(spw[0], spw[1], spw[2], spw[3]);
+      s_zp2[w][lane] = make_uint4(zpw[0], zpw[1], zpw[2], zpw[3]);
     }
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq) {
@@ -353,10 +362,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes_to_f16x8(whi, 0), qa[2], acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes_to_f16x8(whi, 1), qa[3], acc, 0, 0, 0);
     } else {
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant8_channel(wlo & 0xffffu, spair + 0, zpair + 0), qa[0], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant8_channel(wlo >> 16, spair + 4, zpair + 4), qa[1], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant8_channel(whi & 0xffffu, spair + 8, zpair + 8), qa[2], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant8_channel(whi >> 16, spair + 12, zpair + 12), qa[3], acc, 0, 0, 0);
+      f16x8 k[4];
+      dequant16_channel(wlo, spair + 0, zpair + 0, k[0], k[1]);
+      dequant16_channel(whi, spair + 8, zpair + 8, k[2], k[3]);
+#pragma unroll
+      for (int mp = 0; mp < 4; ++mp) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k[mp], qa[mp], acc, 0, 0, 0);
     }
 #pragma unroll
     for (int uu = 0; uu < 4; ++uu) {
@@ -670,10 +680,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
           const uint64_t xx = s_x[slot][tau][lane];
           const uint32_t wlo = (uint32_t)xx, whi = (uint32_t)(xx >> 32);
           f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(add_f16x8(dequant8_channel(wlo & 0xffffu, spair + 0, zpair + 0), fp8x8_to_f16x8<RES>(rr[tau][0].x, rr[tau][0].y)), qa[0], acc, 0, 0, 0);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(add_f16x8(dequant8_channel(wlo >> 16, spair + 4, zpair + 4), fp8x8_to_f16x8<RES>(rr[tau][0].z, rr[tau][0].w)), qa[1], acc, 0, 0, 0);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(add_f16x8(dequant8_channel(whi & 0xffffu, spair + 8, zpair + 8), fp8x8_to_f16x8<RES>(rr[tau][1].x, rr[tau][1].y)), qa[2], acc, 0, 0, 0);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(add_f16x8(dequant8_channel(whi >> 16, spair + 12, zpair + 12), fp8x8_to_f16x8<RES>(rr[tau][1].z, rr[tau][1].w)), qa[3], acc, 0, 0, 0);
+          f16x8 k[4];
+          dequant16_channel(wlo, spair + 0, zpair + 0, k[0], k[1]);
+          dequant16_channel(whi, spair + 8, zpair + 8, k[2], k[3]);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(add_f16x8(k[0], fp8x8_to_f16x8_perm<RES>(rr[tau][0].x, rr[tau][0].y)), qa[0], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(add_f16x8(k[1], fp8x8_to_f16x8_perm<RES>(rr[tau][0].z, rr[tau][0].w)), qa[1], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(add_f16x8(k[2], fp8x8_to_f16x8_perm<RES>(rr[tau][1].x, rr[tau][1].y)), qa[2], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(add_f16x8(k[3], fp8x8_to_f16x8_perm<RES>(rr[tau][1].z, rr[tau][1].w)), qa[3], acc, 0, 0, 0);
 #pragma unroll
           for (int uu = 0; uu < 4; ++uu) {
             float r = acc[uu];
