@@ -13,8 +13,11 @@ constexpr int kPPW = 2;                      // 64-token chunks (pages) per wave
 constexpr int kChunksPerWG = kWaves * kPPW;  // 512 tokens per workgroup
 constexpr int kMinSpan = 2;                  // smallest span (chunks per workgroup) of a small grid
 constexpr int kSmallSpanTokens = 8192;       // sequences up to this many tokens get slots for it
-constexpr int kVRow = 260;      // LDS row pitch (bytes) of a staged V tile: 256 + 4 keeps banks apart
-constexpr int kVRowHalf = 132;  // the same for half a tile (64 columns)
+// LDS row pitch (bytes) of a V tile staged row-major for the transposing reads (vt_operand_lds,
+// 8-byte aligned rows): whole tile (128 columns) 256 + 16; half a tile (64 columns) 128 + 8,
+// which keeps the q2 reference-layout decoder within two workgroups per CU (80.6 KB of LDS)
+constexpr int kVRow = 272;
+constexpr int kVRowHalf = 136;
 
 struct DecodeParams {
   const void *q;
@@ -249,6 +252,23 @@ __device__ __forceinline__ f16x8 fp8x8_to_f16x8_perm(uint32_t lo, uint32_t hi) {
     r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(y, 1.0f, true));
   }
   return __builtin_bit_cast(f16x8, r);
+}
+
+// B operand of a P.V MFMA from a V tile staged row-major in LDS (token rows of `pitch` bytes):
+// lane (kc, n) needs V[16 kc + 8 kap + e][16 nl + n], e = 0..7, i.e. a column of the tile.
+// ds_read_b64_tr_b16 (gfx950) transposes inside each 16-lane group: lane i receives element i % 4
+// of the 4-element rows addressed by lanes i / 4 + 4 e' (e' = 0..3).  So lane n addresses token
+// 16 kc + 8 kap + n / 4 (+ 4 for the second read) at column 16 nl + 4 (n % 4), and receives its
+// column's tokens e = 0..3 (then 4..7); two reads per operand instead of eight 2-byte reads.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4 vt_operand_lds(const uint8_t *st, int pitch, int nl, int kap, int kc, int n) {
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const uint32_t off = (uint32_t)((16 * kc + 8 * kap + (n >> 2)) * pitch + (16 * nl + 4 * (n & 3)) * 2);
+  const auto *p0 = (const lds_s16x4 *)((__attribute__((address_space(3))) const uint8_t *)st + off);
+  const auto *p1 = (const lds_s16x4 *)((__attribute__((address_space(3))) const uint8_t *)st + off + 4 * pitch);
+  const u32x2 a = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)p0));
+  const u32x2 b = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)p1));
+  return u32x4{a[0], a[1], b[0], b[1]};
 }
 
 // P.V runs on fp16 operands whatever V's storage type, as the reference's decode kernels cast

@@ -135,7 +135,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
   __shared__ float s_pm[kChunksPerWG][4], s_pl[kChunksPerWG][4];
   __shared__ float s_po[kChunksPerWG][4][128];
   __shared__ float s_cb[16];
-  __shared__ uint8_t s_vstage[LAYOUT == kContig ? kWaves * kPage * (RELOAD ? kVRowHalf : kVRow) : 4];
+  __shared__ __attribute__((aligned(16))) uint8_t s_vstage[LAYOUT == kContig ? kWaves * kPage * (RELOAD ? kVRowHalf : kVRow) : 16];
 
   auto lds_barrier = []() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
 
@@ -682,11 +682,9 @@ void kfmt_decode_kernel(const DecodeParams p) {
         const int tk = idx >> 4, vc = idx & 15;
         if (kHalves == 1 || (vc >> 3) == hf) {
           const uint4 v4 = vv[r >> 1][r & 1];
-          uint32_t *d = (uint32_t *)(st + tk * kPitch + 16 * (vc % kPieces));
-          d[0] = v4.x;
-          d[1] = v4.y;
-          d[2] = v4.z;
-          d[3] = v4.w;
+          uint2 *d = (uint2 *)(st + tk * kPitch + 16 * (vc % kPieces));  // rows are 8-byte aligned
+          d[0] = make_uint2(v4.x, v4.y);
+          d[1] = make_uint2(v4.z, v4.w);
         }
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -696,18 +694,8 @@ void kfmt_decode_kernel(const DecodeParams p) {
       for (int nl = 0; nl < 8 / kHalves; ++nl) {
         const int nu = (8 / kHalves) * hf + nl;
 #pragma unroll
-        for (int kap = 0; kap < 2; ++kap) {
-          const int vcol = 16 * nl + n;  // column within the staged part
-          const int tk = 16 * kc + 8 * kap;
-          u32x4 w;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t lo = *(const uint16_t *)(st + (tk + 2 * e) * kPitch + 2 * vcol);
-            const uint32_t hi = *(const uint16_t *)(st + (tk + 2 * e + 1) * kPitch + 2 * vcol);
-            w[e] = lo | (hi << 16);
-          }
-          oacc[nu] = VTr::mfma(pa2[kap], VTr::operand(w), oacc[nu]);
-        }
+        for (int kap = 0; kap < 2; ++kap)
+          oacc[nu] = VTr::mfma(pa2[kap], VTr::operand(vt_operand_lds(st, kPitch, nl, kap, kc, n)), oacc[nu]);
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();

@@ -151,7 +151,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   uint4(*const s_qa)[64] = reinterpret_cast<uint4(*)[64]>(&s_po[0][0][0]);
   // g32: partial sums of q16 over 8 channels (read with the operands), after s_qa
   float(*const s_zs)[64] = reinterpret_cast<float(*)[64]>(&s_po[2][0][0]);
-  __shared__ uint8_t s_vstage[LAYOUT == kContig ? kWaves * kPage * kVRowHalf : 4];
+  __shared__ __attribute__((aligned(16))) uint8_t s_vstage[LAYOUT == kContig ? kWaves * kPage * kVRowHalf : 16];
 
   // Workgroup barrier for LDS traffic only: __syncthreads() would also wait for every
   // outstanding global load of the wave (s_waitcnt vmcnt(0)), serialising the page loads
@@ -781,11 +781,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
           const int tk = idx >> 4, vc = idx & 15;
           if ((vc >> 3) == hf) {
             const uint4 v4 = vv[r >> 1][r & 1];
-            uint32_t *d = (uint32_t *)(st + tk * kVRowHalf + 16 * (vc & 7));
-            d[0] = v4.x;
-            d[1] = v4.y;
-            d[2] = v4.z;
-            d[3] = v4.w;
+            uint2 *d = (uint2 *)(st + tk * kVRowHalf + 16 * (vc & 7));  // rows are 8-byte aligned
+            d[0] = make_uint2(v4.x, v4.y);
+            d[1] = make_uint2(v4.z, v4.w);
           }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -795,18 +793,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
         for (int nl = 0; nl < 4; ++nl) {
           const int nu = 4 * hf + nl;
 #pragma unroll
-          for (int kap = 0; kap < 2; ++kap) {
-            const int vcol = 16 * nl + n;  // column within the half
-            const int tk = 16 * kc + 8 * kap;
-            u32x4 w;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const uint32_t lo = *(const uint16_t *)(st + (tk + 2 * e) * kVRowHalf + 2 * vcol);
-              const uint32_t hi = *(const uint16_t *)(st + (tk + 2 * e + 1) * kVRowHalf + 2 * vcol);
-              w[e] = lo | (hi << 16);
-            }
-            oacc[nu] = VTr::mfma(pa2[kap], VTr::operand(w), oacc[nu]);
-          }
+          for (int kap = 0; kap < 2; ++kap)
+            oacc[nu] = VTr::mfma(pa2[kap], VTr::operand(vt_operand_lds(st, kVRowHalf, nl, kap, kc, n)), oacc[nu]);
         }
         // the other half (and the next kept chunk) reuses the staging buffer
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
