@@ -85,6 +85,33 @@ def paged_case(B=1, T=2048, HQ=32, HKV=8, seed=0, n_heavy=16, res="e4m3fn", seq_
                 pools=pools, P=P)
 
 
+def paged_channel_case(B=1, T=2048, HQ=32, HKV=8, tau="bf16", res="e5m2", seed=0, n_heavy=16, seq_lens=None):
+    """Per-channel q2 (the reference quantizer, scale / zero [B, HKV, 128]) with its codes, residual and
+    V in the paged pools: codes pack as in the reference layout, so they scatter like the g32 codes."""
+    q, k, v = synth.attention_inputs(B=B, T=T, HQ=HQ, HKV=HKV, seed=seed, n_heavy=n_heavy, dtype=TORCH_DT[tau],
+                                     seq_lens=seq_lens)
+    lens = [T] * B if seq_lens is None else [int(x) for x in seq_lens]
+    pk, s, z, r = O.quantize_per_channel(f32(k), tau, res)
+    bt, P = synth.page_tables(lens, seed=seed, interleave=True)
+    rng = np.random.default_rng(seed + 7)
+    kq_pool = rng.integers(0, 256, (P, HKV, 4, 64, 8), dtype=np.uint8)
+    r_pool = rng.integers(0, 256, (P, HKV, 64, 128), dtype=np.uint8)
+    v_pool = rng.integers(0, 65536, (P, HKV, 128, 64), dtype=np.uint16)
+    vb = v.view(torch.int16).numpy().view(np.uint16)
+    for b in range(B):
+        for t0 in range(0, lens[b], 64):
+            page = int(bt[b, t0 // 64])
+            n = min(t0 + 64, lens[b]) - t0
+            kq_pool[page, :, :, :n, :] = pk[b, t0:t0 + n].reshape(n, HKV, 4, 8).transpose(1, 2, 0, 3)
+            r_pool[page, :, :n, :] = r[b, t0:t0 + n].transpose(1, 0, 2)
+            v_pool[page, :, :, :n] = vb[b, t0:t0 + n].transpose(1, 2, 0)
+    from ffa_mi355x.paged import CODES_ORDER, RES_ORDER, VT_ORDER, to_tiled
+
+    pools = dict(k_q=to_tiled(kq_pool, CODES_ORDER, 8), k_res=to_tiled(r_pool, RES_ORDER), v=to_tiled(v_pool, VT_ORDER))
+    return dict(q=q, k=k, v=v, k_q=pk, k_scale=s, k_zero=z, k_res=r, tau=tau, res=res, lens=lens, block_table=bt,
+                pools=pools, P=P)
+
+
 def to_gpu_paged(case, dev):
     from ffa_mi355x.paged import PagedQ2Cache
 

@@ -12,8 +12,8 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import (assert_out_close, compare_masks, contig_case, f32, oracle_paged, paged_case, to_gpu_contig,
-                     to_gpu_paged)
+from helpers import (FP8_DT, TORCH_DT, assert_out_close, compare_masks, contig_case, f32, oracle_paged, paged_case,
+                     paged_channel_case, to_gpu_contig, to_gpu_paged)
 from oracle import q2fp8 as O
 
 pytestmark = pytest.mark.gpu
@@ -87,6 +87,41 @@ def test_paged_g32(gpu, B, T, seq_lens, BS, SBS, delta, interleave):
     o_forced, _ = oracle_paged(case, BS=BS, SBS=SBS, delta=delta, force_mask=mask)
     mx, mean = assert_out_close(f32(ws.o), o_forced, "paged")
     print(f"[out] max_abs={mx:.3e} mean_abs={mean:.3e}")
+
+
+@pytest.mark.parametrize("tau,res,seq_lens", [("bf16", "e5m2", None), ("fp16", "e4m3fn", [2048, 777])])
+def test_paged_per_channel(gpu, tau, res, seq_lens):
+    """Paged pools with the reference's per-channel scale / zero ([B, HKV, 128]) through the drop-in:
+    the per-channel dequantization and refine on codes gathered through the page table."""
+    import attn_kernel.attn_kernel_v1210_fused_bsz_q2fp8 as K
+
+    case = paged_channel_case(B=2, T=2048, tau=tau, res=res, seed=23, n_heavy=16, seq_lens=seq_lens)
+    p = case["pools"]
+    dt = TORCH_DT[tau]
+    k_q = torch.from_numpy(p["k_q"]).to(gpu)
+    k_res = torch.from_numpy(p["k_res"]).view(FP8_DT[res]).to(gpu)
+    v = torch.from_numpy(p["v"].view(np.int16)).view(dt).to(gpu)  # V^T pages in the cache's dtype
+    s = torch.from_numpy(case["k_scale"]).to(dt).to(gpu)
+    z = torch.from_numpy(case["k_zero"]).to(dt).to(gpu)
+    kw = dict(block_table=torch.as_tensor(case["block_table"]).to(gpu), T=2048)
+    if seq_lens is not None:
+        kw["seq_lens"] = torch.tensor(case["lens"], dtype=torch.int32, device=gpu)
+    q = case["q"].to(gpu).unsqueeze(1).contiguous()
+    ws = K.allocate_q2fp8_decode_workspace(q, k_q, v, BS=64, SBS=64, **kw)
+    o, sr = K.attn_forward_decode_quantized(q, k_q, s, z, v, k_residual=k_res, BS=64, SBS=64, delta=5.0,
+                                            return_skip_ratio=True, workspace=ws, **kw)
+    torch.cuda.synchronize()
+    args = (f32(case["q"]), case["k_q"], case["k_scale"], case["k_zero"], f32(case["v"]), case["k_res"])
+    okw = dict(res_fmt=res, scale_mode="per_channel", seq_lens=seq_lens, BS=64, SBS=64, delta=5.0, out_dtype=tau)
+    _, diag = O.decode(*args, **okw)
+    mask = ws.mask_buf.cpu().numpy()
+    far, near, near_total = compare_masks(mask, diag)
+    print(f"[paged per-channel] tau={tau} res={res} skip={sr:.3f} oracle_skip={diag['skip_ratio']:.3f} "
+          f"mismatch_far={far} mismatch_near={near} near_blocks={near_total}")
+    assert far == 0
+    assert np.abs(ws.threshold_buf.cpu().numpy() - diag["threshold"]).max() < 1e-4
+    o_forced, _ = O.decode(*args, force_mask=mask, **okw)
+    assert_out_close(f32(o), o_forced, "paged per-channel")
 
 
 def test_paged_page_permutation_invariance(gpu):
