@@ -66,6 +66,23 @@ def test_fp8fp8_decoder(gpu, fmt, tau, vdt, T, BS, SBS, delta):
     _check(o, ws, o_ref, diag, f"fp8fp8 {fmt} T={T}")
 
 
+def test_fp8fp8_decoder_f32_query(gpu):
+    """q in float32 (the 64-byte q window per lane, all four loads used) on the other-format decoder."""
+    T, BS, SBS, delta, fmt = 1500, 64, 64, 4.0, "e4m3fn"
+    q, k, v = _inputs(1, T, "bf16", 1, 16)
+    base, res = OF.quantize_fp8fp8(f32(k), fmt)
+    kh = OF.khat_fp8(base, fmt)
+    o_ref, diag = O.decode(f32(q), base, None, None, f32(v), res, res_fmt=fmt, BS=BS, SBS=SBS, delta=delta,
+                           khat=kh, out_dtype="fp32")
+    qd = q.float().to(gpu).unsqueeze(1).contiguous()
+    ws = F8K.__dict__["DecodeWorkspace"](1, 32, 8, T, BS, SBS, gpu, torch.float32)
+    o = F8K.attn_forward_decode_fp8fp8(
+        qd, torch.from_numpy(base).view(FP8_DT[fmt]).to(gpu), v.to(gpu),
+        k_residual=torch.from_numpy(res).view(FP8_DT[fmt]).to(gpu), BS=BS, SBS=SBS, delta=delta, workspace=ws)
+    assert o.dtype == torch.float32
+    _check(o, ws, o_ref, diag, f"fp8fp8 f32 q T={T}")
+
+
 def test_fp8_scaled_decoder_baseline_config1(gpu):
     """e4m3 + one fp16 scale per token and KV head + e4m3 residual, 4 outlier channels."""
     T = 4096
