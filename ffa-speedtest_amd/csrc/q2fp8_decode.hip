@@ -910,36 +910,26 @@ __device__ __forceinline__ void merge_partials(const DecodeParams &p) {
   const brsrc ro = make_rsrc(p.o_buf + (size_t)row * p.nparts * 128 + 16 * slab, nparts > 0 ? ((nparts - 1) * 128 + 16) * 4 : 0);
   __shared__ float s_o[64][17];
 
-  // first partial of the lane (slots past nparts read as l = 0, o = 0).  Eager (small
-  // batches): its columns are loaded with m and l in one round trip, kept or not.  LAZY (many
-  // rows): only partials with l > 0 are read, a second round trip, since most slots of long
-  // sequences hold pruned spans and reading them all would dominate the traffic.
-  const float m0 = __uint_as_float(bload4(rm, lane * 4));
-  const float l0 = __uint_as_float(bload4(rl, lane * 4));
-  uint4 o0[4];
-  if constexpr (!LAZY) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) o0[e] = bload16(ro, (lane * 128 + 4 * e) * 4);
-  } else {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) o0[e] = make_uint4(0, 0, 0, 0);
-    if (l0 > 0.f) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o0[e] = bload16(ro, (lane * 128 + 4 * e) * 4);
-    }
-  }
-  float M = l0 > 0.f ? m0 : -INFINITY;
-  for (int k = lane + 64; k < nparts; k += 64) {
-    const float l = __uint_as_float(bload4(rl, k * 4));
-    if (l > 0.f) M = fmaxf(M, __uint_as_float(bload4(rm, k * 4)));
-  }
-  M = wave_max(M);
-
+  // The lane's partials k = lane + 64 i (slots past nparts read as l = 0) in batches of four per
+  // lane: one round trip for a batch's m and l, one for the columns of its kept partials (l > 0;
+  // a slot whose span kept nothing holds no defined o), with the running maximum rescaled
+  // between batches.  Eager (small batches): the first partial's columns go out with its m and l,
+  // kept or not.  LAZY (many rows): only kept partials' columns are read, since most slots of
+  // long sequences hold pruned spans and reading them all would dominate the traffic.
+  constexpr int kNB = 4;  // partials per lane and batch
+  const uint32_t o_oob = nparts > 0 ? ((nparts - 1) * 128 + 16) * 4 : 0;  // offset past ro: zeros, no access
+  float M = -INFINITY, A = 0.f;
   float acc[16];
-  float A;
-  {
-    // o is used only where l > 0: a slot whose span kept nothing holds no defined values
+#pragma unroll
+  for (int c = 0; c < 16; ++c) acc[c] = 0.f;
+  if (nparts <= 64) {  // one partial per lane (uniform): a single round trip, no rescaling
+    const float m0 = __uint_as_float(bload4(rm, lane * 4));
+    const float l0 = __uint_as_float(bload4(rl, lane * 4));
     const bool keep = l0 > 0.f;
+    uint4 o0[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o0[e] = bload16(ro, (!LAZY || keep) ? (lane * 128 + 4 * e) * 4 : o_oob);
+    M = wave_max(keep ? m0 : -INFINITY);
     const float wgt = keep ? exp2_hw(m0 - M) : 0.f;
     A = keep ? l0 * wgt : 0.f;
 #pragma unroll
@@ -950,20 +940,55 @@ __device__ __forceinline__ void merge_partials(const DecodeParams &p) {
       acc[4 * e + 3] = keep ? __uint_as_float(o0[e].w) * wgt : 0.f;
     }
   }
-  for (int k = lane + 64; k < nparts; k += 64) {
-    const float l = __uint_as_float(bload4(rl, k * 4));
-    if (l > 0.f) {
-      const float wgt = exp2_hw(__uint_as_float(bload4(rm, k * 4)) - M);
-      A = __builtin_fmaf(l, wgt, A);
+  for (int kb = 0; nparts > 64 && kb < nparts; kb += 64 * kNB) {
+    const int nb = min(kNB, (nparts - kb + 63) >> 6);  // partials per lane in this batch (uniform)
+    float l[kNB], m[kNB];
+    uint4 o[kNB][4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint4 v = bload16(ro, (k * 128 + 4 * e) * 4);
-        acc[4 * e + 0] = __builtin_fmaf(__uint_as_float(v.x), wgt, acc[4 * e + 0]);
-        acc[4 * e + 1] = __builtin_fmaf(__uint_as_float(v.y), wgt, acc[4 * e + 1]);
-        acc[4 * e + 2] = __builtin_fmaf(__uint_as_float(v.z), wgt, acc[4 * e + 2]);
-        acc[4 * e + 3] = __builtin_fmaf(__uint_as_float(v.w), wgt, acc[4 * e + 3]);
+    for (int i = 0; i < kNB; ++i) {
+      const int k = kb + 64 * i + lane;
+      l[i] = 0.f;
+      m[i] = -INFINITY;
+      if (i < nb) {
+        l[i] = __uint_as_float(bload4(rl, k * 4));
+        m[i] = __uint_as_float(bload4(rm, k * 4));
       }
     }
+    if (!LAZY && kb == 0) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[0][e] = bload16(ro, (lane * 128 + 4 * e) * 4);
+    }
+#pragma unroll
+    for (int i = 0; i < kNB; ++i) {
+      if ((!LAZY && kb == 0 && i == 0) || i >= nb) continue;
+      const uint32_t base = l[i] > 0.f ? (uint32_t)(kb + 64 * i + lane) * 128 * 4 : o_oob;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[i][e] = bload16(ro, l[i] > 0.f ? base + 16 * e : o_oob);
+    }
+    float Mb = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < kNB; ++i) Mb = (i < nb && l[i] > 0.f) ? fmaxf(Mb, m[i]) : Mb;
+    const float Mn = fmaxf(M, wave_max(Mb));
+    if (Mn == -INFINITY) continue;  // nothing kept so far (uniform)
+    const float rs = M == -INFINITY ? 0.f : exp2_hw(M - Mn);  // earlier batches to the new maximum
+    A *= rs;
+#pragma unroll
+    for (int c = 0; c < 16; ++c) acc[c] *= rs;
+#pragma unroll
+    for (int i = 0; i < kNB; ++i) {
+      if (i >= nb) continue;  // uniform
+      const bool keep = l[i] > 0.f;
+      const float wgt = keep ? exp2_hw(m[i] - Mn) : 0.f;
+      A = keep ? __builtin_fmaf(l[i], wgt, A) : A;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[4 * e + 0] = keep ? __builtin_fmaf(__uint_as_float(o[i][e].x), wgt, acc[4 * e + 0]) : acc[4 * e + 0];
+        acc[4 * e + 1] = keep ? __builtin_fmaf(__uint_as_float(o[i][e].y), wgt, acc[4 * e + 1]) : acc[4 * e + 1];
+        acc[4 * e + 2] = keep ? __builtin_fmaf(__uint_as_float(o[i][e].z), wgt, acc[4 * e + 2]) : acc[4 * e + 2];
+        acc[4 * e + 3] = keep ? __builtin_fmaf(__uint_as_float(o[i][e].w), wgt, acc[4 * e + 3]) : acc[4 * e + 3];
+      }
+    }
+    M = Mn;
   }
   A = wave_sum(A);
   // mean-V fallback: the pruned tokens' mass of every slot (attn_kernel_v1210_meanv_bsz_q2fp8.py:
