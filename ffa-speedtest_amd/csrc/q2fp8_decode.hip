@@ -997,14 +997,25 @@ __device__ __forceinline__ void merge_partials(const DecodeParams &p) {
   if (p.v_mean != nullptr) {
     const brsrc ram = make_rsrc(p.am_buf + (size_t)row * p.nparts, nparts * 4);
     const brsrc ral = make_rsrc(p.al_buf + (size_t)row * p.nparts, nparts * 4);
-    for (int k = lane; k < nparts; k += 64) {
-      const float l = __uint_as_float(bload4(ral, k * 4));
-      if (l > 0.f) AM = fmaxf(AM, __uint_as_float(bload4(ram, k * 4)));
-    }
-    AM = wave_max(AM);
-    for (int k = lane; k < nparts; k += 64) {
-      const float l = __uint_as_float(bload4(ral, k * 4));
-      if (l > 0.f) AL = __builtin_fmaf(l, exp2_hw(__uint_as_float(bload4(ram, k * 4)) - AM), AL);
+    // the lane's (max, sum) pairs in batches of four per lane, one round trip each, with the
+    // running maximum rescaled between batches (the pairs are small: read whether or not l > 0)
+    for (int kb = 0; kb < nparts; kb += 64 * kNB) {
+      float l[kNB], m[kNB];
+#pragma unroll
+      for (int i = 0; i < kNB; ++i) {
+        const int k = kb + 64 * i + lane;
+        l[i] = __uint_as_float(bload4(ral, k * 4));
+        m[i] = __uint_as_float(bload4(ram, k * 4));
+      }
+      float Mb = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < kNB; ++i) Mb = l[i] > 0.f ? fmaxf(Mb, m[i]) : Mb;
+      const float Mn = fmaxf(AM, wave_max(Mb));
+      if (Mn == -INFINITY) continue;  // no pruned mass so far (uniform)
+      AL *= AM == -INFINITY ? 0.f : exp2_hw(AM - Mn);
+#pragma unroll
+      for (int i = 0; i < kNB; ++i) AL = l[i] > 0.f ? __builtin_fmaf(l[i], exp2_hw(m[i] - Mn), AL) : AL;
+      AM = Mn;
     }
     AL = wave_sum(AL);
   }

@@ -124,3 +124,69 @@ def test_meanv_paged_ragged_and_all_pruned(gpu):
     assert int(ws2.mask_buf.sum().item()) == 0
     want = vm.float().repeat_interleave(4, dim=1)
     assert torch.allclose(ws2.o, want, rtol=1e-6, atol=0)
+
+
+
+@pytest.mark.parametrize("B", [1, 9])  # 32 query rows (eager merge) / 288 rows (lazy merge)
+@pytest.mark.parametrize("with_vmean", [False, True])
+def test_merge_long_rows_in_batches(gpu, B, with_vmean):
+    """Stage 2 alone on synthetic partials of 136,000-token rows: 266 partial slots per row, which
+    the merge takes in two batches of four per lane with the running maximum rescaled between
+    them.  Expected: the reference's log-sum-exp merge (attn_kernel...q2fp8.py:156-171, and the
+    mean-V fold of attn_kernel_v1210_meanv_bsz_q2fp8.py:192-202) in float64."""
+    from ffa_mi355x.decode import DecodeWorkspace
+    from ffa_mi355x.paged import PagedQ2Cache
+
+    T, HQ, HKV, D = 136_000, 32, 8, 128
+    cache = PagedQ2Cache(4, HKV, gpu)  # stage 2 never reads the pools; the call only needs valid ones
+    bt = torch.zeros((B, (T + 63) // 64), dtype=torch.int32, device=gpu)
+    ws = DecodeWorkspace(B, HQ, HKV, T, 64, 64, gpu, torch.float32)
+    n = -(-T // 512)
+    assert ws.nparts >= n > 256
+    rng = np.random.default_rng(61 + B)
+    m = rng.normal(0.0, 3.0, (B, HQ, n)).astype(np.float32)
+    kept = rng.random((B, HQ, n)) < 0.4
+    kept[0, 0] = False  # one row with nothing kept
+    l = np.where(kept, rng.uniform(0.5, 8.0, (B, HQ, n)), 0.0).astype(np.float32)
+    m = np.where(kept, m, -np.inf).astype(np.float32)
+    o = rng.normal(0.0, 1.0, (B, HQ, n, D)).astype(np.float32)
+    ws.m_buf[..., :n].copy_(torch.from_numpy(m))
+    ws.l_buf[..., :n].copy_(torch.from_numpy(l))
+    ws.o_buf[..., :n, :].copy_(torch.from_numpy(o))
+    vm = None
+    if with_vmean:
+        am = rng.normal(0.0, 3.0, (B, HQ, n)).astype(np.float32)
+        al = np.where(rng.random((B, HQ, n)) < 0.7, rng.uniform(0.5, 8.0, (B, HQ, n)), 0.0).astype(np.float32)
+        ws.approx_m[..., :n].copy_(torch.from_numpy(am))
+        ws.approx_l[..., :n].copy_(torch.from_numpy(al))
+        vm_np = rng.normal(0.0, 1.0, (B, HKV, D)).astype(np.float32)
+        vm = torch.from_numpy(vm_np).to(gpu)
+    q = torch.zeros((B, HQ, D), dtype=torch.float32, device=gpu)
+    cache.decode(q, bt, None, T=T, BS=64, SBS=64, delta=5.0, workspace=ws, stage="stage2", v_mean=vm)
+    torch.cuda.synchronize()
+    got = ws.o.cpu().numpy().astype(np.float64)
+
+    md, ld, od = m.astype(np.float64), l.astype(np.float64), o.astype(np.float64)
+    want = np.zeros((B, HQ, D))
+    for b in range(B):
+        for h in range(HQ):
+            k = ld[b, h] > 0
+            M = md[b, h, k].max() if k.any() else -np.inf
+            w = np.where(k, np.exp2(np.where(k, md[b, h], 0.0) - (M if k.any() else 0.0)), 0.0)
+            A = (ld[b, h] * w).sum()
+            acc = (od[b, h] * w[:, None]).sum(0)
+            if not with_vmean:
+                want[b, h] = acc / A if A > 0 else 0.0
+                continue
+            ka = al[b, h] > 0
+            AM = am[b, h, ka].max() if ka.any() else -np.inf
+            AL = (al[b, h, ka] * np.exp2(am[b, h, ka].astype(np.float64) - AM)).sum() if ka.any() else 0.0
+            Mx = max(M if A > 0 else -np.inf, AM if AL > 0 else -np.inf)
+            re = np.exp2(M - Mx) if A > 0 else 0.0
+            ra = np.exp2(AM - Mx) if AL > 0 else 0.0
+            den = A * re + AL * ra
+            want[b, h] = (acc * re + vm_np[b, h // (HQ // HKV)] * AL * ra) / den if den > 0 else 0.0
+    err = np.abs(got - want).max()
+    print(f"[merge batches] B={B} v_mean={with_vmean} partials={n} max_abs={err:.3e}")
+    assert np.isfinite(got).all()
+    assert err < 1e-4
