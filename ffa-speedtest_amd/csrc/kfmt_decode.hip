@@ -134,7 +134,8 @@ void kfmt_decode_kernel(const DecodeParams p) {
   __shared__ uint32_t s_bal[kChunksPerWG][2];
   __shared__ float s_pm[kChunksPerWG][4], s_pl[kChunksPerWG][4];
   __shared__ float s_po[kChunksPerWG][4][128];
-  __shared__ float s_cb[16];
+  // nf4: the codebook levels of both nibbles of every code byte, (low, high) at [byte]
+  __shared__ float2 s_cb2[FMT == kNF4 ? 256 : 1];
   __shared__ __attribute__((aligned(16))) uint8_t s_vstage[LAYOUT == kContig ? kWaves * kPage * (RELOAD ? kVRowHalf : kVRow) : 16];
 
   auto lds_barrier = []() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
@@ -281,7 +282,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
     }
   }
   if constexpr (FMT == kNF4) {
-    if (threadIdx.x < 16) s_cb[threadIdx.x] = kNF4Levels[threadIdx.x];
+    s_cb2[threadIdx.x] = make_float2(kNF4Levels[threadIdx.x & 15], kNF4Levels[threadIdx.x >> 4]);
   }
 
   // ------------------------------------------------ phase 2a: q operands (one per wave)
@@ -353,14 +354,11 @@ void kfmt_decode_kernel(const DecodeParams p) {
         r[3] = pack_f16(v3[0] * sc, v3[1] * sc);
       }
       if constexpr (FMT == kNF4) {
-        // byte offsets of the codebook entries (nibble * 4), four per word: low and high nibbles
-        uint32_t lo4 = (w << 2) & 0x3c3c3c3cu, hi4 = (w >> 2) & 0x3c3c3c3cu;
-        asm("" : "+v"(lo4), "+v"(hi4));  // keep the byte-wise form: one extract per offset
-        const char *cb = (const char *)s_cb;
+        // one 8-byte read per code byte: the levels of its low and high nibbles
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
-          const float l0 = *(const float *)(cb + ((lo4 >> (8 * h)) & 0xffu));
-          const float l1 = *(const float *)(cb + ((hi4 >> (8 * h)) & 0xffu));
+          const float2 lv = s_cb2[(w >> (8 * h)) & 0xffu];
+          const float l0 = lv.x, l1 = lv.y;
           const float s0 = kGrp ? sc : sch[8 * mp + 2 * h], s1 = kGrp ? sc : sch[8 * mp + 2 * h + 1];
           r[h] = mul_pack_f16(l0, s0, l1, s1);
         }
