@@ -206,7 +206,9 @@ __device__ __forceinline__ void write_empty_mask(int8_t *mask_row, int cg, int S
 // fp32 sums' resolution.
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
-enum { kChannel = 0, kG32 = 1 };
+// per-channel scales (fp16: dequantized by packed fp16 FMAs, exact), g32 scales, and per-channel
+// scales of other dtypes (fp32 / bf16: dequantized in fp32 as the reference does)
+enum { kChannel = 0, kG32 = 1, kChannelF32 = 2 };
 enum { kResNone = 0, kResE4M3 = 1, kResE5M2 = 2 };
 enum { kVF16 = 0, kVBF16 = 1 };
 

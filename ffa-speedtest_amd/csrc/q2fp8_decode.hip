@@ -60,8 +60,13 @@ __device__ __forceinline__ f16x8 codes_to_f16x8(uint32_t w, int s) {
 }
 
 // Reference-layout dequantization of 16 channels (one 32-bit code word, code i at bits 2i) into
-// the A operands of two score MFMAs: k_hat = fp16(c * s + z) with one rounding (c*s is exact in
-// fp32, so this equals the reference's fp16(fp32(fp32(c*s) + z))).  A code zero-extended to a
+// the A operands of two score MFMAs, for fp16 scale / zero: k_hat = fp16(c * s + z) with one
+// rounding.  The reference computes fp16(fp32(fp32(c * s) + z)) with s and z in fp32
+// (attn_kernel_v1210_fused_bsz_q2fp8.py:50-53, 93).  For fp16 s and z, c * s (at most 13
+// significant bits) is exact in fp32, and the two results differ only where the fp32 sum drops a
+// zero point below 2^-23 of c * s and c * s lies on an fp16 rounding midpoint (a check over
+// every finite fp16 (s, z) pair and c = 1..3 found no difference with |z| >= 2^-23 c s).  Other
+// scale dtypes take dequant8_channel_f32.  A code zero-extended to a
 // nibble is the e2m1 value c/2, so the hardware fp4 conversion with scale 2 yields c exactly, two
 // codes per instruction: masking with 0x33 leaves codes 4k and 4k+2 in the nibbles of byte k.
 // Element order inside each 8 channels: kChanPerm pairs (0,2) (4,6) (1,3) (5,7); the q operand,
@@ -86,6 +91,31 @@ __device__ __forceinline__ void dequant16_channel(uint32_t w, const uint32_t *sp
 // channel (within 8) of each element of a reference-layout score operand
 __host__ __device__ constexpr int kChanPerm(int e) { return (e & 1) * 2 + ((e >> 1) & 1) * 4 + (e >> 2); }
 
+// The same dequantization for fp32 scale / zero (and bf16, whose values fp16 cannot always
+// hold): k_hat = fp16(fp32(fp32(c * s) + z)), two fp32 roundings and one fp16 rounding, as the
+// reference computes it (attn_kernel_v1210_fused_bsz_q2fp8.py:52-53, 93).  One operand (8
+// channels) at a time: HALF = 0 takes codes 0-7 of the word (bytes 0, 1), HALF = 1 codes 8-15.
+// sz holds the operand's (s, z) in element order: [0], [1] = s of elements 0-3, 4-7; [2], [3] = z.
+template <int HALF>
+__device__ __forceinline__ f16x8 dequant8_channel_f32(uint32_t w, const float4 *sz) {
+#pragma clang fp contract(off)
+  const uint32_t e = w & 0x33333333u;
+  const uint32_t o = (w >> 2) & 0x33333333u;
+  constexpr int b0 = 2 * HALF;
+  // element pairs (0,1) (2,3) (4,5) (6,7) <-> codes (8h+0, 8h+2) (8h+4, 8h+6) (8h+1, 8h+3) (8h+5, 8h+7)
+  const f32x2 c[4] = {__builtin_amdgcn_cvt_scalef32_pk_f32_fp4(e, 2.0f, b0), __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(e, 2.0f, b0 + 1),
+                      __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(o, 2.0f, b0), __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(o, 2.0f, b0 + 1)};
+  const float sv[8] = {sz[0].x, sz[0].y, sz[0].z, sz[0].w, sz[1].x, sz[1].y, sz[1].z, sz[1].w};
+  const float zv[8] = {sz[2].x, sz[2].y, sz[2].z, sz[2].w, sz[3].x, sz[3].y, sz[3].z, sz[3].w};
+  u32x4 r;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float a0 = c[q][0] * sv[2 * q], a1 = c[q][1] * sv[2 * q + 1];
+    r[q] = f32_to_f16_bits(a0 + zv[2 * q]) | (f32_to_f16_bits(a1 + zv[2 * q + 1]) << 16);
+  }
+  return __builtin_bit_cast(f16x8, r);
+}
+
 // Position of token t (0..63) inside a page row of g32 scales / zeros.  Tile-major:
 // the scores of MFMA tile tau hold tokens 16k + 4u + tau (u = 0..3), whose scales
 // then sit at 16k + 4tau + u, one 8-byte load per lane and tile.
@@ -100,6 +130,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     const DecodeParams p) {
   typedef VTraits<VT> VTr;
   constexpr bool kG = SMODE == kG32;
+  constexpr bool kCF = SMODE == kChannelF32;  // per-channel fp32 / bf16 scales: dequantized in fp32
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // grid (span, KV head, sequence), the span along the sequence fastest: consecutive workgroups
@@ -131,8 +162,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   const int hq = un.row0 + (row_ok ? ir : 0);
 
   __shared__ uint4 s_qr[4][64];                    // B operands of the 4 residual MFMAs (g32)
-  __shared__ uint4 s_sp[kG ? 1 : 4][kG ? 1 : 64];   // channel scales: fp16 (scale, scale) pairs of 8 channels
-  __shared__ uint4 s_zp2[kG ? 1 : 4][kG ? 1 : 64];  // channel scales: fp16 (zero, zero) pairs
+  __shared__ uint4 s_sp[kG || kCF ? 1 : 4][kG || kCF ? 1 : 64];   // channel scales: fp16 (scale, scale) pairs of 8 channels
+  __shared__ uint4 s_zp2[kG || kCF ? 1 : 4][kG || kCF ? 1 : 64];  // channel scales: fp16 (zero, zero) pairs
+  // fp32 channel scales: [channel group kc][operand][s of elements 0-3, 4-7, z of 0-3, 4-7] (the
+  // lanes of one kc share them: broadcast reads)
+  __shared__ float4 s_cf[kCF ? 4 : 1][kCF ? 4 : 1][4];
   __shared__ float s_probe[2][4];
   __shared__ float s_wmax[kWaves][4];
   __shared__ int s_keep[kChunksPerWG * kPage / 16];  // pass 2: block decisions of the span
@@ -306,14 +340,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
       float sv[16], zv[16];
       raw16_to_f32(sraw, p.s_dtype, sv);
       raw16_to_f32(zraw, p.s_dtype, zv);
-      uint32_t spw[4], zpw[4];
+      if constexpr (kCF) {
+        if (mrow == 0) {
+          float se[8], ze[8];
 #pragma unroll
-      for (int qq = 0; qq < 4; ++qq) {
-        spw[qq] = f32_to_f16_bits(sv[8 * s + kChanPerm(2 * qq)]) | (f32_to_f16_bits(sv[8 * s + kChanPerm(2 * qq + 1)]) << 16);
-        zpw[qq] = f32_to_f16_bits(zv[8 * s + kChanPerm(2 * qq)]) | (f32_to_f16_bits(zv[8 * s + kChanPerm(2 * qq + 1)]) << 16);
+          for (int e = 0; e < 8; ++e) {
+            se[e] = sv[8 * s + kChanPerm(e)];
+            ze[e] = zv[8 * s + kChanPerm(e)];
+          }
+          s_cf[kc][w][0] = make_float4(se[0], se[1], se[2], se[3]);
+          s_cf[kc][w][1] = make_float4(se[4], se[5], se[6], se[7]);
+          s_cf[kc][w][2] = make_float4(ze[0], ze[1], ze[2], ze[3]);
+          s_cf[kc][w][3] = make_float4(ze[4], ze[5], ze[6], ze[7]);
+        }
+      } else {
+        uint32_t spw[4], zpw[4];
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+          spw[qq] = f32_to_f16_bits(sv[8 * s + kChanPerm(2 * qq)]) | (f32_to_f16_bits(sv[8 * s + kChanPerm(2 * qq + 1)]) << 16);
+          zpw[qq] = f32_to_f16_bits(zv[8 * s + kChanPerm(2 * qq)]) | (f32_to_f16_bits(zv[8 * s + kChanPerm(2 * qq + 1)]) << 16);
+        }
+        s_sp[w][lane] = make_uint4(spw[0], spw[1], spw[2], spw[3]);
+        s_zp2[w][lane] = make_uint4(zpw[0], zpw[1], zpw[2], zpw[3]);
       }
-      s_sp[w][lane] = make_uint4(spw[0], spw[1], spw[2], spw[3]);
-      s_zp2[w][lane] = make_uint4(zpw[0], zpw[1], zpw[2], zpw[3]);
     }
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq) {
@@ -338,7 +387,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   for (int mp = 0; mp < 4; ++mp) {
     const uint4 a = s_qa[mp][lane];
     qa[mp] = __builtin_bit_cast(f16x8, u32x4{a.x, a.y, a.z, a.w});
-    if constexpr (!kG) {
+    if constexpr (!kG && !kCF) {
       const uint4 sp = s_sp[mp][lane], zp = s_zp2[mp][lane];
       spair[4 * mp + 0] = sp.x; spair[4 * mp + 1] = sp.y; spair[4 * mp + 2] = sp.z; spair[4 * mp + 3] = sp.w;
       zpair[4 * mp + 0] = zp.x; zpair[4 * mp + 1] = zp.y; zpair[4 * mp + 2] = zp.z; zpair[4 * mp + 3] = zp.w;
@@ -348,6 +397,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     const int src = (jg << 4) | n;  // lane of the column's own group, same query row
     zq = ((s_zs[0][src] + s_zs[1][src]) + (s_zs[2][src] + s_zs[3][src])) * (1.0f / 16777216.f);
   }
+
+  // per-channel k_hat of the lane's 32 channels (two code words) as the four score operands
+  auto dequant_tile = [&](uint32_t wlo, uint32_t whi, f16x8 *k) {
+    if constexpr (kCF) {
+      k[0] = dequant8_channel_f32<0>(wlo, &s_cf[kc][0][0]);
+      k[1] = dequant8_channel_f32<1>(wlo, &s_cf[kc][1][0]);
+      k[2] = dequant8_channel_f32<0>(whi, &s_cf[kc][2][0]);
+      k[3] = dequant8_channel_f32<1>(whi, &s_cf[kc][3][0]);
+    } else {
+      dequant16_channel(wlo, spair + 0, zpair + 0, k[0], k[1]);
+      dequant16_channel(whi, spair + 8, zpair + 8, k[2], k[3]);
+    }
+  };
 
   // raw scores of one 16-token tile for the lane's column, summed over groups:
   //   g32: R' = sum_j s_j * D_j + z_j * zq_j   (units of 2^-24 of the dot product)
@@ -363,8 +425,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes_to_f16x8(whi, 1), qa[3], acc, 0, 0, 0);
     } else {
       f16x8 k[4];
-      dequant16_channel(wlo, spair + 0, zpair + 0, k[0], k[1]);
-      dequant16_channel(whi, spair + 8, zpair + 8, k[2], k[3]);
+      dequant_tile(wlo, whi, k);
 #pragma unroll
       for (int mp = 0; mp < 4; ++mp) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k[mp], qa[mp], acc, 0, 0, 0);
     }
@@ -681,8 +742,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
           const uint32_t wlo = (uint32_t)xx, whi = (uint32_t)(xx >> 32);
           f32x4 acc = {0.f, 0.f, 0.f, 0.f};
           f16x8 k[4];
-          dequant16_channel(wlo, spair + 0, zpair + 0, k[0], k[1]);
-          dequant16_channel(whi, spair + 8, zpair + 8, k[2], k[3]);
+          dequant_tile(wlo, whi, k);
           acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(add_f16x8(k[0], fp8x8_to_f16x8_perm<RES>(rr[tau][0].x, rr[tau][0].y)), qa[0], acc, 0, 0, 0);
           acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(add_f16x8(k[1], fp8x8_to_f16x8_perm<RES>(rr[tau][0].z, rr[tau][0].w)), qa[1], acc, 0, 0, 0);
           acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(add_f16x8(k[2], fp8x8_to_f16x8_perm<RES>(rr[tau][1].x, rr[tau][1].y)), qa[2], acc, 0, 0, 0);
@@ -1161,7 +1221,10 @@ static hipError_t launch_decode(const ffa::DecodeParams &p, dim3 grid, hipStream
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((ffa::q2fp8_decode_kernel<L, S, R, V, 1>), grid, dim3(256), 0, st, p);
+  // contiguous layout with fp32 channel scales: held to two workgroups per CU (the fp32
+  // dequantization's temporaries would otherwise take the kernel past 256 registers)
+  constexpr int occ = (L == ffa::kContig && S == ffa::kChannelF32) ? 2 : 1;
+  hipLaunchKernelGGL((ffa::q2fp8_decode_kernel<L, S, R, V, occ>), grid, dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
@@ -1278,10 +1341,14 @@ static int launch_stage1(const ffa_q2fp8_decode_args *a, const ffa::DecodeParams
     if (a->layout == FFA_LAYOUT_PAGED) {
       if (a->scale_mode == FFA_SCALE_G32)
         e = dispatch_rv<ffa::kPaged, ffa::kG32>(p, a->res_dtype, a->v_dtype, grid, st);
-      else
+      else if (a->scale_dtype == FFA_DT_F16)
         e = dispatch_rv<ffa::kPaged, ffa::kChannel>(p, a->res_dtype, a->v_dtype, grid, st);
-    } else {
+      else
+        e = dispatch_rv<ffa::kPaged, ffa::kChannelF32>(p, a->res_dtype, a->v_dtype, grid, st);
+    } else if (a->scale_dtype == FFA_DT_F16) {
       e = dispatch_rv<ffa::kContig, ffa::kChannel>(p, a->res_dtype, a->v_dtype, grid, st);
+    } else {  // fp32 / bf16 scale and zero: dequantized in fp32, as the reference does
+      e = dispatch_rv<ffa::kContig, ffa::kChannelF32>(p, a->res_dtype, a->v_dtype, grid, st);
     }
     if (e != hipSuccess) return set_err(FFA_E_LAUNCH, hipGetErrorString(e));
   }
