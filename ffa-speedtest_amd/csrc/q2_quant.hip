@@ -356,6 +356,74 @@ __global__ __launch_bounds__(256) void q2_g32_append_kernel(const void *k, int k
     ((uint16_t *)v_pages)[((size_t)page * HKV + hkv) * (D * 64) + vt_off(c, slot)] = ((const uint16_t *)v_new)[rowid * D + c];
 }
 
+
+// Paged g32 cache -> contiguous K and V (the exact-attention path of the HF integration, which the
+// reference feeds with dequantized keys: ffa-fp8fp8/e2e/fp8fp8_cache.py:60-69, returned by update at
+// :84-89).  One workgroup per (sequence, page of the sequence, KV head): K = c * s + z + r in fp32
+// (c * s is exact, so the fma rounds once, as the sum does), then one rounding to the output dtype;
+// V read from the V^T page through shared memory so that both outputs are written as rows.  Tokens at
+// or past the sequence's length are written as zeros; block-table entries outside the pool read page 0.
+__global__ __launch_bounds__(256) void q2_paged_dequant_kernel(const uint8_t *kq_pages, const uint16_t *s_pages,
+                                                               const uint16_t *z_pages, const uint8_t *r_pages,
+                                                               int res_e4m3, const uint16_t *v_pages, int vdt,
+                                                               const int32_t *bt, int bt_stride, int num_pages,
+                                                               const int32_t *seq_lens, int T, int HKV, void *k_out,
+                                                               void *v_out, int odt) {
+  constexpr int D = 128;
+  const int j = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z;
+  const int Tb = seq_lens ? min(max(seq_lens[b], 0), T) : T;
+  int page = bt[(size_t)b * bt_stride + j];
+  page = (unsigned)page < (unsigned)num_pages ? page : 0;
+  const size_t blk = (size_t)page * HKV + hkv;
+  __shared__ uint16_t s_v[64][D + 2];
+  // V^T: 1024 16-byte pieces (8 tokens of one column); piece P holds column 16 (P >> 7) + (P & 15),
+  // tokens 16 ((P >> 4) & 3) + 8 ((P >> 6) & 1) + (0..7)
+  const uint4 *vp = (const uint4 *)(v_pages + blk * (D * 64));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int P = threadIdx.x + 256 * i;
+    const int c = 16 * (P >> 7) + (P & 15), t0 = 16 * ((P >> 4) & 3) + 8 * ((P >> 6) & 1);
+    const uint4 w = vp[P];
+    const uint32_t e[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      s_v[t0 + 2 * k][c] = (uint16_t)(e[k] & 0xffffu);
+      s_v[t0 + 2 * k + 1][c] = (uint16_t)(e[k] >> 16);
+    }
+  }
+  // K: thread (token t, group g) dequantizes 32 channels
+  const int t = threadIdx.x >> 2, g = threadIdx.x & 3;
+  const int tok = 64 * j + t;
+  const bool valid = tok < Tb;
+  const uint2 cw = *(const uint2 *)(kq_pages + blk * (4 * 64 * 8) + codes_off(g, t));
+  const int ss = 16 * (t >> 4) + 4 * (t & 3) + ((t >> 2) & 3);  // tile-major scale slot, as appended
+  const float sc = f16_bits_to_f32(s_pages[blk * (4 * 64) + gscale_off(g, ss)]);
+  const float zr = f16_bits_to_f32(z_pages[blk * (4 * 64) + gscale_off(g, ss)]);
+  const uint4 r0 = *(const uint4 *)(r_pages + blk * (64 * D) + res_off(t, 32 * g));
+  const uint4 r1 = *(const uint4 *)(r_pages + blk * (64 * D) + res_off(t, 32 * g + 16));
+  const uint32_t rw[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+  const uint32_t cwords[2] = {cw.x, cw.y};
+  const size_t orow = ((size_t)b * T + tok) * HKV + hkv;
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const f16x8 rv = res_e4m3 ? fp8x8_to_f16x8<kResE4M3>(rw[2 * a], rw[2 * a + 1])
+                              : fp8x8_to_f16x8<kResE5M2>(rw[2 * a], rw[2 * a + 1]);  // exact
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int i = 8 * a + e;
+      const uint32_t code = (cwords[i >> 4] >> (2 * (i & 15))) & 3u;
+      const float k = __builtin_fmaf((float)code, sc, zr) + (float)rv[e];
+      store_any(k_out, orow * D + 32 * g + i, odt, valid ? k : 0.f);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const uint32_t bits = s_v[t][32 * g + i];
+    const float x = vdt == FFA_DT_BF16 ? bf16_bits_to_f32(bits) : f16_bits_to_f32(bits);
+    store_any(v_out, orow * D + 32 * g + i, odt, valid ? x : 0.f);
+  }
+}
 }  // namespace ffa
 
 // ============================================================================
@@ -500,4 +568,28 @@ extern "C" int ffa_q2_quantize_g32_append(const void *k, int k_dtype, int B, int
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return ffa_set_error_internal(FFA_E_LAUNCH, hipGetErrorString(e));
   return FFA_OK;
+}
+
+extern "C" int ffa_q2_paged_dequant(const uint8_t *k_q_pages, const void *scale_pages, const void *zero_pages,
+                                    const uint8_t *res_pages, int res_dtype, const void *v_pages, int v_dtype,
+                                    const int32_t *block_table, int bt_stride, int num_pages, const int32_t *seq_lens,
+                                    int B, int T, int HKV, void *k_out, void *v_out, int out_dtype, void *stream) {
+  if (B <= 0 || T <= 0 || HKV <= 0) return ffa_set_error_internal(FFA_E_INVALID, "bad dims");
+  if (B > 65535 || HKV > 65535) return ffa_set_error_internal(FFA_E_UNSUPPORTED, "B and HKV are grid dimensions");
+  if (bt_stride <= 0 || num_pages <= 0) return ffa_set_error_internal(FFA_E_INVALID, "empty block table or pool");
+  if ((long)bt_stride * ffa::kPage < T) return ffa_set_error_internal(FFA_E_INVALID, "block table has fewer than ceil(T/64) columns");
+  if (!(res_dtype == FFA_DT_FP8_E4M3 || res_dtype == FFA_DT_FP8_E5M2))
+    return ffa_set_error_internal(FFA_E_INVALID, "residual dtype must be fp8");
+  if (!(v_dtype == FFA_DT_F16 || v_dtype == FFA_DT_BF16)) return ffa_set_error_internal(FFA_E_INVALID, "v dtype");
+  if (!(out_dtype >= FFA_DT_F16 && out_dtype <= FFA_DT_F32)) return ffa_set_error_internal(FFA_E_INVALID, "out dtype");
+  if (!k_q_pages || !scale_pages || !zero_pages || !res_pages || !v_pages || !block_table || !k_out || !v_out)
+    return ffa_set_error_internal(FFA_E_INVALID, "null pointer");
+  if (T % ffa::kPage) return ffa_set_error_internal(FFA_E_INVALID, "T must be a multiple of the 64-token page");
+  hipLaunchKernelGGL(ffa::q2_paged_dequant_kernel, dim3((unsigned)(T / ffa::kPage), (unsigned)HKV, (unsigned)B),
+                     dim3(256), 0, (hipStream_t)stream, k_q_pages, (const uint16_t *)scale_pages,
+                     (const uint16_t *)zero_pages, res_pages, res_dtype == FFA_DT_FP8_E4M3 ? 1 : 0,
+                     (const uint16_t *)v_pages, v_dtype, block_table, bt_stride, num_pages, seq_lens, T, HKV, k_out,
+                     v_out, out_dtype);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? FFA_OK : ffa_set_error_internal(FFA_E_LAUNCH, hipGetErrorString(e));
 }

@@ -13,18 +13,21 @@ Here, for q2fp8, on the MI355X library:
   (`ffa_q2_quantize_g32_append`) and never dequantizes the cache.
 * `ffa_q2fp8_attention`: registered with transformers' attention registry as "ffa_q2fp8", so an
   unmodified `LlamaForCausalLM` (or any model whose attention goes through `ALL_ATTENTION_FUNCTIONS`)
-  uses it once `enable_ffa_q2fp8(model, ...)` is called.  A step with one query token per sequence runs
-  the pruned decode over the paged cache (`attn_settings`: BS, SBS, delta, use_fp8_residual as in the
-  reference's `config.attn_settings`, e2e/bench_llama_fp8fp8.py:179-189); a prefill into an empty cache
-  runs exact causal attention on the prompt's own K / V (in fp32), as the reference runs FlashAttention
-  for prefill (modeling_llama.py:322-337).
+  uses it once `enable_ffa_q2fp8(model, ...)` is called.  As in the reference's hook
+  (modeling_llama.py:281-337, settings from `config.attn_settings`, e2e/bench_llama_fp8fp8.py:179-189):
+  a step with one query token per sequence, `use_ffa_decode` set and the layer in `pattern_layers`
+  (default: every layer) runs the pruned decode over the paged cache (BS, SBS, delta,
+  use_fp8_residual); every other step -- the prompt, a later multi-token chunk, decode steps of layers
+  outside `pattern_layers` or with `use_ffa_decode=False` -- runs exact causal attention over the
+  cache's own keys and values dequantized by `ffa_q2_paged_dequant` (the reference attends with
+  FlashAttention to the keys its cache returns dequantized from every update, fp8fp8_cache.py:60-69,
+  84-89).  The exact attention itself is fp32 torch matmuls, as the reference's is a library call.
 
 The HF models apply RoPE (their half-split `rotate_half`) before `Cache.update`, so the cache receives
 rotated K and appends it with the quantize-append entry point; the fused K-projection + RoPE producer
 follows the reference producer's interleaved-pair RoPE instead and serves the benchmark path.
 
-Limits: all sequences of a batch have the same length (no padding), one prefill per cache (prefill
-after decode steps would need the dequantized past), no beam search reordering.
+Limits: all sequences of a batch have the same length (no padding), no beam search reordering.
 """
 from __future__ import annotations
 
@@ -45,8 +48,10 @@ from ffa_mi355x.paged import PAGE, PagedQ2Cache  # noqa: E402
 __all__ = ["Q2FP8Cache", "Q2FP8PagedLayer", "ffa_q2fp8_attention", "enable_ffa_q2fp8"]
 
 ATTN_NAME = "ffa_q2fp8"
-DEFAULT_SETTINGS = dict(use_ffa_decode=True, BS=64, SBS=64, delta=5.0, use_fp8_residual=True)
-_current = threading.local()  # the layer whose update() ran last on this thread
+DEFAULT_SETTINGS = dict(use_ffa_decode=True, BS=64, SBS=64, delta=5.0, use_fp8_residual=True, pattern_layers=None)
+# (layer index, layer) of the update() that ran last on this thread; the attention of that layer
+# takes it (and clears it), so a model run without a Q2FP8Cache cannot pick up a stale layer
+_current = threading.local()
 
 
 class Q2FP8PagedLayer(CacheLayerMixin):
@@ -145,36 +150,51 @@ class Q2FP8Cache(Cache):
 
     def update(self, key_states: torch.Tensor, value_states: torch.Tensor, layer_idx: int, *args, **kwargs):
         out = self.layers[layer_idx].update(key_states, value_states)
-        _current.layer = self.layers[layer_idx]  # read by ffa_q2fp8_attention for the same layer
+        _current.entry = (layer_idx, self.layers[layer_idx])  # taken by ffa_q2fp8_attention of that layer
         return out
 
 
-def _prefill_attention(query, key, value, scaling):
-    """Exact causal attention of a prompt on its own K / V (fp32, contiguous operands)."""
+def exact_attention(query: torch.Tensor, layer: Q2FP8PagedLayer, scaling: float) -> torch.Tensor:
+    """Causal attention of the L newest query tokens [B, HQ, L, D] over the whole cache (positions
+    seq_len - L .. seq_len - 1 see the keys up to their own position), on the keys and values the
+    cache holds, dequantized in the model dtype (fp32 arithmetic, contiguous operands).  Returns
+    [B, L, HQ, D]."""
     B, HQ, L, D = query.shape
-    G = HQ // key.shape[1]
-    k = key.float().repeat_interleave(G, dim=1).contiguous()
-    v = value.float().repeat_interleave(G, dim=1).contiguous()
+    S = layer.seq_len
+    k, v = layer.pool.dequantize(layer.block_table, S, layer.seq_lens, out_dtype=layer.dtype)
+    G = HQ // layer.pool.HKV
+    k = k[:, :S].float().transpose(1, 2).repeat_interleave(G, dim=1).contiguous()  # [B, HQ, S, D]
+    v = v[:, :S].float().transpose(1, 2).repeat_interleave(G, dim=1).contiguous()
     s = torch.matmul(query.float().contiguous(), k.transpose(2, 3).contiguous()) * scaling
-    s = s.masked_fill(torch.ones(L, L, dtype=torch.bool, device=s.device).triu(1), float("-inf"))
+    qpos = torch.arange(S - L, S, device=s.device)[:, None]
+    s = s.masked_fill(torch.arange(S, device=s.device)[None, :] > qpos, float("-inf"))
     p = torch.softmax(s, dim=-1)
-    return torch.matmul(p, v).to(query.dtype).transpose(1, 2).contiguous()  # [B, L, HQ, D]
+    return torch.matmul(p, v).to(query.dtype).transpose(1, 2).contiguous()
 
 
 def ffa_q2fp8_attention(module, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, attention_mask,
                         scaling: Optional[float] = None, dropout: float = 0.0, **kwargs):
     """Attention of one layer (the transformers attention-function signature); query [B, HQ, L, D] rotated.
 
-    L == 1: the pruned q2fp8 decode over the layer's paged cache (modeling_llama.py:293-321's branch);
-    otherwise exact causal attention of the prompt on the K / V it just appended."""
+    L == 1 with use_ffa_decode and the layer in pattern_layers: the pruned q2fp8 decode over the
+    layer's paged cache (modeling_llama.py:293-321's branch); otherwise exact causal attention over
+    the cache's dequantized keys and values (:322-337)."""
     settings = dict(DEFAULT_SETTINGS)
     settings.update(getattr(module.config, "attn_settings", None) or {})
-    layer = getattr(_current, "layer", None)
-    if not isinstance(layer, Q2FP8PagedLayer):
-        raise RuntimeError("ffa_q2fp8 attention needs a Q2FP8Cache passed as past_key_values")
+    entry = getattr(_current, "entry", None)
+    _current.entry = None
+    if entry is None or not isinstance(entry[1], Q2FP8PagedLayer):
+        raise RuntimeError("ffa_q2fp8 attention needs a Q2FP8Cache passed as past_key_values (with use_cache)")
+    layer_idx, layer = entry
+    if getattr(module, "layer_idx", layer_idx) != layer_idx:
+        raise RuntimeError(f"ffa_q2fp8 attention of layer {module.layer_idx} after the cache update of layer "
+                           f"{layer_idx}")
     B, HQ, L, D = query.shape
     scale = scaling if scaling is not None else 1.0 / math.sqrt(D)
-    if L == 1 and settings["use_ffa_decode"]:
+    pattern = settings.get("pattern_layers")
+    if pattern is not None and not isinstance(pattern, (list, tuple)):
+        raise TypeError("pattern_layers must be a list of layer indices")
+    if L == 1 and settings["use_ffa_decode"] and (pattern is None or layer_idx in pattern):
         ws = layer.workspace(HQ, settings["BS"], settings["SBS"], query.dtype)
         layer.pool.decode(query[:, :, 0, :].contiguous(), layer.block_table, layer.seq_lens, T=layer.capacity,
                           scale=scale, BS=settings["BS"], SBS=settings["SBS"], delta=settings["delta"],
@@ -182,17 +202,19 @@ def ffa_q2fp8_attention(module, query: torch.Tensor, key: torch.Tensor, value: t
         out = ws.o.unsqueeze(1)  # [B, 1, HQ, D]
         hook: Optional[Callable] = settings.get("on_decode")
         if hook is not None:
-            hook(module.layer_idx, query[:, :, 0, :], out[:, 0], layer)
+            hook(layer_idx, query[:, :, 0, :], out[:, 0], layer)
         return out, None
-    if layer.seq_len != L:
-        raise NotImplementedError("a prefill after earlier tokens (chunked prefill) is not supported: the paged "
-                                  "q2fp8 cache keeps no full-precision keys")
-    return _prefill_attention(query, key, value, scale), None
+    out = exact_attention(query, layer, scale)
+    hook = settings.get("on_exact")
+    if hook is not None:
+        hook(layer_idx, query, out, layer)
+    return out, None
 
 
 def enable_ffa_q2fp8(model, **attn_settings: Any) -> None:
     """Route the model's attention through ffa_q2fp8_attention (registered once) with these settings
-    (BS, SBS, delta, use_fp8_residual, use_ffa_decode; optional on_decode(layer_idx, q, o, cache_layer))."""
+    (BS, SBS, delta, use_fp8_residual, use_ffa_decode, pattern_layers; optional
+    on_decode(layer_idx, q, o, cache_layer) and on_exact(layer_idx, q, o, cache_layer) observers)."""
     AttentionInterface.register(ATTN_NAME, ffa_q2fp8_attention)
     cfg = model.config
     cfg.attn_settings = {**DEFAULT_SETTINGS, **attn_settings}

@@ -36,6 +36,7 @@ EXPORTS = (
     "ffa_kproj_rope_q2_channel",
     "ffa_kproj_rope_q2_append",
     "ffa_q2_quantize_g32_append",
+    "ffa_q2_paged_dequant",
     "ffa_kproj_rope",
     "ffa_fp8fp8_quantize",
     "ffa_fp8_scaled_quantize",
@@ -199,6 +200,8 @@ def lib() -> ctypes.CDLL:
         L.ffa_kproj_rope_q2_append.restype = ci
         L.ffa_q2_quantize_g32_append.argtypes = [vp, ci, ci, ci, ci, vp, vp, ci, ci, vp, vp, vp, vp, ci, vp, vp, vp]
         L.ffa_q2_quantize_g32_append.restype = ci
+        L.ffa_q2_paged_dequant.argtypes = [vp, vp, vp, vp, ci, vp, ci, vp, ci, ci, vp, ci, ci, ci, vp, vp, ci, vp]
+        L.ffa_q2_paged_dequant.restype = ci
         L.ffa_kproj_rope.argtypes = [vp, vp, vp, ci, vp, vp, ci, ci, ci, ci, ci, ci, vp, vp]
         L.ffa_kproj_rope.restype = ci
         L.ffa_fp8fp8_quantize.argtypes = [vp, ci, ctypes.c_size_t, vp, vp, ci, vp]

@@ -122,6 +122,30 @@ class PagedQ2Cache:
             N.stream_of(k.device))
         N.check(rc, "ffa_q2_quantize_g32_append")
 
+    def dequantize(self, block_table: torch.Tensor, T: int, seq_lens: torch.Tensor | None = None,
+                   out_dtype: torch.dtype = torch.float32):
+        """K and V [B, T', HKV, 128] of the first T tokens of every sequence (T' = T rounded up to a
+        page), K = codes * scale + zero + residual in fp32 rounded once to out_dtype, V from the V^T
+        pages; tokens at or past seq_lens[b] are zeros.  The keys an exact attention over the cache
+        sees (the reference returns its cache's dequantized keys from update: ffa-fp8fp8/e2e/
+        fp8fp8_cache.py:60-69, 84-89)."""
+        block_table = block_table.to(torch.int32).contiguous()
+        B = block_table.shape[0]
+        Tp = -(-int(T) // PAGE) * PAGE
+        if Tp > block_table.shape[1] * PAGE:
+            raise ValueError("T exceeds the block table")
+        if seq_lens is not None:
+            seq_lens = seq_lens.to(device=self.device, dtype=torch.int32).contiguous()
+        k = torch.empty((B, Tp, self.HKV, HEAD_DIM), dtype=out_dtype, device=self.device)
+        v = torch.empty_like(k)
+        rc = N.lib().ffa_q2_paged_dequant(
+            self.k_q.data_ptr(), self.k_scale.data_ptr(), self.k_zero.data_ptr(), self.k_res.data_ptr(),
+            N.dtype_code(self.res_dtype), self.v.data_ptr(), N.dtype_code(self.v_dtype), block_table.data_ptr(),
+            block_table.shape[1], self.P, N.ptr(seq_lens), B, Tp, self.HKV, k.data_ptr(), v.data_ptr(),
+            N.dtype_code(out_dtype), N.stream_of(self.device))
+        N.check(rc, "ffa_q2_paged_dequant")
+        return k, v
+
     # ------------------------------------------------------------------ decode
     def value_mean(self, block_table, seq_lens=None, *, T=None, out_dtype=None):
         """Mean over each sequence's tokens of its V pages, [B, HKV, 128] (the mean-V fallback's v_mean)."""

@@ -29,6 +29,9 @@
  *                             reference-layout cache with its existing per-channel scale / zero
  *   ffa_q2_quantize_g32_append no reference counterpart: g32 quantize + paged append of
  *                             given K rows (the paged g32 cache layout)
+ *   ffa_q2_paged_dequant      ffa-fp8fp8/e2e/fp8fp8_cache.py:60-69, 84-89 (_refresh_fp_cache:
+ *                             the cache's keys dequantized for exact attention), for the
+ *                             paged g32 cache
  *   ffa_kproj_rope_q2_append  no reference counterpart: decode-time append of
  *                             K-proj + RoPE + g32 quantize into the paged cache
  *                             (incremental quantisation is a TODO in the reference,
@@ -266,6 +269,19 @@ int ffa_q2_quantize_g32_append(const void *k, int k_dtype, int B, int Tn, int HK
                                const int32_t *block_table, int bt_stride, int num_pages, uint8_t *k_q_pages,
                                void *scale_pages, void *zero_pages, uint8_t *res_pages, int res_dtype,
                                const void *v_new, void *v_pages, void *stream);
+
+/*
+ * Paged g32 cache -> contiguous K and V [B, T, HKV, 128] in out_dtype (F16/BF16/F32), the keys
+ * dequantized as k = c * scale + zero + residual (fp32, one rounding to out_dtype) and V copied
+ * from the V^T pages (v_dtype F16/BF16).  T is a multiple of 64; tokens at or past seq_lens[b]
+ * (seq_lens may be NULL: every sequence holds T tokens) are written as zeros.  Block-table
+ * entries outside [0, num_pages) read page 0.  Feeds exact attention over the cache (prefill,
+ * chunked prefill, and decode steps that do not prune).
+ */
+int ffa_q2_paged_dequant(const uint8_t *k_q_pages, const void *scale_pages, const void *zero_pages,
+                         const uint8_t *res_pages, int res_dtype, const void *v_pages, int v_dtype,
+                         const int32_t *block_table, int bt_stride, int num_pages, const int32_t *seq_lens,
+                         int B, int T, int HKV, void *k_out, void *v_out, int out_dtype, void *stream);
 
 /*
  * K projection + RoPE without quantization (the first half of every producer):
