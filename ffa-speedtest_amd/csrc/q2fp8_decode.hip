@@ -1400,12 +1400,18 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 uint8_t *g_scratch_ptr[kMaxDevices] = {};
 
-int static_scratch_of_current_device(uint8_t **out) {
+int static_scratch_of_current_device(uint8_t **out, hipStream_t st) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
     return set_err(FFA_E_LAUNCH, "no current HIP device for the static scratch");
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr[dev] == nullptr) {
+    // the address is resolved on the first call on a device, which must not be under stream capture
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+      return set_err(FFA_E_INVALID, "ffa_q2fp8_decode_noalloc: the first call on a device must run outside stream "
+                                    "capture (it resolves the static scratch's device address)");
+    if (ffa::device_cus() <= 0) return set_err(FFA_E_LAUNCH, "hipDeviceGetAttribute(multiprocessor count) failed");
     void *ptr = nullptr;
     const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     if (e != hipSuccess || ptr == nullptr) return set_err(FFA_E_LAUNCH, "hipGetSymbolAddress(scratch) failed");
@@ -1454,7 +1460,7 @@ extern "C" int ffa_q2fp8_decode_noalloc(const ffa_q2fp8_decode_args *a, void *st
     return set_err(FFA_E_UNSUPPORTED, msg);
   }
   uint8_t *base = nullptr;
-  const int rc = static_scratch_of_current_device(&base);
+  const int rc = static_scratch_of_current_device(&base, (hipStream_t)stream);
   if (rc != FFA_OK) return rc;
   ffa_q2fp8_decode_args s = *a;
   s.m_buf = reinterpret_cast<float *>(base + m_at);

@@ -22,6 +22,12 @@ the pruned tokens' maximum and mass; the merge folds them with v_mean.  v_mean c
 Extensions through **kwargs, as for the q2fp8 drop-in: block_table / seq_lens / T (paged pools,
 ragged lengths), workspace; and v_mean=[B, HKV, V] to pass a mean the caller keeps (then V is not
 read for it).
+
+Block flags.  The reference keeps its mask_buf / approx_buf inside the call.  A workspace passed
+here holds the q2fp8 decode's survivor mask: `workspace.mask_buf` = 1 for blocks refined exactly.
+The reference's two flags follow from it with `ffa_mi355x.meanv.approx_flags(mask_buf, T, BS, SBS,
+seq_lens)`: approx = pruned blocks that hold tokens (:117-119), and its mask_buf = exact or
+approximated (:118, :151).
 """
 import sys
 from pathlib import Path

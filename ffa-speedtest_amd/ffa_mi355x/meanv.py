@@ -72,3 +72,18 @@ def approx_ratio(mask: torch.Tensor, T: int, BS: int, SBS: int, seq_lens=None) -
         with_tokens = HKV * sum(math.ceil(t / SBS) for t in lens)
         total = HKV * sum(decode_ntbs(t, BS, SBS) for t in lens)
     return max(with_tokens - kept, 0) / max(total, 1)
+
+
+def approx_flags(mask: torch.Tensor, T: int, BS: int, SBS: int, seq_lens=None):
+    """The mean-V variant's per-block flags, from the survivor mask the decode writes (1 = refined
+    exactly): approx = pruned blocks that hold tokens (reference :117-119 writes approx_buf = 1 there,
+    :151-152 writes 0 for exact blocks), and the variant's own mask_buf = exact or approximated
+    (reference :118, :151).  Returns (mask_meanv, approx), int8 [B, HKV, NTBS]; blocks past a
+    sequence's last token are 0 in both."""
+    B, HKV, NTBS = mask.shape
+    lens = [T] * B if seq_lens is None else [min(max(int(t), 0), T) for t in seq_lens.tolist()]
+    nblk = torch.tensor([math.ceil(t / SBS) for t in lens], device=mask.device)
+    has_tokens = torch.arange(NTBS, device=mask.device)[None, :] < nblk[:, None]  # [B, NTBS]
+    kept = mask != 0
+    approx = has_tokens[:, None, :] & ~kept
+    return (kept | approx).to(torch.int8), approx.to(torch.int8)

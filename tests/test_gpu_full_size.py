@@ -232,7 +232,10 @@ def test_config5_full_size(gpu):
         assert np.array_equal(kq, pk[b, 0]), ("codes", b)
         rr = to_logical(cache.k_res[page].view(torch.uint8).cpu().numpy(), RES_ORDER)[:, slot]
         assert np.array_equal(rr, r[b, 0]), ("residual", b)
-    # sampled tokens of the bulk fill
+        sc = to_logical(cache.k_scale[page].float().cpu().numpy(), GSCALE_ORDER)[..., SPOS][:, :, slot]
+        zc = to_logical(cache.k_zero[page].float().cpu().numpy(), GSCALE_ORDER)[..., SPOS][:, :, slot]
+        assert np.array_equal(sc, s[b, 0]) and np.array_equal(zc, z[b, 0]), ("scale / zero", b)
+    # sampled tokens of the bulk fill: every field
     bs, ts, rows = _sample_rows(ks, lens, 256, seed=6)
     pk2, s2, z2, r2 = O.quantize_g32(rows, "e4m3fn")
     for j in range(256):
@@ -242,6 +245,10 @@ def test_config5_full_size(gpu):
         assert np.array_equal(kq, pk2[j]), ("codes", b, t)
         sc = to_logical(cache.k_scale[page].float().cpu().numpy(), GSCALE_ORDER)[..., SPOS][:, :, slot]
         assert np.array_equal(sc, s2[j]), ("scales", b, t)
+        zc = to_logical(cache.k_zero[page].float().cpu().numpy(), GSCALE_ORDER)[..., SPOS][:, :, slot]
+        assert np.array_equal(zc, z2[j]), ("zeros", b, t)
+        rr = to_logical(cache.k_res[page].view(torch.uint8).cpu().numpy(), RES_ORDER)[:, slot]
+        assert np.array_equal(rr, r2[j]), ("residual", b, t)
 
     # sequences alone == rows of the batch (a sample of 4), bit-exact
     for b in (0, 21, 42, 63):

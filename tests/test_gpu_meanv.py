@@ -92,6 +92,14 @@ def test_meanv_contiguous_dropin(gpu, T, HQ, BS, SBS, delta):
     assert far == 0
     if near == 0:
         assert abs(ratio - diag["approx_ratio"]) < 1e-9
+        # the reference's per-block flags (approx_buf, and mask_buf = exact or approximated)
+        from ffa_mi355x.meanv import approx_flags
+
+        m_ref, apx = approx_flags(ws.mask_buf, T, BS, SBSv)
+        n = diag["approx"].shape[-1]
+        assert np.array_equal(apx.cpu().numpy()[..., :n], diag["approx"])
+        assert np.array_equal(m_ref.cpu().numpy()[..., :n], diag["approx"] | diag["mask"])
+        assert int(apx.sum()) == int(diag["approx"].sum())
     o_forced, _ = O.decode(*args, res_fmt="e5m2", BS=BS, SBS=SBSv, delta=delta, out_dtype="bf16", v_mean=vmean,
                            force_mask=mask)
     mx, mean = assert_out_close(f32(o), o_forced, "meanv contiguous")

@@ -1,7 +1,8 @@
 """ffa_q2fp8_decode_noalloc (scratch in the library's static device array) against ffa_q2fp8_decode
 (caller-owned scratch), through the C ABI: two calls in a row, the second with a smaller input
 (and the two-pass path), outputs bit-identical; a shape beyond the static array is refused
-before any launch."""
+before any launch; a call captured into a HIP graph (after one eager call has resolved the
+scratch address) replays to the decode's output."""
 import ctypes
 
 import pytest
@@ -105,3 +106,38 @@ def test_noalloc_mean_v(gpu):
     N.check(rc, "ffa_q2fp8_decode_noalloc")
     torch.cuda.synchronize()
     assert torch.equal(out, ws.o)
+
+
+def test_noalloc_under_graph_capture(gpu):
+    """Captured into a graph (torch.cuda.graph) after an eager call on the device, replayed three times
+    with eager decodes of other inputs in between: every replay equals ffa_q2fp8_decode bit for bit."""
+    c = paged_case(B=2, T=4096, HQ=32, HKV=8, seed=55, n_heavy=16, seq_lens=[4096, 2500])
+    cache = to_gpu_paged(c, gpu)
+    kw, _ = _args(c, cache, gpu, 64, 64, 5.0, c["lens"])
+    ws = D.run_decode(**kw)
+    torch.cuda.synchronize()
+    out0, _, _ = _noalloc(kw, gpu, keep_mask=False)  # eager: resolves the static scratch address
+    assert torch.equal(out0, ws.o)
+    a, _ = D.decode_args(**kw)
+    out = torch.full_like(ws.o, float("nan"))
+    a.out = out.data_ptr()
+    a.m_buf = a.l_buf = a.o_buf = None
+    a.nparts = 0
+    a.mask, a.threshold_out = None, None
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(g, stream=s):
+        rc = N.lib().ffa_q2fp8_decode_noalloc(ctypes.byref(a), ctypes.c_void_p(s.cuda_stream))
+    N.check(rc, "ffa_q2fp8_decode_noalloc (captured)")
+    c2 = paged_case(B=1, T=2000, HQ=32, HKV=8, seed=56, n_heavy=8)
+    cache2 = to_gpu_paged(c2, gpu)
+    kw2, _ = _args(c2, cache2, gpu, 64, 64, 4.0)
+    for _ in range(3):
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ws.o)
+        D.run_decode(**kw2)  # eager work between replays, using the same library
+        _noalloc(kw2, gpu, keep_mask=False)  # and the static scratch itself
+        torch.cuda.synchronize()
