@@ -64,8 +64,9 @@ __device__ __forceinline__ f16x8 codes_to_f16x8(uint32_t w, int s) {
 // rounding.  The reference computes fp16(fp32(fp32(c * s) + z)) with s and z in fp32
 // (attn_kernel_v1210_fused_bsz_q2fp8.py:50-53, 93).  For fp16 s and z, c * s (at most 13
 // significant bits) is exact in fp32, and the two results differ only where the fp32 sum drops a
-// zero point below 2^-23 of c * s and c * s lies on an fp16 rounding midpoint (a check over
-// every finite fp16 (s, z) pair and c = 1..3 found no difference with |z| >= 2^-23 c s).  Other
+// zero point below 2^-23 of c * s and c * s lies on an fp16 rounding midpoint (checked against
+// every finite fp16 z and c = 1..3 over a stride of the fp16 scales: no difference with
+// |z| >= 2^-23 c s).  Other
 // scale dtypes take dequant8_channel_f32.  A code zero-extended to a
 // nibble is the e2m1 value c/2, so the hardware fp4 conversion with scale 2 yields c exactly, two
 // codes per instruction: masking with 0x33 leaves codes 4k and 4k+2 in the nibbles of byte k.
