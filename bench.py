@@ -1,5 +1,5 @@
 #!/usr/bin/env python
-"""Benchmark of the MI355X q2fp8 pruned decode.
+"""Benchmark of the MI355X q2fp8 pruned decode (benchmark config 2).
 
 Workload: one decode-attention step ("layer-step") of batch 1 over a 32K
 context, 32 query / 8 KV heads, head dim 128.  K is 2-bit (groups of 32 along
@@ -138,16 +138,16 @@ def cpu_baseline(q, k, v, BS, SBS, delta, seconds):
 
 
 WORKLOADS = {
-    "config2ref": "BASELINE config 2 in the reference's own layout: per-channel q2 scale/zero over T, e5m2 "
+    "config2ref": "benchmark config 2 in the reference's own layout: per-channel q2 scale/zero over T, e5m2 "
                   "residual, contiguous [B, T, HKV, D] cache (ffa-q2fp8/run_attn_bench_q2.py:78-105), bs=1, 32K ctx, "
                   "32/8/128, BS=SBS=64, delta=5",
-    "config1": "BASELINE config 1: fp8 e4m3 K with one fp16 scale per token and KV head + e4m3 residual, bf16 V, "
+    "config1": "benchmark config 1: fp8 e4m3 K with one fp16 scale per token and KV head + e4m3 residual, bf16 V, "
                "B=1, T=4096, 32/8/128, 4 of 128 K channels x10, contiguous cache, BS=SBS=64, delta=5",
-    "config3": "BASELINE config 3: nvfp4-g16 + e4m3 residual pruned decode, B=4 x 128K, 32/8/128, 64-token pages "
+    "config3": "benchmark config 3: nvfp4-g16 + e4m3 residual pruned decode, B=4 x 128K, 32/8/128, 64-token pages "
                "interleaved across sequences",
-    "config4": "BASELINE config 4: nf4-g64 + e4m3 residual pruned decode, B=16 ragged 8K-64K (seeded), 32/8/128, "
+    "config4": "benchmark config 4: nf4-g64 + e4m3 residual pruned decode, B=16 ragged 8K-64K (seeded), 32/8/128, "
                "64-token pages interleaved across sequences",
-    "config5": "BASELINE config 5: K-proj (4096 -> 8x128) + RoPE (theta 5e5, positions 65536..65599) + g32 q2 + "
+    "config5": "benchmark config 5: K-proj (4096 -> 8x128) + RoPE (theta 5e5, positions 65536..65599) + g32 q2 + "
                "e4m3 quantize, appending token 65536+b to sequence b of 64, then one q2fp8 pruned decode over "
                "the 65537..65600-token contexts at B=64",
 }
@@ -290,7 +290,7 @@ def _bench_contiguous(args, q, k, v, t_setup, workload, metric, data):
 
 
 def bench_config1(args):
-    """BASELINE config 1 on the GPU (the reference runs it on the CPU): HIP quantizer, then the fp8 decode over
+    """Benchmark config 1 on the GPU (the reference runs it on the CPU): HIP quantizer, then the fp8 decode over
     the contiguous cache; 24 rotated copies defeat the MALL.  cpu_baseline: the numpy oracle, 1 thread."""
     import numpy as np
     import torch
@@ -373,7 +373,7 @@ def bench_config1(args):
 
 
 def bench_workload(args):
-    """BASELINE configs 3, 4 and 5 at their full sizes: one JSON line with the step time and its bandwidth.
+    """Benchmark configs 3, 4 and 5 at their full sizes: one JSON line with the step time and its bandwidth.
 
     K and V are drawn on the device per sequence (synth.sequence_inputs_device), quantized and appended by
     the library's own append kernels, so no host copy of the multi-GB caches exists.
@@ -513,7 +513,7 @@ def main():
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run 5 device copies of 256 MiB (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--workload", choices=("config2", "layerdata") + tuple(WORKLOADS), default="config2",
-                    help="config2 (default) is the metric's line; config2ref, config1/3/4/5 time the other BASELINE "
+                    help="config2 (default) is the metric's line; config2ref, config1/3/4/5 time the other benchmark "
                          "decodes; layerdata times recorded layers (--layer-data)")
     ap.add_argument("--layer-data", default=None, help="layerdata: a layer_data directory (layer_0, layer_1, ...)")
     ap.add_argument("--layer", type=int, default=0, help="layerdata: first layer")
@@ -681,7 +681,7 @@ def main():
         "hbm_tbps": round(achieved_gbs / 1e3, 4),
         "hbm_pct_peak": round(100.0 * achieved_gbs / HBM_PEAK_GBS, 2),
         "config": {
-            "workload": "BASELINE config 2: q2fp8 pruned decode, bs=1, 32K ctx, 32/8/128, 64-token pages",
+            "workload": "benchmark config 2: q2fp8 pruned decode, bs=1, 32K ctx, 32/8/128, 64-token pages",
             "B": B, "T": T, "HQ": HQ, "HKV": HKV, "D": D, "BS": args.BS, "SBS": args.SBS, "delta": args.delta,
             "keep_fraction": round(keep_frac, 4), "algorithmic_bytes": nbytes, "rotations": R,
             "timing": "HIP graph of R rotated steps, hipEvent over the replays",

@@ -11,7 +11,7 @@ from oracle import q2fp8 as O
 TORCH_DT = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}
 FP8_DT = {"e4m3fn": torch.float8_e4m3fn, "e5m2": torch.float8_e5m2}
 
-# BASELINE tolerances (north_star): output within max-abs 2e-2 and mean-abs 2e-3;
+# Decode tolerances: output within max-abs 2e-2 and mean-abs 2e-3;
 # survivor mask identical except blocks within 1e-3 (log2 units) of the threshold.
 OUT_MAX_ABS = 2e-2
 OUT_MEAN_ABS = 2e-3
@@ -44,7 +44,7 @@ def to_gpu_contig(case, dev):
 
 def paged_case(B=1, T=2048, HQ=32, HKV=8, seed=0, n_heavy=16, res="e4m3fn", seq_lens=None, garbage=True,
                interleave=True):
-    """BASELINE layout: g32 q2 + fp8 residual in 64-token pages with a random page table."""
+    """Benchmark layout: g32 q2 + fp8 residual in 64-token pages with a random page table."""
     q, k, v = synth.attention_inputs(B=B, T=T, HQ=HQ, HKV=HKV, seed=seed, n_heavy=n_heavy, seq_lens=seq_lens)
     lens = [T] * B if seq_lens is None else [int(x) for x in seq_lens]
     pk, s, z, r = O.quantize_g32(f32(k), res)  # [B,T,HKV,32], [B,T,HKV,4] x2, [B,T,HKV,128]

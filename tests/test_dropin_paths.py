@@ -1,4 +1,4 @@
-"""Module resolution as the reference's benchmark scripts see it, under INTEGRATION.md's recipe.
+"""Module resolution as the reference's benchmark scripts see it, with the drop-in directories on PYTHONPATH.
 
 The reference's ffa-q2fp8/ holds namespace directories (no __init__.py): `utils/` with bench.py,
 cache.py, flash.py, load.py, plot.py and `attn_kernel/` with the decode modules.  Its scripts run
@@ -52,7 +52,7 @@ def _reference_shaped_tree(root: Path) -> Path:
 def test_reference_scripts_resolve_their_modules(tmp_path):
     ref = _reference_shaped_tree(tmp_path)
     env = dict(os.environ)
-    env["PYTHONPATH"] = os.pathsep.join([str(DROPIN), str(PKG)])
+    env["PYTHONPATH"] = os.pathsep.join([str(DROPIN), str(PKG)])  # the drop-in, then the package
     r = subprocess.run([sys.executable, "run_probe.py"], cwd=ref, env=env, capture_output=True, text=True,
                        timeout=300)
     assert r.returncode == 0, r.stderr

@@ -1,6 +1,6 @@
 """GPU parity of the q2fp8 pruned decode (HIP kernels through the C ABI) against the CPU oracle.
 
-Bar (BASELINE north_star): survivor mask identical except blocks whose
+Bar: survivor mask identical except blocks whose
 margin max_g(block_max - th) is within 1e-3 (their count is printed);
 attention output within max-abs 2e-2 and mean-abs 2e-3 in bf16.  The output
 is compared with the oracle evaluated under the GPU's own mask, so that a

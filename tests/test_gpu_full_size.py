@@ -1,4 +1,4 @@
-"""GPU parity at BASELINE's full sizes (configs 2-5), through the library's own append and decode.
+"""GPU parity at the benchmark configs' full sizes (configs 2-5), through the library's own append and decode.
 
 Config 2 (B=1, 32K) is small enough for the whole oracle: bytes, mask, threshold and output.
 For configs 3-5 (0.5-4.2M tokens) the oracle quantizers would take minutes, so:

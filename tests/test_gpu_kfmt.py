@@ -84,7 +84,7 @@ def test_fp8fp8_decoder_f32_query(gpu):
 
 
 def test_fp8_scaled_decoder_baseline_config1(gpu):
-    """e4m3 + one fp16 scale per token and KV head + e4m3 residual, 4 outlier channels."""
+    """Benchmark config 1: e4m3 + one fp16 scale per token and KV head + e4m3 residual, 4 outlier channels."""
     T = 4096
     q, k, v = _inputs(1, T, "bf16", 0, 0)
     kf = f32(k)

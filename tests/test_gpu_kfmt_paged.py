@@ -1,10 +1,10 @@
-"""GPU parity of the BASELINE paged nvfp4-g16 / nf4-g64 modes (configs 3 and 4) against the oracle.
+"""GPU parity of the benchmark's paged nvfp4-g16 / nf4-g64 modes (configs 3 and 4) against the oracle.
 
 Append: every byte written to the pools (codes, scales, residual, V^T) equals the
 oracle's quantization of the same K (oracle/formats.py quantize_nvfp4_g16 /
 quantize_nf4_g64, pinned on the CPU), also when the cache is filled by several
 appends and the pools start with garbage.  Decode: mask identical to the oracle's
-except near-threshold blocks, output within the BASELINE tolerance; the oracle sees
+except near-threshold blocks, output within the decode tolerance; the oracle sees
 the logical (contiguous) sequence, so the page table is only storage.
 """
 import importlib.util

@@ -3,7 +3,7 @@
 v_mean: the kernels' fp32 sums against the oracle's exact mean, both rounded once to the output
 type: equal but for rounding ties (at most one unit in the last place).  Decode: the survivor
 mask as in the q2fp8 tests (no mismatch away from the threshold), the output under the GPU's own
-mask and v_mean within the north_star tolerance, and the approximated-block ratio.
+mask and v_mean within the decode tolerance, and the approximated-block ratio.
 """
 import math
 

@@ -229,7 +229,7 @@ def test_nvfp4_second_probe_window_uses_last_block_scale():
     assert np.array_equal(diag["threshold"][0], th.astype(np.float32))
 
 
-# ----------------------------------------------------------------------------- BASELINE group-scale modes
+# ----------------------------------------------------------------------------- benchmark group-scale modes
 def test_nvfp4_g16_quantizer_pins():
     """Scales are torch's e4m3 cast of amax/6; codes are the nearest e2m1 level of k/s (ties to the
     larger level, the encoder's right=True rule); k_hat = level * s exactly; residual = torch's fp8 cast."""
