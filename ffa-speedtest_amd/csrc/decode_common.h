@@ -4,6 +4,8 @@
 
 #include "ffa_common.h"
 
+#include <type_traits>
+
 namespace ffa {
 
 constexpr int kD = 128;
@@ -206,6 +208,54 @@ __device__ __forceinline__ void write_empty_mask(int8_t *mask_row, int cg, int S
 // fp32 sums' resolution.
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// exp2 softmax partial of one 64-token chunk in the exact pass.  Each lane holds the refined raw
+// scores R[k] of 16 tokens of one query row (token 16 kc + k; the row's 64 tokens lie in the four
+// lanes l, l ^ 16, l ^ 32, l ^ 48); its tokens k < nact are active (valid, in a kept prune block, a
+// row of the group).  P[k] = 2^(s_k - m) for active tokens and 0 otherwise, with s = R * cs1 *
+// log2(e) and m the row's maximum over active tokens; lsum = sum of P over the row.  When every lane
+// of the wave has all 16 active (a full page of a kept block) a copy without the masks runs, so that
+// no per-token compare or select sits on the exact pass's chain.
+template <bool SPLIT = true>
+__device__ __forceinline__ void chunk_softmax(const float *R, float cs1, int nact, float *P, float &mrow_max,
+                                              float &lsum) {
+  mrow_max = -INFINITY;
+  lsum = 0.f;
+  auto body = [&](auto FULL) {
+    constexpr bool kFull = decltype(FULL)::value;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      P[k] = (R[k] * cs1) * kLog2e;
+      mrow_max = (kFull || k < nact) ? fmaxf(mrow_max, P[k]) : mrow_max;
+    }
+    mrow_max = xor_max(mrow_max, 16);
+    mrow_max = xor_max(mrow_max, 32);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {  // a row without an active token never reads its -inf maximum
+      P[k] = (kFull || k < nact) ? exp2_hw(P[k] - mrow_max) : 0.f;
+      lsum += P[k];
+    }
+  };
+  if (SPLIT && __builtin_amdgcn_ballot_w64(nact == 16) == __builtin_amdgcn_read_exec())
+    body(std::true_type());
+  else
+    body(std::false_type());
+  lsum = xor_sum(lsum, 16);
+  lsum = xor_sum(lsum, 32);
+}
+
+// AND masks of a lane's V^T words (P.V B operand, K-chunk kap: tokens 16 kc + 8 kap + (0..7), two
+// per word) that keep only the first nvs tokens of a partial page: the pool slots past the sequence
+// end are not data (they may hold NaN patterns, which a zero P would not cancel)
+__device__ __forceinline__ void partial_page_masks(int kc, int nvs, u32x4 *keepw) {
+#pragma unroll
+  for (int kap = 0; kap < 2; ++kap)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int tk = 16 * kc + 8 * kap + 2 * e;
+      keepw[kap][e] = (tk < nvs ? 0x0000ffffu : 0u) | (tk + 1 < nvs ? 0xffff0000u : 0u);
+    }
+}
+
 // per-channel scales (fp16: dequantized by packed fp16 FMAs, exact), g32 scales, and per-channel
 // scales of other dtypes (fp32 / bf16: dequantized in fp32 as the reference does)
 enum { kChannel = 0, kG32 = 1, kChannelF32 = 2 };
@@ -286,7 +336,7 @@ struct VTraits<kVF16> {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
   __device__ static __forceinline__ uint32_t pack2(float x, float y) {
-    return f32_to_f16_bits(x) | (f32_to_f16_bits(y) << 16);
+    return pk_f16_bits(x, y);
   }
   // 8 stored V elements (4 words) -> the B operand
   __device__ static __forceinline__ vec operand(u32x4 w) { return __builtin_bit_cast(vec, w); }
@@ -298,7 +348,7 @@ struct VTraits<kVBF16> : VTraits<kVF16> {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float lo = __uint_as_float(w[e] << 16), hi = __uint_as_float(w[e] & 0xffff0000u);
-      r[e] = f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16);
+      r[e] = pk_f16_bits(lo, hi);
     }
     return __builtin_bit_cast(vec, r);
   }

@@ -37,6 +37,13 @@ __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
   return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
+// fp16(a) in the low half and fp16(b) in the high half, each rounded to nearest even as
+// f32_to_f16_bits rounds it: gfx950 converts the pair with one v_cvt_pk_f16_f32 (two conversions,
+// a shift and an OR otherwise)
+__device__ __forceinline__ uint32_t pk_f16_bits(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
+}
+
 // load element i of a float tensor of runtime dtype (0=f16, 1=bf16, 2=f32)
 __device__ __forceinline__ float load_any(const void *p, size_t i, int dt) {
   if (dt == 2) return ((const float *)p)[i];

@@ -64,8 +64,8 @@ __device__ __forceinline__ f32x2 fp8pair_f32(uint32_t w) {
   else return __builtin_amdgcn_cvt_scalef32_pk_f32_bf8(w, 1.0f, HI);
 }
 
-__device__ __forceinline__ uint32_t pack_f16(float a, float b) {  // two RNE conversions
-  return f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16);
+__device__ __forceinline__ uint32_t pack_f16(float a, float b) {  // two RNE conversions, one instruction
+  return pk_f16_bits(a, b);
 }
 
 // Scale value i of a float tensor of dtype dt (0=f16, 1=bf16, 2=f32), in two steps: scale_word
@@ -611,26 +611,11 @@ void kfmt_decode_kernel(const DecodeParams p) {
         }
       }
     }
-    float P[16];
-    float mrow_max = -INFINITY;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const int t = t0 + 16 * kc + k;
-      const bool act = row_ok && t < Tb && keep16;
-      P[k] = act ? (Rj[k] * cs1) * kLog2e : -INFINITY;
-      mrow_max = fmaxf(mrow_max, P[k]);
-    }
-    mrow_max = xor_max(mrow_max, 16);
-    mrow_max = xor_max(mrow_max, 32);
-    float lsum = 0.f;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const float e = (P[k] == -INFINITY) ? 0.f : exp2_hw(P[k] - mrow_max);
-      P[k] = e;
-      lsum += e;
-    }
-    lsum = xor_sum(lsum, 16);
-    lsum = xor_sum(lsum, 32);
+    // softmax partial over the active tokens (valid, in a kept prune block, a row of the group)
+    const int nact = (row_ok && keep16) ? min(max(Tb - (t0 + 16 * kc), 0), 16) : 0;
+    float P[16], mrow_max, lsum;
+    // (the paged build, at 128 registers, keeps one masked copy of the softmax and of P.V)
+    chunk_softmax<LAYOUT != kPaged>(Rj, cs1, nact, P, mrow_max, lsum);
     typename VTr::vec pa2[2];
 #pragma unroll
     for (int kap = 0; kap < 2; ++kap) {
@@ -643,24 +628,16 @@ void kfmt_decode_kernel(const DecodeParams p) {
 #pragma unroll
     for (int nu = 0; nu < 8; ++nu) oacc[nu] = f32x4{0.f, 0.f, 0.f, 0.f};
     if constexpr (LAYOUT == kPaged) {
-      const bool partial = nvs < kPage;
+      // each lane's V words ANDed with the mask of its valid tokens (all ones on a full page; one
+      // copy of the loop, at 128 registers)
+      u32x4 keepw[2];
+      partial_page_masks(kc, nvs, keepw);
 #pragma unroll
       for (int nu = 0; nu < 8; ++nu) {
 #pragma unroll
         for (int kap = 0; kap < 2; ++kap) {
-          uint4 v4 = vv[nu][kap];
-          if (partial) {
-            // V of page slots past the sequence end is not data: zero it
-            const int tk = 16 * kc + 8 * kap;
-            uint32_t w4[4] = {v4.x, v4.y, v4.z, v4.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              if (tk + 2 * e >= nvs) w4[e] &= 0xffff0000u;
-              if (tk + 2 * e + 1 >= nvs) w4[e] &= 0x0000ffffu;
-            }
-            v4 = make_uint4(w4[0], w4[1], w4[2], w4[3]);
-          }
-          const u32x4 w = {v4.x, v4.y, v4.z, v4.w};
+          const uint4 v4 = vv[nu][kap];
+          const u32x4 w = u32x4{v4.x, v4.y, v4.z, v4.w} & keepw[kap];
           oacc[nu] = VTr::mfma(pa2[kap], VTr::operand(w), oacc[nu]);
         }
       }

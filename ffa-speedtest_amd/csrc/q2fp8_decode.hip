@@ -112,7 +112,7 @@ __device__ __forceinline__ f16x8 dequant8_channel_f32(uint32_t w, const float4 *
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const float a0 = c[q][0] * sv[2 * q], a1 = c[q][1] * sv[2 * q + 1];
-    r[q] = f32_to_f16_bits(a0 + zv[2 * q]) | (f32_to_f16_bits(a1 + zv[2 * q + 1]) << 16);
+    r[q] = pk_f16_bits(a0 + zv[2 * q], a1 + zv[2 * q + 1]);
   }
   return __builtin_bit_cast(f16x8, r);
 }
@@ -707,6 +707,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
       }
     }
     if constexpr (OCC > 1) __builtin_amdgcn_s_setprio(0);  // back to normal once the chunk's loads are out
+    __builtin_amdgcn_sched_barrier(0);  // every load of the chunk goes out before the refine
     // refined scores
     float Rj[16];
     if constexpr (kG) {
@@ -768,27 +769,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
         for (int uu = 0; uu < 4; ++uu) Rj[4 * uu + tau] = r4[uu];
       }
     }
-    // softmax partial over the active tokens (valid and in a kept sub-block)
-    float P[16];
-    float mrow_max = -INFINITY;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const int t = t0 + 16 * kc + k;
-      const bool act = row_ok && t < Tb && keep16;
-      P[k] = act ? (Rj[k] * cs1) * kLog2e : -INFINITY;
-      mrow_max = fmaxf(mrow_max, P[k]);
-    }
-    mrow_max = xor_max(mrow_max, 16);
-    mrow_max = xor_max(mrow_max, 32);
-    float lsum = 0.f;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const float e = (P[k] == -INFINITY) ? 0.f : exp2_hw(P[k] - mrow_max);
-      P[k] = e;
-      lsum += e;
-    }
-    lsum = xor_sum(lsum, 16);
-    lsum = xor_sum(lsum, 32);
+    // softmax partial over the active tokens (valid, in a kept prune block, a row of the group)
+    const int nact = (row_ok && keep16) ? min(max(Tb - (t0 + 16 * kc), 0), 16) : 0;
+    float P[16], mrow_max, lsum;
+    // (the large-batch build keeps one masked copy of the softmax and of P.V: the fast copies' extra
+    // registers would spill at 128)
+    chunk_softmax<OCC == 1>(Rj, cs1, nact, P, mrow_max, lsum);
     // P operand (A) of P.V for K-chunk kap: element e <-> token 16*kc + 8*kap + e
     typename VTr::vec pa2[2];
 #pragma unroll
@@ -803,32 +789,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
 #pragma unroll
     for (int nu = 0; nu < 8; ++nu) oacc[nu] = f32x4{0.f, 0.f, 0.f, 0.f};
     if constexpr (LAYOUT == kPaged) {
+      // a partial page ANDs each lane's V words with the mask of its valid tokens; two copies of the
+      // loop (one in the large-batch build), so that the full pages' loop holds no per-element test
+      auto pv_loop = [&](auto PART) {
+        constexpr bool kPart = decltype(PART)::value;
+        u32x4 keepw[2];
+        if constexpr (kPart) partial_page_masks(kc, nvs, keepw);
 #pragma unroll
-      for (int nu = 0; nu < 8; ++nu) {
-        if (nu == VH) {  // the second half of V^T, into the registers the first half has freed
+        for (int nu = 0; nu < 8; ++nu) {
+          if (nu == VH) {  // the second half of V^T, into the registers the first half has freed
 #pragma unroll
-          for (int n2 = VH; n2 < 8; ++n2)
+            for (int n2 = VH; n2 < 8; ++n2)
 #pragma unroll
-            for (int kap = 0; kap < 2; ++kap) vv[n2][kap] = bload16_nt(vs_p, ((n2 * 2 + kap) * 64 + lane) * 16);
-        }
-#pragma unroll
-        for (int kap = 0; kap < 2; ++kap) {
-          uint4 v4 = vv[nu][kap];
-          if (partial) {
-            // V of page slots past the sequence end is not data: zero it
-            const int tk = 16 * kc + 8 * kap;
-            uint32_t w4[4] = {v4.x, v4.y, v4.z, v4.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              if (tk + 2 * e >= nvs) w4[e] &= 0xffff0000u;
-              if (tk + 2 * e + 1 >= nvs) w4[e] &= 0x0000ffffu;
-            }
-            v4 = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+              for (int kap = 0; kap < 2; ++kap) vv[n2][kap] = bload16_nt(vs_p, ((n2 * 2 + kap) * 64 + lane) * 16);
           }
-          const u32x4 w = {v4.x, v4.y, v4.z, v4.w};
-          oacc[nu] = VTr::mfma(pa2[kap], VTr::operand(w), oacc[nu]);
+#pragma unroll
+          for (int kap = 0; kap < 2; ++kap) {
+            const uint4 v4 = vv[nu][kap];
+            u32x4 w = {v4.x, v4.y, v4.z, v4.w};
+            if constexpr (kPart) w &= keepw[kap];
+            oacc[nu] = VTr::mfma(pa2[kap], VTr::operand(w), oacc[nu]);
+          }
         }
-      }
+      };
+      if (OCC > 1 || partial) [[unlikely]]
+        pv_loop(std::true_type());
+      else
+        pv_loop(std::false_type());
     } else {
       // contiguous layout: stage the V tile through LDS one half at a time ([64 tokens][64
       // columns], a 132-byte row pitch keeps banks apart), then read columns (rows past the
@@ -1222,9 +1209,9 @@ static hipError_t launch_decode(const ffa::DecodeParams &p, dim3 grid, hipStream
       return hipGetLastError();
     }
   }
-  // contiguous layout with fp32 channel scales: held to two workgroups per CU (the fp32
-  // dequantization's temporaries would otherwise take the kernel past 256 registers)
-  constexpr int occ = (L == ffa::kContig && S == ffa::kChannelF32) ? 2 : 1;
+  // fp32 channel scales: held to two workgroups per CU (the fp32 dequantization's temporaries would
+  // otherwise take the kernel to 256 registers, one workgroup per CU)
+  constexpr int occ = S == ffa::kChannelF32 ? 2 : 1;
   hipLaunchKernelGGL((ffa::q2fp8_decode_kernel<L, S, R, V, occ>), grid, dim3(256), 0, st, p);
   return hipGetLastError();
 }
