@@ -790,11 +790,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     for (int nu = 0; nu < 8; ++nu) oacc[nu] = f32x4{0.f, 0.f, 0.f, 0.f};
     if constexpr (LAYOUT == kPaged) {
       // a partial page ANDs each lane's V words with the mask of its valid tokens; two copies of the
-      // loop (one in the large-batch build), so that the full pages' loop holds no per-element test
+      // loop, so that the full pages' loop holds no per-element test (the large-batch build, at 128
+      // registers: one copy with a uniform branch per V block)
       auto pv_loop = [&](auto PART) {
         constexpr bool kPart = decltype(PART)::value;
         u32x4 keepw[2];
-        if constexpr (kPart) partial_page_masks(kc, nvs, keepw);
+        if (kPart && (OCC == 1 || partial)) partial_page_masks(kc, nvs, keepw);
 #pragma unroll
         for (int nu = 0; nu < 8; ++nu) {
           if (nu == VH) {  // the second half of V^T, into the registers the first half has freed
@@ -807,7 +808,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
           for (int kap = 0; kap < 2; ++kap) {
             const uint4 v4 = vv[nu][kap];
             u32x4 w = {v4.x, v4.y, v4.z, v4.w};
-            if constexpr (kPart) w &= keepw[kap];
+            if (kPart && (OCC == 1 || partial)) w &= keepw[kap];
             oacc[nu] = VTr::mfma(pa2[kap], VTr::operand(w), oacc[nu]);
           }
         }
@@ -1326,16 +1327,20 @@ static int launch_stage1(const ffa_q2fp8_decode_args *a, const ffa::DecodeParams
     ffa::DecodeParams p = p0;
     p.pass = pass;
     hipError_t e;
+    // channel scales: the packed fp16 dequantization for fp16 scale / zero, and for bf16 / fp32 ones
+    // that the caller declares exactly representable in fp16 (scale_exact_f16); otherwise fp32
+    // arithmetic, as the reference dequantizes (fp16(fp32(fp32(c s) + z)))
+    const bool f16_scales = a->scale_dtype == FFA_DT_F16 || a->scale_exact_f16 != 0;
     if (a->layout == FFA_LAYOUT_PAGED) {
       if (a->scale_mode == FFA_SCALE_G32)
         e = dispatch_rv<ffa::kPaged, ffa::kG32>(p, a->res_dtype, a->v_dtype, grid, st);
-      else if (a->scale_dtype == FFA_DT_F16)
+      else if (f16_scales)
         e = dispatch_rv<ffa::kPaged, ffa::kChannel>(p, a->res_dtype, a->v_dtype, grid, st);
       else
         e = dispatch_rv<ffa::kPaged, ffa::kChannelF32>(p, a->res_dtype, a->v_dtype, grid, st);
-    } else if (a->scale_dtype == FFA_DT_F16) {
+    } else if (f16_scales) {
       e = dispatch_rv<ffa::kContig, ffa::kChannel>(p, a->res_dtype, a->v_dtype, grid, st);
-    } else {  // fp32 / bf16 scale and zero: dequantized in fp32, as the reference does
+    } else {
       e = dispatch_rv<ffa::kContig, ffa::kChannelF32>(p, a->res_dtype, a->v_dtype, grid, st);
     }
     if (e != hipSuccess) return set_err(FFA_E_LAUNCH, hipGetErrorString(e));

@@ -107,6 +107,7 @@ class DecodeArgs(ctypes.Structure):
         ("v_mean_dtype", ctypes.c_int),
         ("approx_m", ctypes.c_void_p),
         ("approx_l", ctypes.c_void_p),
+        ("scale_exact_f16", ctypes.c_int),
     ]
 
 

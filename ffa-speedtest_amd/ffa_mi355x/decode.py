@@ -106,6 +106,40 @@ def run_decode(*, workspace: DecodeWorkspace | None = None, stage: str = "both",
     return workspace
 
 
+_EXACT_ATTR = "_ffa_scales_exact_f16"
+
+
+def scales_exact_f16(k_scale: torch.Tensor, k_zero: torch.Tensor) -> bool:
+    """Whether every per-channel scale and zero point is exactly representable in fp16.
+
+    The decode then dequantizes bf16 / fp32 scales as it does fp16 ones (one packed fp16 FMA per
+    channel pair, the reference's k_hat for such values); otherwise it keeps fp32 arithmetic
+    (attn_kernel_v1210_fused_bsz_q2fp8.py:52-53, 93).  fp16 tensors are exact by definition.  The
+    answer is computed on the device once (a synchronising reduction) and remembered on the scale
+    tensor (and its base) with both tensors' version counters, so that an in-place change of either
+    checks again; during stream capture an unknown answer is False (fp32 arithmetic, correct for
+    any values), as a capture cannot synchronise."""
+    if k_scale.dtype == torch.float16 and k_zero.dtype == torch.float16:
+        return True
+    key = (k_scale.data_ptr(), tuple(k_scale.shape), k_scale._version, k_scale.dtype,
+           k_zero.data_ptr(), tuple(k_zero.shape), k_zero._version, k_zero.dtype)
+    for t in (k_scale, k_scale._base):
+        memo = getattr(t, _EXACT_ATTR, None) if t is not None else None
+        if memo is not None and memo[0] == key:
+            return memo[1]
+    if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+        return False
+
+    def exact(t):
+        return bool(torch.equal(t.to(torch.float16).to(t.dtype), t))
+
+    ok = exact(k_scale) and exact(k_zero)
+    for t in (k_scale, k_scale._base):
+        if t is not None:
+            setattr(t, _EXACT_ATTR, (key, ok))
+    return ok
+
+
 def decode_args(
     *,
     q: torch.Tensor,  # [B, HQ, 128]
@@ -155,6 +189,8 @@ def decode_args(
     a.k_zero = k_zero.data_ptr()
     a.scale_dtype = N.dtype_code(k_scale.dtype)
     a.scale_mode = scale_mode
+    if scale_mode == N.SCALE_CHANNEL and k_scale.dtype != torch.float16:
+        a.scale_exact_f16 = 1 if scales_exact_f16(k_scale, k_zero) else 0
     a.k_residual = k_residual.data_ptr() if use_res else None
     a.res_dtype = _res_code(k_residual, use_res)
     a.v = v.data_ptr()

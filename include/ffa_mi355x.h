@@ -160,6 +160,14 @@ typedef struct ffa_q2fp8_decode_args {
   const void *v_mean; /* [B, HKV, 128], dtype v_mean_dtype (F16 / BF16 / F32), e.g. from ffa_v_mean */
   int v_mean_dtype;
   float *approx_m, *approx_l; /* with v_mean: [B, HQ, nparts] f32 each */
+  /* CHANNEL mode with BF16 / F32 k_scale and k_zero: non-zero when the caller knows that every
+   * value of both is exactly representable in fp16 (bf16 scales within fp16's range, the usual
+   * case).  The decode then dequantizes as for fp16 scales (one packed fp16 FMA per pair of
+   * channels, the same k_hat as the reference's fp16(fp32(fp32(c * s) + z)) for such values);
+   * 0 keeps the fp32 arithmetic, correct for any values.  A non-zero flag on values fp16 does not
+   * hold rounds them to fp16 first.  No counterpart in the reference, which always computes in fp32
+   * (attn_kernel_v1210_fused_bsz_q2fp8.py:52-53, 93). */
+  int scale_exact_f16;
 } ffa_q2fp8_decode_args;
 
 /* Number of partial slots per query row the scratch buffers must hold for max length T. */

@@ -139,3 +139,49 @@ def test_producer_fp32_output_feeds_decode(gpu):
     o_forced, _ = O.decode(*args, force_mask=mask, **okw)
     mx, mean = assert_out_close(f32(o), o_forced, "producer fp32")
     print(f"[out] max_abs={mx:.3e} mean_abs={mean:.3e}")
+
+
+@pytest.mark.parametrize("layout", ["contig"])
+def test_exact_bf16_scales_take_the_fp16_dequantization(gpu, layout):
+    """bf16 scale / zero within fp16's range (the usual case: bf16 K quantized per channel) are
+    exactly fp16 values, for which the packed fp16 dequantization gives the reference's k_hat.
+    decode_args marks them (scale_exact_f16 = 1); that decode must agree with the oracle and with
+    the same call forced onto the fp32 arithmetic (flag cleared)."""
+    import ctypes
+
+    from ffa_mi355x import _native as N
+    from ffa_mi355x.decode import DecodeWorkspace, decode_args, scales_exact_f16
+
+    T = 2048
+    q, k, v = synth.attention_inputs(B=2, T=T, HQ=32, HKV=8, seed=41, n_heavy=16)  # bf16
+    pk, s, z, r = O.quantize_per_channel(f32(k), "bf16", "e5m2")
+    qg = q.to(gpu)
+    sg = torch.from_numpy(s).to(torch.bfloat16).to(gpu)
+    zg = torch.from_numpy(z).to(torch.bfloat16).to(gpu)
+    assert scales_exact_f16(sg, zg)
+    k_q = torch.from_numpy(pk).to(gpu)
+    k_res = torch.from_numpy(r).view(FP8_DT["e5m2"]).to(gpu)
+    vg = v.to(gpu)
+    B, HQ = q.shape[0], q.shape[1]
+    outs = []
+    for flag in (1, 0):
+        ws = DecodeWorkspace(B, HQ, 8, T, 64, 64, gpu, torch.bfloat16)
+        a, ws = decode_args(q=qg, k_q=k_q, k_scale=sg, k_zero=zg, v=vg, k_residual=k_res, layout=N.LAYOUT_CONTIG,
+                            scale_mode=N.SCALE_CHANNEL, T=T, HKV=8, scale=1.0 / np.sqrt(128), BS=64, SBS=64,
+                            delta=5.0, use_res=True, workspace=ws)
+        assert a.scale_exact_f16 == 1
+        a.scale_exact_f16 = flag
+        N.check(N.lib().ffa_q2fp8_decode(ctypes.byref(a), ctypes.c_void_p(N.stream_of(gpu))), "ffa_q2fp8_decode")
+        torch.cuda.synchronize()
+        outs.append((f32(ws.o), ws.threshold_buf.cpu().numpy(), ws.mask_buf.cpu().numpy()))
+    (o16, th16, m16), (o32, th32, m32) = outs
+    _, diag = _oracle(q, v, pk, s, z, r, BS=64, SBS=64, delta=5.0)
+    err = np.abs(th16 - diag["threshold"]).max()
+    far, near, near_total = compare_masks(m16, diag)
+    print(f"[{layout} bf16 exact] threshold err {err:.2e} mismatch_far={far} near={near}/{near_total}; "
+          f"fp16 vs fp32 path: threshold {np.abs(th16 - th32).max():.2e} out {np.abs(o16 - o32).max():.2e}")
+    assert err < TH_TOL and far == 0
+    assert np.array_equal(m16, m32)
+    assert np.abs(th16 - th32).max() <= 1e-6 and np.abs(o16 - o32).max() <= 1e-6
+    o_forced, _ = _oracle(q, v, pk, s, z, r, BS=64, SBS=64, delta=5.0, force_mask=m16)
+    assert_out_close(o16, o_forced, f"{layout} bf16 exact")
