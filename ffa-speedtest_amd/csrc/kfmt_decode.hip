@@ -32,6 +32,16 @@ extern "C" int ffa_decode_shape_check(int B, int T, int HQ, int HKV, int BS, int
                                       const float *th_in, const float *th_out, ffa::DecodeParams *p);
 extern "C" int ffa_decode_slots(int T, int BS, int span);
 
+// Timeline build (-DFFA_TIMELINE only): per-wave s_memrealtime stamps at the FFA_STAMP points, 16
+// words per wave into the buffer ffa_debug_set_timeline_kfmt sets (stamps 0-12, the chunks the wave
+// refined, 0, and XCC_ID << 32 | HW_ID), as in the q2 decoder.
+#ifdef FFA_TIMELINE
+__device__ unsigned long long *g_timeline_k = nullptr;
+#define FFA_STAMP(i) (st_[i] = __builtin_amdgcn_s_memrealtime())
+#else
+#define FFA_STAMP(i) ((void)0)
+#endif
+
 namespace ffa {
 
 enum { kF8E4M3 = 0, kF8E5M2 = 1, kFP4 = 2, kNF4 = 3 };
@@ -90,6 +100,10 @@ template <int LAYOUT, int FMT, int SCL, int RES, int VT, bool RELOAD>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LAYOUT == kPaged ? 4 : (RELOAD ? 2 : 1))))
 void kfmt_decode_kernel(const DecodeParams p) {
   typedef VTraits<VT> VTr;
+#ifdef FFA_TIMELINE
+  unsigned long long st_[16] = {0};
+  int n_exact_ = 0;
+#endif
   constexpr bool k4 = FMT == kFP4 || FMT == kNF4;
   constexpr bool kGrp = SCL == kSclG16 || SCL == kSclG64;  // per-token group scales (paged modes)
   static_assert(kGrp == (LAYOUT == kPaged), "group scales go with the paged layout");
@@ -146,6 +160,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
     if (p.pass != 1 && un.quad == 0) write_empty_mask(p.mask + ((size_t)b * p.HKV + hkv) * p.ntbs, cg, SBS, p.ntbs, span);
     return;
   }
+  FFA_STAMP(0);
   if (threadIdx.x < kChunksPerWG * kPage / 16) s_keep[threadIdx.x] = 0;
   const int NTB = (Tb + p.BS - 1) / p.BS;
   const int NTBS_b = NTB * (p.BS / p.SBS);
@@ -285,6 +300,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
     s_cb2[threadIdx.x] = make_float2(kNF4Levels[threadIdx.x & 15], kNF4Levels[threadIdx.x >> 4]);
   }
 
+  FFA_STAMP(1);
   // ------------------------------------------------ phase 2a: q operands (one per wave)
   auto build_operands = [&](auto W) {
     constexpr int w = decltype(W)::value;
@@ -307,6 +323,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
     default: build_operands(std::integral_constant<int, 3>()); break;
   }
   lds_barrier();
+  FFA_STAMP(2);
   f16x8 qa[4];
 #pragma unroll
   for (int mp = 0; mp < 4; ++mp) {
@@ -463,7 +480,9 @@ void kfmt_decode_kernel(const DecodeParams p) {
   }
   if (SBS >= 128) mb[0] = mb[1] = fmaxf(mb[0], mb[1]);
   if (SBS > 128 && lane < 4) s_wmax[wv][lane] = mb[0];
+  FFA_STAMP(3);
   lds_barrier();  // probe maxima (and per-wave block maxima)
+  FFA_STAMP(4);
   if (p.th_in != nullptr) th = row_ok ? th_pre : INFINITY;
   else th = row_ok ? fmaxf(s_probe[0][ir], s_probe[1][ir]) - p.delta : INFINITY;
   if (SBS > 128) {
@@ -496,6 +515,10 @@ void kfmt_decode_kernel(const DecodeParams p) {
 
   // ------------------------------------------------ phase 3: exact pass over this wave's kept chunks
   auto exact_chunk = [&](auto J) {
+    FFA_STAMP(5);
+#ifdef FFA_TIMELINE
+    ++n_exact_;
+#endif
     constexpr int j = decltype(J)::value;
     const int slot = wv * kPPW + j;
     const int t0 = (c0 + j) * kPage;
@@ -586,6 +609,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
 #pragma unroll
       for (int tau = 0; tau < 4; ++tau) ksc[tau] = scale_value(ksw[tau], (ksodd >> tau) & 1u, p.s_dtype);
     }
+    FFA_STAMP(6);
     float Rj[16];
 #pragma unroll
     for (int k = 0; k < 16; ++k) Rj[k] = R[j][k];
@@ -611,11 +635,13 @@ void kfmt_decode_kernel(const DecodeParams p) {
         }
       }
     }
+    FFA_STAMP(7);
     // softmax partial over the active tokens (valid, in a kept prune block, a row of the group)
     const int nact = (row_ok && keep16) ? min(max(Tb - (t0 + 16 * kc), 0), 16) : 0;
     float P[16], mrow_max, lsum;
     // (the paged build, at 128 registers, keeps one masked copy of the softmax and of P.V)
     chunk_softmax<LAYOUT != kPaged>(Rj, cs1, nact, P, mrow_max, lsum);
+    FFA_STAMP(8);
     typename VTr::vec pa2[2];
 #pragma unroll
     for (int kap = 0; kap < 2; ++kap) {
@@ -680,6 +706,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
     }
+    FFA_STAMP(9);
     if (lane < 16) {
 #pragma unroll
       for (int uu = 0; uu < 4; ++uu)
@@ -702,8 +729,10 @@ void kfmt_decode_kernel(const DecodeParams p) {
   if (nv[1] > 0 && bal[1] != 0) exact_chunk(std::integral_constant<int, 1>());
   else empty_chunk(wv * kPPW + 1);
 
+  FFA_STAMP(10);
   // ------------------------------------------------ phase 4: mask, threshold, workgroup partial
   __syncthreads();
+  FFA_STAMP(11);
   if (un.quad == 0) {
     int8_t *mrow_ptr = p.mask + ((size_t)b * p.HKV + hkv) * p.ntbs;
     const int t = threadIdx.x;
@@ -762,6 +791,18 @@ void kfmt_decode_kernel(const DecodeParams p) {
       if (A > 0.f) *(float2 *)(p.o_buf + (row * p.nparts + cg) * 128 + c2) = make_float2(ox, oy);
     }
   }
+#ifdef FFA_TIMELINE
+  FFA_STAMP(12);
+  if (g_timeline_k != nullptr && lane == 0) {
+    st_[13] = (unsigned long long)n_exact_;
+    st_[14] = 0;
+    st_[15] = ((unsigned long long)__builtin_amdgcn_s_getreg((31 << 11) | 20) << 32) |
+              (unsigned long long)__builtin_amdgcn_s_getreg((31 << 11) | 4);
+    const size_t wid = (((size_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * 4 + wv;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) g_timeline_k[wid * 16 + i] = st_[i];
+  }
+#endif
 }
 
 }  // namespace ffa
@@ -919,3 +960,10 @@ extern "C" int ffa_kfmt_decode(const ffa_kfmt_decode_args *a, void *stream) {
   if (e != hipSuccess) return ffa_set_error_internal(FFA_E_LAUNCH, hipGetErrorString(e));
   return FFA_OK;
 }
+
+#ifdef FFA_TIMELINE
+// Timeline build only: the buffer (16 words per wave of a stage-1 grid) the other-format decode writes to.
+extern "C" int ffa_debug_set_timeline_kfmt(void *ptr) {
+  return (int)hipMemcpyToSymbol(HIP_SYMBOL(g_timeline_k), &ptr, sizeof(ptr));
+}
+#endif

@@ -44,6 +44,18 @@
 #include <mutex>
 #include <type_traits>
 
+// Timeline build (compiled with -DFFA_TIMELINE, never in the library that ffa_mi355x.build makes):
+// each wave records s_memrealtime (the 100 MHz constant clock) at the points STAMP marks and, at
+// its end, 16 words per wave into the buffer ffa_debug_set_timeline sets: stamps 0-12, then the
+// kept chunks it refined, the workgroup's kept chunks, and (XCC_ID << 32 | HW_ID).  The stamps are
+// SMEM reads that share lgkmcnt with LDS, so they shift what they measure by a little.
+#ifdef FFA_TIMELINE
+__device__ unsigned long long *g_timeline = nullptr;
+#define FFA_STAMP(i) (st_[i] = __builtin_amdgcn_s_memrealtime())
+#else
+#define FFA_STAMP(i) ((void)0)
+#endif
+
 namespace ffa {
 
 // A-operand words of the score MFMAs from 16 packed codes (one 32-bit word).
@@ -130,6 +142,10 @@ template <int LAYOUT, int SMODE, int RES, int VT, int OCC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void q2fp8_decode_kernel(
     const DecodeParams p) {
   typedef VTraits<VT> VTr;
+#ifdef FFA_TIMELINE
+  unsigned long long st_[16] = {0};
+  int n_exact_ = 0;
+#endif
   constexpr bool kG = SMODE == kG32;
   constexpr bool kCF = SMODE == kChannelF32;  // per-channel fp32 / bf16 scales: dequantized in fp32
   const int lane = threadIdx.x & 63;
@@ -205,6 +221,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     if (p.pass != 1 && un.quad == 0) write_empty_mask(p.mask + ((size_t)b * p.HKV + hkv) * p.ntbs, cg, SBS, p.ntbs, span);
     return;
   }
+  FFA_STAMP(0);
   if (threadIdx.x < kChunksPerWG * kPage / 16) s_keep[threadIdx.x] = 0;
   const int NTB = (Tb + p.BS - 1) / p.BS;
   const int NTBS_b = NTB * (p.BS / p.SBS);
@@ -246,6 +263,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
 #pragma unroll
     for (int j = 0; j < kPPW; ++j) pg[j] = __builtin_amdgcn_readlane(pg_lane, j);
     ppg = __builtin_amdgcn_readlane(pg_lane, kPPW);
+    FFA_STAMP(1);
   }
   // probe tile: MFMA row m <-> token pa + 4(m & 3) + (m >> 2), so that the output rows
   // 4kc + u hold tokens pa + 4u + kc, whose g32 scales are contiguous (scale_pos)
@@ -381,6 +399,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     default: build_operands(std::integral_constant<int, 3>()); break;
   }
   lds_barrier();
+  FFA_STAMP(2);
   f16x8 qa[4];
   uint32_t spair[16], zpair[16];
   float zq = 0.f;
@@ -519,7 +538,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   }
   if (SBS >= 128) mb[0] = mb[1] = fmaxf(mb[0], mb[1]);
   if (SBS > 128 && lane < 4) s_wmax[wv][lane] = mb[0];
+  FFA_STAMP(3);
   lds_barrier();  // probe maxima (and per-wave block maxima)
+  FFA_STAMP(4);
   if (p.th_in != nullptr) {
     th = row_ok ? th_pre : INFINITY;
   } else {
@@ -613,6 +634,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     }
   }
   lds_barrier();
+  FFA_STAMP(5);
 
   // ------------------------------------------------ phase 3: exact pass over the kept chunks
   // The i-th kept chunk of the workgroup (in chunk order) goes to wave i % 4, so a
@@ -708,6 +730,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     }
     if constexpr (OCC > 1) __builtin_amdgcn_s_setprio(0);  // back to normal once the chunk's loads are out
     __builtin_amdgcn_sched_barrier(0);  // every load of the chunk goes out before the refine
+    FFA_STAMP(6);
     // refined scores
     float Rj[16];
     if constexpr (kG) {
@@ -772,9 +795,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     // softmax partial over the active tokens (valid, in a kept prune block, a row of the group)
     const int nact = (row_ok && keep16) ? min(max(Tb - (t0 + 16 * kc), 0), 16) : 0;
     float P[16], mrow_max, lsum;
+    FFA_STAMP(7);
     // (the large-batch build keeps one masked copy of the softmax and of P.V: the fast copies' extra
     // registers would spill at 128)
     chunk_softmax<OCC == 1>(Rj, cs1, nact, P, mrow_max, lsum);
+    FFA_STAMP(8);
     // P operand (A) of P.V for K-chunk kap: element e <-> token 16*kc + 8*kap + e
     typename VTr::vec pa2[2];
 #pragma unroll
@@ -851,6 +876,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       }
     }
+    FFA_STAMP(9);
     // chunk partial into LDS: lanes 0..15 hold rows 0..3 of columns 16*nu + n
     if (lane < 16) {
 #pragma unroll
@@ -868,15 +894,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
 #pragma unroll 1
   for (int sl = 0; sl < kChunksPerWG; ++sl) {
     if ((km >> sl) & 1u) {
-      if ((rank & (kWaves - 1)) == wv) exact_chunk(sl);
+      if ((rank & (kWaves - 1)) == wv) {
+        exact_chunk(sl);
+#ifdef FFA_TIMELINE
+        ++n_exact_;
+#endif
+      }
       ++rank;
     }
   }
 
   // ------------------------------------------------ phase 4: workgroup partial (8 chunks) -> global
+  FFA_STAMP(10);
   // Global stores come last: on gfx9 stores share the vector memory counter with loads, and a
   // pending store would make every later load wait a full write round trip.
   __syncthreads();
+  FFA_STAMP(11);
   if (mask_at >= 0) p.mask[((size_t)b * p.HKV + hkv) * p.ntbs + mask_at] = mask_byte;
   if (p.pass == 0 && p.th_out != nullptr && cg == 0 && threadIdx.x < un.Gu)
     p.th_out[(size_t)b * p.HQ + un.row0 + threadIdx.x] = th;  // (pass 2: written by pass 1)
@@ -936,6 +969,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
       if (A > 0.f) *(float2 *)(p.o_buf + (row * p.nparts + cg) * 128 + c2) = make_float2(ox, oy);
     }
   }
+#ifdef FFA_TIMELINE
+  FFA_STAMP(12);
+  if (g_timeline != nullptr && lane == 0) {
+    st_[13] = (unsigned long long)n_exact_;
+    st_[14] = (unsigned long long)__builtin_popcount(km);
+    st_[15] = ((unsigned long long)__builtin_amdgcn_s_getreg((31 << 11) | 20) << 32) |
+              (unsigned long long)__builtin_amdgcn_s_getreg((31 << 11) | 4);
+    const size_t wid = (((size_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * 4 + wv;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) g_timeline[wid * 16 + i] = st_[i];
+  }
+#endif
 }
 
 // --------------------------------------------------------------------------
@@ -1471,3 +1516,10 @@ extern "C" int ffa_q2fp8_decode_noalloc(const ffa_q2fp8_decode_args *a, void *st
   s.approx_l = a->v_mean ? reinterpret_cast<float *>(base + al_at) : nullptr;
   return ffa_q2fp8_decode(&s, stream);
 }
+
+#ifdef FFA_TIMELINE
+// Timeline build only: the buffer (16 words per wave of a stage-1 grid) the q2 decode writes to.
+extern "C" int ffa_debug_set_timeline(void *ptr) {
+  return (int)hipMemcpyToSymbol(HIP_SYMBOL(g_timeline), &ptr, sizeof(ptr));
+}
+#endif

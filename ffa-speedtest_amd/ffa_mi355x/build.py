@@ -40,17 +40,19 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build libffa_mi355x.so)")
 
 
-def build(verbose: bool = False, jobs: int = 4) -> Path:
-    """Compile every HIP source for gfx950 and link the shared library."""
+def build(verbose: bool = False, jobs: int = 4, extra_flags=(), lib_path: Path = LIB_PATH) -> Path:
+    """Compile every HIP source for gfx950 and link the shared library (extra_flags / lib_path: a
+    variant build, such as the timeline build of ffa_mi355x.timeline)."""
     hipcc = _hipcc()
-    objdir = PKG_DIR / "_obj"
+    lib_path = Path(lib_path)
+    objdir = PKG_DIR / ("_obj" if lib_path == LIB_PATH else "_obj_" + lib_path.stem)
     objdir.mkdir(exist_ok=True)
     procs = []
     objs = []
     for src in SOURCES:
         obj = objdir / (Path(src).stem + ".o")
         objs.append(obj)
-        cmd = [hipcc, *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(CSRC / src), "-o", str(obj)]
+        cmd = [hipcc, *HIPCC_FLAGS, *extra_flags, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(CSRC / src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
@@ -58,13 +60,13 @@ def build(verbose: bool = False, jobs: int = 4) -> Path:
             _wait(procs.pop(0))
     for pr in procs:
         _wait(pr)
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+    tmp = lib_path.with_suffix(".so.tmp")
     cmd = [hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)
     _run(cmd)
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, lib_path)
+    return lib_path
 
 
 def _wait(item):
