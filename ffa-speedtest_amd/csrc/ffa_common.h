@@ -213,9 +213,13 @@ __device__ __forceinline__ uint64_t bload8u(brsrc r, uint32_t off) {
   return ((uint64_t)v.y << 32) | v.x;
 }
 // The same loads with the non-temporal hint (cache-policy bit 1, `nt` on gfx950), for data one
-// workgroup reads once: the paged (page, KV head) blocks of codes and scales, and the residual and
-// V rows.  Data that several workgroups read keeps the default policy: q, probe windows, page ids,
-// and the reference layout's code rows, whose cache lines hold several KV heads' codes.
+// workgroup reads once in whole cache lines per load: the paged (page, KV head) blocks of codes,
+// scales, residual and V, and the contiguous layouts' V rows.  Data that several workgroups read
+// keeps the default policy: q, probe windows, page ids, and the reference layout's code rows, whose
+// cache lines hold several KV heads' codes; so do the other-format decoder's contiguous residual
+// rows, which a wave reads in two loads of alternate 16-byte pieces of each line (with the hint, a
+// load-only probe of config 1's reads took 4.55 against 4.10 us; the q2 decoder's contiguous
+// residual, read for about a tenth of the chunks at config 2, measured 0.15 us slower without it).
 constexpr int kNonTemporal = 2;
 __device__ __forceinline__ uint4 bload16_nt(brsrc r, uint32_t off) {
   const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kNonTemporal);

@@ -96,9 +96,13 @@ __device__ __forceinline__ float scale_value(uint32_t w, uint32_t odd, int dt) {
 // layout: always, with four waves per SIMD (at most 128 registers, one or two spilled).
 // Contiguous layouts (54.7 KB of LDS, two workgroups per CU): when the grid is larger than the
 // CU count; small grids keep the registers, one latency chain per wave being all they have.
-template <int LAYOUT, int FMT, int SCL, int RES, int VT, bool RELOAD>
+// SPEC (contiguous, two-chunk spans only): waves 2 and 3 own the two chunks and issue each chunk's
+// residual and V loads with its codes, before the prune decides it; waves 0 and 1 score the probe
+// windows.
+template <int LAYOUT, int FMT, int SCL, int RES, int VT, bool RELOAD, bool SPEC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LAYOUT == kPaged ? 4 : (RELOAD ? 2 : 1))))
 void kfmt_decode_kernel(const DecodeParams p) {
+  static_assert(!SPEC || (LAYOUT == kContig && !RELOAD), "speculative loads go with the small-grid contiguous build");
   typedef VTraits<VT> VTr;
 #ifdef FFA_TIMELINE
   unsigned long long st_[16] = {0};
@@ -121,14 +125,16 @@ void kfmt_decode_kernel(const DecodeParams p) {
   // span: chunks of this workgroup (8, or 4 / 2 for small grids, where each wave owns one chunk
   // and waves past the span own none); slot (w, j) = wave w's j-th chunk.  The paged build serves
   // large batches and keeps the whole span as a constant (the runtime form costs it registers)
-  const int span = LAYOUT == kPaged ? kChunksPerWG : decode_span(p);
+  const int span = LAYOUT == kPaged ? kChunksPerWG : (SPEC ? kMinSpan : decode_span(p));
   const int ppw = span >= kChunksPerWG ? kPPW : 1;
   const int cw = cg * span;
-  const int c0 = cw + wv * ppw;
+  // the wave's place in the chunk order: its own index, or (SPEC) waves 2, 3 first
+  const int wch = SPEC ? (wv ^ 2) : wv;
+  const int c0 = cw + wch * ppw;
   const int SBS = p.SBS;
   bool own[kPPW];
 #pragma unroll
-  for (int j = 0; j < kPPW; ++j) own[j] = j < ppw && wv * ppw + j < span;
+  for (int j = 0; j < kPPW; ++j) own[j] = j < ppw && wch * ppw + j < span;
   // first chunk of slot sl (and whether the slot holds a chunk of this workgroup)
   auto slot_chunk = [&](int sl) { return cw + (sl >> 1) * ppw + (sl & 1); };
   auto slot_owned = [&](int sl) { return (sl & 1) < ppw && (sl >> 1) * ppw + (sl & 1) < span; };
@@ -259,6 +265,43 @@ void kfmt_decode_kernel(const DecodeParams p) {
       }
     }
   }
+  // residual and V loads of one chunk (page pg, or the contiguous rows of tokens t0 .. t0 + nvs;
+  // nvs = 0 gives empty resources: the loads return zeros without a memory access)
+  auto issue_rv = [&](int pgid, int t0, int nvs, uint4 (&rr)[4][2], uint4 (&vv)[8][2]) {
+    if constexpr (RES != kResNone) {
+      const brsrc rs = LAYOUT == kPaged ? page_rows(p.kr, pgid, kD, true)
+                                        : make_rsrc(p.kr + (((size_t)b * p.T + t0) * p.HKV + hkv) * kD,
+                                                    nvs > 0 ? ((nvs - 1) * p.HKV + 1) * kD : 0);
+#pragma unroll
+      for (int tau = 0; tau < 4; ++tau) {
+        if constexpr (LAYOUT == kPaged) {  // blocks (tau, h) of the page's residual
+          rr[tau][0] = bload16_nt(rs, ((tau * 2 + 0) * 64 + lane) * 16);
+          rr[tau][1] = bload16_nt(rs, ((tau * 2 + 1) * 64 + lane) * 16);
+        } else {  // two loads of alternate 16-byte pieces of the same lines: default cache policy
+          const uint32_t off = (4 * mrow + tau) * p.HKV * kD + 32 * kc;
+          rr[tau][0] = bload16(rs, off);
+          rr[tau][1] = bload16(rs, off + 16);
+        }
+      }
+    }
+    if constexpr (LAYOUT == kPaged) {
+      // V^T page: lane (n, kc) reads column 16 nu + n, tokens 16 kc + 8 kap .. + 8 (vt_off order)
+      const brsrc vs = make_rsrc((const uint16_t *)p.v + ((size_t)pgid * p.HKV + hkv) * (kD * kPage), kD * kPage * 2);
+#pragma unroll
+      for (int nu = 0; nu < 8; ++nu)
+#pragma unroll
+        for (int kap = 0; kap < 2; ++kap) vv[nu][kap] = bload16_nt(vs, ((nu * 2 + kap) * 64 + lane) * 16);  // block (nu, kap)
+    } else {
+      const brsrc vs = make_rsrc((const uint16_t *)p.v + (((size_t)b * p.T + t0) * p.HKV + hkv) * kD,
+                                 nvs > 0 ? ((nvs - 1) * p.HKV + 1) * kD * 2 : 0);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int idx = r * 64 + lane;
+        const int tk = idx >> 4, vc = idx & 15;
+        vv[r >> 1][r & 1] = bload16_nt(vs, tk * p.HKV * kD * 2 + 16 * vc);
+      }
+    }
+  };
   uint4 xa[kPPW][4], xb[kPPW][4];
   float xs[kPPW][4];
   uint32_t xsw[kPPW][4], xsodd = 0;  // token / block scale words (bit 4j + tau of xsodd: odd index)
@@ -296,6 +339,10 @@ void kfmt_decode_kernel(const DecodeParams p) {
       }
     }
   }
+  // SPEC: the chunk's residual and V rows now, behind its codes (the waves without a chunk issue
+  // the same loads on empty resources, so that every wave's waits count the same loads)
+  uint4 srr[4][2], svv[8][2];
+  if constexpr (SPEC) issue_rv(0, c0 * kPage, nv[0], srr, svv);
   if constexpr (FMT == kNF4) {
     s_cb2[threadIdx.x] = make_float2(kNF4Levels[threadIdx.x & 15], kNF4Levels[threadIdx.x >> 4]);
   }
@@ -506,7 +553,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
   for (int j = 0; j < kPPW; ++j) {
     bal[j] = chunk_ballot(p, row_ok, mb[j], th, s_keep, cw, c0 + j, kc);
     if (nv[j] <= 0) bal[j] = 0;  // past the sequence end, or not this wave's chunk
-    const int slot = wv * kPPW + j;
+    const int slot = wch * kPPW + j;
     if (lane == 0) {
       s_bal[slot][0] = (uint32_t)bal[j];
       s_bal[slot][1] = (uint32_t)(bal[j] >> 32);
@@ -520,7 +567,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
     ++n_exact_;
 #endif
     constexpr int j = decltype(J)::value;
-    const int slot = wv * kPPW + j;
+    const int slot = wch * kPPW + j;
     const int t0 = (c0 + j) * kPage;
     const int nvs = min(Tb - t0, kPage);
     const uint64_t bl = bal[j];
@@ -571,38 +618,13 @@ void kfmt_decode_kernel(const DecodeParams p) {
         kg[tau] = f32x2{1.f, 1.f};
       }
     }
-    if constexpr (RES != kResNone) {
-      const brsrc rs = LAYOUT == kPaged ? page_rows(p.kr, pg[j], kD, true)
-                                        : make_rsrc(p.kr + (((size_t)b * p.T + t0) * p.HKV + hkv) * kD,
-                                                    ((nvs - 1) * p.HKV + 1) * kD);
+    if constexpr (SPEC) {
 #pragma unroll
-      for (int tau = 0; tau < 4; ++tau) {
-        if constexpr (LAYOUT == kPaged) {  // blocks (tau, h) of the page's residual
-          rr[tau][0] = bload16_nt(rs, ((tau * 2 + 0) * 64 + lane) * 16);
-          rr[tau][1] = bload16_nt(rs, ((tau * 2 + 1) * 64 + lane) * 16);
-        } else {
-          const uint32_t off = (4 * mrow + tau) * p.HKV * kD + 32 * kc;
-          rr[tau][0] = bload16_nt(rs, off);
-          rr[tau][1] = bload16_nt(rs, off + 16);
-        }
-      }
-    }
-    if constexpr (LAYOUT == kPaged) {
-      // V^T page: lane (n, kc) reads column 16 nu + n, tokens 16 kc + 8 kap .. + 8 (vt_off order)
-      const brsrc vs = make_rsrc((const uint16_t *)p.v + ((size_t)pg[j] * p.HKV + hkv) * (kD * kPage), kD * kPage * 2);
+      for (int tau = 0; tau < 4; ++tau) rr[tau][0] = srr[tau][0], rr[tau][1] = srr[tau][1];
 #pragma unroll
-      for (int nu = 0; nu < 8; ++nu)
-#pragma unroll
-        for (int kap = 0; kap < 2; ++kap) vv[nu][kap] = bload16_nt(vs, ((nu * 2 + kap) * 64 + lane) * 16);  // block (nu, kap)
+      for (int nu = 0; nu < 8; ++nu) vv[nu][0] = svv[nu][0], vv[nu][1] = svv[nu][1];
     } else {
-      const brsrc vs = make_rsrc((const uint16_t *)p.v + (((size_t)b * p.T + t0) * p.HKV + hkv) * kD,
-                                 ((nvs - 1) * p.HKV + 1) * kD * 2);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int idx = r * 64 + lane;
-        const int tk = idx >> 4, vc = idx & 15;
-        vv[r >> 1][r & 1] = bload16_nt(vs, tk * p.HKV * kD * 2 + 16 * vc);
-      }
+      issue_rv(pg[j], t0, nvs, rr, vv);
     }
     if constexpr (LAYOUT != kPaged && RELOAD && kTokScale) {
       __builtin_amdgcn_sched_barrier(0);
@@ -725,9 +747,9 @@ void kfmt_decode_kernel(const DecodeParams p) {
     }
   };
   if (nv[0] > 0 && bal[0] != 0) exact_chunk(std::integral_constant<int, 0>());
-  else empty_chunk(wv * kPPW);
+  else empty_chunk(wch * kPPW);
   if (nv[1] > 0 && bal[1] != 0) exact_chunk(std::integral_constant<int, 1>());
-  else empty_chunk(wv * kPPW + 1);
+  else empty_chunk(wch * kPPW + 1);
 
   FFA_STAMP(10);
   // ------------------------------------------------ phase 4: mask, threshold, workgroup partial
@@ -813,13 +835,15 @@ void kfmt_decode_kernel(const DecodeParams p) {
 template <int L, int F, int S, int R, int V>
 static hipError_t kfmt_launch(const ffa::DecodeParams &p, dim3 grid, hipStream_t st) {
   if constexpr (L == ffa::kPaged) {
-    hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, true>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, true, false>), grid, dim3(256), 0, st, p);
   } else {
     const int cus = ffa::device_cus();
     if (cus > 0 && grid.x * grid.y * grid.z > (unsigned)cus)
-      hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, true>), grid, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, true, false>), grid, dim3(256), 0, st, p);
+    else if (p.span == ffa::kMinSpan)
+      hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, false, true>), grid, dim3(256), 0, st, p);
     else
-      hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, false>), grid, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, false, false>), grid, dim3(256), 0, st, p);
   }
   return hipGetLastError();
 }
