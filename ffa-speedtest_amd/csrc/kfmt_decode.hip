@@ -431,10 +431,15 @@ void kfmt_decode_kernel(const DecodeParams p) {
     return __builtin_bit_cast(f16x8, r);
   };
   // dot products of one 16-token tile with the lane's column, summed over the four groups
-  auto score_tile = [&](const uint4 &a, const uint4 &bq, float sc, f32x2 gs, float *out) {
+  // (kh: where to keep the tile's fp16 K operands, or nullptr)
+  auto score_tile = [&](const uint4 &a, const uint4 &bq, float sc, f32x2 gs, float *out, f16x8 *kh) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int mp = 0; mp < 4; ++mp) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant(a, bq, mp, sc, gs), qa[mp], acc, 0, 0, 0);
+    for (int mp = 0; mp < 4; ++mp) {
+      const f16x8 k = dequant(a, bq, mp, sc, gs);
+      if (kh != nullptr) kh[mp] = k;
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k, qa[mp], acc, 0, 0, 0);
+    }
 #pragma unroll
     for (int uu = 0; uu < 4; ++uu) {
       float r = acc[uu];
@@ -473,11 +478,15 @@ void kfmt_decode_kernel(const DecodeParams p) {
     }
   }
   float R[kPPW][16];
+  // SPEC with a residual: the chunk's fp16 K operands from the scoring, kept for the refine (a
+  // second dequantization would sit on the wave's chain after the prune decision)
+  constexpr bool kKeepK = SPEC && RES != kResNone;
+  f16x8 khat[4][4];
   uint64_t bal[kPPW] = {0, 0};
   float th = INFINITY;
   if (do_probe) {
     float r4[4];
-    score_tile(pxa, pxb, psc, pgs, r4);
+    score_tile(pxa, pxb, psc, pgs, r4, nullptr);
     float mx = -INFINITY;
 #pragma unroll
     for (int uu = 0; uu < 4; ++uu) {
@@ -496,7 +505,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
 #pragma unroll
       for (int tau = 0; tau < 4; ++tau) {
         float r4[4];
-        score_tile(xa[j][tau], xb[j][tau], xs[j][tau], xg[j][tau], r4);
+        score_tile(xa[j][tau], xb[j][tau], xs[j][tau], xg[j][tau], r4, kKeepK && j == 0 ? khat[tau] : nullptr);
 #pragma unroll
         for (int uu = 0; uu < 4; ++uu) R[j][4 * uu + tau] = r4[uu];
       }
@@ -645,7 +654,8 @@ void kfmt_decode_kernel(const DecodeParams p) {
           const uint4 &rs4 = rr[tau][mp >> 1];
           const uint32_t lo = (mp & 1) ? rs4.z : rs4.x, hi = (mp & 1) ? rs4.w : rs4.y;
           acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-              add_f16x8(dequant(ka[tau], kb[tau], mp, ksc[tau], kg[tau]), fp8x8_to_f16x8<RES>(lo, hi)),
+              add_f16x8(kKeepK && j == 0 ? khat[tau][mp] : dequant(ka[tau], kb[tau], mp, ksc[tau], kg[tau]),
+                        fp8x8_to_f16x8<RES>(lo, hi)),
               qa[mp], acc, 0, 0, 0);
         }
 #pragma unroll
