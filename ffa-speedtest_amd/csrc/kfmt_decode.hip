@@ -267,7 +267,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
   }
   // residual and V loads of one chunk (page pg, or the contiguous rows of tokens t0 .. t0 + nvs;
   // nvs = 0 gives empty resources: the loads return zeros without a memory access)
-  auto issue_rv = [&](int pgid, int t0, int nvs, uint4 (&rr)[4][2], uint4 (&vv)[8][2]) {
+  auto issue_res = [&](int pgid, int t0, int nvs, uint4 (&rr)[4][2]) {
     if constexpr (RES != kResNone) {
       const brsrc rs = LAYOUT == kPaged ? page_rows(p.kr, pgid, kD, true)
                                         : make_rsrc(p.kr + (((size_t)b * p.T + t0) * p.HKV + hkv) * kD,
@@ -284,6 +284,8 @@ void kfmt_decode_kernel(const DecodeParams p) {
         }
       }
     }
+  };
+  auto issue_v = [&](int pgid, int t0, int nvs, uint4 (&vv)[8][2]) {
     if constexpr (LAYOUT == kPaged) {
       // V^T page: lane (n, kc) reads column 16 nu + n, tokens 16 kc + 8 kap .. + 8 (vt_off order)
       const brsrc vs = make_rsrc((const uint16_t *)p.v + ((size_t)pgid * p.HKV + hkv) * (kD * kPage), kD * kPage * 2);
@@ -300,6 +302,20 @@ void kfmt_decode_kernel(const DecodeParams p) {
         const int tk = idx >> 4, vc = idx & 15;
         vv[r >> 1][r & 1] = bload16_nt(vs, tk * p.HKV * kD * 2 + 16 * vc);
       }
+    }
+  };
+  // the contiguous V tile [64 tokens][128] loaded by issue_v, row-major into LDS rows of kVRow bytes,
+  // rounded to fp16 (rows past the sequence end were loaded as zeros)
+  auto stage_v_f16 = [&](const uint4 (&vv)[8][2], uint8_t *st) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int idx = r * 64 + lane;
+      const int tk = idx >> 4, vc = idx & 15;
+      const uint4 v4 = vv[r >> 1][r & 1];
+      const u32x4 w = __builtin_bit_cast(u32x4, VTr::operand(u32x4{v4.x, v4.y, v4.z, v4.w}));
+      uint2 *d = (uint2 *)(st + tk * kVRow + 16 * vc);  // rows are 8-byte aligned
+      d[0] = make_uint2(w[0], w[1]);
+      d[1] = make_uint2(w[2], w[3]);
     }
   };
   uint4 xa[kPPW][4], xb[kPPW][4];
@@ -339,10 +355,15 @@ void kfmt_decode_kernel(const DecodeParams p) {
       }
     }
   }
-  // SPEC: the chunk's residual and V rows now, behind its codes (the waves without a chunk issue
-  // the same loads on empty resources, so that every wave's waits count the same loads)
+  // SPEC: the chunk's residual rows now, behind its codes, and the V rows of the chunk of wave
+  // wv + 2 by waves 0 and 1, which stage it in LDS for that wave (each wave issues the other role's
+  // loads on empty resources, so that every wave's waits count the same loads)
   uint4 srr[4][2], svv[8][2];
-  if constexpr (SPEC) issue_rv(0, c0 * kPage, nv[0], srr, svv);
+  if constexpr (SPEC) {
+    issue_res(0, c0 * kPage, nv[0], srr);
+    const int vc0 = cw + (wv & 1);  // the chunk of wave (wv & 1) + 2
+    issue_v(0, vc0 * kPage, wv < 2 ? min(max(Tb - vc0 * kPage, 0), kPage) : 0, svv);
+  }
   if constexpr (FMT == kNF4) {
     s_cb2[threadIdx.x] = make_float2(kNF4Levels[threadIdx.x & 15], kNF4Levels[threadIdx.x >> 4]);
   }
@@ -630,10 +651,9 @@ void kfmt_decode_kernel(const DecodeParams p) {
     if constexpr (SPEC) {
 #pragma unroll
       for (int tau = 0; tau < 4; ++tau) rr[tau][0] = srr[tau][0], rr[tau][1] = srr[tau][1];
-#pragma unroll
-      for (int nu = 0; nu < 8; ++nu) vv[nu][0] = svv[nu][0], vv[nu][1] = svv[nu][1];
     } else {
-      issue_rv(pg[j], t0, nvs, rr, vv);
+      issue_res(pg[j], t0, nvs, rr);
+      issue_v(pg[j], t0, nvs, vv);
     }
     if constexpr (LAYOUT != kPaged && RELOAD && kTokScale) {
       __builtin_amdgcn_sched_barrier(0);
@@ -702,6 +722,16 @@ void kfmt_decode_kernel(const DecodeParams p) {
           oacc[nu] = VTr::mfma(pa2[kap], VTr::operand(w), oacc[nu]);
         }
       }
+    } else if constexpr (SPEC) {
+      // the V tile staged in fp16 by wave wv - 2, visible after this barrier (which the other waves
+      // reach after staging, or after an empty chunk)
+      lds_barrier();
+      const uint8_t *st = s_vstage + wv * kPage * kVRow;
+#pragma unroll
+      for (int nu = 0; nu < 8; ++nu)
+#pragma unroll
+        for (int kap = 0; kap < 2; ++kap)
+          oacc[nu] = VTr::mfma(pa2[kap], VTraits<kVF16>::operand(vt_operand_lds(st, kVRow, nu, kap, kc, n)), oacc[nu]);
     } else {
     // stage the V tile [64 tokens][128] through LDS (rows past the sequence end were loaded as
     // zeros): whole in the register-holding build (one workgroup per CU anyway), one half of the
@@ -756,10 +786,26 @@ void kfmt_decode_kernel(const DecodeParams p) {
       s_pl[slot][lane] = 0.f;
     }
   };
-  if (nv[0] > 0 && bal[0] != 0) exact_chunk(std::integral_constant<int, 0>());
-  else empty_chunk(wch * kPPW);
-  if (nv[1] > 0 && bal[1] != 0) exact_chunk(std::integral_constant<int, 1>());
-  else empty_chunk(wch * kPPW + 1);
+  if constexpr (SPEC) {
+    // one chunk per wave of 2 and 3; waves 0 and 1 stage their V tiles.  Every wave reaches the V
+    // barrier once (inside exact_chunk before P.V, or here).
+    if (wv < 2) {
+      stage_v_f16(svv, s_vstage + (wv + 2) * kPage * kVRow);
+      empty_chunk(wch * kPPW);
+      lds_barrier();
+    } else if (nv[0] > 0 && bal[0] != 0) {
+      exact_chunk(std::integral_constant<int, 0>());
+    } else {
+      empty_chunk(wch * kPPW);
+      lds_barrier();
+    }
+    empty_chunk(wch * kPPW + 1);
+  } else {
+    if (nv[0] > 0 && bal[0] != 0) exact_chunk(std::integral_constant<int, 0>());
+    else empty_chunk(wch * kPPW);
+    if (nv[1] > 0 && bal[1] != 0) exact_chunk(std::integral_constant<int, 1>());
+    else empty_chunk(wch * kPPW + 1);
+  }
 
   FFA_STAMP(10);
   // ------------------------------------------------ phase 4: mask, threshold, workgroup partial
