@@ -171,8 +171,9 @@ void kfmt_decode_kernel(const DecodeParams p) {
   const int NTB = (Tb + p.BS - 1) / p.BS;
   const int NTBS_b = NTB * (p.BS / p.SBS);
   const int NTBk = (p.T + p.BS - 1) / p.BS;  // blocks of the block-scale tensor
-  const bool do_probe = (p.th_in == nullptr) && wv < 2;
-  const int pa = wv == 0 ? 0 : max(NTB - 1, 0) * 16;  // probe window (attn_kernel...q2fp8.py:58-73)
+  // probe windows: waves 0 and 1 (SPEC: 2 and 3, the waves with the operands)
+  const bool do_probe = (p.th_in == nullptr) && wch < 2;
+  const int pa = wch == 0 ? 0 : max(NTB - 1, 0) * 16;  // probe window (attn_kernel...q2fp8.py:58-73)
   int nv[kPPW];  // valid tokens of the wave's chunks (0 for a chunk it does not own)
 #pragma unroll
   for (int j = 0; j < kPPW; ++j) nv[j] = own[j] ? min(max(Tb - (c0 + j) * kPage, 0), kPage) : 0;
@@ -188,9 +189,19 @@ void kfmt_decode_kernel(const DecodeParams p) {
   }
   const uint32_t es_q = p.q_dtype == 2 ? 4u : 2u;
   const int hwin = wv >> 1;
-  Raw16 qraw;
-  raw16_load(qraw, make_rsrc((const char *)p.q + (size_t)b * p.HQ * kD * es_q, p.HQ * kD * es_q),
-             (hq * kD + 32 * kc + 16 * hwin) * es_q, es_q, p.HQ * kD * es_q);
+  // the lane's 16 q channels of its wave's operand (SPEC: the 32 of all four operands, in waves 2
+  // and 3; waves 0 and 1 read nothing)
+  Raw16 qraw, qraw2;
+  {
+    const uint32_t qb = p.HQ * kD * es_q;
+    const brsrc qrs = make_rsrc((const char *)p.q + (size_t)b * p.HQ * kD * es_q, SPEC && wv < 2 ? 0u : qb);
+    if constexpr (SPEC) {
+      raw16_load(qraw, qrs, (hq * kD + 32 * kc) * es_q, es_q, qb);
+      raw16_load(qraw2, qrs, (hq * kD + 32 * kc + 16) * es_q, es_q, qb);
+    } else {
+      raw16_load(qraw, qrs, (hq * kD + 32 * kc + 16 * hwin) * es_q, es_q, qb);
+    }
+  }
   const float th_pre = __uint_as_float(
       bload8(make_rsrc(p.th_in + (p.th_in ? (size_t)b * p.HQ : 0), p.th_in ? p.HQ * 4 : 0), hq * 4).x);
   int pg[kPPW] = {0, 0};
@@ -259,7 +270,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
       if constexpr (!k4) pxb = bload16(rc, off + 16);
       // nvfp4: window 0 uses block 0's scale, window 1 block NTB-1's (attn_kernel...nvfp4fp8.py:86-97)
       if constexpr (kTokScale) {
-        const uint32_t si = scale_index(pa + mrow, wv == 0 ? 0 : max(NTB - 1, 0));
+        const uint32_t si = scale_index(pa + mrow, wch == 0 ? 0 : max(NTB - 1, 0));
         psw = scale_word(rsc, si, p.s_dtype);
         psodd = si & 1u;
       }
@@ -355,26 +366,35 @@ void kfmt_decode_kernel(const DecodeParams p) {
       }
     }
   }
-  // SPEC: the chunk's residual rows now, behind its codes, and the V rows of the chunk of wave
-  // wv + 2 by waves 0 and 1, which stage it in LDS for that wave (each wave issues the other role's
-  // loads on empty resources, so that every wave's waits count the same loads)
+  // SPEC: waves 0 and 1 load the residual and V rows of the chunk of wave wv + 2, before the prune
+  // decides it, and stage them in LDS for that wave (the chunk waves' own loads, issued above on
+  // empty resources in waves 0 and 1, go out first; no load follows them in waves 2 and 3)
   uint4 srr[4][2], svv[8][2];
   if constexpr (SPEC) {
-    issue_res(0, c0 * kPage, nv[0], srr);
-    const int vc0 = cw + (wv & 1);  // the chunk of wave (wv & 1) + 2
-    issue_v(0, vc0 * kPage, wv < 2 ? min(max(Tb - vc0 * kPage, 0), kPage) : 0, svv);
+    if (wv < 2) {
+      const int lc = cw + wv;
+      const int nl = min(max(Tb - lc * kPage, 0), kPage);
+      issue_res(0, lc * kPage, nl, srr);
+      issue_v(0, lc * kPage, nl, svv);
+    }
   }
   if constexpr (FMT == kNF4) {
-    s_cb2[threadIdx.x] = make_float2(kNF4Levels[threadIdx.x & 15], kNF4Levels[threadIdx.x >> 4]);
+    if constexpr (SPEC) {  // no barrier before the scoring: each chunk wave writes the whole table
+      if (wv >= 2)
+#pragma unroll
+        for (int i = lane; i < 256; i += 64) s_cb2[i] = make_float2(kNF4Levels[i & 15], kNF4Levels[i >> 4]);
+    } else {
+      s_cb2[threadIdx.x] = make_float2(kNF4Levels[threadIdx.x & 15], kNF4Levels[threadIdx.x >> 4]);
+    }
   }
 
   FFA_STAMP(1);
   // ------------------------------------------------ phase 2a: q operands (one per wave)
-  auto build_operands = [&](auto W) {
-    constexpr int w = decltype(W)::value;
-    constexpr int s = w & 1;
-    float qv[16];  // channels 32kc + 16h + (0..15)
-    raw16_to_f32(qraw, p.q_dtype, qv);
+  // operand of MFMA m' = 2h + s from the lane's 16 channels 32kc + 16h + (0..15)
+  auto operand_of = [&](const Raw16 &raw, auto S) -> u32x4 {
+    constexpr int s = decltype(S)::value;
+    float qv[16];
+    raw16_to_f32(raw, p.q_dtype, qv);
     u32x4 a4;
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq) {
@@ -382,21 +402,29 @@ void kfmt_decode_kernel(const DecodeParams p) {
       const float e1 = (row_ok && kc == jg) ? (float)(_Float16)qv[8 * s + 2 * qq + 1] : 0.f;
       a4[qq] = f32_to_f16_bits(e0) | (f32_to_f16_bits(e1) << 16);
     }
-    s_qa[w][lane] = make_uint4(a4[0], a4[1], a4[2], a4[3]);
+    return a4;
   };
-  switch (wv) {
-    case 0: build_operands(std::integral_constant<int, 0>()); break;
-    case 1: build_operands(std::integral_constant<int, 1>()); break;
-    case 2: build_operands(std::integral_constant<int, 2>()); break;
-    default: build_operands(std::integral_constant<int, 3>()); break;
-  }
-  lds_barrier();
-  FFA_STAMP(2);
   f16x8 qa[4];
+  if constexpr (SPEC) {  // waves 2 and 3 build all four (waves 0 and 1 score nothing)
+    if (wv >= 2) {
+      qa[0] = __builtin_bit_cast(f16x8, operand_of(qraw, std::integral_constant<int, 0>()));
+      qa[1] = __builtin_bit_cast(f16x8, operand_of(qraw, std::integral_constant<int, 1>()));
+      qa[2] = __builtin_bit_cast(f16x8, operand_of(qraw2, std::integral_constant<int, 0>()));
+      qa[3] = __builtin_bit_cast(f16x8, operand_of(qraw2, std::integral_constant<int, 1>()));
+    }
+    FFA_STAMP(2);
+  } else {  // one per wave, shared through LDS
+    u32x4 a4;
+    if (wv & 1) a4 = operand_of(qraw, std::integral_constant<int, 1>());
+    else a4 = operand_of(qraw, std::integral_constant<int, 0>());
+    s_qa[wv][lane] = make_uint4(a4[0], a4[1], a4[2], a4[3]);
+    lds_barrier();
+    FFA_STAMP(2);
 #pragma unroll
-  for (int mp = 0; mp < 4; ++mp) {
-    const uint4 a = s_qa[mp][lane];
-    qa[mp] = __builtin_bit_cast(f16x8, u32x4{a.x, a.y, a.z, a.w});
+    for (int mp = 0; mp < 4; ++mp) {
+      const uint4 a = s_qa[mp][lane];
+      qa[mp] = __builtin_bit_cast(f16x8, u32x4{a.x, a.y, a.z, a.w});
+    }
   }
 
   // fp16 K of MFMA m' (channels 32kc + 8m' + e) from the lane's row bytes
@@ -472,6 +500,15 @@ void kfmt_decode_kernel(const DecodeParams p) {
   const float cs1 = p.scale;
 
   // ------------------------------------------------ phase 2b: probe, scores, prune
+  float R[kPPW][16];
+  // SPEC with a residual: the chunk's fp16 K operands from the scoring, kept for the refine (a
+  // second dequantization would sit on the wave's chain after the prune decision)
+  constexpr bool kKeepK = SPEC && RES != kResNone;
+  f16x8 khat[4][4];
+  uint64_t bal[kPPW] = {0, 0};
+  float th = INFINITY;
+  float mb[kPPW] = {-INFINITY, -INFINITY};
+  if (!SPEC || wv >= 2) {  // (SPEC: waves 0 and 1 stage the residual rows instead, below)
   // token / block scales: converted here, after the operands, so that the dtype branches' waits
   // (which cover every load issued before them) come after the q operands are built
   if constexpr (LAYOUT != kPaged && kTokScale) {
@@ -498,13 +535,6 @@ void kfmt_decode_kernel(const DecodeParams p) {
       }
     }
   }
-  float R[kPPW][16];
-  // SPEC with a residual: the chunk's fp16 K operands from the scoring, kept for the refine (a
-  // second dequantization would sit on the wave's chain after the prune decision)
-  constexpr bool kKeepK = SPEC && RES != kResNone;
-  f16x8 khat[4][4];
-  uint64_t bal[kPPW] = {0, 0};
-  float th = INFINITY;
   if (do_probe) {
     float r4[4];
     score_tile(pxa, pxb, psc, pgs, r4, nullptr);
@@ -516,7 +546,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
     }
     mx = xor_max(mx, 16);
     mx = xor_max(mx, 32);
-    if (lane < 4) s_probe[wv][lane] = mx;
+    if (lane < 4) s_probe[wch][lane] = mx;
   }
   // R[j][k] = raw score of token (c0+j)*64 + 16kc + k (k = 4u + tau)
   auto score_page = [&](auto J) {
@@ -546,7 +576,8 @@ void kfmt_decode_kernel(const DecodeParams p) {
   };
   score_page(std::integral_constant<int, 0>());
   score_page(std::integral_constant<int, 1>());
-  float mb[kPPW] = {lane_max(0), lane_max(1)};
+  mb[0] = lane_max(0);
+  mb[1] = lane_max(1);
   if (SBS >= 32) {
     mb[0] = xor_max(mb[0], 16);
     mb[1] = xor_max(mb[1], 16);
@@ -557,6 +588,15 @@ void kfmt_decode_kernel(const DecodeParams p) {
   }
   if (SBS >= 128) mb[0] = mb[1] = fmaxf(mb[0], mb[1]);
   if (SBS > 128 && lane < 4) s_wmax[wv][lane] = mb[0];
+  } else if constexpr (SPEC) {
+    // the residual rows of the chunk of wave wv + 2 into LDS, in the lane order of the loads (the
+    // staging buffer of this wave, unused otherwise)
+    uint4 *dst = (uint4 *)(s_vstage + wv * kPage * kVRow);
+#pragma unroll
+    for (int tau = 0; tau < 4; ++tau)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) dst[(tau * 2 + h) * 64 + lane] = srr[tau][h];
+  }
   FFA_STAMP(3);
   lds_barrier();  // probe maxima (and per-wave block maxima)
   FFA_STAMP(4);
@@ -648,9 +688,12 @@ void kfmt_decode_kernel(const DecodeParams p) {
         kg[tau] = f32x2{1.f, 1.f};
       }
     }
-    if constexpr (SPEC) {
+    if constexpr (SPEC) {  // staged by wave wv - 2 before the probe barrier
+      const uint4 *src = (const uint4 *)(s_vstage + (wv - 2) * kPage * kVRow);
 #pragma unroll
-      for (int tau = 0; tau < 4; ++tau) rr[tau][0] = srr[tau][0], rr[tau][1] = srr[tau][1];
+      for (int tau = 0; tau < 4; ++tau)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) rr[tau][h] = src[(tau * 2 + h) * 64 + lane];
     } else {
       issue_res(pg[j], t0, nvs, rr);
       issue_v(pg[j], t0, nvs, vv);
