@@ -3,6 +3,7 @@
     python -m ffa_mi355x.timeline build                      # CPU: compile the timeline library
     python -m ffa_mi355x.timeline run --workload config2     # GPU: benchmark config 2's stage 1
     python -m ffa_mi355x.timeline run --workload config1     # GPU: benchmark config 1's step
+    python -m ffa_mi355x.timeline run --workload config2ref  # GPU: config 2's stage 1, reference layout
 
 `build` compiles every HIP source with -DFFA_TIMELINE into libffa_mi355x_timeline.so beside the
 library.  In that build each wave of the q2 and other-format decoders reads the 100 MHz constant
@@ -10,8 +11,8 @@ clock (s_memrealtime) at 13 points of its path and stores them, with the kept ch
 its hardware ids, into a buffer set through ffa_debug_set_timeline(_kfmt).  `run` replays a HIP
 graph of 24 rotated stage-1 launches (config 2, as bench.py times its roofline) or steps (config 1),
 keeps the stamps of the last launch and prints, in microseconds from the first wave's start, the
-median / 90th percentile / maximum of every point, and (config 2) the workgroups' end times by kept
-chunks per workgroup, per CU and per XCD.  The stamps are scalar-memory reads that share lgkmcnt
+median / 90th percentile / maximum of every point, and (config 2 in either layout) the workgroups'
+end times by kept chunks per workgroup, per CU and per XCD.  The stamps are scalar-memory reads that share lgkmcnt
 with LDS traffic, so the timeline build runs a little slower than the library.
 """
 from __future__ import annotations
@@ -31,9 +32,11 @@ POINTS = {
                 "chunk loads issued", "refined", "softmax", "P.V", "exact pass done", "final barrier", "end"],
     "config1": ["entry", "loads issued", "operands built", "pages scored", "probe barrier", "exact pass start",
                 "chunk loads issued", "refined", "softmax", "P.V", "exact pass done", "final barrier", "end"],
+    "config2ref": ["entry", "-", "operands built", "pages scored", "probe barrier", "published",
+                   "chunk loads issued", "refined", "softmax", "P.V", "exact pass done", "final barrier", "end"],
 }
 # points recorded inside a wave's exact pass (only waves that refine a chunk have them)
-EXACT_POINTS = {"config2": range(6, 10), "config1": range(5, 10)}
+EXACT_POINTS = {"config2": range(6, 10), "config1": range(5, 10), "config2ref": range(6, 10)}
 
 
 def build_lib(verbose: bool = False) -> Path:
@@ -93,6 +96,33 @@ def _config2(N, R=24):
     return us, buf.cpu().numpy().reshape(-1, 16).astype(np.int64), "stage 1 per launch"
 
 
+def _config2ref(N, R=24):
+    import torch
+
+    from . import quant, synth
+    from .decode import DecodeWorkspace, run_decode
+
+    dev = torch.device("cuda:0")
+    T, HKV = 32768, 8
+    q, k, v = synth.attention_inputs(B=1, T=T, HQ=32, HKV=HKV, D=128, seed=0, n_heavy=16, cos=0.8)
+    qd, vd = q.to(dev), v.to(dev)
+    kq, ks, kz, kr = quant.quantize_per_channel(k.to(dev), torch.float8_e5m2)
+    copies = [(kq.clone(), kr.clone(), vd.clone()) for _ in range(R)]
+    ws = DecodeWorkspace(1, 32, HKV, T, 64, 64, dev, qd.dtype)
+    buf = torch.zeros(64 * HKV * 4 * 16, dtype=torch.int64, device=dev)
+    N.lib().ffa_debug_set_timeline.argtypes = [ctypes.c_void_p]
+    assert N.lib().ffa_debug_set_timeline(ctypes.c_void_p(buf.data_ptr())) == 0
+
+    def step(r):
+        kq_, kr_, v_ = copies[r]
+        run_decode(q=qd, k_q=kq_, k_scale=ks, k_zero=kz, v=v_, k_residual=kr_, layout=N.LAYOUT_CONTIG,
+                   scale_mode=N.SCALE_CHANNEL, T=T, HKV=HKV, scale=128 ** -0.5, BS=64, SBS=64, delta=5.0,
+                   use_res=True, workspace=ws, stage="stage1")
+
+    us = _graph(step, R)
+    return us, buf.cpu().numpy().reshape(-1, 16).astype(np.int64), "stage 1 per launch"
+
+
 def _config1(N, R=24):
     import torch
 
@@ -129,6 +159,8 @@ def summarize(st: np.ndarray, names, per_wg: bool, exact_points=range(6, 10)) ->
     nex = st[:, 13]
     print(f"{'point':22s} {'median':>7s} {'p90':>7s} {'max':>7s}   (us from the first wave's start)")
     for i, nm in enumerate(names):
+        if nm == "-":  # a point this layout does not stamp
+            continue
         col = rel[nex > 0, i] if i in exact_points else rel[:, i]
         print(f"{nm:22s} {np.median(col):7.2f} {np.percentile(col, 90):7.2f} {col.max():7.2f}")
     ex = nex > 0
@@ -174,9 +206,9 @@ def main(argv=None) -> None:
     if not LIB.exists():
         raise SystemExit(f"{LIB} is missing: run `python -m ffa_mi355x.timeline build` first")
     N.LIB_PATH = LIB  # this process loads the timeline build instead of the library
-    us, st, what = (_config2 if args.workload == "config2" else _config1)(N)
+    us, st, what = {"config2": _config2, "config1": _config1, "config2ref": _config2ref}[args.workload](N)
     print(f"{args.workload}: {us:.2f} us {what} in the timeline build; {len(st)} waves")
-    summarize(st, POINTS[args.workload], per_wg=args.workload == "config2", exact_points=EXACT_POINTS[args.workload])
+    summarize(st, POINTS[args.workload], per_wg=args.workload != "config1", exact_points=EXACT_POINTS[args.workload])
 
 
 if __name__ == "__main__":
