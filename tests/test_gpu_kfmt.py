@@ -224,3 +224,33 @@ def test_contiguous_large_grid_reload_build(gpu, fmt):
             qd, torch.from_numpy(pk).to(gpu), torch.from_numpy(sc).to(torch.bfloat16).to(gpu), v.to(gpu),
             k_residual=torch.from_numpy(res).view(torch.float8_e5m2).to(gpu), BS=64, delta=5.0, workspace=ws)
     _check(o, ws, o_ref, diag, f"{fmt} contiguous, large grid")
+
+
+@pytest.mark.parametrize("T,th_given", [(4096, False), (4096, True), (8192, False), (16384, False)])
+def test_fp8_scaled_small_grid_spans(gpu, T, th_given):
+    """The contiguous small-grid builds at B=1, 8 KV heads: T=4096 gives two-chunk spans (waves 2
+    and 3 score, waves 0 and 1 load and stage the residual / V rows before the prune), 8192
+    four-chunk spans, 16384 eight-chunk spans in 256 workgroups (the register-holding build); with
+    a caller's threshold the two-chunk build scores no probe window."""
+    from ffa_mi355x import _native as N
+    from ffa_mi355x.decode import DecodeWorkspace
+    from ffa_mi355x.kfmt import run_kfmt_decode
+
+    q, k, v = _inputs(1, T, "bf16", 12, 16)
+    base, s, res = OF.quantize_fp8_scaled(f32(k), "e4m3fn")
+    kh = OF.khat_fp8_scaled(base, s, "e4m3fn")
+    th = None
+    if th_given:
+        _, d0 = O.decode(f32(q), base, None, None, f32(v), res, res_fmt="e4m3fn", BS=64, SBS=64, delta=5.0,
+                         khat=kh, out_dtype="bf16")
+        th = d0["threshold"] + 0.5  # a different threshold than the probe's: more blocks pruned
+    o_ref, diag = O.decode(f32(q), base, None, None, f32(v), res, res_fmt="e4m3fn", BS=64, SBS=64, delta=5.0,
+                           khat=kh, out_dtype="bf16", precomputed_threshold=th)
+    ws = DecodeWorkspace(1, 32, 8, T, 64, 64, gpu, torch.bfloat16)
+    run_kfmt_decode(q=q.to(gpu), k=torch.from_numpy(base).view(torch.float8_e4m3fn).to(gpu),
+                    k_format=N.KFMT_FP8_E4M3, k_scale=torch.from_numpy(s).to(torch.float16).to(gpu),
+                    scale_kind=N.KSCALE_TOKEN, v=v.to(gpu),
+                    k_residual=torch.from_numpy(res).view(torch.float8_e4m3fn).to(gpu), use_res=True, T=T, HKV=8,
+                    scale=128 ** -0.5, BS=64, SBS=64, delta=5.0,
+                    precomputed_threshold=None if th is None else torch.from_numpy(th).to(gpu), workspace=ws)
+    _check(ws.o, ws, o_ref, diag, f"fp8 scaled T={T} threshold given={th_given}")
