@@ -178,6 +178,18 @@ void kfmt_decode_kernel(const DecodeParams p) {
 #pragma unroll
   for (int j = 0; j < kPPW; ++j) nv[j] = own[j] ? min(max(Tb - (c0 + j) * kPage, 0), kPage) : 0;
 
+  // nf4: this thread's entries of the LDS level-pair table, loaded (constant memory) before every
+  // other load, so that writing the table later waits for these loads only (loaded after the code
+  // rows, the write waited for the codes and held the operand build behind them)
+  float2 cbv[SPEC ? 4 : 1];
+  if constexpr (FMT == kNF4) {
+#pragma unroll
+    for (int r = 0; r < (SPEC ? 4 : 1); ++r) {
+      const int i = SPEC ? lane + 64 * r : (int)threadIdx.x;
+      cbv[r] = make_float2(kNF4Levels[i & 15], kNF4Levels[i >> 4]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
   uint32_t pg_lane = 0;
   if constexpr (LAYOUT == kPaged) {
     // page ids: one vector load per wave, issued first (lanes 0, 1: the wave's chunks, lane 2: its
@@ -382,9 +394,9 @@ void kfmt_decode_kernel(const DecodeParams p) {
     if constexpr (SPEC) {  // no barrier before the scoring: each chunk wave writes the whole table
       if (wv >= 2)
 #pragma unroll
-        for (int i = lane; i < 256; i += 64) s_cb2[i] = make_float2(kNF4Levels[i & 15], kNF4Levels[i >> 4]);
+        for (int r = 0; r < 4; ++r) s_cb2[lane + 64 * r] = cbv[r];
     } else {
-      s_cb2[threadIdx.x] = make_float2(kNF4Levels[threadIdx.x & 15], kNF4Levels[threadIdx.x >> 4]);
+      s_cb2[threadIdx.x] = cbv[0];
     }
   }
 
