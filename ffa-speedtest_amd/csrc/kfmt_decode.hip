@@ -380,10 +380,14 @@ void kfmt_decode_kernel(const DecodeParams p) {
   }
   // SPEC: waves 0 and 1 load the residual and V rows of the chunk of wave wv + 2, before the prune
   // decides it, and stage them in LDS for that wave (the chunk waves' own loads, issued above on
-  // empty resources in waves 0 and 1, go out first; no load follows them in waves 2 and 3)
+  // empty resources in waves 0 and 1, go out first; no load follows them in waves 2 and 3).  They
+  // sleep about 0.25 us first, so that the chunk waves' code rows, which gate the decision, meet
+  // fewer of these rows in the memory queues (config 1: 10.27 -> 10.14 us per step; twice as long
+  // gave nothing)
   uint4 srr[4][2], svv[8][2];
   if constexpr (SPEC) {
     if (wv < 2) {
+      __builtin_amdgcn_s_sleep(10);
       const int lc = cw + wv;
       const int nl = min(max(Tb - lc * kPage, 0), kPage);
       issue_res(0, lc * kPage, nl, srr);
