@@ -96,9 +96,13 @@ __device__ __forceinline__ float scale_value(uint32_t w, uint32_t odd, int dt) {
 // layout: always, with four waves per SIMD (at most 128 registers, one or two spilled).
 // Contiguous layouts (54.7 KB of LDS, two workgroups per CU): when the grid is larger than the
 // CU count; small grids keep the registers, one latency chain per wave being all they have.
-// SPEC (contiguous, two-chunk spans only): waves 2 and 3 own the two chunks and issue each chunk's
-// residual and V loads with its codes, before the prune decides it; waves 0 and 1 score the probe
-// windows.
+// SPEC (contiguous, two-chunk spans only, where two of the four waves would own no chunk): a split by
+// role.  Waves 2 and 3 own the two chunks: they load q, a probe window each and their chunk's codes,
+// build all four q operands themselves and score.  Waves 0 and 1 load the residual and V rows of
+// chunk wv (the chunk of wave wv + 2) before the prune decides it, and stage them in LDS: the
+// residual before the probe barrier, the V tile rounded to fp16 after it (a second barrier hands
+// it over).  Every load a chunk wave waits for is then its own, and the V rounding and staging
+// leave its path.
 template <int LAYOUT, int FMT, int SCL, int RES, int VT, bool RELOAD, bool SPEC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LAYOUT == kPaged ? 4 : (RELOAD ? 2 : 1))))
 void kfmt_decode_kernel(const DecodeParams p) {
@@ -123,7 +127,8 @@ void kfmt_decode_kernel(const DecodeParams p) {
   const int hkv = un.hkv;
   const int b = blockIdx.z;
   // span: chunks of this workgroup (8, or 4 / 2 for small grids, where each wave owns one chunk
-  // and waves past the span own none); slot (w, j) = wave w's j-th chunk.  The paged build serves
+  // and waves past the span own none); slot (w, j) = the j-th chunk of the wave in place w of the
+  // chunk order (wch below: the wave itself, or in SPEC wave w ^ 2).  The paged build serves
   // large batches and keeps the whole span as a constant (the runtime form costs it registers)
   const int span = LAYOUT == kPaged ? kChunksPerWG : (SPEC ? kMinSpan : decode_span(p));
   const int ppw = span >= kChunksPerWG ? kPPW : 1;
