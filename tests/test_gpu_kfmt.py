@@ -254,3 +254,34 @@ def test_fp8_scaled_small_grid_spans(gpu, T, th_given):
                     scale=128 ** -0.5, BS=64, SBS=64, delta=5.0,
                     precomputed_threshold=None if th is None else torch.from_numpy(th).to(gpu), workspace=ws)
     _check(ws.o, ws, o_ref, diag, f"fp8 scaled T={T} threshold given={th_given}")
+
+
+def test_fp8_scaled_small_grid_ragged_with_empty_sequence(gpu):
+    """Two-chunk spans (B=3, T=1024) over lengths 0, 37 and 1024: an empty sequence (output 0), a
+    sequence inside its first chunk, and a full one."""
+    from ffa_mi355x import _native as N
+    from ffa_mi355x.decode import DecodeWorkspace
+    from ffa_mi355x.kfmt import run_kfmt_decode
+
+    lens = [0, 37, 1024]
+    B, T = 3, 1024
+    q, k, v = _inputs(B, T, "bf16", 13, 16, seq_lens=lens)
+    base, s, res = OF.quantize_fp8_scaled(f32(k), "e4m3fn")
+    kh = OF.khat_fp8_scaled(base, s, "e4m3fn")
+    o_ref, diag = O.decode(f32(q), base, None, None, f32(v), res, res_fmt="e4m3fn", BS=64, SBS=64, delta=5.0,
+                           khat=kh, out_dtype="bf16", seq_lens=lens)
+    ws = DecodeWorkspace(B, 32, 8, T, 64, 64, gpu, torch.bfloat16)
+    run_kfmt_decode(q=q.to(gpu), k=torch.from_numpy(base).view(torch.float8_e4m3fn).to(gpu),
+                    k_format=N.KFMT_FP8_E4M3, k_scale=torch.from_numpy(s).to(torch.float16).to(gpu),
+                    scale_kind=N.KSCALE_TOKEN, v=v.to(gpu),
+                    k_residual=torch.from_numpy(res).view(torch.float8_e4m3fn).to(gpu), use_res=True, T=T, HKV=8,
+                    scale=128 ** -0.5, BS=64, SBS=64, delta=5.0,
+                    seq_lens=torch.tensor(lens, dtype=torch.int32, device=gpu), workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(ws.o[0]).item() == 0, "an empty sequence decodes to 0"
+    far, near, n_near = compare_masks(ws.mask_buf.cpu().numpy(), diag)
+    assert far == 0, f"{far} mask mismatches away from the threshold"
+    th = ws.threshold_buf.cpu().numpy()[1:]
+    assert np.abs(th - diag["threshold"][1:]).max() < 1e-4, "threshold"
+    mx, mean = assert_out_close(f32(ws.o), o_ref, "fp8 scaled ragged small grid")
+    print(f"[out] ragged small grid max_abs={mx:.3e} mean_abs={mean:.3e}")
