@@ -138,9 +138,13 @@ __host__ __device__ constexpr int scale_pos(int t) { return 16 * (t >> 4) + 4 * 
 // workgroups share a CU (29 KB of LDS each): used when the grid has more workgroups than two per
 // CU can hold (large batches), where it trades a few spilled registers for two more workgroups
 // in flight.
-template <int LAYOUT, int SMODE, int RES, int VT, int OCC>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void q2fp8_decode_kernel(
-    const DecodeParams p) {
+// SPEC (the paged g32 build for two-chunk spans, q2fp8_decode_2span_kernel): waves 2 and 3 own
+// the two chunks and score them and the probe windows; waves 0 and 1, which would own none, load
+// the residual and V^T pages of chunk wv (the chunk of wave wv + 2) right after the operand barrier,
+// before the prune decides it, and refine that chunk from their registers if it is kept.
+template <int LAYOUT, int SMODE, int RES, int VT, int OCC, bool SPEC>
+__device__ __forceinline__ void q2fp8_decode_body(const DecodeParams &p) {
+  static_assert(!SPEC || (LAYOUT == kPaged && SMODE == kG32 && OCC == 1), "the two-chunk build is paged g32");
   typedef VTraits<VT> VTr;
 #ifdef FFA_TIMELINE
   unsigned long long st_[16] = {0};
@@ -159,14 +163,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   const int b = blockIdx.z;
   // span: chunks of this workgroup (8, or 4 / 2 for small grids, where each wave owns one chunk and
   // waves past the span own none); slot (w, j) = wave w's j-th chunk
-  const int span = decode_span(p);
+  const int span = SPEC ? kMinSpan : decode_span(p);
   const int ppw = span >= kChunksPerWG ? kPPW : 1;
-  const int cw = cg * span;      // first chunk of the workgroup
-  const int c0 = cw + wv * ppw;  // first chunk scored by this wave
+  const int cw = cg * span;  // first chunk of the workgroup
+  // the wave's place in the chunk order: its own index, or (SPEC) waves 2, 3 first
+  const int wch = SPEC ? (wv ^ 2) : wv;
+  const int c0 = cw + wch * ppw;  // first chunk scored by this wave
   const int SBS = p.SBS;
   bool own[kPPW];
 #pragma unroll
-  for (int j = 0; j < kPPW; ++j) own[j] = j < ppw && wv * ppw + j < span;
+  for (int j = 0; j < kPPW; ++j) own[j] = j < ppw && wch * ppw + j < span;
   auto slot_chunk = [&](int sl) { return cw + (sl >> 1) * ppw + (sl & 1); };  // chunk of slot sl
   auto slot_owned = [&](int sl) { return (sl & 1) < ppw && (sl >> 1) * ppw + (sl & 1) < span; };
 
@@ -225,11 +231,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   if (threadIdx.x < kChunksPerWG * kPage / 16) s_keep[threadIdx.x] = 0;
   const int NTB = (Tb + p.BS - 1) / p.BS;
   const int NTBS_b = NTB * (p.BS / p.SBS);
-  const bool do_probe = (p.th_in == nullptr) && wv < 2;
-  const int pa = wv == 0 ? 0 : max(NTB - 1, 0) * 16;  // probe window (attn_kernel...q2fp8.py:58-73)
+  // probe windows: waves 0 and 1 (SPEC: 2 and 3, which score)
+  const bool do_probe = (p.th_in == nullptr) && wch < 2;
+  const int pa = wch == 0 ? 0 : max(NTB - 1, 0) * 16;  // probe window (attn_kernel...q2fp8.py:58-73)
   int nv[kPPW];  // valid tokens of the wave's chunks (0 for a chunk it does not own)
 #pragma unroll
   for (int j = 0; j < kPPW; ++j) nv[j] = own[j] ? min(max(Tb - (c0 + j) * kPage, 0), kPage) : 0;
+  // SPEC: the chunk whose residual and V^T waves 0 and 1 load (chunk wv), and its valid tokens
+  const int lc = cw + (wv & 1);
+  const int nl = SPEC && wv < 2 ? min(max(Tb - lc * kPage, 0), kPage) : 0;
 
   int pg[kPPW] = {0, 0};
   int ppg = 0;
@@ -237,8 +247,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   if constexpr (LAYOUT == kPaged) {
     // page ids: one vector load per wave, issued first (lanes 0, 1: the wave's chunks, lane 2: its
     // probe window; the other lanes read past the resource and get 0)
-    const bool need = lane < kPPW ? nv[lane & 1] > 0 : (lane == kPPW && do_probe && pa < Tb);
-    const int idx = lane < kPPW ? c0 + lane : (pa >> 6);
+    // (SPEC, waves 0 and 1: lane 0 reads the page of chunk lc)
+    const bool ld = SPEC && wv < 2;
+    const bool need = lane < kPPW ? (ld ? lane == 0 && nl > 0 : nv[lane & 1] > 0) : (lane == kPPW && do_probe && pa < Tb);
+    const int idx = lane < kPPW ? (ld ? lc : c0 + lane) : (pa >> 6);
     pg_lane = bload4(make_rsrc(p.bt + (size_t)b * p.bt_stride, p.bt_stride * 4), need ? idx * 4 : p.bt_stride * 4);
     pg_lane = pg_lane < (uint32_t)p.num_pages ? pg_lane : 0u;  // ids outside the pools read page 0
   }
@@ -400,6 +412,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   }
   lds_barrier();
   FFA_STAMP(2);
+  // SPEC: waves 0 and 1 load the residual and V^T pages of chunk lc now (after the operand barrier:
+  // issued before it, they would sit between the q loads and the operand build's wait).  Nothing
+  // these waves wait for before the exact pass comes after them; the chunk waves issue none.
+  uint4 srr[4][2], svv[8][2];
+  if constexpr (SPEC) {
+    if (wv < 2) {
+      const size_t blk = (size_t)pg[0] * p.HKV + hkv;
+      if constexpr (RES != kResNone) {
+        const brsrc rs = make_rsrc(p.kr + blk * (kPage * kD), nl > 0 ? kPage * kD : 0);
+#pragma unroll
+        for (int tau = 0; tau < 4; ++tau) {
+          srr[tau][0] = bload16_nt(rs, ((tau * 2 + 0) * 64 + lane) * 16);
+          srr[tau][1] = bload16_nt(rs, ((tau * 2 + 1) * 64 + lane) * 16);
+        }
+      }
+      const brsrc vs = make_rsrc((const uint16_t *)p.v + blk * (kD * kPage), nl > 0 ? kD * kPage * 2 : 0);
+#pragma unroll
+      for (int nu = 0; nu < 8; ++nu)
+#pragma unroll
+        for (int kap = 0; kap < 2; ++kap) svv[nu][kap] = bload16_nt(vs, ((nu * 2 + kap) * 64 + lane) * 16);
+    }
+  }
   f16x8 qa[4];
   uint32_t spair[16], zpair[16];
   float zq = 0.f;
@@ -485,7 +519,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     }
     mx = xor_max(mx, 16);
     mx = xor_max(mx, 32);
-    if (lane < 4) s_probe[wv][lane] = mx;  // lane == ir here
+    if (lane < 4) s_probe[wch][lane] = mx;  // lane == ir here
   }
 
   // R[j][k] = raw score of token (c0+j)*64 + 16kc + k (k = 4u + tau)
@@ -611,7 +645,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   // publish the kept chunks: coarse scores (g32) or codes (channel scales), page, ballot
 #pragma unroll
   for (int j = 0; j < kPPW; ++j) {
-    const int slot = wv * kPPW + j;
+    const int slot = wch * kPPW + j;
     const bool kept = nv[j] > 0 && bal[j] != 0;
     if (lane == 0) {
       s_kept[slot] = kept ? 1 : 0;
@@ -687,6 +721,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     if constexpr (OCC > 1) __builtin_amdgcn_s_setprio(2);
     uint4 rr[4][2];
     uint4 vv[8][2];
+    // paged V^T: VH column blocks (of 8) are loaded with the residual; the large-batch build loads
+    // the second half after the first half's products, which keeps 32 fewer registers live
+    constexpr int VH = (LAYOUT == kPaged && OCC > 1) ? 4 : 8;
+    brsrc vs_p;
+    if constexpr (SPEC) {  // loaded by this wave after the operand barrier
+#pragma unroll
+      for (int tau = 0; tau < 4; ++tau) rr[tau][0] = srr[tau][0], rr[tau][1] = srr[tau][1];
+#pragma unroll
+      for (int nu = 0; nu < 8; ++nu) vv[nu][0] = svv[nu][0], vv[nu][1] = svv[nu][1];
+    } else {
     if constexpr (RES != kResNone) {
       brsrc rr_s;
       uint32_t ro[4];
@@ -708,10 +752,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
         }
       }
     }
-    // paged V^T: VH column blocks (of 8) are loaded with the residual; the large-batch build loads
-    // the second half after the first half's products, which keeps 32 fewer registers live
-    constexpr int VH = (LAYOUT == kPaged && OCC > 1) ? 4 : 8;
-    brsrc vs_p;
     if constexpr (LAYOUT == kPaged) {
       vs_p = make_rsrc((const uint16_t *)p.v + ((size_t)pgs_ * p.HKV + hkv) * (kD * kPage), kD * kPage * 2);
 #pragma unroll
@@ -727,6 +767,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
         const int tk = idx >> 4, vc = idx & 15;
         vv[r >> 1][r & 1] = bload16_nt(vs, tk * p.HKV * kD * 2 + 16 * vc);
       }
+    }
     }
     if constexpr (OCC > 1) __builtin_amdgcn_s_setprio(0);  // back to normal once the chunk's loads are out
     __builtin_amdgcn_sched_barrier(0);  // every load of the chunk goes out before the refine
@@ -889,18 +930,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
       s_pl[slot][lane] = row_ok ? lsum : 0.f;
     }
   };
-  // this wave's kept chunks: the (wv + 4a)-th set bit of km
-  int rank = 0;
-#pragma unroll 1
-  for (int sl = 0; sl < kChunksPerWG; ++sl) {
-    if ((km >> sl) & 1u) {
-      if ((rank & (kWaves - 1)) == wv) {
-        exact_chunk(sl);
+  if constexpr (SPEC) {
+    // waves 0 and 1 refine chunk wv (slot 2 wv), whose residual and V^T they hold, if it is kept
+    if (wv < 2 && ((km >> (2 * wv)) & 1u)) {
+      exact_chunk(2 * wv);
 #ifdef FFA_TIMELINE
-        ++n_exact_;
+      ++n_exact_;
 #endif
+    }
+  } else {
+    // this wave's kept chunks: the (wv + 4a)-th set bit of km
+    int rank = 0;
+#pragma unroll 1
+    for (int sl = 0; sl < kChunksPerWG; ++sl) {
+      if ((km >> sl) & 1u) {
+        if ((rank & (kWaves - 1)) == wv) {
+          exact_chunk(sl);
+#ifdef FFA_TIMELINE
+          ++n_exact_;
+#endif
+        }
+        ++rank;
       }
-      ++rank;
     }
   }
 
@@ -981,6 +1032,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     for (int i = 0; i < 16; ++i) g_timeline[wid * 16 + i] = st_[i];
   }
 #endif
+}
+
+template <int LAYOUT, int SMODE, int RES, int VT, int OCC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void q2fp8_decode_kernel(
+    const DecodeParams p) {
+  q2fp8_decode_body<LAYOUT, SMODE, RES, VT, OCC, false>(p);
+}
+
+// the paged g32 decode of two-chunk spans (small grids of at most one workgroup per CU)
+template <int RES, int VT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1))) void q2fp8_decode_2span_kernel(
+    const DecodeParams p) {
+  q2fp8_decode_body<kPaged, kG32, RES, VT, 1, true>(p);
 }
 
 // --------------------------------------------------------------------------
@@ -1252,6 +1316,11 @@ static hipError_t launch_decode(const ffa::DecodeParams &p, dim3 grid, hipStream
     const int cus = ffa::device_cus();
     if (cus > 0 && grid.x * grid.y * grid.z > 2u * (unsigned)cus) {
       hipLaunchKernelGGL((ffa::q2fp8_decode_kernel<L, S, R, V, 4>), grid, dim3(256), 0, st, p);
+      return hipGetLastError();
+    }
+    // two-chunk spans, at most one workgroup per CU: the role-split build
+    if (p.span == ffa::kMinSpan && cus > 0 && grid.x * grid.y * grid.z <= (unsigned)cus) {
+      hipLaunchKernelGGL((ffa::q2fp8_decode_2span_kernel<R, V>), grid, dim3(256), 0, st, p);
       return hipGetLastError();
     }
   }
