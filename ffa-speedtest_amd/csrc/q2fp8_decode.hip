@@ -719,18 +719,15 @@ __device__ __forceinline__ void q2fp8_decode_body(const DecodeParams &p) {
     // other workgroups on the CU (config 5's decode 658 -> 599 us; at config 2, where every
     // workgroup reaches its exact pass at about the same time, it cost 0.2 us)
     if constexpr (OCC > 1) __builtin_amdgcn_s_setprio(2);
-    uint4 rr[4][2];
-    uint4 vv[8][2];
+    // the chunk's residual and V rows (SPEC: loaded by this wave after the operand barrier, used in
+    // place, so that the refine waits for the residual alone and P.V for V)
+    uint4(&rr)[4][2] = srr;
+    uint4(&vv)[8][2] = svv;
     // paged V^T: VH column blocks (of 8) are loaded with the residual; the large-batch build loads
     // the second half after the first half's products, which keeps 32 fewer registers live
     constexpr int VH = (LAYOUT == kPaged && OCC > 1) ? 4 : 8;
     brsrc vs_p;
-    if constexpr (SPEC) {  // loaded by this wave after the operand barrier
-#pragma unroll
-      for (int tau = 0; tau < 4; ++tau) rr[tau][0] = srr[tau][0], rr[tau][1] = srr[tau][1];
-#pragma unroll
-      for (int nu = 0; nu < 8; ++nu) vv[nu][0] = svv[nu][0], vv[nu][1] = svv[nu][1];
-    } else {
+    if constexpr (!SPEC) {
     if constexpr (RES != kResNone) {
       brsrc rr_s;
       uint32_t ro[4];
