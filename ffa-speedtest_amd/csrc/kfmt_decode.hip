@@ -92,10 +92,12 @@ __device__ __forceinline__ float scale_value(uint32_t w, uint32_t odd, int dt) {
 }
 
 // RELOAD: the exact pass loads a kept chunk's codes and scales again instead of keeping the
-// scoring registers of the wave's other chunk, which roughly halves the registers.  Paged
-// layout: always, with four waves per SIMD (at most 128 registers, one or two spilled).
-// Contiguous layouts (54.7 KB of LDS, two workgroups per CU): when the grid is larger than the
-// CU count; small grids keep the registers, one latency chain per wave being all they have.
+// scoring registers of the wave's other chunk, which roughly halves the registers.  RELOAD builds
+// serve grids larger than the CU count: the paged one with four waves per SIMD (at most 128
+// registers, one or two spilled) and the whole 8-chunk span as a constant, the contiguous one (54.7
+// KB of LDS) with two workgroups per CU.  Small grids (at most one workgroup per CU) take the other
+// build, with the span a runtime value: contiguous layouts keep the scoring registers, one latency
+// chain per wave being all they have (the paged exact pass reloads its page either way).
 // SPEC (contiguous, two-chunk spans only, where two of the four waves would own no chunk): a split by
 // role.  Waves 2 and 3 own the two chunks: they load q, a probe window each and their chunk's codes,
 // build all four q operands themselves and score.  Waves 0 and 1 load the residual and V rows of
@@ -104,7 +106,7 @@ __device__ __forceinline__ float scale_value(uint32_t w, uint32_t odd, int dt) {
 // it over).  Every load a chunk wave waits for is then its own, and the V rounding and staging
 // leave its path.
 template <int LAYOUT, int FMT, int SCL, int RES, int VT, bool RELOAD, bool SPEC>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LAYOUT == kPaged ? 4 : (RELOAD ? 2 : 1))))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LAYOUT == kPaged && RELOAD ? 4 : (RELOAD ? 2 : 1))))
 void kfmt_decode_kernel(const DecodeParams p) {
   static_assert(!SPEC || (LAYOUT == kContig && !RELOAD), "speculative loads go with the small-grid contiguous build");
   typedef VTraits<VT> VTr;
@@ -128,9 +130,10 @@ void kfmt_decode_kernel(const DecodeParams p) {
   const int b = blockIdx.z;
   // span: chunks of this workgroup (8, or 4 / 2 for small grids, where each wave owns one chunk
   // and waves past the span own none); slot (w, j) = the j-th chunk of the wave in place w of the
-  // chunk order (wch below: the wave itself, or in SPEC wave w ^ 2).  The paged build serves
-  // large batches and keeps the whole span as a constant (the runtime form costs it registers)
-  const int span = LAYOUT == kPaged ? kChunksPerWG : (SPEC ? kMinSpan : decode_span(p));
+  // chunk order (wch below: the wave itself, or in SPEC wave w ^ 2).  The paged large-batch build
+  // keeps the whole span as a constant (the runtime form costs it registers)
+  constexpr bool kPagedBig = LAYOUT == kPaged && RELOAD;
+  const int span = kPagedBig ? kChunksPerWG : (SPEC ? kMinSpan : decode_span(p));
   const int ppw = span >= kChunksPerWG ? kPPW : 1;
   const int cw = cg * span;
   // the wave's place in the chunk order: its own index, or (SPEC) waves 2, 3 first
@@ -755,8 +758,8 @@ void kfmt_decode_kernel(const DecodeParams p) {
     // softmax partial over the active tokens (valid, in a kept prune block, a row of the group)
     const int nact = (row_ok && keep16) ? min(max(Tb - (t0 + 16 * kc), 0), 16) : 0;
     float P[16], mrow_max, lsum;
-    // (the paged build, at 128 registers, keeps one masked copy of the softmax and of P.V)
-    chunk_softmax<LAYOUT != kPaged>(Rj, cs1, nact, P, mrow_max, lsum);
+    // (the paged large-batch build, at 128 registers, keeps one masked copy of the softmax)
+    chunk_softmax<!kPagedBig>(Rj, cs1, nact, P, mrow_max, lsum);
     FFA_STAMP(8);
     typename VTr::vec pa2[2];
 #pragma unroll
@@ -955,7 +958,14 @@ void kfmt_decode_kernel(const DecodeParams p) {
 template <int L, int F, int S, int R, int V>
 static hipError_t kfmt_launch(const ffa::DecodeParams &p, dim3 grid, hipStream_t st) {
   if constexpr (L == ffa::kPaged) {
-    hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, true, false>), grid, dim3(256), 0, st, p);
+    // the runtime-span build for small grids and for every span shorter than 8 chunks (the last
+    // halving of a small grid's span can take it past the CU count); the large-batch build's span
+    // is the constant 8
+    const int cus = ffa::device_cus();
+    if (p.span < ffa::kChunksPerWG || (cus > 0 && grid.x * grid.y * grid.z <= (unsigned)cus))
+      hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, false, false>), grid, dim3(256), 0, st, p);
+    else
+      hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, true, false>), grid, dim3(256), 0, st, p);
   } else {
     const int cus = ffa::device_cus();
     if (cus > 0 && grid.x * grid.y * grid.z > (unsigned)cus)
@@ -1073,10 +1083,10 @@ extern "C" int ffa_kfmt_decode(const ffa_kfmt_decode_args *a, void *stream) {
   p.ntbs = a->ntbs;
   p.nwg = need;
   p.span = ffa::kChunksPerWG;
-  // small grids (fewer workgroups than CUs) of the contiguous layouts: shorter spans, one chunk
-  // per wave, while the slots fit the caller's scratch.  One pass with prune blocks of at most one
-  // chunk only (the longer blocks' maxima span two chunks of a wave).
-  if (!paged && p.pmax == nullptr && a->SBS <= ffa::kPage) {
+  // small grids (fewer workgroups than CUs): shorter spans, one chunk per wave, while the slots fit
+  // the caller's scratch.  One pass with prune blocks of at most one chunk only (the longer blocks'
+  // maxima span two chunks of a wave).
+  if (p.pmax == nullptr && a->SBS <= ffa::kPage) {
     const int cus = ffa::device_cus();
     const long units = (long)a->B * a->HKV * p.nq;
     for (int span = ffa::kChunksPerWG / 2; span >= ffa::kMinSpan; span /= 2) {

@@ -82,9 +82,11 @@ def test_paged_append_bit_exact(gpu, fmt):
 
 @pytest.mark.parametrize("fmt", ["nvfp4", "nf4"])
 @pytest.mark.parametrize("B,T,lens,BS,SBS,delta", [
-    (2, 3000, [3000, 1777], 64, 64, 5.0),
-    (1, 4096, None, 128, 32, 4.0),
+    (2, 3000, [3000, 1777], 64, 64, 5.0),     # two-chunk spans, 384 workgroups (runtime-span build)
+    (1, 4096, None, 128, 32, 4.0),            # two-chunk spans, 256 workgroups
     (3, 2500, [2500, 64, 1000], 64, 16, 3.0),
+    (1, 8192, None, 64, 64, 5.0),             # four-chunk spans
+    (2, 8192, [8192, 5000], 64, 64, 5.0),     # eight-chunk spans in 256 workgroups (runtime-span build)
 ])
 def test_paged_decode_parity(gpu, fmt, B, T, lens, BS, SBS, delta):
     q, k, v, lens, bt, btd, cache = _build(fmt, B, T, lens, seed=T + B)
