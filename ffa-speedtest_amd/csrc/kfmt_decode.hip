@@ -108,7 +108,7 @@ __device__ __forceinline__ float scale_value(uint32_t w, uint32_t odd, int dt) {
 template <int LAYOUT, int FMT, int SCL, int RES, int VT, bool RELOAD, bool SPEC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LAYOUT == kPaged && RELOAD ? 4 : (RELOAD ? 2 : 1))))
 void kfmt_decode_kernel(const DecodeParams p) {
-  static_assert(!SPEC || (LAYOUT == kContig && !RELOAD), "speculative loads go with the small-grid contiguous build");
+  static_assert(!SPEC || !RELOAD, "speculative loads go with the small-grid build");
   typedef VTraits<VT> VTr;
 #ifdef FFA_TIMELINE
   unsigned long long st_[16] = {0};
@@ -164,7 +164,11 @@ void kfmt_decode_kernel(const DecodeParams p) {
   __shared__ float s_po[kChunksPerWG][4][128];
   // nf4: the codebook levels of both nibbles of every code byte, (low, high) at [byte]
   __shared__ float2 s_cb2[FMT == kNF4 ? 256 : 1];
-  __shared__ __attribute__((aligned(16))) uint8_t s_vstage[LAYOUT == kContig ? kWaves * kPage * (RELOAD ? kVRowHalf : kVRow) : 16];
+  // V staging (contiguous layouts), and in SPEC the residual and V handed from waves 0 and 1 to
+  // waves 2 and 3: per-wave regions of kStage bytes (a row-major V tile, or a paged V^T block of
+  // 16 KB in the lanes' load order)
+  constexpr int kStage = LAYOUT == kContig ? kPage * (RELOAD ? kVRowHalf : kVRow) : (SPEC ? kPage * kD * 2 : 0);
+  __shared__ __attribute__((aligned(16))) uint8_t s_vstage[kStage > 0 ? kWaves * kStage : 16];
 
   auto lds_barrier = []() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
 
@@ -202,8 +206,12 @@ void kfmt_decode_kernel(const DecodeParams p) {
   if constexpr (LAYOUT == kPaged) {
     // page ids: one vector load per wave, issued first (lanes 0, 1: the wave's chunks, lane 2: its
     // probe window; the other lanes read past the resource and get 0)
-    const bool need = lane < kPPW ? nv[lane & 1] > 0 : (lane == kPPW && do_probe && pa < Tb);
-    const int idx = lane < kPPW ? c0 + lane : (pa >> 6);
+    // (SPEC, waves 0 and 1: lane 0 reads the page of chunk cw + wv, whose rows they load)
+    const bool ld = SPEC && wv < 2;
+    const int lc = cw + (wv & 1);
+    const bool need = lane < kPPW ? (ld ? lane == 0 && lc * kPage < Tb : nv[lane & 1] > 0)
+                                  : (lane == kPPW && do_probe && pa < Tb);
+    const int idx = lane < kPPW ? (ld ? lc : c0 + lane) : (pa >> 6);
     pg_lane = bload4(make_rsrc(p.bt + (size_t)b * p.bt_stride, p.bt_stride * 4), need ? idx * 4 : p.bt_stride * 4);
     pg_lane = pg_lane < (uint32_t)p.num_pages ? pg_lane : 0u;  // ids outside the pools read page 0
   }
@@ -300,7 +308,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
   // nvs = 0 gives empty resources: the loads return zeros without a memory access)
   auto issue_res = [&](int pgid, int t0, int nvs, uint4 (&rr)[4][2]) {
     if constexpr (RES != kResNone) {
-      const brsrc rs = LAYOUT == kPaged ? page_rows(p.kr, pgid, kD, true)
+      const brsrc rs = LAYOUT == kPaged ? page_rows(p.kr, pgid, kD, !SPEC || nvs > 0)
                                         : make_rsrc(p.kr + (((size_t)b * p.T + t0) * p.HKV + hkv) * kD,
                                                     nvs > 0 ? ((nvs - 1) * p.HKV + 1) * kD : 0);
 #pragma unroll
@@ -319,7 +327,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
   auto issue_v = [&](int pgid, int t0, int nvs, uint4 (&vv)[8][2]) {
     if constexpr (LAYOUT == kPaged) {
       // V^T page: lane (n, kc) reads column 16 nu + n, tokens 16 kc + 8 kap .. + 8 (vt_off order)
-      const brsrc vs = make_rsrc((const uint16_t *)p.v + ((size_t)pgid * p.HKV + hkv) * (kD * kPage), kD * kPage * 2);
+      const brsrc vs = make_rsrc((const uint16_t *)p.v + ((size_t)pgid * p.HKV + hkv) * (kD * kPage), !SPEC || nvs > 0 ? kD * kPage * 2 : 0);
 #pragma unroll
       for (int nu = 0; nu < 8; ++nu)
 #pragma unroll
@@ -398,8 +406,8 @@ void kfmt_decode_kernel(const DecodeParams p) {
       __builtin_amdgcn_s_sleep(10);
       const int lc = cw + wv;
       const int nl = min(max(Tb - lc * kPage, 0), kPage);
-      issue_res(0, lc * kPage, nl, srr);
-      issue_v(0, lc * kPage, nl, svv);
+      issue_res(pg[0], lc * kPage, nl, srr);
+      issue_v(pg[0], lc * kPage, nl, svv);
     }
   }
   if constexpr (FMT == kNF4) {
@@ -615,7 +623,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
   } else if constexpr (SPEC) {
     // the residual rows of the chunk of wave wv + 2 into LDS, in the lane order of the loads (the
     // staging buffer of this wave, unused otherwise)
-    uint4 *dst = (uint4 *)(s_vstage + wv * kPage * kVRow);
+    uint4 *dst = (uint4 *)(s_vstage + wv * kStage);
 #pragma unroll
     for (int tau = 0; tau < 4; ++tau)
 #pragma unroll
@@ -676,7 +684,9 @@ void kfmt_decode_kernel(const DecodeParams p) {
     float ksc[4];
     f32x2 kg[4];
     uint32_t ksw[4], ksodd = 0;  // reloaded scale words, converted once the residual and V loads are out
-    if constexpr (LAYOUT == kPaged) {
+    if constexpr (kKeepK) {
+      // the fp16 K operands kept from the scoring (khat): no codes or scales here
+    } else if constexpr (LAYOUT == kPaged) {
       const brsrc rc = page_rows(p.kq, pg[j], kRow, true);
       const brsrc rs = page_rows((const uint8_t *)p.ks, pg[j], SCL == kSclG16 ? 8 : 4, true);
 #pragma unroll
@@ -713,7 +723,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
       }
     }
     if constexpr (SPEC) {  // staged by wave wv - 2 before the probe barrier
-      const uint4 *src = (const uint4 *)(s_vstage + (wv - 2) * kPage * kVRow);
+      const uint4 *src = (const uint4 *)(s_vstage + (wv - 2) * kStage);
 #pragma unroll
       for (int tau = 0; tau < 4; ++tau)
 #pragma unroll
@@ -779,6 +789,14 @@ void kfmt_decode_kernel(const DecodeParams p) {
       const bool partial = nvs < kPage;
       u32x4 keepw[2];
       if (partial) partial_page_masks(kc, nvs, keepw);
+      if constexpr (SPEC) {  // the V^T page staged by wave wv - 2 in the lanes' load order
+        lds_barrier();
+        const uint4 *src = (const uint4 *)(s_vstage + wv * kStage);
+#pragma unroll
+        for (int nu = 0; nu < 8; ++nu)
+#pragma unroll
+          for (int kap = 0; kap < 2; ++kap) vv[nu][kap] = src[(nu * 2 + kap) * 64 + lane];
+      }
 #pragma unroll
       for (int nu = 0; nu < 8; ++nu) {
 #pragma unroll
@@ -793,7 +811,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
       // the V tile staged in fp16 by wave wv - 2, visible after this barrier (which the other waves
       // reach after staging, or after an empty chunk)
       lds_barrier();
-      const uint8_t *st = s_vstage + wv * kPage * kVRow;
+      const uint8_t *st = s_vstage + wv * kStage;
 #pragma unroll
       for (int nu = 0; nu < 8; ++nu)
 #pragma unroll
@@ -857,7 +875,15 @@ void kfmt_decode_kernel(const DecodeParams p) {
     // one chunk per wave of 2 and 3; waves 0 and 1 stage their V tiles.  Every wave reaches the V
     // barrier once (inside exact_chunk before P.V, or here).
     if (wv < 2) {
-      stage_v_f16(svv, s_vstage + (wv + 2) * kPage * kVRow);
+      if constexpr (LAYOUT == kPaged) {
+        uint4 *dst = (uint4 *)(s_vstage + (wv + 2) * kStage);
+#pragma unroll
+        for (int nu = 0; nu < 8; ++nu)
+#pragma unroll
+          for (int kap = 0; kap < 2; ++kap) dst[(nu * 2 + kap) * 64 + lane] = svv[nu][kap];
+      } else {
+        stage_v_f16(svv, s_vstage + (wv + 2) * kStage);
+      }
       empty_chunk(wch * kPPW);
       lds_barrier();
     } else if (nv[0] > 0 && bal[0] != 0) {
@@ -962,7 +988,10 @@ static hipError_t kfmt_launch(const ffa::DecodeParams &p, dim3 grid, hipStream_t
     // halving of a small grid's span can take it past the CU count); the large-batch build's span
     // is the constant 8
     const int cus = ffa::device_cus();
-    if (p.span < ffa::kChunksPerWG || (cus > 0 && grid.x * grid.y * grid.z <= (unsigned)cus))
+    const bool small = cus > 0 && grid.x * grid.y * grid.z <= (unsigned)cus;
+    if (small && p.span == ffa::kMinSpan)  // the role split of two-chunk spans
+      hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, false, true>), grid, dim3(256), 0, st, p);
+    else if (small || p.span < ffa::kChunksPerWG)
       hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, false, false>), grid, dim3(256), 0, st, p);
     else
       hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, true, false>), grid, dim3(256), 0, st, p);
