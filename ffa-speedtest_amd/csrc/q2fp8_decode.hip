@@ -138,13 +138,15 @@ __host__ __device__ constexpr int scale_pos(int t) { return 16 * (t >> 4) + 4 * 
 // workgroups share a CU (29 KB of LDS each): used when the grid has more workgroups than two per
 // CU can hold (large batches), where it trades a few spilled registers for two more workgroups
 // in flight.
-// SPEC (the paged g32 build for two-chunk spans, q2fp8_decode_2span_kernel): waves 2 and 3 own
-// the two chunks and score them and the probe windows; waves 0 and 1, which would own none, load
-// the residual and V^T pages of chunk wv (the chunk of wave wv + 2) right after the operand barrier,
-// before the prune decides it, and refine that chunk from their registers if it is kept.
+// SPEC (the builds for two-chunk spans, q2fp8_decode_2span_kernel: paged g32 and the contiguous
+// per-channel layouts): waves 2 and 3 own the two chunks and score them and the probe windows;
+// waves 0 and 1, which would own none, load the residual and V rows of chunk wv (the chunk of wave
+// wv + 2) right after the operand barrier, before the prune decides it, and refine that chunk from
+// their registers if it is kept.
 template <int LAYOUT, int SMODE, int RES, int VT, int OCC, bool SPEC>
 __device__ __forceinline__ void q2fp8_decode_body(const DecodeParams &p) {
-  static_assert(!SPEC || (LAYOUT == kPaged && SMODE == kG32 && OCC == 1), "the two-chunk build is paged g32");
+  static_assert(!SPEC || (OCC == 1 && (LAYOUT == kPaged) == (SMODE == kG32)),
+                "the two-chunk builds: paged g32, contiguous per-channel");
   typedef VTraits<VT> VTr;
 #ifdef FFA_TIMELINE
   unsigned long long st_[16] = {0};
@@ -416,7 +418,7 @@ __device__ __forceinline__ void q2fp8_decode_body(const DecodeParams &p) {
   // issued before it, they would sit between the q loads and the operand build's wait).  Nothing
   // these waves wait for before the exact pass comes after them; the chunk waves issue none.
   uint4 srr[4][2], svv[8][2];
-  if constexpr (SPEC) {
+  if constexpr (SPEC && LAYOUT == kPaged) {
     if (wv < 2) {
       const size_t blk = (size_t)pg[0] * p.HKV + hkv;
       if constexpr (RES != kResNone) {
@@ -432,6 +434,26 @@ __device__ __forceinline__ void q2fp8_decode_body(const DecodeParams &p) {
       for (int nu = 0; nu < 8; ++nu)
 #pragma unroll
         for (int kap = 0; kap < 2; ++kap) svv[nu][kap] = bload16_nt(vs, ((nu * 2 + kap) * 64 + lane) * 16);
+    }
+  } else if constexpr (SPEC) {  // contiguous rows of tokens lc * 64 .. (the exact pass's load pattern)
+    if (wv < 2) {
+      const size_t row0 = ((size_t)b * p.T + (size_t)lc * kPage) * p.HKV + hkv;
+      if constexpr (RES != kResNone) {
+        const brsrc rs = make_rsrc(p.kr + row0 * kD, nl > 0 ? ((nl - 1) * p.HKV + 1) * kD : 0);
+#pragma unroll
+        for (int tau = 0; tau < 4; ++tau) {
+          const uint32_t ro = (4 * mrow + tau) * p.HKV * kD + 32 * kc;
+          srr[tau][0] = bload16_nt(rs, ro);
+          srr[tau][1] = bload16_nt(rs, ro + 16);
+        }
+      }
+      const brsrc vs = make_rsrc((const uint16_t *)p.v + row0 * kD, nl > 0 ? ((nl - 1) * p.HKV + 1) * kD * 2 : 0);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int idx = r * 64 + lane;
+        const int tk = idx >> 4, vc = idx & 15;
+        svv[r >> 1][r & 1] = bload16_nt(vs, tk * p.HKV * kD * 2 + 16 * vc);
+      }
     }
   }
   f16x8 qa[4];
@@ -1037,11 +1059,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
   q2fp8_decode_body<LAYOUT, SMODE, RES, VT, OCC, false>(p);
 }
 
-// the paged g32 decode of two-chunk spans (small grids of at most one workgroup per CU)
-template <int RES, int VT>
+// the decode of two-chunk spans (small grids of at most one workgroup per CU): paged g32 and the
+// contiguous per-channel layouts
+template <int LAYOUT, int SMODE, int RES, int VT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1))) void q2fp8_decode_2span_kernel(
     const DecodeParams p) {
-  q2fp8_decode_body<kPaged, kG32, RES, VT, 1, true>(p);
+  q2fp8_decode_body<LAYOUT, SMODE, RES, VT, 1, true>(p);
 }
 
 // --------------------------------------------------------------------------
@@ -1315,9 +1338,12 @@ static hipError_t launch_decode(const ffa::DecodeParams &p, dim3 grid, hipStream
       hipLaunchKernelGGL((ffa::q2fp8_decode_kernel<L, S, R, V, 4>), grid, dim3(256), 0, st, p);
       return hipGetLastError();
     }
-    // two-chunk spans, at most one workgroup per CU: the role-split build
+  }
+  // two-chunk spans, at most one workgroup per CU: the role-split build (paged g32, contiguous)
+  if constexpr ((L == ffa::kPaged) == (S == ffa::kG32)) {
+    const int cus = ffa::device_cus();
     if (p.span == ffa::kMinSpan && cus > 0 && grid.x * grid.y * grid.z <= (unsigned)cus) {
-      hipLaunchKernelGGL((ffa::q2fp8_decode_2span_kernel<R, V>), grid, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((ffa::q2fp8_decode_2span_kernel<L, S, R, V>), grid, dim3(256), 0, st, p);
       return hipGetLastError();
     }
   }
