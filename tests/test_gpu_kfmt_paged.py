@@ -105,6 +105,42 @@ def test_paged_decode_parity(gpu, fmt, B, T, lens, BS, SBS, delta):
 
 
 @pytest.mark.parametrize("fmt", ["nvfp4", "nf4"])
+def test_paged_ragged_large_grid_items(gpu, fmt):
+    """A ragged batch on the large-batch build (6 x 8 x 32 = 1536 workgroup spans): only the spans that
+    hold tokens are launched as work, so the mask bytes past each sequence's end (written by its last
+    span) and every row's partials must come out as the oracle's from a workspace holding garbage;
+    lengths include an empty sequence, a one-page one and a partial last page."""
+    from ffa_mi355x.decode import DecodeWorkspace
+
+    B, T = 6, 16384
+    lens = [16384, 0, 700, 9000, 64, 12345]
+    q, k, v, lens, bt, btd, cache = _build(fmt, B, T, lens, seed=77)
+    lens_d = torch.tensor(lens, dtype=torch.int32, device=gpu)
+    ws = DecodeWorkspace(B, 32, 8, T, 64, 64, gpu, torch.bfloat16)
+    ws.mask_buf.fill_(5)
+    for t in (ws.m_buf, ws.l_buf, ws.o_buf, ws.o, ws.threshold_buf):
+        t.fill_(float("nan"))
+    for rep in range(2):  # twice into the same workspace
+        cache.decode(q.to(gpu), btd, lens_d, T=T, BS=64, SBS=64, delta=5.0, workspace=ws)
+        torch.cuda.synchronize()
+        if rep == 0:
+            pk, sc, res = QUANT[fmt](f32(k))
+            o_ref, diag = O.decode(f32(q), pk, None, None, f32(v), res, res_fmt="e4m3fn", BS=64, SBS=64,
+                                   delta=5.0, khat=_khat(fmt, pk, sc), seq_lens=lens, out_dtype="bf16")
+        m = ws.mask_buf.cpu().numpy()
+        for b, L in enumerate(lens):
+            assert (m[b, :, -(-L // 64):] == 0).all(), f"mask bytes past the end of sequence {b}"
+        far, near, n_near = compare_masks(m, diag)
+        print(f"[mask] {fmt} items rep={rep} keep={ws.mask_buf.float().mean().item():.3f} far={far} near={near}/{n_near}")
+        assert far == 0
+        full = [b for b, L in enumerate(lens) if L > 0]  # (an empty sequence's threshold is not defined)
+        assert np.abs(ws.threshold_buf.cpu().numpy()[full] - diag["threshold"][full]).max() < 1e-4
+        mx, mean = assert_out_close(f32(ws.o), o_ref, f"{fmt} paged items")
+        print(f"[out] {fmt} paged items max_abs={mx:.3e} mean_abs={mean:.3e}")
+        assert (f32(ws.o)[1] == 0).all(), "an empty sequence decodes to 0"
+
+
+@pytest.mark.parametrize("fmt", ["nvfp4", "nf4"])
 def test_paged_drop_in_block_table_kwargs(gpu, fmt):
     """The reference entry points with block_table= select the paged pools; skip ratio and the
     no-residual path follow the reference's rules."""
