@@ -1080,12 +1080,16 @@ __device__ __forceinline__ void merge_partials(const DecodeParams &p) {
   const int slab = blockIdx.x & 7;  // 16-column slab
   const int b = row / p.HQ;
   const int lane = threadIdx.x;
-  const int Tb = p.seq_lens ? min(max(p.seq_lens[b], 0), p.T) : p.T;  // lengths beyond T are clamped to T
   const int span_tok = decode_span(p) * kPage;
+  // the launch's slots (from T): the m, l (and eager o) loads are sized by them and issued before
+  // the sequence length arrives; slots past the sequence's own partials (stale workspace) are
+  // masked to l = 0 once it has
+  const int nslots = min((p.T + span_tok - 1) / span_tok, p.nparts);
+  const int Tb = p.seq_lens ? min(max(p.seq_lens[b], 0), p.T) : p.T;  // lengths beyond T are clamped to T
   const int nparts = min((Tb + span_tok - 1) / span_tok, p.nparts);
-  const brsrc rm = make_rsrc(p.m_buf + (size_t)row * p.nparts, nparts * 4);
-  const brsrc rl = make_rsrc(p.l_buf + (size_t)row * p.nparts, nparts * 4);
-  const brsrc ro = make_rsrc(p.o_buf + (size_t)row * p.nparts * 128 + 16 * slab, nparts > 0 ? ((nparts - 1) * 128 + 16) * 4 : 0);
+  const brsrc rm = make_rsrc(p.m_buf + (size_t)row * p.nparts, nslots * 4);
+  const brsrc rl = make_rsrc(p.l_buf + (size_t)row * p.nparts, nslots * 4);
+  const brsrc ro = make_rsrc(p.o_buf + (size_t)row * p.nparts * 128 + 16 * slab, nslots > 0 ? ((nslots - 1) * 128 + 16) * 4 : 0);
   __shared__ float s_o[64][17];
 
   // The lane's partials k = lane + 64 i (slots past nparts read as l = 0) in batches of four per
@@ -1095,15 +1099,15 @@ __device__ __forceinline__ void merge_partials(const DecodeParams &p) {
   // kept or not.  LAZY (many rows): only kept partials' columns are read, since most slots of
   // long sequences hold pruned spans and reading them all would dominate the traffic.
   constexpr int kNB = 4;  // partials per lane and batch
-  const uint32_t o_oob = nparts > 0 ? ((nparts - 1) * 128 + 16) * 4 : 0;  // offset past ro: zeros, no access
+  const uint32_t o_oob = nslots > 0 ? ((nslots - 1) * 128 + 16) * 4 : 0;  // offset past ro: zeros, no access
   float M = -INFINITY, A = 0.f;
   float acc[16];
 #pragma unroll
   for (int c = 0; c < 16; ++c) acc[c] = 0.f;
-  if (nparts <= 64) {  // one partial per lane (uniform): a single round trip, no rescaling
+  if (nslots <= 64) {  // one partial per lane (uniform): a single round trip, no rescaling
     const float m0 = __uint_as_float(bload4(rm, lane * 4));
     const float l0 = __uint_as_float(bload4(rl, lane * 4));
-    const bool keep = l0 > 0.f;
+    const bool keep = lane < nparts && l0 > 0.f;
     uint4 o0[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) o0[e] = bload16(ro, (!LAZY || keep) ? (lane * 128 + 4 * e) * 4 : o_oob);
@@ -1118,8 +1122,8 @@ __device__ __forceinline__ void merge_partials(const DecodeParams &p) {
       acc[4 * e + 3] = keep ? __uint_as_float(o0[e].w) * wgt : 0.f;
     }
   }
-  for (int kb = 0; nparts > 64 && kb < nparts; kb += 64 * kNB) {
-    const int nb = min(kNB, (nparts - kb + 63) >> 6);  // partials per lane in this batch (uniform)
+  for (int kb = 0; nslots > 64 && kb < nslots; kb += 64 * kNB) {
+    const int nb = min(kNB, (nslots - kb + 63) >> 6);  // partials per lane in this batch (uniform)
     float l[kNB], m[kNB];
     uint4 o[kNB][4];
 #pragma unroll
@@ -1132,6 +1136,9 @@ __device__ __forceinline__ void merge_partials(const DecodeParams &p) {
         m[i] = __uint_as_float(bload4(rm, k * 4));
       }
     }
+#pragma unroll
+    for (int i = 0; i < kNB; ++i)
+      if (kb + 64 * i + lane >= nparts) l[i] = 0.f;  // past the sequence's partials
     if (!LAZY && kb == 0) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) o[0][e] = bload16(ro, (lane * 128 + 4 * e) * 4);
