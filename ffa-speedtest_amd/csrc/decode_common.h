@@ -76,13 +76,35 @@ __device__ __forceinline__ int decode_span(const DecodeParams &p) { return p.spa
 struct DecodeUnit {
   int hkv, quad, Gu, row0;
 };
-__device__ __forceinline__ DecodeUnit decode_unit(const DecodeParams &p) {
+__device__ __forceinline__ DecodeUnit decode_unit(const DecodeParams &p, int y) {
   DecodeUnit u;
-  u.hkv = p.nq == 1 ? (int)blockIdx.y : (int)blockIdx.y / p.nq;
-  u.quad = (int)blockIdx.y - u.hkv * p.nq;
+  u.hkv = p.nq == 1 ? y : y / p.nq;
+  u.quad = y - u.hkv * p.nq;
   u.Gu = min(4, p.G - 4 * u.quad);
   u.row0 = u.hkv * p.G + 4 * u.quad;
   return u;
+}
+
+// Workgroup coordinates (span cg, unit y, sequence b) of a decode grid (span, unit, sequence).
+// Dispatch is round-robin over the 8 XCDs in linear workgroup order.  The paged layouts take the
+// unit fastest instead of the span: the spans of a (sequence, KV head) then land on one XCD
+// (with 8 or 16 units per sequence), whose L2 still holds their partials when the merge
+// workgroups of those rows, placed on the same XCD (merge_partials), read them in the next
+// kernel (config 2's step 12.78 -> 12.40 us).  The contiguous layouts keep the span fastest: four
+// KV heads share each 128-byte code line there, and their workgroups share it through one XCD's L2
+// (the paged order took the reference-layout config 2 from 16.1 to 17.9 us).
+struct GridPos {
+  int cg, y, b;
+};
+template <bool kUnitFastest>
+__device__ __forceinline__ GridPos grid_pos() {
+  if constexpr (!kUnitFastest) {
+    return GridPos{(int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z};
+  } else {
+    const int gl = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    const int r = gl / (int)gridDim.y;
+    return GridPos{r % (int)gridDim.x, gl - r * (int)gridDim.y, r / (int)gridDim.x};
+  }
 }
 
 // Pass 2: whether each prune block of the workgroup's span survives, from the coarse maxima pass 1

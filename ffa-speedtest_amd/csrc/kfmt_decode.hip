@@ -123,11 +123,14 @@ void kfmt_decode_kernel(const DecodeParams p) {
   constexpr int kLane = kRow / 4;      // bytes of one lane's 32 channels
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // grid (span, KV head, sequence), the span fastest (consecutive workgroups on different XCDs)
-  const int cg = blockIdx.x;  // workgroup index along the sequence = partial slot
-  const DecodeUnit un = decode_unit(p);  // KV head and the (at most 4) query rows of this workgroup
+  // grid (span, KV head, sequence), the span fastest (consecutive workgroups on different XCDs):
+  // the q2 decoder's paged order, the KV head fastest, took config 4 from 139.8 to 141.7 us (config
+  // 3 86.6 -> 86.1 us)
+  const GridPos gp = grid_pos<false>();
+  const int cg = gp.cg;  // workgroup index along the sequence = partial slot
+  const DecodeUnit un = decode_unit(p, gp.y);  // KV head and the (at most 4) query rows of this workgroup
   const int hkv = un.hkv;
-  const int b = blockIdx.z;
+  const int b = gp.b;
   // span: chunks of this workgroup (8, or 4 / 2 for small grids, where each wave owns one chunk
   // and waves past the span own none); slot (w, j) = the j-th chunk of the wave in place w of the
   // chunk order (wch below: the wave itself, or in SPEC wave w ^ 2).  The paged large-batch build

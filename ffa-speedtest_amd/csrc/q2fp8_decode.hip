@@ -156,13 +156,14 @@ __device__ __forceinline__ void q2fp8_decode_body(const DecodeParams &p) {
   constexpr bool kCF = SMODE == kChannelF32;  // per-channel fp32 / bf16 scales: dequantized in fp32
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // grid (span, KV head, sequence), the span along the sequence fastest: consecutive workgroups
-  // land on different XCDs (dispatch is round-robin over the 8 XCDs), so the residual/V traffic
-  // of a (sequence, KV head) with many kept chunks is spread over every XCD's memory path.
-  const int cg = blockIdx.x;  // workgroup index along the sequence = partial slot
-  const DecodeUnit un = decode_unit(p);  // KV head and the (at most 4) query rows of this workgroup
+  // grid (span, KV head, sequence); the paged layouts (small grids aside) place the workgroups
+  // with the KV head fastest, so that a (sequence, KV head)'s partials stay in one XCD's L2 for
+  // the merge (grid_pos)
+  const GridPos gp = grid_pos<LAYOUT == kPaged && !SPEC>();
+  const int cg = gp.cg;  // workgroup index along the sequence = partial slot
+  const DecodeUnit un = decode_unit(p, gp.y);  // KV head and the (at most 4) query rows of this workgroup
   const int hkv = un.hkv;
-  const int b = blockIdx.z;
+  const int b = gp.b;
   // span: chunks of this workgroup (8, or 4 / 2 for small grids, where each wave owns one chunk and
   // waves past the span own none); slot (w, j) = wave w's j-th chunk
   const int span = SPEC ? kMinSpan : decode_span(p);
@@ -1076,9 +1077,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1))) void q
 // --------------------------------------------------------------------------
 template <bool LAZY>
 __device__ __forceinline__ void merge_partials(const DecodeParams &p) {
-  const int row = blockIdx.x >> 3;  // b * HQ + hq
-  const int slab = blockIdx.x & 7;  // 16-column slab
-  const int b = row / p.HQ;
+  // workgroup (KV head fastest, then 16-column slab, then the head's query rows): the paged decoders'
+  // partials of a KV head sit in one XCD's L2, and so does every slab workgroup of a row (one read
+  // of its m and l from the HBM)
+  const int mh = (int)blockIdx.x % p.HKV;
+  const int mr = (int)blockIdx.x / p.HKV;
+  const int slab = mr & 7;  // 16-column slab
+  const int mq = mr >> 3;   // b * G + query row within the group
+  const int b = mq / p.G;
+  const int row = b * p.HQ + mh * p.G + (mq - b * p.G);  // b * HQ + hq
   const int lane = threadIdx.x;
   const int span_tok = decode_span(p) * kPage;
   // the launch's slots (from T): the m, l (and eager o) loads are sized by them and issued before
