@@ -1134,6 +1134,8 @@ extern "C" int ffa_kfmt_decode(const ffa_kfmt_decode_args *a, void *stream) {
 
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid(p.nwg, a->HKV * p.nq, a->B);
+  if ((long long)grid.x * grid.y * grid.z > 0x7fffffffLL)  // the kernels number workgroups in 32 bits
+    return ffa_set_error_internal(FFA_E_UNSUPPORTED, "decode grid of more than 2^31 - 1 workgroups");
   // one pass (pass 0), or (G > 4, SBS > 512) the maxima pass 1 and then the deciding pass 2
   const bool two = p.pmax != nullptr;
   for (int pass = two ? 1 : 0; pass <= (two ? 2 : 0); ++pass) {

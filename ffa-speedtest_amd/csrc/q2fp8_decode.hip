@@ -1472,6 +1472,8 @@ static int decode_params(const ffa_q2fp8_decode_args *a, ffa::DecodeParams &p) {
 
 static int launch_stage1(const ffa_q2fp8_decode_args *a, const ffa::DecodeParams &p0, hipStream_t st) {
   dim3 grid(p0.nwg, a->HKV * p0.nq, a->B);
+  if ((long long)grid.x * grid.y * grid.z > 0x7fffffffLL)  // the kernels number workgroups in 32 bits
+    return ffa_set_error_internal(FFA_E_UNSUPPORTED, "decode grid of more than 2^31 - 1 workgroups");
   // one pass (pass 0), or (G > 4, SBS > 512) the maxima pass 1 and then the deciding pass 2
   const bool two = p0.pmax != nullptr;
   for (int pass = two ? 1 : 0; pass <= (two ? 2 : 0); ++pass) {

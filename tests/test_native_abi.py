@@ -136,6 +136,20 @@ def test_invalid_arguments_are_rejected_without_launch():
     assert L.ffa_kfmt_decode(ctypes.byref(k), None) == -1 and b"num_pages" in L.ffa_last_error()
     k.num_pages, k.bt_stride = 4, 1
     assert L.ffa_kfmt_decode(ctypes.byref(k), None) == -1 and b"block table" in L.ffa_last_error()
+    # a grid of more than 2^31 - 1 workgroups (the kernels number them in 32 bits): 32768 spans of
+    # 512 tokens x 8 KV heads x 65535 sequences, refused before any launch
+    k = N.KfmtArgs()
+    k.B, k.T, k.HQ, k.HKV, k.BS, k.SBS = 65535, 1 << 24, 32, 8, 64, 64
+    k.q_dtype, k.out_dtype, k.v_dtype, k.res_dtype = N.DT_BF16, N.DT_BF16, N.DT_BF16, N.DT_NONE
+    k.layout, k.k_format, k.scale_kind = N.LAYOUT_CONTIG, N.KFMT_FP8_E4M3, N.KSCALE_NONE
+    k.nparts, k.ntbs = 1 << 15, (1 << 24) // 64
+    assert L.ffa_kfmt_decode(ctypes.byref(k), None) == -2 and b"2^31" in L.ffa_last_error()
+    a = N.DecodeArgs()
+    a.B, a.T, a.HQ, a.HKV, a.BS, a.SBS = 65535, 1 << 24, 32, 8, 64, 64
+    a.q_dtype, a.out_dtype, a.v_dtype, a.res_dtype = N.DT_BF16, N.DT_BF16, N.DT_BF16, N.DT_NONE
+    a.scale_dtype, a.scale_mode, a.layout = N.DT_F16, N.SCALE_CHANNEL, N.LAYOUT_CONTIG
+    a.nparts, a.ntbs = 1 << 15, (1 << 24) // 64
+    assert L.ffa_q2fp8_decode(ctypes.byref(a), None) == -2 and b"2^31" in L.ffa_last_error()
 
 
 def test_drop_in_signatures_match_reference():
