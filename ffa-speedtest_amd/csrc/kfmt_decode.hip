@@ -128,7 +128,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
   // place the KV head fastest instead, so that a (sequence, KV head)'s partials stay in one XCD's
   // L2 for the merge (grid_pos).  The paged order of the q2 decoder, the KV head fastest, took
   // config 4 from 139.8 to 141.7 us (config 3 86.6 -> 86.1 us)
-  const GridPos gp = grid_pos<LAYOUT == kContig && !k4>();
+  const GridPos gp = grid_pos<(LAYOUT == kContig && !k4) || (LAYOUT == kPaged && SPEC)>();
   const int cg = gp.cg;  // workgroup index along the sequence = partial slot
   const DecodeUnit un = decode_unit(p, gp.y);  // KV head and the (at most 4) query rows of this workgroup
   const int hkv = un.hkv;

@@ -159,7 +159,7 @@ __device__ __forceinline__ void q2fp8_decode_body(const DecodeParams &p) {
   // grid (span, KV head, sequence); the paged layouts (small grids aside) place the workgroups
   // with the KV head fastest, so that a (sequence, KV head)'s partials stay in one XCD's L2 for
   // the merge (grid_pos)
-  const GridPos gp = grid_pos<LAYOUT == kPaged && !SPEC>();
+  const GridPos gp = grid_pos<LAYOUT == kPaged>();
   const int cg = gp.cg;  // workgroup index along the sequence = partial slot
   const DecodeUnit un = decode_unit(p, gp.y);  // KV head and the (at most 4) query rows of this workgroup
   const int hkv = un.hkv;
