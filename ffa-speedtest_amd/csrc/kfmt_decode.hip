@@ -124,11 +124,11 @@ void kfmt_decode_kernel(const DecodeParams p) {
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // grid (span, KV head, sequence), the span fastest (consecutive workgroups on different XCDs);
-  // the contiguous 8-bit formats, whose K and V rows of a token give each KV head whole lines,
-  // place the KV head fastest instead, so that a (sequence, KV head)'s partials stay in one XCD's
-  // L2 for the merge (grid_pos).  The paged order of the q2 decoder, the KV head fastest, took
-  // config 4 from 139.8 to 141.7 us (config 3 86.6 -> 86.1 us)
-  const GridPos gp = grid_pos<(LAYOUT == kContig && !k4) || (LAYOUT == kPaged && SPEC)>();
+  // the contiguous 8-bit formats, whose K and V rows of a token give each KV head whole lines, and
+  // the paged small-grid builds place the KV head fastest instead, so that a (sequence, KV head)'s
+  // partials stay in one XCD's L2 for the merge (grid_pos).  In the paged large-batch build the KV
+  // head fastest took config 4 from 139.8 to 141.7 us (config 3 86.6 -> 86.1 us)
+  const GridPos gp = grid_pos<(LAYOUT == kContig && !k4) || (LAYOUT == kPaged && !RELOAD)>();
   const int cg = gp.cg;  // workgroup index along the sequence = partial slot
   const DecodeUnit un = decode_unit(p, gp.y);  // KV head and the (at most 4) query rows of this workgroup
   const int hkv = un.hkv;
