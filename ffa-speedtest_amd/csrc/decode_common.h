@@ -85,26 +85,24 @@ __device__ __forceinline__ DecodeUnit decode_unit(const DecodeParams &p, int y) 
   return u;
 }
 
-// Workgroup coordinates (span cg, unit y, sequence b) of a decode grid (span, unit, sequence).
-// Dispatch is round-robin over the 8 XCDs in linear workgroup order.  The paged layouts take the
-// unit fastest instead of the span: the spans of a (sequence, KV head) then land on one XCD
-// (with 8 or 16 units per sequence), whose L2 still holds their partials when the merge
-// workgroups of those rows, placed on the same XCD (merge_partials), read them in the next
-// kernel (config 2's step 12.78 -> 12.40 us).  The contiguous layouts keep the span fastest: four
-// KV heads share each 128-byte code line there, and their workgroups share it through one XCD's L2
-// (the paged order took the reference-layout config 2 from 16.1 to 17.9 us).
+// Workgroup coordinates (span cg, unit y, sequence b) of a decode workgroup.  Dispatch is
+// round-robin over the 8 XCDs in linear workgroup order (x fastest).  The grid is (span, unit,
+// sequence), or, for the builds that place the unit fastest, (unit, span, sequence), launched so
+// by the host: with 8 or 16 units per sequence the spans of a (sequence, KV head) then land on one
+// XCD, whose L2 still holds their partials when the merge workgroups of those rows, placed on the
+// same XCD (merge_partials), read them in the next kernel (config 2's step 12.78 -> 12.40 us).  The
+// layouts whose code lines hold several KV heads (the per-channel q2 rows, the 4-bit formats'
+// contiguous rows) keep the span fastest, so that the workgroups of one span's heads share each
+// line through one XCD's L2 (the unit first took the reference-layout config 2 from 16.1 to 17.9
+// us), and so does the other-format large-batch build (configs 3 and 4).  No division: the order
+// is the grid's own (the position arithmetic of a rotated order cost config 2 0.2 us).
 struct GridPos {
   int cg, y, b;
 };
 template <bool kUnitFastest>
 __device__ __forceinline__ GridPos grid_pos() {
-  if constexpr (!kUnitFastest) {
-    return GridPos{(int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z};
-  } else {
-    const int gl = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-    const int r = gl / (int)gridDim.y;
-    return GridPos{r % (int)gridDim.x, gl - r * (int)gridDim.y, r / (int)gridDim.x};
-  }
+  if constexpr (kUnitFastest) return GridPos{(int)blockIdx.y, (int)blockIdx.x, (int)blockIdx.z};
+  else return GridPos{(int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z};
 }
 
 // Pass 2: whether each prune block of the workgroup's span survives, from the coarse maxima pass 1

@@ -988,6 +988,8 @@ void kfmt_decode_kernel(const DecodeParams p) {
 // --------------------------------------------------------------------------
 template <int L, int F, int S, int R, int V>
 static hipError_t kfmt_launch(const ffa::DecodeParams &p, dim3 grid, hipStream_t st) {
+  // the builds that place the KV head fastest (grid_pos) take the grid (unit, span, sequence)
+  const dim3 gsw(grid.y, grid.x, grid.z);
   if constexpr (L == ffa::kPaged) {
     // the runtime-span build for small grids and for every span shorter than 8 chunks (the last
     // halving of a small grid's span can take it past the CU count); the large-batch build's span
@@ -995,19 +997,21 @@ static hipError_t kfmt_launch(const ffa::DecodeParams &p, dim3 grid, hipStream_t
     const int cus = ffa::device_cus();
     const bool small = cus > 0 && grid.x * grid.y * grid.z <= (unsigned)cus;
     if (small && p.span == ffa::kMinSpan)  // the role split of two-chunk spans
-      hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, false, true>), grid, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, false, true>), gsw, dim3(256), 0, st, p);
     else if (small || p.span < ffa::kChunksPerWG)
-      hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, false, false>), grid, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, false, false>), gsw, dim3(256), 0, st, p);
     else
       hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, true, false>), grid, dim3(256), 0, st, p);
   } else {
+    constexpr bool k4 = F == ffa::kFP4 || F == ffa::kNF4;
+    const dim3 g = k4 ? grid : gsw;  // the contiguous 8-bit formats place the KV head fastest
     const int cus = ffa::device_cus();
     if (cus > 0 && grid.x * grid.y * grid.z > (unsigned)cus)
-      hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, true, false>), grid, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, true, false>), g, dim3(256), 0, st, p);
     else if (p.span == ffa::kMinSpan)
-      hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, false, true>), grid, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, false, true>), g, dim3(256), 0, st, p);
     else
-      hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, false, false>), grid, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((ffa::kfmt_decode_kernel<L, F, S, R, V, false, false>), g, dim3(256), 0, st, p);
   }
   return hipGetLastError();
 }
@@ -1136,6 +1140,8 @@ extern "C" int ffa_kfmt_decode(const ffa_kfmt_decode_args *a, void *stream) {
   const dim3 grid(p.nwg, a->HKV * p.nq, a->B);
   if ((long long)grid.x * grid.y * grid.z > 0x7fffffffLL)  // the kernels number workgroups in 32 bits
     return ffa_set_error_internal(FFA_E_UNSUPPORTED, "decode grid of more than 2^31 - 1 workgroups");
+  if (grid.x > 65535)  // the builds that place the KV head fastest launch the spans as grid y
+    return ffa_set_error_internal(FFA_E_UNSUPPORTED, "more than 65535 workgroup spans per sequence");
   // one pass (pass 0), or (G > 4, SBS > 512) the maxima pass 1 and then the deciding pass 2
   const bool two = p.pmax != nullptr;
   for (int pass = two ? 1 : 0; pass <= (two ? 2 : 0); ++pass) {

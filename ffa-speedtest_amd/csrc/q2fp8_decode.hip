@@ -1077,15 +1077,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1))) void q
 // --------------------------------------------------------------------------
 template <bool LAZY>
 __device__ __forceinline__ void merge_partials(const DecodeParams &p) {
-  // workgroup (KV head fastest, then 16-column slab, then the head's query rows): the paged decoders'
-  // partials of a KV head sit in one XCD's L2, and so does every slab workgroup of a row (one read
-  // of its m and l from the HBM)
-  const int mh = (int)blockIdx.x % p.HKV;
-  const int mr = (int)blockIdx.x / p.HKV;
-  const int slab = mr & 7;  // 16-column slab
-  const int mq = mr >> 3;   // b * G + query row within the group
-  const int b = mq / p.G;
-  const int row = b * p.HQ + mh * p.G + (mq - b * p.G);  // b * HQ + hq
+  // grid (KV head, 8 x query row of the group + slab, sequence), the KV head fastest: the paged
+  // decoders' partials of a KV head sit in one XCD's L2, and so does every slab workgroup of a row
+  // (one read of its m and l from the HBM)
+  const int slab = blockIdx.y & 7;  // 16-column slab
+  const int b = blockIdx.z;
+  const int row = b * p.HQ + (int)blockIdx.x * p.G + (int)(blockIdx.y >> 3);  // b * HQ + hq
   const int lane = threadIdx.x;
   const int span_tok = decode_span(p) * kPage;
   // the launch's slots (from T): the m, l (and eager o) loads are sized by them and issued before
@@ -1248,7 +1245,7 @@ __global__ __launch_bounds__(64) void q2fp8_merge_sparse_kernel(const DecodePara
 
 // more than 256 query rows (8 sequences of 32 heads): the lazy merge
 hipError_t launch_merge(const DecodeParams &p, hipStream_t st) {
-  const dim3 grid((unsigned)(p.B * p.HQ * 8));
+  const dim3 grid((unsigned)p.HKV, (unsigned)(8 * p.G), (unsigned)p.B);
   if (p.B * p.HQ > 256)
     hipLaunchKernelGGL(q2fp8_merge_sparse_kernel, grid, dim3(64), 0, st, p);
   else
@@ -1344,7 +1341,9 @@ int device_cus() {
 }  // namespace ffa
 
 template <int L, int S, int R, int V>
-static hipError_t launch_decode(const ffa::DecodeParams &p, dim3 grid, hipStream_t st) {
+static hipError_t launch_decode(const ffa::DecodeParams &p, dim3 g0, hipStream_t st) {
+  // the paged builds place the KV head fastest: grid (unit, span, sequence) (grid_pos)
+  const dim3 grid = L == ffa::kPaged ? dim3(g0.y, g0.x, g0.z) : g0;
   // paged g32 with more workgroups than two per CU: the four-per-CU build of the kernel
   if constexpr (L == ffa::kPaged && S == ffa::kG32) {
     const int cus = ffa::device_cus();
@@ -1474,6 +1473,8 @@ static int launch_stage1(const ffa_q2fp8_decode_args *a, const ffa::DecodeParams
   dim3 grid(p0.nwg, a->HKV * p0.nq, a->B);
   if ((long long)grid.x * grid.y * grid.z > 0x7fffffffLL)  // the kernels number workgroups in 32 bits
     return ffa_set_error_internal(FFA_E_UNSUPPORTED, "decode grid of more than 2^31 - 1 workgroups");
+  if (grid.x > 65535)  // the builds that place the KV head fastest launch the spans as grid y
+    return ffa_set_error_internal(FFA_E_UNSUPPORTED, "more than 65535 workgroup spans per sequence");
   // one pass (pass 0), or (G > 4, SBS > 512) the maxima pass 1 and then the deciding pass 2
   const bool two = p0.pmax != nullptr;
   for (int pass = two ? 1 : 0; pass <= (two ? 2 : 0); ++pass) {

@@ -178,8 +178,9 @@ int ffa_q2fp8_decode_nparts(int T, int BS, int SBS);
 int ffa_q2fp8_decode_pieces(int HQ, int HKV, int T, int BS, int SBS);
 
 /* Both stages back to back on `stream`.  A stage-1 grid of more than 2^31 - 1 workgroups
- * (ceil(T / 512) x HKV * ceil(G / 4) x B) returns FFA_E_UNSUPPORTED before any launch; the same
- * holds for ffa_kfmt_decode. */
+ * (ceil(T / 512) x HKV * ceil(G / 4) x B), or of more than 65535 workgroup spans per sequence
+ * (T above 32M tokens), returns FFA_E_UNSUPPORTED before any launch; the same holds for
+ * ffa_kfmt_decode. */
 int ffa_q2fp8_decode(const ffa_q2fp8_decode_args *args, void *stream);
 
 /*

@@ -150,6 +150,13 @@ def test_invalid_arguments_are_rejected_without_launch():
     a.scale_dtype, a.scale_mode, a.layout = N.DT_F16, N.SCALE_CHANNEL, N.LAYOUT_CONTIG
     a.nparts, a.ntbs = 1 << 15, (1 << 24) // 64
     assert L.ffa_q2fp8_decode(ctypes.byref(a), None) == -2 and b"2^31" in L.ffa_last_error()
+    # more than 65535 spans of 512 tokens in one sequence (the span count is a grid dimension)
+    a.B, a.T = 1, (1 << 25) + 512
+    a.nparts, a.ntbs = 65537, a.T // 64
+    assert L.ffa_q2fp8_decode(ctypes.byref(a), None) == -2 and b"65535 workgroup spans" in L.ffa_last_error()
+    k.B, k.T = 1, (1 << 25) + 512
+    k.nparts, k.ntbs = 65537, k.T // 64
+    assert L.ffa_kfmt_decode(ctypes.byref(k), None) == -2 and b"65535 workgroup spans" in L.ffa_last_error()
 
 
 def test_drop_in_signatures_match_reference():
