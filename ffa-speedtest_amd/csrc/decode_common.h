@@ -85,6 +85,16 @@ __device__ __forceinline__ DecodeUnit decode_unit(const DecodeParams &p, int y) 
   return u;
 }
 
+// x / d for x >= 0 and d a power of two (SBS, spans of 64-token chunks): one shift.  A division by a
+// runtime value is a sequence of dependent scalar and vector instructions, which at the head of a
+// workgroup's chain costs it time (the position arithmetic of a rotated grid order cost config 2
+// 0.2 us per step).
+__device__ __forceinline__ int div_pow2(int x, int d) { return x >> __builtin_ctz((unsigned)d); }
+// x / BS for x >= 0: a shift when BS is a power of two (the usual case), else the division
+__device__ __forceinline__ int div_bs(const DecodeParams &p, int x) {
+  return (p.BS & (p.BS - 1)) == 0 ? div_pow2(x, p.BS) : x / p.BS;
+}
+
 // Workgroup coordinates (span cg, unit y, sequence b) of a decode workgroup.  Dispatch is
 // round-robin over the 8 XCDs in linear workgroup order (x fastest).  The grid is (span, unit,
 // sequence), or, for the builds that place the unit fastest, (unit, span, sequence), launched so
@@ -113,9 +123,9 @@ __device__ __forceinline__ GridPos grid_pos() {
 __device__ __forceinline__ void decide_blocks(const DecodeParams &p, int b, int hkv, int cw, int Tb, int *s_keep) {
   const int G = p.G, SBS = p.SBS;
   const int span_tok = 8 * 64;  // tokens of one workgroup span
-  const int nblk = SBS <= span_tok ? span_tok / SBS : 1;
-  const int per = SBS <= span_tok ? 1 : SBS / span_tok;                    // pieces per block
-  const int piece0 = SBS <= span_tok ? cw * 64 / SBS : (cw * 64 / SBS) * per;  // first piece of block 0
+  const int nblk = SBS <= span_tok ? div_pow2(span_tok, SBS) : 1;
+  const int per = SBS <= span_tok ? 1 : div_pow2(SBS, span_tok);  // pieces per block
+  const int piece0 = div_pow2(cw * 64, SBS) * per;                  // first piece of block 0
   const float *thr = p.th_in != nullptr ? p.th_in : p.th_out;
   for (int idx = threadIdx.x; idx < nblk * G; idx += blockDim.x) {
     const int blk = idx / G, r = idx - blk * G;
@@ -138,7 +148,7 @@ __device__ __forceinline__ uint64_t chunk_ballot(const DecodeParams &p, bool row
                                                  const int *s_keep, int cw, int c, int kc) {
   if (p.pass == 2) {
     const int rel = (c - cw) * 64 + 16 * kc;  // lane's first token relative to the span
-    const int blk = p.SBS <= 512 ? rel / p.SBS : 0;
+    const int blk = p.SBS <= 512 ? div_pow2(rel, p.SBS) : 0;
     return __ballot(row_ok && s_keep[blk] != 0);
   }
   return __ballot(row_ok && !(mb < th));
@@ -155,13 +165,13 @@ __device__ __forceinline__ void write_piece_max(const DecodeParams &p, size_t ro
     const bool first = SBS == 16 || (SBS == 32 ? (kc & 1) == 0 : kc == 0);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int jb = ((c0 + j) * 64 + 16 * kc) / SBS;
+      const int jb = div_pow2((c0 + j) * 64 + 16 * kc, SBS);
       if (first && jb < p.npieces) dst[jb] = mb[j];
     }
   } else if (SBS <= 512) {
-    const int wpb = max(SBS / 128, 1);  // waves per block
-    const int jb = c0 * 64 / SBS;
-    if (kc == 0 && wv % wpb == 0 && jb < p.npieces) dst[jb] = mb[0];
+    const int wpb = max(SBS >> 7, 1);  // waves per block
+    const int jb = div_pow2(c0 * 64, SBS);
+    if (kc == 0 && (wv & (wpb - 1)) == 0 && jb < p.npieces) dst[jb] = mb[0];
   } else if (kc == 0 && wv == 0 && cg < p.npieces) {
     dst[cg] = mb[0];
   }
@@ -212,11 +222,11 @@ __device__ __forceinline__ int append_page(const int32_t *bt, int bt_stride, int
 // sequence end, and the threshold is written by the sequence's first workgroup.
 __device__ __forceinline__ void write_empty_mask(int8_t *mask_row, int cg, int SBS, int ntbs, int span = kChunksPerWG) {
   if (SBS > span * kPage) {  // a block of several spans: its first span writes its byte
-    const int jb = cg * span * kPage / SBS;
-    if (threadIdx.x == 0 && (cg * span * kPage) % SBS == 0 && jb < ntbs) mask_row[jb] = 0;
+    const int jb = div_pow2(cg * span * kPage, SBS);
+    if (threadIdx.x == 0 && ((cg * span * kPage) & (SBS - 1)) == 0 && jb < ntbs) mask_row[jb] = 0;
     return;
   }
-  const int nblk = span * kPage / SBS;
+  const int nblk = div_pow2(span * kPage, SBS);
   for (int t = threadIdx.x; t < nblk; t += blockDim.x) {
     const int jb = cg * nblk + t;
     if (jb < ntbs) mask_row[jb] = 0;

@@ -185,9 +185,9 @@ void kfmt_decode_kernel(const DecodeParams p) {
   }
   FFA_STAMP(0);
   if (threadIdx.x < kChunksPerWG * kPage / 16) s_keep[threadIdx.x] = 0;
-  const int NTB = (Tb + p.BS - 1) / p.BS;
-  const int NTBS_b = NTB * (p.BS / p.SBS);
-  const int NTBk = (p.T + p.BS - 1) / p.BS;  // blocks of the block-scale tensor
+  const int NTB = div_bs(p, Tb + p.BS - 1);
+  const int NTBS_b = NTB * div_pow2(p.BS, p.SBS);
+  const int NTBk = div_bs(p, p.T + p.BS - 1);  // blocks of the block-scale tensor
   // probe windows: waves 0 and 1 (SPEC: 2 and 3, the waves with the operands)
   const bool do_probe = (p.th_in == nullptr) && wch < 2;
   const int pa = wch == 0 ? 0 : max(NTB - 1, 0) * 16;  // probe window (attn_kernel...q2fp8.py:58-73)
@@ -391,7 +391,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
         const int t = t0 + 4 * mrow + tau;
         xs[j][tau] = 1.f;
         if constexpr (kTokScale) {
-          const uint32_t si = scale_index(t, min(t, max(Tb - 1, 0)) / p.BS);
+          const uint32_t si = scale_index(t, div_bs(p, min(t, max(Tb - 1, 0))));
           xsw[j][tau] = scale_word(rsc, si, p.s_dtype);
           xsodd |= (si & 1u) << (4 * j + tau);
         }
@@ -640,7 +640,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
   if (p.th_in != nullptr) th = row_ok ? th_pre : INFINITY;
   else th = row_ok ? fmaxf(s_probe[0][ir], s_probe[1][ir]) - p.delta : INFINITY;
   if (SBS > 128) {
-    const int wpb = min(SBS / (kPage * kPPW), kWaves);  // waves per block (a block of several spans: all)
+    const int wpb = min(div_pow2(SBS, kPage * kPPW), kWaves);  // waves per block (a block of several spans: all)
     const int w0 = (wv / wpb) * wpb;
     float m2 = -INFINITY;
     for (int w = w0; w < w0 + wpb; ++w) m2 = fmaxf(m2, s_wmax[w][ir]);
@@ -720,7 +720,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
         const int t = t0 + 4 * mrow + tau;
         ksc[tau] = 1.f;
         if constexpr (kTokScale) {
-          const uint32_t si = scale_index(t, min(t, max(Tb - 1, 0)) / p.BS);
+          const uint32_t si = scale_index(t, div_bs(p, min(t, max(Tb - 1, 0))));
           ksw[tau] = scale_word(rsc, si, p.s_dtype);
           ksodd |= (si & 1u) << tau;
         }
@@ -913,7 +913,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
     int8_t *mrow_ptr = p.mask + ((size_t)b * p.HKV + hkv) * p.ntbs;
     const int t = threadIdx.x;
     if (SBS <= kPage) {
-      const int per = kPage / SBS;
+      const int per = div_pow2(kPage, SBS);
       if (t < kChunksPerWG * per && slot_owned(t / per)) {
         const int slot = t / per, k = t - slot * per;
         const uint64_t bl = ((uint64_t)s_bal[slot][1] << 32) | s_bal[slot][0];
@@ -923,8 +923,8 @@ void kfmt_decode_kernel(const DecodeParams p) {
                                     : bl != 0;
         if (jb < p.ntbs) mrow_ptr[jb] = (jb < NTBS_b && kk) ? 1 : 0;
       }
-    } else if (t < kChunksPerWG && ((cw + t) * kPage) % SBS == 0) {
-      const int jb = (cw + t) * kPage / SBS;
+    } else if (t < kChunksPerWG && (((cw + t) * kPage) & (SBS - 1)) == 0) {
+      const int jb = div_pow2((cw + t) * kPage, SBS);
       const bool kk = (s_bal[t][0] | s_bal[t][1]) != 0;
       if (jb < p.ntbs) mrow_ptr[jb] = (jb < NTBS_b && kk) ? 1 : 0;
     }

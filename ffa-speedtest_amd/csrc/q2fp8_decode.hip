@@ -232,8 +232,8 @@ __device__ __forceinline__ void q2fp8_decode_body(const DecodeParams &p) {
   }
   FFA_STAMP(0);
   if (threadIdx.x < kChunksPerWG * kPage / 16) s_keep[threadIdx.x] = 0;
-  const int NTB = (Tb + p.BS - 1) / p.BS;
-  const int NTBS_b = NTB * (p.BS / p.SBS);
+  const int NTB = div_bs(p, Tb + p.BS - 1);
+  const int NTBS_b = NTB * div_pow2(p.BS, p.SBS);
   // probe windows: waves 0 and 1 (SPEC: 2 and 3, which score)
   const bool do_probe = (p.th_in == nullptr) && wch < 2;
   const int pa = wch == 0 ? 0 : max(NTB - 1, 0) * 16;  // probe window (attn_kernel...q2fp8.py:58-73)
@@ -604,7 +604,7 @@ __device__ __forceinline__ void q2fp8_decode_body(const DecodeParams &p) {
     th = row_ok ? fmaxf(s_probe[0][ir], s_probe[1][ir]) - p.delta : INFINITY;
   }
   if (SBS > 128) {
-    const int wpb = min(SBS / (kPage * kPPW), kWaves);  // waves per block (a block of several spans: all)
+    const int wpb = min(div_pow2(SBS, kPage * kPPW), kWaves);  // waves per block (a block of several spans: all)
     const int w0 = (wv / wpb) * wpb;
     float m2 = -INFINITY;
     for (int w = w0; w < w0 + wpb; ++w) m2 = fmaxf(m2, s_wmax[w][ir]);
@@ -722,8 +722,8 @@ __device__ __forceinline__ void q2fp8_decode_body(const DecodeParams &p) {
           mask_byte = (jb < NTBS_b && kk) ? 1 : 0;
         }
       }
-    } else if (t < kChunksPerWG && ((cw + t) * kPage) % SBS == 0) {
-      const int jb = (cw + t) * kPage / SBS;
+    } else if (t < kChunksPerWG && (((cw + t) * kPage) & (SBS - 1)) == 0) {
+      const int jb = div_pow2((cw + t) * kPage, SBS);
       const bool kk = (s_bal[t][0] | s_bal[t][1]) != 0;
       if (jb < p.ntbs) {
         mask_at = jb;
@@ -1088,9 +1088,9 @@ __device__ __forceinline__ void merge_partials(const DecodeParams &p) {
   // the launch's slots (from T): the m, l (and eager o) loads are sized by them and issued before
   // the sequence length arrives; slots past the sequence's own partials (stale workspace) are
   // masked to l = 0 once it has
-  const int nslots = min((p.T + span_tok - 1) / span_tok, p.nparts);
+  const int nslots = min(div_pow2(p.T + span_tok - 1, span_tok), p.nparts);
   const int Tb = p.seq_lens ? min(max(p.seq_lens[b], 0), p.T) : p.T;  // lengths beyond T are clamped to T
-  const int nparts = min((Tb + span_tok - 1) / span_tok, p.nparts);
+  const int nparts = min(div_pow2(Tb + span_tok - 1, span_tok), p.nparts);
   const brsrc rm = make_rsrc(p.m_buf + (size_t)row * p.nparts, nslots * 4);
   const brsrc rl = make_rsrc(p.l_buf + (size_t)row * p.nparts, nslots * 4);
   const brsrc ro = make_rsrc(p.o_buf + (size_t)row * p.nparts * 128 + 16 * slab, nslots > 0 ? ((nslots - 1) * 128 + 16) * 4 : 0);
