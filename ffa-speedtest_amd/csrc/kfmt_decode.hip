@@ -641,7 +641,7 @@ void kfmt_decode_kernel(const DecodeParams p) {
   else th = row_ok ? fmaxf(s_probe[0][ir], s_probe[1][ir]) - p.delta : INFINITY;
   if (SBS > 128) {
     const int wpb = min(div_pow2(SBS, kPage * kPPW), kWaves);  // waves per block (a block of several spans: all)
-    const int w0 = (wv / wpb) * wpb;
+    const int w0 = wv & ~(wpb - 1);  // wpb is 1, 2 or 4
     float m2 = -INFINITY;
     for (int w = w0; w < w0 + wpb; ++w) m2 = fmaxf(m2, s_wmax[w][ir]);
     mb[0] = mb[1] = m2;
@@ -914,8 +914,8 @@ void kfmt_decode_kernel(const DecodeParams p) {
     const int t = threadIdx.x;
     if (SBS <= kPage) {
       const int per = div_pow2(kPage, SBS);
-      if (t < kChunksPerWG * per && slot_owned(t / per)) {
-        const int slot = t / per, k = t - slot * per;
+      if (t < kChunksPerWG * per && slot_owned(div_pow2(t, per))) {
+        const int slot = div_pow2(t, per), k = t & (per - 1);
         const uint64_t bl = ((uint64_t)s_bal[slot][1] << 32) | s_bal[slot][0];
         const int jb = slot_chunk(slot) * per + k;
         const bool kk = SBS == 16   ? ((bl >> (16 * k)) & 0xffffull) != 0

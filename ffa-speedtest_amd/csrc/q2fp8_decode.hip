@@ -605,7 +605,7 @@ __device__ __forceinline__ void q2fp8_decode_body(const DecodeParams &p) {
   }
   if (SBS > 128) {
     const int wpb = min(div_pow2(SBS, kPage * kPPW), kWaves);  // waves per block (a block of several spans: all)
-    const int w0 = (wv / wpb) * wpb;
+    const int w0 = wv & ~(wpb - 1);  // wpb is 1, 2 or 4
     float m2 = -INFINITY;
     for (int w = w0; w < w0 + wpb; ++w) m2 = fmaxf(m2, s_wmax[w][ir]);
     mb[0] = mb[1] = m2;
